@@ -1,0 +1,203 @@
+"""Benchmark of the mivi-v4 quantized-inference hot path on one MI355X.
+
+Default line (BASELINE.json metric, configs[1]): the Q6_K output-head GEMV,
+W [65536 x 2048] from seeded N(0, 0.02), x [2048] ~ N(0, 1), reported as HBM
+GB/s of algorithmic bytes (W + x + y = 110,370,816 B per call). Weights are
+rotated over enough distinct copies (> 1 GB) that the 256 MB Infinity Cache
+cannot serve repeats; inputs are resident in HBM before timing.
+
+`extra` carries the other configs measured in the same run: the Q4_K GEMV
+(config 1) and, unless --no-decode, the 1.2B-shape hybrid decode (config 4:
+fp16 KV prefilled with 4096 tokens, 256 greedy steps) in tok/s.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-decode] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mivi-v4_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak); 1.2B hybrid decode tok/s at batch 1"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gemv_bench(torch, hip, t, rows, cols, steps, warmup, seed):
+    """Times `steps` launches over rotating weight copies; returns dict."""
+    stream = torch.cuda.current_stream()
+    w_host = hip.synth_random_weights(t, seed, rows, cols, 0.02)
+    x_host = hip.synth_normal(seed + 1, cols)
+    wbytes = w_host.nbytes
+    copies = max(4, -(-1_100_000_000 // wbytes))
+    base = torch.from_numpy(w_host).cuda()
+    ws = [base] + [base.clone() for _ in range(copies - 1)]
+    x = torch.from_numpy(x_host).cuda()
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    for i in range(warmup):
+        hip.quantized_matvec(y, t, ws[i % copies], x, rows, cols, stream=stream)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        hip.quantized_matvec(y, t, ws[i % copies], x, rows, cols, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1) / steps
+    algo = wbytes + cols * 4 + rows * 4
+    return dict(rows=rows, cols=cols, weight_bytes=wbytes, algo_bytes=algo, copies=copies,
+                ms_per_call=ev_ms, wall_ms_per_call=1e3 * wall / steps, gbs=algo / (ev_ms * 1e-3) / 1e9,
+                w_host=w_host, x_host=x_host)
+
+
+def cpu_gemv_baseline(t, w, x, rows, cols, budget_s):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    threads = min(os.cpu_count() or 1, 16)
+    pyoracle.set_threads(threads)
+    pyoracle.quantized_matvec(int(t), w, x, rows, cols)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        pyoracle.quantized_matvec(int(t), w, x, rows, cols)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    sec = (time.perf_counter() - t0) / n
+    algo = w.nbytes + cols * 4 + rows * 4
+    return dict(value=algo / sec / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"{n} calls of the oracle's AVX2 restatement of try_matvec (same {rows}x{cols} bytes), "
+                       f"{sec * 1e3:.2f} ms/call")
+
+
+def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
+    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid, weight_bytes_per_token
+    t0 = time.perf_counter()
+    ctx = prefill + steps
+    img = build_hybrid(**LFM2_1B2, ctx_len=65536, seed=2024)
+    log(f"decode: model built ({img.nbytes / 1e6:.0f} MB) in {time.perf_counter() - t0:.1f}s")
+    m = hip.Model(img, max_ctx=ctx, kv_precision=hip.KvPrecision.F16)
+    rng = __import__("numpy").random.default_rng(11)
+    prompt = rng.integers(0, LFM2_1B2["vocab"], prefill + 1)
+    t1 = time.perf_counter()
+    m.prefill(prompt[:-1])
+    log(f"decode: prefill {prefill} tokens in {time.perf_counter() - t1:.1f}s")
+    m.generate_greedy([int(prompt[-1])], [prefill], 8)   # warm-up + graph capture (re-prefills below)
+    m.reset_context()
+    m.prefill(prompt[:-1])
+    state = m.export_state(prefill) if cpu_budget_s > 0 else None
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    toks = m.generate_greedy([int(prompt[-1])], [prefill], steps)
+    dt = time.perf_counter() - t2
+    wb = weight_bytes_per_token(**LFM2_1B2)
+    kv_per_tok = 2 * 6 * 512 * 2  # fp16 K+V bytes per cached token (6 attention layers)
+    mean_t = prefill + (steps + 1) / 2
+    out = dict(tok_s=steps / dt, ms_per_token=1e3 * dt / steps, prefill=prefill, steps=steps,
+               bytes_per_token=wb + kv_per_tok * mean_t, weight_bytes_per_token=wb, kv_precision="f16",
+               working_ctx=ctx, first_tokens=[int(v) for v in toks[:8, 0]])
+    out["gbs"] = out["bytes_per_token"] * out["tok_s"] / 1e9
+    if cpu_budget_s > 0:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle
+        threads = min(os.cpu_count() or 1, 16)
+        pyoracle.set_threads(threads)
+        o = pyoracle.Model(img, max_ctx=ctx, kv_precision=pyoracle.KV_F16RT)
+        k, v, conv = state
+        ok, ov = o.kv_views()
+        row = m.kv_row_bytes()
+        per = ok.size // 6
+        import numpy as np
+        for l in range(6):
+            kh = k[l * prefill * row:(l + 1) * prefill * row].view(np.float16).astype(np.float32).view(np.uint8)
+            vh = v[l * prefill * row:(l + 1) * prefill * row].view(np.float16).astype(np.float32).view(np.uint8)
+            ok[l * per:l * per + kh.size] = kh
+            ov[l * per:l * per + vh.size] = vh
+        o.conv_view()[:] = conv
+        tok, n, t3 = int(prompt[-1]), 0, time.perf_counter()
+        while n < steps:
+            lg = o.forward(tok, prefill + n)
+            tok = pyoracle.argmax(lg)
+            n += 1
+            if time.perf_counter() - t3 > cpu_budget_s:
+                break
+        sec = (time.perf_counter() - t3) / n
+        out["cpu_tok_s"] = 1.0 / sec
+        out["cpu_sample"] = f"{n} greedy steps of the oracle forward_step after importing the GPU-built state"
+        out["cpu_threads"] = threads
+        out["speedup_vs_cpu"] = out["tok_s"] / out["cpu_tok_s"]
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--decode-prefill", type=int, default=4096)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the GEMV and decode shard by rows / sequences without exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import mivi_hip as hip
+    torch.cuda.set_device(0)
+    log(f"{hip.version()} on {torch.cuda.get_device_name(0)}")
+
+    q6 = gemv_bench(torch, hip, hip.GgmlType.Q6_K, 65536, 2048, a.steps, a.warmup, 100)
+    log(f"Q6_K GEMV 65536x2048: {q6['ms_per_call'] * 1e3:.1f} us/call, {q6['gbs']:.0f} GB/s")
+    q4 = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200)
+    log(f"Q4_K GEMV 8192x2048: {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s")
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_gemv_baseline(hip.GgmlType.Q6_K, q6["w_host"], q6["x_host"], 65536, 2048, a.cpu_seconds)
+        log(f"CPU oracle Q6_K GEMV: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    extra = {
+        "q4k_gemv_config1": {k: q4[k] for k in ("rows", "cols", "algo_bytes", "ms_per_call", "gbs", "copies")},
+    }
+    extra["q4k_gemv_config1"]["frac_of_peak"] = q4["gbs"] / HBM_PEAK_GBS
+    if not a.no_decode:
+        dec = decode_bench(torch, hip, a.decode_prefill, a.decode_steps, 0 if a.no_cpu else a.cpu_seconds)
+        log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['gbs']:.0f} GB/s)"
+            + (f", CPU {dec['cpu_tok_s']:.2f} tok/s" if "cpu_tok_s" in dec else ""))
+        extra["decode_config4"] = dec
+    line = {
+        "metric": METRIC,
+        "value": round(q6["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": q6["ms_per_call"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to Q6_K by this build's encoder; x ~ N(0,1))",
+        "config": {"workload": "config2_q6k_head_gemv", "rows": 65536, "cols": 2048, "weight_type": "Q6_K",
+                   "weight_copies": q6["copies"], "algo_bytes_per_call": q6["algo_bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(q6["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(q6["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

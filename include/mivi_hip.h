@@ -1,0 +1,216 @@
+/*
+ * mivi-hip: MI355X (gfx950) implementation of mivi-v4's quantized-inference
+ * hot path behind a plain C ABI.
+ *
+ * Every entry point replaces one function of the reference's Rust surface
+ * (crates/mivi-quant, crates/mivi-model); the citation on each declaration
+ * names it. Conventions:
+ *
+ *  - Buffers passed to compute entry points are GPU-accessible pointers
+ *    (hipMalloc'd device memory); their lengths are given in elements (f32)
+ *    or bytes (u8), exactly like the reference's slices, so the host can run
+ *    the reference's validation before anything is launched.
+ *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *    on it and the call returns; results are ready once the stream is
+ *    synchronized. Validation errors are returned synchronously and nothing
+ *    is written to `out` (reference: validate-before-write, types.rs:146-235,
+ *    lib.rs:152-169).
+ *  - Return value: 0 = Ok; 1..4 = the QuantError variants in declaration
+ *    order (types.rs:5-15); >= 100 = HIP / model errors. Details of the last
+ *    failure on the calling thread: mivi_hip_last_error().
+ */
+#ifndef MIVI_HIP_H
+#define MIVI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GgmlType ids (crates/mivi-quant/src/types.rs:22-52) */
+#define MIVI_GGML_F32 0
+#define MIVI_GGML_F16 1
+#define MIVI_GGML_Q8_0 8
+#define MIVI_GGML_Q4_K 12
+#define MIVI_GGML_Q6_K 14
+#define MIVI_GGML_BF16 30
+
+/* status codes */
+#define MIVI_OK 0
+#define MIVI_ERR_UNSUPPORTED_TYPE 1      /* QuantError::UnsupportedType(u32) */
+#define MIVI_ERR_BUFFER_TOO_SMALL 2      /* QuantError::BufferTooSmall{expected,actual} */
+#define MIVI_ERR_DIMENSION_MISALIGNED 3  /* QuantError::DimensionMisaligned{dim,block_size} */
+#define MIVI_ERR_ARITHMETIC_OVERFLOW 4   /* QuantError::ArithmeticOverflow */
+#define MIVI_ERR_HIP 100                 /* a HIP runtime call failed */
+#define MIVI_ERR_INVALID_ARGUMENT 101    /* null pointer / bad handle */
+#define MIVI_ERR_INVALID_TOKEN 110       /* ModelError::InvalidToken (model.rs:41-42) */
+#define MIVI_ERR_CONTEXT_OVERFLOW 111    /* ModelError::ContextOverflow (model.rs:43-44) */
+#define MIVI_ERR_GGUF 112                /* ModelError::Gguf (model.rs:27-28) */
+#define MIVI_ERR_MISSING_WEIGHT 113      /* ModelError::MissingWeight (model.rs:35-36) */
+#define MIVI_ERR_INVALID_CONFIG 114      /* ModelError::InvalidConfig (model.rs:37-38) */
+#define MIVI_ERR_KV_CACHE 115            /* ModelError::KvCache (model.rs:33-34) */
+#define MIVI_ERR_UNSUPPORTED 116         /* a model feature this build does not run */
+
+typedef struct mivi_error {
+    int32_t code;          /* one of MIVI_* above */
+    uint32_t type_id;      /* UnsupportedType payload */
+    size_t expected;       /* BufferTooSmall payload */
+    size_t actual;
+    size_t dim;            /* DimensionMisaligned payload */
+    size_t block_size;
+    char message[256];     /* formatted like the reference's Display impls */
+} mivi_error;
+
+/* Details of the last non-zero status returned on this thread. */
+int32_t mivi_hip_last_error(mivi_error* out);
+/* Library version string. */
+const char* mivi_hip_version(void);
+
+/* ---------------------------------------------------------------------
+ * mivi-quant
+ * ------------------------------------------------------------------- */
+
+/* crates/mivi-quant/src/lib.rs:75-134 quantized_matvec:
+ * out[n] = W[n, d] * x[d] for W in `ggml_type` (Q4_K, Q6_K, Q8_0, F16, BF16,
+ * F32). `out_len` may exceed n; the tail is left untouched (types.rs:312-328). */
+int32_t mivi_hip_quantized_matvec(float* out, size_t out_len, int32_t ggml_type,
+                                  const uint8_t* weights, size_t weights_len,
+                                  const float* x, size_t x_len, size_t n, size_t d,
+                                  void* stream);
+
+/* crates/mivi-quant/src/q4_k_m.rs:217-237 try_matvec_q4_k_m */
+int32_t mivi_hip_try_matvec_q4_k_m(float* out, size_t out_len, const uint8_t* weights,
+                                   size_t weights_len, const float* x, size_t x_len,
+                                   size_t n, size_t d, void* stream);
+/* crates/mivi-quant/src/q6_k.rs:202-221 try_matvec_q6_k */
+int32_t mivi_hip_try_matvec_q6_k(float* out, size_t out_len, const uint8_t* weights,
+                                 size_t weights_len, const float* x, size_t x_len,
+                                 size_t n, size_t d, void* stream);
+/* crates/mivi-quant/src/q8_0.rs:127-147 try_matvec_q8_0 */
+int32_t mivi_hip_try_matvec_q8_0(float* out, size_t out_len, const uint8_t* weights,
+                                 size_t weights_len, const float* x, size_t x_len,
+                                 size_t n, size_t d, void* stream);
+/* crates/mivi-quant/src/f16.rs:42-64 try_matvec_f16 */
+int32_t mivi_hip_try_matvec_f16(float* out, size_t out_len, const uint8_t* weights,
+                                size_t weights_len, const float* x, size_t x_len,
+                                size_t n, size_t d, void* stream);
+/* crates/mivi-quant/src/f16.rs:75-97 try_matvec_bf16 */
+int32_t mivi_hip_try_matvec_bf16(float* out, size_t out_len, const uint8_t* weights,
+                                 size_t weights_len, const float* x, size_t x_len,
+                                 size_t n, size_t d, void* stream);
+
+/* crates/mivi-quant/src/lib.rs:143-251 quantized_matmul_rows:
+ * out[batch, rows] = inputs[batch, cols] * W[rows, cols]^T. batch == 1 is the
+ * matvec path (lib.rs:173-182); batch >= 16 runs the MFMA tile kernel. */
+int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t ggml_type,
+                                       const uint8_t* weights, size_t weights_len,
+                                       const float* inputs, size_t inputs_len, size_t batch,
+                                       size_t rows, size_t cols, void* stream);
+
+/* crates/mivi-quant/src/lib.rs:35-72 dequantize_slice: bit-exact decode of
+ * out_len / block_size blocks (Q4_K, Q6_K, Q8_0) or of bytes_len / type_size
+ * elements (F16, BF16, F32). */
+int32_t mivi_hip_dequantize_slice(int32_t ggml_type, const uint8_t* bytes, size_t bytes_len,
+                                  float* out, size_t out_len, void* stream);
+
+/* crates/mivi-quant/src/q8_0.rs:31-58 quantize_f32_to_q8_0_block, applied to
+ * n_blocks consecutive 32-element blocks: dst holds n_blocks * 34 bytes. */
+int32_t mivi_hip_quantize_q8_0(const float* src, size_t src_len, uint8_t* dst, size_t dst_len,
+                               size_t n_blocks, void* stream);
+
+/* crates/mivi-quant/src/q8_0.rs:60-124 dot_q8_0_f32, applied to n pairs:
+ * out[i] = dot(q[32 i .. 32 i + 32], k_blocks[34 i .. 34 i + 34]). */
+int32_t mivi_hip_dot_q8_0_f32(const float* q, size_t q_len, const uint8_t* k_blocks,
+                              size_t k_len, float* out, size_t out_len, size_t n, void* stream);
+
+/* ---------------------------------------------------------------------
+ * mivi-model: one hybrid (ShortConv + GQA) model resident on the GPU
+ * ------------------------------------------------------------------- */
+
+/* KvPrecision (crates/mivi-kv/src/cache.rs:5-15) plus the half-precision
+ * layout this build adds. */
+#define MIVI_KV_F32 0
+#define MIVI_KV_Q8_0 1
+#define MIVI_KV_F16 2
+
+typedef struct mivi_model mivi_model;
+
+typedef struct mivi_model_info {
+    size_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, kv_dim;
+    size_t vocab_size, max_seq_len, ssm_conv_kernel, n_attn_layers, max_batch;
+    float rope_base, rms_norm_eps;
+    int32_t kv_precision, yarn;
+    float yarn_scale;
+    size_t weight_bytes;   /* device bytes of the packed weights */
+    size_t kv_bytes;       /* device bytes of K + V for all sequences */
+} mivi_model_info;
+
+/* crates/mivi-model/src/model.rs:105-233 Model::load_with_options, from an
+ * in-memory GGUF image (host memory; copied to the device, so the image may
+ * be freed afterwards). max_ctx = 0 selects the reference default (16384,
+ * capped at 65536, model.rs:132-138). max_batch >= 1 independent sequences
+ * (each with its own KV cache and ShortConv state). */
+int32_t mivi_hip_model_create(const uint8_t* gguf, size_t gguf_len, size_t max_ctx,
+                              int32_t kv_precision, size_t max_batch, mivi_model** out);
+void mivi_hip_model_destroy(mivi_model* m);
+int32_t mivi_hip_model_info(const mivi_model* m, mivi_model_info* out);
+
+/* model.rs:494-497 Model::reset_context (all sequences) */
+int32_t mivi_hip_model_reset(mivi_model* m);
+
+/* model.rs:336-433 Model::forward_step for sequence `seq`. With
+ * compute_logits != 0 the logits are copied to `logits_host` (vocab_size
+ * floats, host memory) when it is non-NULL. Synchronous. */
+int32_t mivi_hip_model_forward_step(mivi_model* m, size_t seq, uint32_t token, size_t pos,
+                                    int32_t compute_logits, float* logits_host);
+
+/* model.rs:488-491 Model::forward: forward_step with logits. */
+int32_t mivi_hip_model_forward(mivi_model* m, size_t seq, uint32_t token, size_t pos,
+                               float* logits_host);
+
+/* Greedy decode loop (the argmax feedback of oracle_comparison_test.rs:37-50
+ * and sampler.rs:305-316, without penalties): feeds `token` at `pos`, then
+ * n_steps - 1 times the argmax of the previous logits; writes the n_steps
+ * argmax tokens to tokens_out (host). All sequences 0..batch-1 advance
+ * together, each from tokens[i] at pos[i] (host arrays). Runs from one
+ * captured HIP graph; synchronous. */
+int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, const uint32_t* tokens,
+                                       const size_t* pos, size_t n_steps, uint32_t* tokens_out);
+
+/* Token-by-token prompt prefill of one sequence (model.rs:499-606 with
+ * PrefillStrategy::Token): forward_step(tokens[i], pos0 + i, false). */
+int32_t mivi_hip_model_prefill(mivi_model* m, size_t seq, const uint32_t* tokens, size_t n,
+                               size_t pos0);
+
+/* State export/import for one sequence (cache.rs:682-914, arena.rs:110-123
+ * semantics with raw layouts): K and V are [n_attn_layers, tokens, row] with
+ * row = kv_dim floats (F32), kv_dim halves (F16) or kv_dim/32*34 bytes
+ * (Q8_0); conv is [n_layers, dim, ssm_conv_kernel] floats. Host buffers. */
+int32_t mivi_hip_model_export_state(mivi_model* m, size_t seq, size_t tokens, void* k_out,
+                                    void* v_out, size_t kv_len, float* conv_out,
+                                    size_t conv_len);
+int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t tokens, const void* k_in,
+                                    const void* v_in, size_t kv_len, const float* conv_in,
+                                    size_t conv_len);
+
+/* ---------------------------------------------------------------------
+ * Synthetic inputs (no counterpart in the reference, which ships no K-quant
+ * quantizer): seeded SplitMix64 + Box-Muller normals and f32 -> Q4_K / Q6_K /
+ * Q8_0 encoders, host side, multithreaded. Used to build test and benchmark
+ * inputs; parity is always defined on the packed bytes they produce.
+ * ------------------------------------------------------------------- */
+/* n normals N(mean, std) from stream `seed` into out (host) */
+void mivi_synth_normal(uint64_t seed, float mean, float std, float* out, size_t n);
+/* rows x cols f32 (host) -> packed blocks (host); cols % block == 0 */
+int32_t mivi_synth_quantize(int32_t ggml_type, const float* src, size_t rows, size_t cols,
+                            uint8_t* dst, size_t dst_len);
+/* seeded N(0, std) weights directly into packed blocks (host) */
+int32_t mivi_synth_random_weights(int32_t ggml_type, uint64_t seed, float std, size_t rows,
+                                  size_t cols, uint8_t* dst, size_t dst_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,102 @@
+// Shared device helpers and host error plumbing for the mivi-hip library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/mivi_hip.h"
+
+// ---------------------------------------------------------------- host side
+namespace mivi {
+
+// Records the details of a failing call in a thread-local slot and returns
+// its code (read back through mivi_hip_last_error).
+int32_t set_error(int32_t code, const char* fmt, ...);
+int32_t err_buffer_too_small(size_t expected, size_t actual);
+int32_t err_misaligned(size_t dim, size_t block_size);
+int32_t err_unsupported(int32_t type_id);
+int32_t err_overflow();
+int32_t clear_error();
+
+#define MIVI_HIP_CHECK(expr)                                                          \
+    do {                                                                              \
+        hipError_t e_ = (expr);                                                       \
+        if (e_ != hipSuccess)                                                         \
+            return ::mivi::set_error(MIVI_ERR_HIP, "%s failed: %s", #expr,            \
+                                     hipGetErrorString(e_));                          \
+    } while (0)
+
+inline int num_cus() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    }
+    return n;
+}
+
+}  // namespace mivi
+
+// -------------------------------------------------------------- device side
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
+    // exact widening (v_cvt_f32_f16)
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
+    return __uint_as_float((bits & 0xFFFFu) << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_half_bits(float f) {
+    // round to nearest even (v_cvt_f16_f32 under the default rounding mode)
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return (uint32_t)*(const uint16_t*)p;
+}
+
+// 16 bytes starting at a 2-byte aligned address. Never touches memory past
+// p + 16: reads [p - 2, p + 16) when p is 2 mod 4 (aligned dwords plus a
+// 16-bit tail) and [p, p + 16) otherwise.
+__device__ __forceinline__ u32x4 ld16_a2(const uint8_t* p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t* base = (const uint32_t*)(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3);
+    u32x4_a4 v = *(const u32x4_a4*)base;
+    const uint32_t tail16 = (uint32_t)*(const uint16_t*)(p + 14);
+    const uint32_t e = sh ? tail16 : v.w;
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
+    return r;
+}
+
+__device__ __forceinline__ float ubyte_f32(uint32_t w, int k) {
+    return (float)((w >> (8 * k)) & 0xFFu);
+}
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int s = WIDTH / 2; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));
+    return v;
+}

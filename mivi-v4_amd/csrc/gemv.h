@@ -1,0 +1,46 @@
+// Arguments of the dequant-fused GEMV launcher shared by the C ABI and the
+// decode step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mivi {
+
+// How a workgroup forms the activation vector it stages in LDS.
+enum GemvPrologue : int {
+    PRO_NONE = 0,     // x as given
+    PRO_RMSNORM = 1,  // (x * 1/sqrt(mean(x^2)+eps)) * w        (norm.rs:38-72)
+    PRO_SWIGLU = 2,   // silu(x) * x2                          (math.rs:76-100)
+    PRO_CONV = 3,     // ShortConv gate over in_proj = [B|C|X] (ssm.rs:80-140)
+};
+
+struct GemvSeg {
+    const uint8_t* W;  // rows of this segment
+    float* y;          // outputs of this segment
+    int n;             // rows
+};
+
+// y_s[r] (=|+=) W_s[r, :] . prologue(x) for up to three weight matrices that
+// share the input (q/k/v, gate/up).
+struct GemvArgs {
+    GemvSeg seg[3];
+    int nseg;
+    int K;                 // columns (multiple of the block size)
+    const float* x;        // input (dim K; for PRO_CONV the 3K in_proj output)
+    const float* x2;       // PRO_SWIGLU: up
+    const float* norm_w;   // PRO_RMSNORM: weight
+    float eps;
+    const float* conv_w;   // PRO_CONV: [K * ksize] weights (or shared [ksize])
+    int conv_mode;         // 0 full per-channel, 1 shared, 2 default 1/ksize
+    int ksize;
+    const float* st_in;    // PRO_CONV: previous state [K * ksize]
+    float* st_out;         // PRO_CONV: next state, written by workgroup 0
+    const int* phase;      // PRO_CONV: if set, st_in/st_out swap when *phase is odd
+    int accumulate;        // 1: y += result (residual add, vec_add of ffn.rs:106)
+};
+
+int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
+
+}  // namespace mivi

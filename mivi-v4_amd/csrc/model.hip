@@ -1,0 +1,1160 @@
+// The mivi-v4 hybrid (ShortConv + GQA) decode step on one MI355X.
+//
+// Reference: crates/mivi-model/src/{model,ssm,transformer,ffn,loader,gguf}.rs
+// and crates/mivi-kv/src/cache.rs. One `mivi_model` owns the packed weights
+// (the GGUF tensor-data section copied once to HBM), per-sequence run state,
+// the KV caches and the RoPE table. A decode step is a fixed sequence of
+// kernel launches that read the token/position of each sequence from device
+// memory, so one captured HIP graph replays every greedy step.
+//
+// Per layer (launches):
+//   ShortConv: in_proj GEMV with the RMSNorm fused into its input staging;
+//              out_proj GEMV whose staging computes B*X, the causal depthwise
+//              conv and the C gate (state ping-pong by a per-sequence phase)
+//              and whose output accumulates into the residual.
+//   GQA:       q|k|v as one 3-segment GEMV with fused RMSNorm; split-T
+//              attention (QK-norm, RoPE, KV store of the current token and
+//              online softmax fused); combine; wo GEMV accumulating into x.
+//   FFN:       gate|up as one 2-segment GEMV with fused RMSNorm; down GEMV
+//              with SwiGLU fused into its staging, accumulating into x.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "gemv.h"
+
+namespace mivi {
+int32_t launch_dequant(int32_t t, const uint8_t* src, float* out, size_t count, hipStream_t s);
+bool ggml_sizes(int32_t t, size_t* bs, size_t* ts);
+bool format_sizes(int32_t t, size_t* bs, size_t* ts);
+}  // namespace mivi
+
+using namespace mivi;
+
+namespace {
+
+constexpr int kWG = 256;
+constexpr int kChunk = 64;      // tokens per attention inner iteration
+constexpr int kMaxHd = 128;     // head_dim supported by the attention kernel
+constexpr int kMaxSplits = 512;
+
+// ------------------------------------------------------------------ GGUF
+
+struct GTensor {
+    int32_t type = 0;
+    std::vector<size_t> dims;
+    size_t offset = 0;  // absolute offset in the image
+    size_t nbytes = 0;
+};
+
+struct GMeta {
+    bool is_uint = false, is_float = false, is_u32 = false, is_array = false;
+    uint64_t u = 0;
+    double f = 0;
+    size_t n_strings = 0;       // array: number of string elements
+    uint64_t max_positive = 0;  // array: largest positive integer element
+};
+
+struct Gguf {
+    std::map<std::string, GMeta> meta;
+    std::map<std::string, GTensor> tensors;
+    size_t data_offset = 0;
+};
+
+struct Reader {
+    const uint8_t* p;
+    size_t n, pos = 0;
+    bool bad = false;
+    uint64_t u(int bytes) {
+        if (pos + (size_t)bytes > n) { bad = true; return 0; }
+        uint64_t v = 0;
+        for (int i = 0; i < bytes; i++) v |= (uint64_t)p[pos + i] << (8 * i);
+        pos += (size_t)bytes;
+        return v;
+    }
+    bool str(std::string* out) {
+        uint64_t len = u(8);
+        if (bad || len > (1u << 20) || pos + len > n) { bad = true; return false; }
+        if (out) out->assign((const char*)p + pos, (size_t)len);
+        pos += (size_t)len;
+        return true;
+    }
+};
+
+// gguf.rs:264-310 value types; records the as_usize / as_f32 views
+// (gguf.rs:59-84) of scalars and summaries of arrays.
+bool read_value(Reader& r, uint32_t type, GMeta* m, bool top) {
+    switch (type) {
+    case 0: case 1: case 2: case 3: case 4: case 5: case 10: case 11: {
+        static const int sz[] = {1, 1, 2, 2, 4, 4, 0, 0, 0, 0, 8, 8};
+        int b = sz[type];
+        uint64_t v = r.u(b);
+        bool sgn = type == 1 || type == 3 || type == 5 || type == 11;
+        int64_t sv = sgn ? (int64_t)(v << (64 - 8 * b)) >> (64 - 8 * b) : (int64_t)v;
+        if (m && (!sgn || sv >= 0)) {
+            uint64_t uv = sgn ? (uint64_t)sv : v;
+            if (top) { m->is_uint = true; m->u = uv; m->is_u32 = type == 4; }
+            else if (uv > m->max_positive) m->max_positive = uv;
+        }
+        return !r.bad;
+    }
+    case 6: {
+        uint32_t v = (uint32_t)r.u(4);
+        float f;
+        memcpy(&f, &v, 4);
+        if (m && top) { m->is_float = true; m->f = f; }
+        return !r.bad;
+    }
+    case 12: {
+        uint64_t v = r.u(8);
+        double f;
+        memcpy(&f, &v, 8);
+        if (m && top) { m->is_float = true; m->f = (double)(float)f; }
+        return !r.bad;
+    }
+    case 7: r.u(1); return !r.bad;
+    case 8:
+        if (m && !top) m->n_strings++;
+        return r.str(nullptr);
+    case 9: {
+        uint32_t et = (uint32_t)r.u(4);
+        uint64_t len = r.u(8);
+        if (r.bad || len > 10000000ull) return false;
+        if (m && top) m->is_array = true;
+        for (uint64_t i = 0; i < len; i++)
+            if (!read_value(r, et, top ? m : nullptr, false)) return false;
+        return true;
+    }
+    default: return false;
+    }
+}
+
+// gguf.rs:106-253
+int32_t parse_gguf(const uint8_t* p, size_t n, Gguf* g) {
+    Reader r{p, n};
+    if (n < 16) return set_error(MIVI_ERR_GGUF, "GGUF loading error: file too small");
+    uint32_t magic = (uint32_t)r.u(4);
+    if (magic != 0x46554747u) return set_error(MIVI_ERR_GGUF, "GGUF loading error: invalid magic 0x%X", magic);
+    uint32_t ver = (uint32_t)r.u(4);
+    if (ver != 2 && ver != 3) return set_error(MIVI_ERR_GGUF, "GGUF loading error: unsupported version %u", ver);
+    uint64_t nt = r.u(8), nm = r.u(8);
+    if (nt > 50000 || nm > 100000) return set_error(MIVI_ERR_GGUF, "GGUF loading error: counts exceed limits");
+    for (uint64_t i = 0; i < nm; i++) {
+        std::string key;
+        if (!r.str(&key)) break;
+        GMeta m;
+        uint32_t t = (uint32_t)r.u(4);
+        if (!read_value(r, t, &m, true)) { r.bad = true; break; }
+        g->meta[key] = m;
+    }
+    std::vector<std::pair<std::string, GTensor>> infos;
+    for (uint64_t i = 0; i < nt && !r.bad; i++) {
+        std::string name;
+        r.str(&name);
+        uint32_t nd = (uint32_t)r.u(4);
+        GTensor t;
+        for (uint32_t d = 0; d < nd && !r.bad; d++) t.dims.push_back((size_t)r.u(8));
+        t.type = (int32_t)r.u(4);
+        t.offset = (size_t)r.u(8);
+        infos.emplace_back(name, t);
+    }
+    if (r.bad) return set_error(MIVI_ERR_GGUF, "GGUF loading error: malformed file");
+    size_t align = 32;
+    auto it = g->meta.find("general.alignment");
+    if (it != g->meta.end() && it->second.is_u32 && it->second.u > 0) align = (size_t)it->second.u;
+    g->data_offset = (r.pos + align - 1) / align * align;
+    for (auto& kv : infos) {
+        GTensor t = kv.second;
+        size_t bs, ts, ne = 1;
+        if (!ggml_sizes(t.type, &bs, &ts))
+            return set_error(MIVI_ERR_GGUF, "GGUF loading error: unsupported type %d for tensor '%s'", t.type,
+                             kv.first.c_str());
+        for (size_t d : t.dims) ne *= d;
+        t.offset = g->data_offset + t.offset;
+        t.nbytes = (ne + bs - 1) / bs * ts;
+        if (t.offset + t.nbytes > n)
+            return set_error(MIVI_ERR_GGUF, "GGUF loading error: tensor '%s' exceeds the file", kv.first.c_str());
+        g->tensors[kv.first] = t;
+    }
+    return MIVI_OK;
+}
+
+// ------------------------------------------------------------- kernels
+
+struct AttnArgs {
+    const float* q;        // [n_heads * hd] raw projections of this sequence
+    const float* k;        // [kv_dim]
+    const float* v;
+    const float* q_norm;   // optional [hd]
+    const float* k_norm;
+    float eps;
+    const float* rope_cos; // [max_seq * hd/2]
+    const float* rope_sin;
+    uint8_t* kc;           // this sequence's cache for this layer: [max_seq * row_bytes]
+    uint8_t* vc;
+    size_t row_bytes;
+    const int* pos;        // device position of this sequence
+    int n_heads, n_kv_heads, hd, nsplit;
+    float scale;
+    float* part_m;         // [n_heads * nsplit]
+    float* part_l;
+    float* part_acc;       // [n_heads * nsplit * hd]
+};
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+// Embedding row of token tok (model.rs:355-366): bit-exact dequantization of
+// one row, generic over the stored format.
+__global__ void __launch_bounds__(kWG) embed_kernel(int32_t type, const uint8_t* table, size_t row_bytes,
+                                                    const uint32_t* tok, float* x, int dim) {
+    const uint8_t* row = table + (size_t)(*tok) * row_bytes;
+    for (int i = threadIdx.x; i < dim; i += kWG) {
+        float y = 0.f;
+        if (type == MIVI_GGML_Q6_K) {
+            const uint8_t* blk = row + (size_t)(i / 256) * 210;
+            int e = i % 256, half = e / 128, r = e % 128, grp = r / 32, l = r % 32;
+            const uint8_t* ql = blk + half * 64;
+            const uint8_t* qh = blk + 128 + half * 32;
+            const int8_t* sc = (const int8_t*)(blk + 192 + half * 8);
+            float d = half_bits_to_f32(ld_u16(blk + 208));
+            int lo = (grp & 1) ? ql[l + 32] : ql[l];
+            int nib = grp < 2 ? (lo & 0xF) : (lo >> 4);
+            int q = (nib | (((qh[l] >> (2 * grp)) & 3) << 4)) - 32;
+            y = d * (float)sc[l / 16 + 2 * grp] * (float)q;
+        } else if (type == MIVI_GGML_Q4_K) {
+            const uint8_t* blk = row + (size_t)(i / 256) * 144;
+            int e = i % 256, j = e / 64, r = e % 64, hi = r / 32, l = r % 32;
+            float d = half_bits_to_f32(ld_u16(blk)), dmin = half_bits_to_f32(ld_u16(blk + 2));
+            const uint8_t* sc = blk + 4;
+            int jj = 2 * j + hi;
+            uint32_t s, m;
+            if (jj < 4) { s = sc[jj] & 63; m = sc[jj + 4] & 63; }
+            else { s = (sc[jj + 4] & 0xF) | ((sc[jj - 4] >> 6) << 4); m = (sc[jj + 4] >> 4) | ((sc[jj] >> 6) << 4); }
+            uint32_t qb = blk[16 + j * 32 + l];
+            float dd = d * (float)s, mm = dmin * (float)m;
+            y = dd * (float)(hi ? (qb >> 4) : (qb & 0xF)) - mm;
+        } else if (type == MIVI_GGML_Q8_0) {
+            const uint8_t* blk = row + (size_t)(i / 32) * 34;
+            y = (float)(int8_t)blk[2 + i % 32] * half_bits_to_f32(ld_u16(blk));
+        } else if (type == MIVI_GGML_F16) {
+            y = half_bits_to_f32(ld_u16(row + 2 * (size_t)i));
+        } else if (type == MIVI_GGML_BF16) {
+            y = bf16_bits_to_f32(ld_u16(row + 2 * (size_t)i));
+        } else {
+            const uint8_t* p = row + 4 * (size_t)i;
+            y = __uint_as_float(p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24));
+        }
+        x[i] = y;
+    }
+}
+
+// Current token's head vector: optional per-head RMSNorm (transformer.rs:81-96)
+// then interleaved-pair RoPE (rope.rs:452-473). One thread per pair.
+__device__ __forceinline__ void prep_head(float* dst, const float* src, const float* nw, float eps, int hd,
+                                          const float* cs, const float* sn, float* red) {
+    // dst/src: hd values; executed by the whole workgroup
+    float ss = 0.f;
+    if (nw) {
+        for (int i = threadIdx.x; i < hd; i += kWG) ss = fmaf(src[i], src[i], ss);
+        ss = block_sum256(ss, red);
+    }
+    const float sc = nw ? 1.0f / sqrtf(ss / (float)hd + eps) : 1.0f;
+    for (int i = threadIdx.x; i < hd / 2; i += kWG) {
+        float v0 = src[2 * i], v1 = src[2 * i + 1];
+        if (nw) {
+            v0 = v0 * sc * nw[2 * i];
+            v1 = v1 * sc * nw[2 * i + 1];
+        }
+        float c = cs[i], s = sn[i];
+        dst[2 * i] = v0 * c - v1 * s;
+        dst[2 * i + 1] = v0 * s + v1 * c;
+    }
+}
+
+// Split-T GQA attention over one kv head (transformer.rs:112-301 with the KV
+// store of cache.rs:395-461). grid = (n_kv_heads, nsplit); each workgroup
+// scores a contiguous token range for the heads_per_kv query heads of its kv
+// head, one wave per query head, with an online softmax per 64-token chunk.
+// The workgroup whose range holds `pos` also quantizes the current K/V row
+// into the cache and uses that stored value for t = pos.
+template <int KVP>  // MIVI_KV_F32, MIVI_KV_Q8_0, MIVI_KV_F16
+__global__ void __launch_bounds__(kWG) attn_split_kernel(const AttnArgs a) {
+    __shared__ float kf[kChunk][kMaxHd + 1];
+    __shared__ float vf[kChunk][kMaxHd];
+    __shared__ float qs[4][kMaxHd];
+    __shared__ float ps[4][kChunk];
+    __shared__ float kcur[kMaxHd], vcur[kMaxHd];
+    __shared__ float red[4];
+    const int kvh = blockIdx.x, s = blockIdx.y;
+    const int hd = a.hd, half = hd / 2;
+    const int hpk = a.n_heads / a.n_kv_heads;
+    const int pos = *a.pos;
+    const int T = pos + 1;
+    const int per = (T + a.nsplit - 1) / a.nsplit;
+    const int t0 = s * per, t1 = min(T, t0 + per);
+    const float* cs = a.rope_cos + (size_t)pos * half;
+    const float* sn = a.rope_sin + (size_t)pos * half;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+    const bool owner = t0 <= pos && pos < t1;
+    if (owner) {
+        // current token: k rotated (and normed), v as is; store quantized
+        prep_head(kcur, a.k + kvh * hd, a.k_norm, a.eps, hd, cs, sn, red);
+        for (int i = threadIdx.x; i < hd; i += kWG) vcur[i] = a.v[kvh * hd + i];
+        __syncthreads();
+        uint8_t* krow = a.kc + (size_t)pos * a.row_bytes;
+        uint8_t* vrow = a.vc + (size_t)pos * a.row_bytes;
+        if (KVP == MIVI_KV_F32) {
+            for (int i = threadIdx.x; i < hd; i += kWG) {
+                ((float*)krow)[kvh * hd + i] = kcur[i];
+                ((float*)vrow)[kvh * hd + i] = vcur[i];
+            }
+        } else if (KVP == MIVI_KV_F16) {
+            for (int i = threadIdx.x; i < hd; i += kWG) {
+                uint32_t kb = f32_to_half_bits(kcur[i]), vb = f32_to_half_bits(vcur[i]);
+                ((uint16_t*)krow)[kvh * hd + i] = (uint16_t)kb;
+                ((uint16_t*)vrow)[kvh * hd + i] = (uint16_t)vb;
+                kcur[i] = half_bits_to_f32(kb);
+                vcur[i] = half_bits_to_f32(vb);
+            }
+        } else {
+            // q8_0.rs:31-58 per 32-value block; head kvh owns blocks
+            // [kvh*hd/32, (kvh+1)*hd/32) of the row (transformer.rs:170-171)
+            const int nbk = hd / 32;
+            if (threadIdx.x < 64 * 2 && (threadIdx.x >> 6) < 2) {
+                const bool isv = threadIdx.x >= 64;
+                float* cur = isv ? vcur : kcur;
+                uint8_t* row = isv ? vrow : krow;
+                for (int bi = 0; bi < nbk; bi++) {
+                    const int i = lane & 31;
+                    float xv = cur[bi * 32 + i];
+                    float am = fabsf(xv);
+#pragma unroll
+                    for (int sh = 16; sh >= 1; sh >>= 1) am = fmaxf(am, __shfl_xor(am, sh, 32));
+                    float d = am / 127.0f;
+                    float id = d != 0.0f ? 1.0f / d : 0.0f;
+                    float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
+                    uint32_t dh = f32_to_half_bits(d);
+                    uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
+                    if (lane < 32) {
+                        blk[2 + i] = (uint8_t)(int8_t)q;
+                        if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
+                        cur[bi * 32 + i] = q * half_bits_to_f32(dh);
+                    }
+                }
+            }
+        }
+    }
+    // query heads of this kv head: normed, rotated
+    for (int w = 0; w < hpk && w < 4; w++)
+        prep_head(qs[w], a.q + (kvh * hpk + w) * hd, a.q_norm, a.eps, hd, cs, sn, red);
+    __syncthreads();
+
+    float m_run = -INFINITY, l_run = 0.f;
+    float acc0 = 0.f, acc1 = 0.f;  // dims lane and lane + 64
+    const int h = kvh * hpk + wave;
+    for (int c0 = t0; c0 < t1; c0 += kChunk) {
+        const int nt = min(kChunk, t1 - c0);
+        // stage K/V rows [c0, c0+nt) of this kv head into LDS as f32
+        for (int idx = threadIdx.x; idx < nt * (hd / 4); idx += kWG) {
+            const int j = idx / (hd / 4), q4 = idx % (hd / 4);
+            const int t = c0 + j;
+            if (t == pos) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    kf[j][4 * q4 + e] = kcur[4 * q4 + e];
+                    vf[j][4 * q4 + e] = vcur[4 * q4 + e];
+                }
+                continue;
+            }
+            const uint8_t* kr = a.kc + (size_t)t * a.row_bytes;
+            const uint8_t* vr = a.vc + (size_t)t * a.row_bytes;
+            if (KVP == MIVI_KV_F32) {
+                f32x4 kv = *(const f32x4*)((const float*)kr + kvh * hd + 4 * q4);
+                f32x4 vv = *(const f32x4*)((const float*)vr + kvh * hd + 4 * q4);
+                kf[j][4 * q4] = kv.x; kf[j][4 * q4 + 1] = kv.y; kf[j][4 * q4 + 2] = kv.z; kf[j][4 * q4 + 3] = kv.w;
+                vf[j][4 * q4] = vv.x; vf[j][4 * q4 + 1] = vv.y; vf[j][4 * q4 + 2] = vv.z; vf[j][4 * q4 + 3] = vv.w;
+            } else if (KVP == MIVI_KV_F16) {
+                uint2 kb = *(const uint2*)((const uint16_t*)kr + kvh * hd + 4 * q4);
+                uint2 vb = *(const uint2*)((const uint16_t*)vr + kvh * hd + 4 * q4);
+                kf[j][4 * q4] = half_bits_to_f32(kb.x); kf[j][4 * q4 + 1] = half_bits_to_f32(kb.x >> 16);
+                kf[j][4 * q4 + 2] = half_bits_to_f32(kb.y); kf[j][4 * q4 + 3] = half_bits_to_f32(kb.y >> 16);
+                vf[j][4 * q4] = half_bits_to_f32(vb.x); vf[j][4 * q4 + 1] = half_bits_to_f32(vb.x >> 16);
+                vf[j][4 * q4 + 2] = half_bits_to_f32(vb.y); vf[j][4 * q4 + 3] = half_bits_to_f32(vb.y >> 16);
+            } else {
+                const int e = 4 * q4, bi = e / 32, w8 = e % 32;
+                const uint8_t* kb = kr + (size_t)(kvh * (hd / 32) + bi) * 34;
+                const uint8_t* vb = vr + (size_t)(kvh * (hd / 32) + bi) * 34;
+                const float kd = half_bits_to_f32(ld_u16(kb)), vd = half_bits_to_f32(ld_u16(vb));
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    kf[j][e + u] = (float)(int8_t)kb[2 + w8 + u] * kd;
+                    vf[j][e + u] = (float)(int8_t)vb[2 + w8 + u] * vd;
+                }
+            }
+        }
+        __syncthreads();
+        if (wave < hpk) {
+            // scores: lane j <-> token c0 + j
+            float sc = -INFINITY;
+            if (lane < nt) {
+                float d0 = 0.f, d1 = 0.f;
+                for (int i = 0; i < hd; i += 2) {
+                    d0 = fmaf(qs[wave][i], kf[lane][i], d0);
+                    d1 = fmaf(qs[wave][i + 1], kf[lane][i + 1], d1);
+                }
+                sc = (d0 + d1) * a.scale;
+            }
+            const float mc = wave_max(sc);
+            const float m_new = fmaxf(m_run, mc);
+            const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+            const float p = lane < nt ? expf(sc - m_new) : 0.f;
+            l_run = l_run * alpha + wave_sum(p);
+            ps[wave][lane] = p;
+            m_run = m_new;
+            // ps[wave] is written and read by this wave only
+            __builtin_amdgcn_wave_barrier();
+            float o0 = 0.f, o1 = 0.f;
+            for (int j = 0; j < nt; j++) {
+                const float pj = ps[wave][j];
+                if (lane < hd) o0 = fmaf(pj, vf[j][lane], o0);
+                if (lane + 64 < hd) o1 = fmaf(pj, vf[j][lane + 64], o1);
+            }
+            acc0 = acc0 * alpha + o0;
+            acc1 = acc1 * alpha + o1;
+        }
+        __syncthreads();
+    }
+    if (wave < hpk) {
+        const size_t pi = (size_t)h * a.nsplit + s;
+        if (lane == 0) {
+            a.part_m[pi] = m_run;
+            a.part_l[pi] = l_run;
+        }
+        if (lane < hd) a.part_acc[pi * hd + lane] = acc0;
+        if (lane + 64 < hd) a.part_acc[pi * hd + lane + 64] = acc1;
+    }
+}
+
+// Merges the split partials of every query head: out = sum_s acc_s e^(m_s-M)
+// / sum_s l_s e^(m_s-M), multiplied by the reciprocal like transformer.rs:293-298.
+__global__ void __launch_bounds__(128) attn_combine_kernel(const float* part_m, const float* part_l,
+                                                           const float* part_acc, float* out, int nsplit, int hd) {
+    const int h = blockIdx.x;
+    const float* pm = part_m + (size_t)h * nsplit;
+    const float* pl = part_l + (size_t)h * nsplit;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pm[s]);
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        float L = 0.f, o = 0.f;
+        if (M != -INFINITY) {
+            for (int s = 0; s < nsplit; s++) {
+                if (pm[s] == -INFINITY) continue;
+                const float w = expf(pm[s] - M);
+                L = fmaf(pl[s], w, L);
+                o = fmaf(part_acc[((size_t)h * nsplit + s) * hd + i], w, o);
+            }
+        }
+        out[(size_t)h * hd + i] = L > 0.f ? o * (1.0f / L) : 0.f;
+    }
+}
+
+// sampler.rs:305-316: index of the first strict maximum (NaN never wins).
+// Writes the token for the next step, records it, advances pos and the
+// ShortConv phase of the sequence.
+__global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, int n, uint32_t* tok, int* pos,
+                                                              int* phase, uint32_t* history, const int* step,
+                                                              int stride, int seq, int do_argmax) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    if (do_argmax) {
+        float best = -INFINITY;
+        int idx = 0x7FFFFFFF;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            float v = logits[i];
+            if (v > best || (v == best && i < idx)) { best = v; idx = i; }
+        }
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) {
+            float ov = __shfl_xor(best, sh, 64);
+            int oi = __shfl_xor(idx, sh, 64);
+            if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+        }
+        if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float b = bv[0];
+            int id = bi[0];
+            for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+                if (bv[w] > b || (bv[w] == b && bi[w] < id)) { b = bv[w]; id = bi[w]; }
+            if (id == 0x7FFFFFFF) id = 0;
+            *tok = (uint32_t)id;
+            if (history) history[(size_t)(*step) * stride + seq] = (uint32_t)id;
+        }
+    }
+    if (threadIdx.x == 0) {
+        *pos += 1;
+        *phase += 1;
+    }
+}
+
+__global__ void step_counter_kernel(int* step) { *step += 1; }
+
+__global__ void set_ctrl_kernel(uint32_t* tok, int* pos, uint32_t t, int p) {
+    *tok = t;
+    *pos = p;
+}
+
+__global__ void set_int_kernel(int* dst, int v) { *dst = v; }
+
+// --------------------------------------------------------------- model
+
+struct Mat {
+    int32_t type = 0;
+    const uint8_t* w = nullptr;  // device
+    size_t rows = 0, cols = 0;
+};
+
+struct Layer {
+    bool attn = false;
+    const float* norm = nullptr;       // attn_norm / ssm_norm (device f32)
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    Mat wq, wk, wv, wo, in_proj, out_proj, gate, up, down;
+    const float* conv = nullptr;
+    size_t conv_len = 0;
+    const float* ffn_norm = nullptr;
+    int cache_idx = -1;
+};
+
+struct SeqState {
+    float *x, *sc_in, *hb, *hb2, *q, *k, *v, *attn_out, *logits;
+    float *conv_a, *conv_b;  // ping-pong [n_layers * dim * ksize]
+    float *part_m, *part_l, *part_acc;
+    uint8_t *kc, *vc;        // [n_attn * max_seq * row_bytes]
+};
+
+struct Ctrl {  // device control block
+    uint32_t tok[64];
+    int pos[64];
+    int phase[64];
+    int step;
+};
+
+}  // namespace
+
+struct mivi_model {
+    mivi_model_info info{};
+    hipStream_t stream = nullptr;
+    uint8_t* d_weights = nullptr;
+    float* d_aux = nullptr;  // decoded f32 vectors
+    Mat embd, head;
+    const float* out_norm = nullptr;
+    std::vector<Layer> layers;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    std::vector<SeqState> seqs;
+    std::vector<void*> allocs;
+    Ctrl* ctrl = nullptr;
+    uint32_t* history = nullptr;  // [max_seq * max_batch]
+    size_t kv_row_bytes = 0;
+    int nsplit = 1;
+    hipGraphExec_t graph = nullptr;
+    size_t graph_batch = 0;
+
+    ~mivi_model() {
+        if (graph) hipGraphExecDestroy(graph);
+        for (void* p : allocs) hipFree(p);
+        if (stream) hipStreamDestroy(stream);
+    }
+    template <typename T>
+    int32_t alloc(T** p, size_t count) {
+        void* q = nullptr;
+        hipError_t e = hipMalloc(&q, std::max<size_t>(1, count * sizeof(T)));
+        if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "hipMalloc(%zu) failed: %s", count * sizeof(T), hipGetErrorString(e));
+        hipMemset(q, 0, std::max<size_t>(1, count * sizeof(T)));
+        allocs.push_back(q);
+        *p = (T*)q;
+        return MIVI_OK;
+    }
+};
+
+namespace {
+
+int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s) {
+    const mivi_model_info& c = m->info;
+    SeqState& st = m->seqs[b];
+    int32_t rc;
+    const int D = (int)c.dim, H = (int)c.hidden_dim, KV = (int)c.kv_dim;
+    {
+        size_t bs, ts;
+        format_sizes(m->embd.type, &bs, &ts);
+        size_t row_bytes = (c.dim * ts) / bs;  // model.rs:358-360
+        hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kWG), 0, s, m->embd.type, m->embd.w, row_bytes,
+                           &m->ctrl->tok[b], st.x, D);
+    }
+    for (size_t l = 0; l < c.n_layers; l++) {
+        const Layer& L = m->layers[l];
+        GemvArgs g = {};
+        if (!L.attn) {
+            if (c.ssm_conv_kernel == 0) continue;  // ssm.rs:60-62
+            // in_proj on rms_norm(x, ssm_norm)
+            g.seg[0] = {L.in_proj.w, st.sc_in, 3 * D};
+            g.nseg = 1; g.K = D; g.x = st.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            if ((rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
+            // out_proj on the gated conv, residual add into x
+            const size_t ks = c.ssm_conv_kernel;
+            g = {};
+            g.seg[0] = {L.out_proj.w, st.x, D};
+            g.nseg = 1; g.K = D; g.x = st.sc_in;
+            g.conv_w = L.conv;
+            g.conv_mode = (L.conv && L.conv_len >= (size_t)D * ks) ? 0 : (L.conv && L.conv_len >= ks) ? 1 : 2;
+            g.ksize = (int)ks;
+            g.st_in = st.conv_a + l * (size_t)D * ks;
+            g.st_out = st.conv_b + l * (size_t)D * ks;
+            g.phase = &m->ctrl->phase[b];
+            g.accumulate = 1;
+            if ((rc = launch_gemv_ex(L.out_proj.type, PRO_CONV, g, s))) return rc;
+        } else {
+            g.seg[0] = {L.wq.w, st.q, D};
+            g.seg[1] = {L.wk.w, st.k, KV};
+            g.seg[2] = {L.wv.w, st.v, KV};
+            g.nseg = 3; g.K = D; g.x = st.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
+                if ((rc = launch_gemv_ex(L.wq.type, PRO_RMSNORM, g, s))) return rc;
+            } else {
+                const Mat* ms[3] = {&L.wq, &L.wk, &L.wv};
+                for (int i = 0; i < 3; i++) {
+                    GemvArgs g1 = g;
+                    g1.seg[0] = g.seg[i];
+                    g1.nseg = 1;
+                    if ((rc = launch_gemv_ex(ms[i]->type, PRO_RMSNORM, g1, s))) return rc;
+                }
+            }
+            AttnArgs a = {};
+            a.q = st.q; a.k = st.k; a.v = st.v;
+            a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
+            a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
+            size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
+            a.kc = st.kc + (size_t)L.cache_idx * layer_bytes;
+            a.vc = st.vc + (size_t)L.cache_idx * layer_bytes;
+            a.row_bytes = m->kv_row_bytes;
+            a.pos = &m->ctrl->pos[b];
+            a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
+            a.nsplit = m->nsplit;
+            a.scale = 1.0f / sqrtf((float)c.head_dim);
+            a.part_m = st.part_m; a.part_l = st.part_l; a.part_acc = st.part_acc;
+            dim3 grid((unsigned)c.n_kv_heads, (unsigned)m->nsplit);
+            if (c.kv_precision == MIVI_KV_F32) hipLaunchKernelGGL(attn_split_kernel<MIVI_KV_F32>, grid, dim3(kWG), 0, s, a);
+            else if (c.kv_precision == MIVI_KV_F16) hipLaunchKernelGGL(attn_split_kernel<MIVI_KV_F16>, grid, dim3(kWG), 0, s, a);
+            else hipLaunchKernelGGL(attn_split_kernel<MIVI_KV_Q8_0>, grid, dim3(kWG), 0, s, a);
+            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads), dim3(64), 0, s, st.part_m, st.part_l,
+                               st.part_acc, st.attn_out, m->nsplit, (int)c.head_dim);
+            g = {};
+            g.seg[0] = {L.wo.w, st.x, D};
+            g.nseg = 1; g.K = D; g.x = st.attn_out; g.accumulate = 1;
+            if ((rc = launch_gemv_ex(L.wo.type, PRO_NONE, g, s))) return rc;
+        }
+        // ffn.rs:56-108
+        g = {};
+        g.seg[0] = {L.gate.w, st.hb, H};
+        g.seg[1] = {L.up.w, st.hb2, H};
+        g.nseg = 2; g.K = D; g.x = st.x; g.norm_w = L.ffn_norm; g.eps = c.rms_norm_eps;
+        if (L.gate.type == L.up.type) {
+            if ((rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g, s))) return rc;
+        } else {
+            GemvArgs g1 = g;
+            g1.nseg = 1;
+            if ((rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g1, s))) return rc;
+            g1.seg[0] = g.seg[1];
+            if ((rc = launch_gemv_ex(L.up.type, PRO_RMSNORM, g1, s))) return rc;
+        }
+        g = {};
+        g.seg[0] = {L.down.w, st.x, D};
+        g.nseg = 1; g.K = H; g.x = st.hb; g.x2 = st.hb2; g.accumulate = 1;
+        if ((rc = launch_gemv_ex(L.down.type, PRO_SWIGLU, g, s))) return rc;
+    }
+    if (logits) {
+        // model.rs:435-473
+        GemvArgs g = {};
+        g.seg[0] = {m->head.w, st.logits, (int)c.vocab_size};
+        g.nseg = 1; g.K = D; g.x = st.x; g.norm_w = m->out_norm; g.eps = c.rms_norm_eps;
+        if ((rc = launch_gemv_ex(m->head.type, m->out_norm ? PRO_RMSNORM : PRO_NONE, g, s))) return rc;
+    }
+    hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, st.logits, (int)c.vocab_size,
+                       &m->ctrl->tok[b], &m->ctrl->pos[b], &m->ctrl->phase[b], argmax ? m->history : nullptr,
+                       &m->ctrl->step, (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+void host_rope_table(std::vector<float>& cs, std::vector<float>& sn, size_t hd, size_t max_seq, float base,
+                     bool yarn, float scale) {
+    // rope.rs:50-122 with the YaRN parameters of model.rs:194-206
+    size_t half = hd / 2;
+    std::vector<float> inv(half);
+    for (size_t i = 0; i < half; i++) {
+        float bf = 1.0f / powf(base, (float)(2 * i) / (float)hd);
+        float f = bf;
+        if (yarn && scale > 1.0f) {
+            float orig = 4096.0f, beta_fast = 32.0f, beta_slow = 1.0f;
+            float low_rot = orig / std::max(beta_slow, 0.01f);
+            float high_rot = orig / std::max(beta_fast, 0.01f);
+            float wl = 2.0f * (float)M_PI / bf;
+            float ramp;
+            if (high_rot >= low_rot) ramp = wl < high_rot ? 0.0f : 1.0f;
+            else if (wl < high_rot) ramp = 0.0f;
+            else if (wl > low_rot) ramp = 1.0f;
+            else ramp = (wl - high_rot) / (low_rot - high_rot);
+            float sf = bf / scale;
+            f = (1.0f - ramp) * bf + ramp * sf;
+        }
+        inv[i] = f;
+    }
+    cs.resize(max_seq * half);
+    sn.resize(max_seq * half);
+    for (size_t p = 0; p < max_seq; p++)
+        for (size_t i = 0; i < half; i++) {
+            float ang = (float)p * inv[i];
+            cs[p * half + i] = cosf(ang);
+            sn[p * half + i] = sinf(ang);
+        }
+}
+
+int32_t model_error(int32_t code, const char* fmt, ...) {
+    char buf[240];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return set_error(code, "%s", buf);
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------- C ABI
+
+extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t max_ctx, int32_t kv_precision,
+                                         size_t max_batch, mivi_model** out) {
+    if (!img || !out) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (max_batch == 0 || max_batch > 64) return set_error(MIVI_ERR_INVALID_ARGUMENT, "max_batch must be 1..64");
+    if (kv_precision != MIVI_KV_F32 && kv_precision != MIVI_KV_F16 && kv_precision != MIVI_KV_Q8_0)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "unknown kv precision %d", kv_precision);
+    Gguf g;
+    int32_t rc = parse_gguf(img, len, &g);
+    if (rc) return rc;
+    auto meta_u = [&](const char* k2, const char* k1, size_t* dst) {
+        for (const char* k : {k2, k1}) {
+            auto it = g.meta.find(k);
+            if (it != g.meta.end() && it->second.is_uint) *dst = (size_t)it->second.u;
+        }
+    };
+    auto meta_f = [&](const char* k2, const char* k1, float* dst) {
+        for (const char* k : {k2, k1}) {
+            auto it = g.meta.find(k);
+            if (it != g.meta.end() && it->second.is_float) *dst = (float)it->second.f;
+        }
+    };
+    auto has = [&](const std::string& n) { return g.tensors.count(n) > 0; };
+    mivi_model_info c{};
+    // config.rs:123-159 defaults, loader.rs:44-177 overrides
+    c.dim = 1024; c.hidden_dim = 4608; c.n_layers = 16; c.n_heads = 16; c.n_kv_heads = 8;
+    c.vocab_size = 65536; c.max_seq_len = 128000; c.rope_base = 1000000.0f; c.rms_norm_eps = 1e-5f;
+    c.ssm_conv_kernel = 3;
+    meta_u("lfm2.context_length", "lfm.context_length", &c.max_seq_len);
+    meta_u("lfm2.embedding_length", "lfm.embedding_length", &c.dim);
+    meta_u("lfm2.feed_forward_length", "lfm.feed_forward_length", &c.hidden_dim);
+    meta_u("lfm2.block_count", "lfm.block_count", &c.n_layers);
+    meta_u("lfm2.attention.head_count", "lfm.attention.head_count", &c.n_heads);
+    for (const char* k : {"lfm2.attention.head_count_kv", "lfm.attention.head_count_kv"}) {
+        auto it = g.meta.find(k);
+        if (it == g.meta.end()) continue;
+        if (it->second.is_array) {
+            if (it->second.max_positive > 0) c.n_kv_heads = (size_t)it->second.max_positive;
+        } else if (it->second.is_uint) {
+            c.n_kv_heads = (size_t)it->second.u;
+        }
+    }
+    meta_f("lfm2.rope.freq_base", "lfm.rope.freq_base", &c.rope_base);
+    meta_f("lfm2.attention.layer_norm_rms_epsilon", "lfm.attention.layer_norm_rms_epsilon", &c.rms_norm_eps);
+    meta_u("lfm2.ssm.conv_kernel", "lfm.ssm.conv_kernel", &c.ssm_conv_kernel);
+    for (size_t i = 0; i < c.n_layers; i++) {
+        std::string a = "blk." + std::to_string(i) + ".ssm_conv.weight";
+        std::string b = "blk." + std::to_string(i) + ".shortconv.conv.weight";
+        const GTensor* t = has(a) ? &g.tensors[a] : has(b) ? &g.tensors[b] : nullptr;
+        if (t) {
+            size_t tot = 1;
+            for (size_t d : t->dims) tot *= d;
+            if (c.dim > 0 && tot >= c.dim && tot % c.dim == 0) { c.ssm_conv_kernel = tot / c.dim; break; }
+        }
+    }
+    {
+        auto it = g.meta.find("tokenizer.ggml.tokens");
+        if (it != g.meta.end() && it->second.is_array && it->second.n_strings > 0) c.vocab_size = it->second.n_strings;
+    }
+    c.head_dim = c.n_heads ? c.dim / c.n_heads : 64;
+    c.kv_dim = c.n_kv_heads * c.head_dim;
+    if (!c.dim || !c.n_heads || !c.n_kv_heads || c.dim % c.n_heads || c.n_heads % c.n_kv_heads || !c.n_layers)
+        return model_error(MIVI_ERR_INVALID_CONFIG, "Invalid model configuration");
+    size_t cap = max_ctx ? max_ctx : 16384;
+    cap = std::min<size_t>(cap, 65536);
+    c.max_seq_len = std::min(c.max_seq_len, cap);
+    c.max_batch = max_batch;
+    c.kv_precision = kv_precision;
+    if (c.head_dim > kMaxHd || c.head_dim % 4 != 0)
+        return model_error(MIVI_ERR_UNSUPPORTED, "head_dim %zu not supported (max %d, multiple of 4)", c.head_dim, kMaxHd);
+    if (c.n_heads / c.n_kv_heads > 4)
+        return model_error(MIVI_ERR_UNSUPPORTED, "more than 4 query heads per kv head");
+    if (kv_precision == MIVI_KV_Q8_0 && c.head_dim % 32 != 0)
+        return model_error(MIVI_ERR_UNSUPPORTED, "Q8_0 KV needs head_dim % 32 == 0");
+
+    mivi_model* m = new mivi_model();
+    auto fail = [&](int32_t code) { delete m; return code; };
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess)
+        return fail(set_error(MIVI_ERR_HIP, "hipStreamCreate failed"));
+
+    // weights: the tensor-data section, copied once
+    size_t data_len = len - g.data_offset;
+    if ((rc = m->alloc(&m->d_weights, data_len))) return fail(rc);
+    if (hipMemcpy(m->d_weights, img + g.data_offset, data_len, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(set_error(MIVI_ERR_HIP, "weight upload failed"));
+    c.weight_bytes = data_len;
+    auto dev = [&](const GTensor& t) { return m->d_weights + (t.offset - g.data_offset); };
+
+    // f32 vectors: F32 tensors are used in place; others are decoded once
+    std::vector<std::pair<const GTensor*, const float**>> to_decode;
+    size_t aux_len = 0;
+    auto vec = [&](const std::string& name, const float** dst, size_t* n_out) -> bool {
+        auto it = g.tensors.find(name);
+        if (it == g.tensors.end()) return false;
+        const GTensor& t = it->second;
+        size_t ne = 1;
+        for (size_t d : t.dims) ne *= d;
+        if (n_out) *n_out = ne;
+        if (t.type == MIVI_GGML_F32 && t.offset % 4 == 0) {
+            *dst = (const float*)dev(t);
+        } else {
+            size_t bs, ts;
+            if (!format_sizes(t.type, &bs, &ts)) return false;
+            to_decode.push_back({&t, dst});
+            aux_len += (ne + bs - 1) / bs * bs;
+        }
+        return true;
+    };
+    auto mat = [&](const std::string& name, Mat* dst) -> bool {
+        auto it = g.tensors.find(name);
+        if (it == g.tensors.end()) return false;
+        const GTensor& t = it->second;
+        dst->type = t.type;
+        dst->w = dev(t);
+        dst->cols = t.dims.empty() ? 0 : t.dims[0];
+        dst->rows = t.dims.size() > 1 ? t.dims[1] : dst->cols;
+        return true;
+    };
+    m->layers.resize(c.n_layers);
+    int n_attn = 0;
+    for (size_t i = 0; i < c.n_layers; i++) {
+        Layer& L = m->layers[i];
+        std::string p = "blk." + std::to_string(i) + ".";
+        L.attn = !(has(p + "ssm_in.weight") || has(p + "shortconv.in_proj.weight") || has(p + "shortconv.conv.weight"));
+        if (L.attn) {
+            L.cache_idx = n_attn++;
+            if (!vec(p + "attn_norm.weight", &L.norm, nullptr))
+                return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: %sattn_norm.weight", p.c_str()));
+            vec(p + "attn_q_norm.weight", &L.q_norm, nullptr);
+            vec(p + "attn_k_norm.weight", &L.k_norm, nullptr);
+            for (auto& nm : {std::make_pair("attn_q", &L.wq), std::make_pair("attn_k", &L.wk),
+                             std::make_pair("attn_v", &L.wv), std::make_pair("attn_output", &L.wo)})
+                if (!mat(p + nm.first + ".weight", nm.second))
+                    return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: %s%s.weight", p.c_str(), nm.first));
+        } else {
+            if (!vec(p + "ssm_norm.weight", &L.norm, nullptr) && !vec(p + "attn_norm.weight", &L.norm, nullptr))
+                return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: %sssm_norm.weight", p.c_str()));
+            if (!mat(p + "ssm_in.weight", &L.in_proj) && !mat(p + "shortconv.in_proj.weight", &L.in_proj))
+                return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: %sssm_in.weight", p.c_str()));
+            if (!mat(p + "ssm_out.weight", &L.out_proj) && !mat(p + "shortconv.out_proj.weight", &L.out_proj))
+                return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: %sssm_out.weight", p.c_str()));
+            if (!vec(p + "ssm_conv.weight", &L.conv, &L.conv_len)) vec(p + "shortconv.conv.weight", &L.conv, &L.conv_len);
+        }
+        if (!vec(p + "ffn_norm.weight", &L.ffn_norm, nullptr) || !mat(p + "ffn_gate.weight", &L.gate) ||
+            !mat(p + "ffn_up.weight", &L.up) || !mat(p + "ffn_down.weight", &L.down))
+            return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: %sffn_*", p.c_str()));
+    }
+    c.n_attn_layers = (size_t)n_attn;
+    if (!mat("token_embd.weight", &m->embd) && !mat("model.embed_tokens.weight", &m->embd))
+        return fail(model_error(MIVI_ERR_MISSING_WEIGHT, "Missing model weight: token_embd.weight"));
+    if (!vec("output_norm.weight", &m->out_norm, nullptr) && !vec("token_embd_norm.weight", &m->out_norm, nullptr))
+        vec("token_embd_norm", &m->out_norm, nullptr);
+    if (!mat("output.weight", &m->head) && !mat("lm_head.weight", &m->head)) m->head = m->embd;  // model.rs:455-459
+
+    // every projection must be a format the GEMV runs, with matching shapes
+    auto check = [&](const Mat& M, size_t rows, size_t cols, const char* what) -> int32_t {
+        size_t bs, ts;
+        if (!format_sizes(M.type, &bs, &ts)) return err_unsupported(M.type);
+        if (cols % bs) return err_misaligned(cols, bs);
+        size_t need = rows * (cols / bs) * ts;
+        (void)what;
+        if (M.rows * (M.cols / bs) * ts < need) return err_buffer_too_small(need, M.rows * (M.cols / bs) * ts);
+        return MIVI_OK;
+    };
+    for (size_t i = 0; i < c.n_layers; i++) {
+        const Layer& L = m->layers[i];
+        if (L.attn) {
+            if ((rc = check(L.wq, c.dim, c.dim, "q")) || (rc = check(L.wk, c.kv_dim, c.dim, "k")) ||
+                (rc = check(L.wv, c.kv_dim, c.dim, "v")) || (rc = check(L.wo, c.dim, c.dim, "o")))
+                return fail(rc);
+        } else {
+            if ((rc = check(L.in_proj, 3 * c.dim, c.dim, "in")) || (rc = check(L.out_proj, c.dim, c.dim, "out")))
+                return fail(rc);
+        }
+        if ((rc = check(L.gate, c.hidden_dim, c.dim, "gate")) || (rc = check(L.up, c.hidden_dim, c.dim, "up")) ||
+            (rc = check(L.down, c.dim, c.hidden_dim, "down")))
+            return fail(rc);
+    }
+    if ((rc = check(m->head, c.vocab_size, c.dim, "head"))) return fail(rc);
+    {
+        size_t bs, ts;
+        if (!format_sizes(m->embd.type, &bs, &ts) || c.dim % bs) return fail(err_unsupported(m->embd.type));
+        // every token id below vocab_size must have a row (model.rs:357-364)
+        if (m->embd.rows < c.vocab_size || m->embd.cols != c.dim)
+            return fail(model_error(MIVI_ERR_INVALID_CONFIG, "token_embd is %zux%zu, vocab %zu x dim %zu",
+                                    m->embd.rows, m->embd.cols, c.vocab_size, c.dim));
+    }
+
+    // decode non-F32 vectors
+    if (aux_len) {
+        if ((rc = m->alloc(&m->d_aux, aux_len))) return fail(rc);
+        size_t off = 0;
+        for (auto& td : to_decode) {
+            const GTensor& t = *td.first;
+            size_t bs, ts, ne = 1;
+            format_sizes(t.type, &bs, &ts);
+            for (size_t d : t.dims) ne *= d;
+            size_t count = bs == 1 ? ne : (ne + bs - 1) / bs;
+            if ((rc = launch_dequant(t.type, dev(t), m->d_aux + off, count, m->stream))) return fail(rc);
+            *td.second = m->d_aux + off;
+            off += (ne + bs - 1) / bs * bs;
+        }
+    }
+
+    // RoPE table (model.rs:194-212)
+    c.yarn = c.max_seq_len > 4096;
+    c.yarn_scale = c.yarn ? (float)c.max_seq_len / 4096.0f : 1.0f;
+    {
+        std::vector<float> cs, sn;
+        host_rope_table(cs, sn, c.head_dim, c.max_seq_len, c.rope_base, c.yarn, c.yarn_scale);
+        if ((rc = m->alloc(&m->rope_cos, cs.size())) || (rc = m->alloc(&m->rope_sin, sn.size()))) return fail(rc);
+        hipMemcpy(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
+        hipMemcpy(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+    }
+
+    // run state, KV caches
+    m->kv_row_bytes = kv_precision == MIVI_KV_Q8_0 ? (c.kv_dim / 32) * 34
+                    : kv_precision == MIVI_KV_F16 ? c.kv_dim * 2 : c.kv_dim * 4;
+    m->nsplit = (int)std::min<size_t>(kMaxSplits, std::max<size_t>(1, (c.max_seq_len + kChunk - 1) / kChunk));
+    size_t ks = std::max<size_t>(1, c.ssm_conv_kernel);
+    m->seqs.resize(max_batch);
+    for (auto& st : m->seqs) {
+        if ((rc = m->alloc(&st.x, c.dim)) || (rc = m->alloc(&st.sc_in, 3 * c.dim)) ||
+            (rc = m->alloc(&st.hb, c.hidden_dim)) || (rc = m->alloc(&st.hb2, c.hidden_dim)) ||
+            (rc = m->alloc(&st.q, c.dim)) || (rc = m->alloc(&st.k, c.kv_dim)) || (rc = m->alloc(&st.v, c.kv_dim)) ||
+            (rc = m->alloc(&st.attn_out, c.dim)) || (rc = m->alloc(&st.logits, c.vocab_size)) ||
+            (rc = m->alloc(&st.conv_a, c.n_layers * c.dim * ks)) || (rc = m->alloc(&st.conv_b, c.n_layers * c.dim * ks)) ||
+            (rc = m->alloc(&st.part_m, c.n_heads * m->nsplit)) || (rc = m->alloc(&st.part_l, c.n_heads * m->nsplit)) ||
+            (rc = m->alloc(&st.part_acc, c.n_heads * m->nsplit * c.head_dim)) ||
+            (rc = m->alloc(&st.kc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)) ||
+            (rc = m->alloc(&st.vc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)))
+            return fail(rc);
+    }
+    c.kv_bytes = 2 * max_batch * c.n_attn_layers * c.max_seq_len * m->kv_row_bytes;
+    if ((rc = m->alloc(&m->ctrl, 1)) || (rc = m->alloc(&m->history, c.max_seq_len * max_batch))) return fail(rc);
+    if (hipStreamSynchronize(m->stream) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return fail(set_error(MIVI_ERR_HIP, "model setup failed"));
+    m->info = c;
+    *out = m;
+    return clear_error();
+}
+
+extern "C" void mivi_hip_model_destroy(mivi_model* m) { delete m; }
+
+extern "C" int32_t mivi_hip_model_info(const mivi_model* m, mivi_model_info* out) {
+    if (!m || !out) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
+    *out = m->info;
+    return MIVI_OK;
+}
+
+extern "C" int32_t mivi_hip_model_reset(mivi_model* m) {
+    if (!m) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null model");
+    // arena.rs:90-108 clears the run state; cache.rs:287-289 only rewinds
+    const mivi_model_info& c = m->info;
+    size_t ks = std::max<size_t>(1, c.ssm_conv_kernel);
+    for (auto& st : m->seqs) {
+        MIVI_HIP_CHECK(hipMemsetAsync(st.x, 0, c.dim * 4, m->stream));
+        MIVI_HIP_CHECK(hipMemsetAsync(st.conv_a, 0, c.n_layers * c.dim * ks * 4, m->stream));
+        MIVI_HIP_CHECK(hipMemsetAsync(st.conv_b, 0, c.n_layers * c.dim * ks * 4, m->stream));
+        MIVI_HIP_CHECK(hipMemsetAsync(st.logits, 0, c.vocab_size * 4, m->stream));
+    }
+    MIVI_HIP_CHECK(hipMemsetAsync(m->ctrl, 0, sizeof(Ctrl), m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return clear_error();
+}
+
+static int32_t check_tok_pos(mivi_model* m, uint32_t token, size_t pos) {
+    if ((size_t)token >= m->info.vocab_size)
+        return set_error(MIVI_ERR_INVALID_TOKEN, "Invalid token ID: %u", token);  // model.rs:342-344
+    if (pos >= m->info.max_seq_len)
+        return set_error(MIVI_ERR_CONTEXT_OVERFLOW, "Context overflow: current pos %zu >= max_seq_len %zu", pos,
+                         m->info.max_seq_len);  // model.rs:345-350
+    return MIVI_OK;
+}
+
+static int32_t set_ctrl(mivi_model* m, size_t seq, uint32_t token, size_t pos) {
+    // the phase counter keeps running; only token and position are set
+    hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->tok[seq], &m->ctrl->pos[seq],
+                       token, (int)pos);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+extern "C" int32_t mivi_hip_model_forward_step(mivi_model* m, size_t seq, uint32_t token, size_t pos,
+                                               int32_t compute_logits, float* logits_host) {
+    if (!m || seq >= m->info.max_batch) return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad model or sequence");
+    int32_t rc = check_tok_pos(m, token, pos);
+    if (rc) return rc;
+    if ((rc = set_ctrl(m, seq, token, pos))) return rc;
+    if ((rc = enqueue_step(m, seq, compute_logits != 0, false, m->stream))) return rc;
+    if (compute_logits && logits_host)
+        MIVI_HIP_CHECK(hipMemcpyAsync(logits_host, m->seqs[seq].logits, m->info.vocab_size * 4,
+                                      hipMemcpyDeviceToHost, m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return clear_error();
+}
+
+extern "C" int32_t mivi_hip_model_forward(mivi_model* m, size_t seq, uint32_t token, size_t pos, float* logits) {
+    return mivi_hip_model_forward_step(m, seq, token, pos, 1, logits);
+}
+
+extern "C" int32_t mivi_hip_model_prefill(mivi_model* m, size_t seq, const uint32_t* tokens, size_t n, size_t pos0) {
+    if (!m || seq >= m->info.max_batch || (n && !tokens)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    for (size_t i = 0; i < n; i++) {
+        int32_t rc = check_tok_pos(m, tokens[i], pos0 + i);
+        if (rc) return rc;
+    }
+    for (size_t i = 0; i < n; i++) {
+        int32_t rc = set_ctrl(m, seq, tokens[i], pos0 + i);
+        if (rc) return rc;
+        if ((rc = enqueue_step(m, seq, false, false, m->stream))) return rc;
+        if ((i & 255) == 255) MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    }
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return clear_error();
+}
+
+extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, const uint32_t* tokens,
+                                                  const size_t* pos, size_t n_steps, uint32_t* tokens_out) {
+    if (!m || batch == 0 || batch > m->info.max_batch || !tokens || !pos || (n_steps && !tokens_out))
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    for (size_t b = 0; b < batch; b++) {
+        int32_t rc = check_tok_pos(m, tokens[b], pos[b]);
+        if (rc) return rc;
+        if (pos[b] + n_steps > m->info.max_seq_len)
+            return set_error(MIVI_ERR_CONTEXT_OVERFLOW, "Context overflow: current pos %zu >= max_seq_len %zu",
+                             pos[b] + n_steps - 1, m->info.max_seq_len);
+    }
+    if (n_steps == 0) return clear_error();
+    for (size_t b = 0; b < batch; b++) {
+        int32_t rc = set_ctrl(m, b, tokens[b], pos[b]);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step, 0);
+    if (!m->graph || m->graph_batch != batch) {
+        if (m->graph) {
+            hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+        hipGraph_t gr;
+        MIVI_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        int32_t rc = MIVI_OK;
+        for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, m->stream);
+        if (!rc) hipLaunchKernelGGL(step_counter_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step);
+        hipError_t e = hipStreamEndCapture(m->stream, &gr);
+        if (rc) return rc;
+        if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&m->graph, gr, nullptr, nullptr, 0);
+        hipGraphDestroy(gr);
+        if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "graph instantiate failed: %s", hipGetErrorString(e));
+        m->graph_batch = batch;
+    }
+    for (size_t i = 0; i < n_steps; i++) MIVI_HIP_CHECK(hipGraphLaunch(m->graph, m->stream));
+    std::vector<uint32_t> hist(n_steps * m->info.max_batch);
+    MIVI_HIP_CHECK(hipMemcpyAsync(hist.data(), m->history, hist.size() * 4, hipMemcpyDeviceToHost, m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    for (size_t i = 0; i < n_steps; i++)
+        for (size_t b = 0; b < batch; b++) tokens_out[i * batch + b] = hist[i * m->info.max_batch + b];
+    return clear_error();
+}
+
+static int32_t state_sizes(mivi_model* m, size_t seq, size_t tokens, size_t kv_len, size_t conv_len) {
+    if (!m || seq >= m->info.max_batch) return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad model or sequence");
+    if (tokens > m->info.max_seq_len)
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: Context length exceeded: attempted pos %zu >= max_seq_len %zu",
+                         tokens, m->info.max_seq_len);
+    size_t need = m->info.n_attn_layers * tokens * m->kv_row_bytes;
+    if (kv_len < need) return err_buffer_too_small(need, kv_len);
+    size_t cl = m->info.n_layers * m->info.dim * std::max<size_t>(1, m->info.ssm_conv_kernel);
+    if (conv_len < cl) return err_buffer_too_small(cl, conv_len);
+    return MIVI_OK;
+}
+
+extern "C" int32_t mivi_hip_model_export_state(mivi_model* m, size_t seq, size_t tokens, void* k_out, void* v_out,
+                                               size_t kv_len, float* conv_out, size_t conv_len) {
+    int32_t rc = state_sizes(m, seq, tokens, kv_len, conv_len);
+    if (rc) return rc;
+    const mivi_model_info& c = m->info;
+    SeqState& st = m->seqs[seq];
+    size_t lb = c.max_seq_len * m->kv_row_bytes, tb = tokens * m->kv_row_bytes;
+    for (size_t l = 0; l < c.n_attn_layers; l++) {
+        MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)k_out + l * tb, st.kc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
+        MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)v_out + l * tb, st.vc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
+    }
+    Ctrl ctl;
+    MIVI_HIP_CHECK(hipMemcpyAsync(&ctl, m->ctrl, sizeof(Ctrl), hipMemcpyDeviceToHost, m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    size_t cl = c.n_layers * c.dim * std::max<size_t>(1, c.ssm_conv_kernel);
+    const float* cur = (ctl.phase[seq] & 1) ? st.conv_b : st.conv_a;
+    MIVI_HIP_CHECK(hipMemcpy(conv_out, cur, cl * 4, hipMemcpyDeviceToHost));
+    return clear_error();
+}
+
+extern "C" int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t tokens, const void* k_in,
+                                               const void* v_in, size_t kv_len, const float* conv_in,
+                                               size_t conv_len) {
+    int32_t rc = state_sizes(m, seq, tokens, kv_len, conv_len);
+    if (rc) return rc;
+    const mivi_model_info& c = m->info;
+    SeqState& st = m->seqs[seq];
+    size_t lb = c.max_seq_len * m->kv_row_bytes, tb = tokens * m->kv_row_bytes;
+    for (size_t l = 0; l < c.n_attn_layers; l++) {
+        MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb, (const uint8_t*)k_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
+        MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb, (const uint8_t*)v_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
+    }
+    size_t cl = c.n_layers * c.dim * std::max<size_t>(1, c.ssm_conv_kernel);
+    // the imported state becomes phase 0's input buffer
+    MIVI_HIP_CHECK(hipMemcpyAsync(st.conv_a, conv_in, cl * 4, hipMemcpyHostToDevice, m->stream));
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->phase[seq], 0);
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return clear_error();
+}

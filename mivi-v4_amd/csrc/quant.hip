@@ -1,0 +1,802 @@
+// K-quant dequantization and dequant-fused GEMV kernels for gfx950, plus the
+// C-ABI entry points that mirror crates/mivi-quant's public functions.
+//
+// Layout of the packed formats (identical bytes to the reference):
+//   Q4_K  144 B / 256 values: f16 d | f16 dmin | 12 B 6-bit scales+mins | 128 B nibbles
+//         (crates/mivi-quant/src/q4_k_m.rs:11-58)
+//   Q6_K  210 B / 256 values: 128 B ql | 64 B qh | 16 x i8 scales | f16 d
+//         (crates/mivi-quant/src/q6_k.rs:8-38)
+//   Q8_0   34 B /  32 values: f16 d | 32 x i8 (crates/mivi-quant/src/q8_0.rs:11-22)
+//
+// GEMV design (one weight row = nb superblocks): a wave owns a tile of rows
+// and streams it with 16-byte loads; each lane owns one "unit" of a
+// superblock (a quarter: 64 values) and keeps it for U rows at once, so the
+// activation slice it reads from LDS is reused U times. Partial row sums are
+// reduced across the LPR lanes that share a row. Activations are staged once
+// per workgroup in LDS together with per-sub-block sums (the min term of
+// Q4_K and the -32 offset of Q6_K need sum(x) per sub-block).
+#include <algorithm>
+
+#include "common.h"
+#include "gemv.h"
+
+namespace {
+
+constexpr int kWG = 256;
+constexpr size_t kMaxLdsK = 12288;  // x in LDS up to this many columns
+
+// ------------------------------------------------------------------ dequant
+
+// q4_k_m.rs:24-58. One thread per (block, j, l): two outputs. The products
+// and the subtraction are separate roundings, like the reference.
+__global__ void __launch_bounds__(kWG) dequant_q4k_kernel(const uint8_t* __restrict__ src,
+                                                          float* __restrict__ out, size_t nblocks) {
+    size_t t = (size_t)blockIdx.x * kWG + threadIdx.x;
+    size_t b = t >> 7;
+    if (b >= nblocks) return;
+    int r = (int)(t & 127), j = r >> 5, l = r & 31;
+    const uint8_t* blk = src + b * 144;
+    float d = half_bits_to_f32(ld_u16(blk)), dmin = half_bits_to_f32(ld_u16(blk + 2));
+    const uint8_t* sc = blk + 4;
+    int j0 = 2 * j, j1 = 2 * j + 1;
+    uint32_t s0, m0, s1, m1;
+    if (j0 < 4) {
+        s0 = sc[j0] & 63; m0 = sc[j0 + 4] & 63;
+    } else {
+        s0 = (sc[j0 + 4] & 0xF) | ((sc[j0 - 4] >> 6) << 4);
+        m0 = (sc[j0 + 4] >> 4) | ((sc[j0] >> 6) << 4);
+    }
+    if (j1 < 4) {
+        s1 = sc[j1] & 63; m1 = sc[j1 + 4] & 63;
+    } else {
+        s1 = (sc[j1 + 4] & 0xF) | ((sc[j1 - 4] >> 6) << 4);
+        m1 = (sc[j1 + 4] >> 4) | ((sc[j1] >> 6) << 4);
+    }
+    float d1 = d * (float)s0, mv1 = dmin * (float)m0;
+    float d2 = d * (float)s1, mv2 = dmin * (float)m1;
+    uint32_t q = blk[16 + j * 32 + l];
+    float* o = out + b * 256 + j * 64;
+    o[l] = d1 * (float)(q & 0xF) - mv1;
+    o[l + 32] = d2 * (float)(q >> 4) - mv2;
+}
+
+// q6_k.rs:8-38. One thread per (block, half, l): four outputs, y = (d*sc)*q.
+__global__ void __launch_bounds__(kWG) dequant_q6k_kernel(const uint8_t* __restrict__ src,
+                                                          float* __restrict__ out, size_t nblocks) {
+    size_t t = (size_t)blockIdx.x * kWG + threadIdx.x;
+    size_t b = t >> 6;
+    if (b >= nblocks) return;
+    int r = (int)(t & 63), half = r >> 5, l = r & 31;
+    const uint8_t* blk = src + b * 210;
+    const uint8_t* ql = blk + half * 64;
+    const uint8_t* qh = blk + 128 + half * 32;
+    const int8_t* sc = (const int8_t*)(blk + 192 + half * 8);
+    float d = half_bits_to_f32(ld_u16(blk + 208));
+    int is = l / 16;
+    int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+    int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+    int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+    int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+    float* y = out + b * 256 + half * 128;
+    y[l] = d * (float)sc[is] * (float)q1;
+    y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+    y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+    y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+}
+
+// q8_0.rs:11-22
+__global__ void __launch_bounds__(kWG) dequant_q80_kernel(const uint8_t* __restrict__ src,
+                                                          float* __restrict__ out, size_t nblocks) {
+    size_t t = (size_t)blockIdx.x * kWG + threadIdx.x;
+    size_t b = t >> 5;
+    if (b >= nblocks) return;
+    int i = (int)(t & 31);
+    const uint8_t* blk = src + b * 34;
+    float d = half_bits_to_f32(ld_u16(blk));
+    out[b * 32 + i] = (float)(int8_t)blk[2 + i] * d;
+}
+
+// f16.rs:24-39 and lib.rs:57-69: element-wise widening (kind 0 f16, 1 bf16, 2 f32)
+__global__ void __launch_bounds__(kWG) dequant_dense_kernel(const uint8_t* __restrict__ src,
+                                                            float* __restrict__ out, size_t n, int kind) {
+    size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= n) return;
+    if (kind == 0) out[i] = half_bits_to_f32(src[2 * i] | (src[2 * i + 1] << 8));
+    else if (kind == 1) out[i] = bf16_bits_to_f32(src[2 * i] | (src[2 * i + 1] << 8));
+    else out[i] = __uint_as_float(src[4 * i] | (src[4 * i + 1] << 8) | (src[4 * i + 2] << 16) |
+                                  ((uint32_t)src[4 * i + 3] << 24));
+}
+
+// -------------------------------------------------------------- x staging
+
+__device__ __forceinline__ float silu_f(float g) {
+    // math.rs:76-82
+    return g <= -50.0f ? 0.0f : g / (1.0f + expf(-g));
+}
+
+// Workgroup-wide sum (all threads get the result). `red` holds >= 4 floats.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWG / 64; i++) s += red[i];
+    __syncthreads();
+    return s;
+}
+
+// Forms the activation vector for this GEMV in LDS (K floats) followed by
+// per-`G`-value sums taken sequentially in element order (G = 0: none).
+template <int PRO, int G>
+__device__ __forceinline__ void stage_input(float* lds, const mivi::GemvArgs& a) {
+    const int K = a.K;
+    __shared__ float red[kWG / 64];
+    if (PRO == mivi::PRO_NONE) {
+        if ((K & 3) == 0 && ((uintptr_t)a.x & 15) == 0) {
+            for (int i = threadIdx.x; i < K / 4; i += kWG) *(f32x4*)(lds + 4 * i) = *(const f32x4*)(a.x + 4 * i);
+        } else {
+            for (int i = threadIdx.x; i < K; i += kWG) lds[i] = a.x[i];
+        }
+    } else if (PRO == mivi::PRO_RMSNORM) {
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < K; i += kWG) {
+            float v = a.x[i];
+            lds[i] = v;
+            ss = fmaf(v, v, ss);
+        }
+        ss = block_sum(ss, red);
+        const float scale = 1.0f / sqrtf(ss / (float)K + a.eps);
+        for (int i = threadIdx.x; i < K; i += kWG) lds[i] = lds[i] * scale * a.norm_w[i];
+    } else if (PRO == mivi::PRO_SWIGLU) {
+        for (int i = threadIdx.x; i < K; i += kWG) lds[i] = silu_f(a.x[i]) * a.x2[i];
+    } else {  // PRO_CONV, ssm.rs:80-140: bx = B*X; shift state; conv; gate by C
+        const float* Bv = a.x;
+        const float* Cv = a.x + K;
+        const float* Xv = a.x + 2 * K;
+        const int ks = a.ksize;
+        const bool writer = blockIdx.x == 0;
+        const bool swap = a.phase && ((*a.phase) & 1);
+        const float* st_in = swap ? a.st_out : a.st_in;
+        float* st_out = swap ? (float*)a.st_in : a.st_out;
+        for (int d = threadIdx.x; d < K; d += kWG) {
+            const float bx = Bv[d] * Xv[d];
+            const float* old = st_in + (size_t)d * ks;
+            float conv = 0.0f;
+            for (int k = 0; k < ks; k++) {
+                const float sv = k + 1 < ks ? old[k + 1] : bx;
+                const float wv = a.conv_mode == 0 ? a.conv_w[(size_t)d * ks + k]
+                               : a.conv_mode == 1 ? a.conv_w[k] : 1.0f / (float)ks;
+                conv += wv * sv;
+                if (writer) st_out[(size_t)d * ks + k] = sv;
+            }
+            lds[d] = Cv[d] * conv;
+        }
+    }
+    __syncthreads();
+    if (G > 0) {
+        float* sums = lds + K;
+        for (int i = threadIdx.x; i < K / G; i += kWG) {
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < G; k++) s += lds[G * i + k];
+            sums[i] = s;
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ int seg_of(const mivi::GemvArgs& a, int r, int* local) {
+    int n0 = a.seg[0].n;
+    if (r < n0 || a.nseg == 1) { *local = r; return 0; }
+    int n1 = a.seg[1].n;
+    if (r < n0 + n1 || a.nseg == 2) { *local = r - n0; return 1; }
+    *local = r - n0 - n1;
+    return 2;
+}
+
+__device__ __forceinline__ const uint8_t* row_ptr(const mivi::GemvArgs& a, int r, size_t row_bytes) {
+    int lr;
+    int s = seg_of(a, r, &lr);
+    return a.seg[s].W + (size_t)lr * row_bytes;
+}
+
+__device__ __forceinline__ void store_row(const mivi::GemvArgs& a, int r, float v) {
+    int lr;
+    int s = seg_of(a, r, &lr);
+    float* y = a.seg[s].y + lr;
+    *y = a.accumulate ? *y + v : v;
+}
+
+// ------------------------------------------------------------------- Q4_K
+
+// Scale/min pair for sub-blocks 2g and 2g+1 (q4_k_m.rs:11-22) from the 12
+// scale bytes s0|s1|s2 (header dwords 1..3); g is per lane.
+__device__ __forceinline__ void q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2, int g,
+                                           uint32_t& sc0, uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
+    const uint32_t sh = 16u * (uint32_t)(g & 1);
+    if (g < 2) {
+        uint32_t lo = s0 >> sh, bm = s1 >> sh;
+        sc0 = lo & 63; sc1 = (lo >> 8) & 63;
+        m0 = bm & 63; m1 = (bm >> 8) & 63;
+    } else {
+        uint32_t lo = s2 >> sh, hy = s0 >> sh, hz = s1 >> sh;
+        sc0 = (lo & 0xF) | (((hy >> 6) & 3) << 4);
+        m0 = ((lo >> 4) & 0xF) | (((hz >> 6) & 3) << 4);
+        sc1 = ((lo >> 8) & 0xF) | (((hy >> 14) & 3) << 4);
+        m1 = ((lo >> 12) & 0xF) | (((hz >> 14) & 3) << 4);
+    }
+}
+
+// Partial dot of one Q4_K quarter (64 values: sub-blocks 2g, 2g+1) with x;
+// the reference's d1*sum(q x) - m1*sum(x) + d2*... form (q4_k_m.rs:144-214).
+__device__ __forceinline__ float q4k_unit(u32x4 hdr, u32x4 qa, u32x4 qb, int g, const float* xv,
+                                          float X0, float X1) {
+    float d = half_bits_to_f32(hdr.x), dmin = half_bits_to_f32(hdr.x >> 16);
+    uint32_t sc0, m0, sc1, m1;
+    q4k_scales(hdr.y, hdr.z, hdr.w, g, sc0, m0, sc1, m1);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+        const float* x0 = xv + 4 * i;       // low nibbles: values 4i..4i+3
+        const float* x1 = xv + 32 + 4 * i;  // high nibbles: values 32+4i..
+        a0 = fmaf(ubyte_f32(lo, 0), x0[0], a0);
+        a1 = fmaf(ubyte_f32(lo, 1), x0[1], a1);
+        a0 = fmaf(ubyte_f32(lo, 2), x0[2], a0);
+        a1 = fmaf(ubyte_f32(lo, 3), x0[3], a1);
+        b0 = fmaf(ubyte_f32(hi, 0), x1[0], b0);
+        b1 = fmaf(ubyte_f32(hi, 1), x1[1], b1);
+        b0 = fmaf(ubyte_f32(hi, 2), x1[2], b0);
+        b1 = fmaf(ubyte_f32(hi, 3), x1[3], b1);
+    }
+    float d1 = d * (float)sc0, mv1 = dmin * (float)m0;
+    float d2 = d * (float)sc1, mv2 = dmin * (float)m1;
+    return d1 * (a0 + a1) - mv1 * X0 + d2 * (b0 + b1) - mv2 * X1;
+}
+
+template <int LPR, int U, int PRO>
+__global__ void __launch_bounds__(kWG) gemv_q4k_kernel(const mivi::GemvArgs a) {
+    extern __shared__ float lds[];
+    stage_input<PRO, 32>(lds, a);
+    const int K = a.K, nb = K / 256;
+    const size_t row_bytes = (size_t)nb * 144;
+    const float* xsum = lds + K;
+    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    constexpr int RPG = 64 / LPR;   // rows per lane group
+    constexpr int RPT = RPG * U;    // rows per wave tile
+    const int lane = threadIdx.x & 63, lr = lane % LPR, sub = lane / LPR;
+    const int units = nb * 4;
+    const int ntiles = (n + RPT - 1) / RPT;
+    const int nwaves = gridDim.x * (kWG / 64);
+    for (int tile = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); tile < ntiles; tile += nwaves) {
+        const uint8_t* rows[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) rows[k] = row_ptr(a, min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
+        float acc[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) acc[k] = 0.f;
+        for (int u = lr; u < units; u += LPR) {
+            const int b = u >> 2, g = u & 3;
+            u32x4 hdr[U], qa[U], qb[U];
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                const uint8_t* blk = rows[k] + (size_t)b * 144;
+                hdr[k] = *(const u32x4_a4*)blk;
+                qa[k] = *(const u32x4_a4*)(blk + 16 + 32 * g);
+                qb[k] = *(const u32x4_a4*)(blk + 32 + 32 * g);
+            }
+            float xv[64];
+            const float* xp = lds + b * 256 + g * 64;
+#pragma unroll
+            for (int i = 0; i < 16; i++) *(f32x4*)(xv + 4 * i) = *(const f32x4*)(xp + 4 * i);
+            const float X0 = xsum[b * 8 + 2 * g], X1 = xsum[b * 8 + 2 * g + 1];
+#pragma unroll
+            for (int k = 0; k < U; k++) acc[k] += q4k_unit(hdr[k], qa[k], qb[k], g, xv, X0, X1);
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            float s = group_sum<LPR>(acc[k]);
+            int r = tile * RPT + k * RPG + sub;
+            if (lr == 0 && r < n) store_row(a, r, s);
+        }
+    }
+}
+
+// ------------------------------------------------------------------- Q6_K
+
+// Partial dot of one Q6_K quarter: half h, l in [16j, 16j+16), the four
+// 16-value sub-blocks l, l+32, l+64, l+96 (q6_k.rs:68-111). sum(sc*(q-32)*x)
+// is formed as sc*(sum(q*x) - 32*sum(x)); both sums run over the same 16
+// values in the same order, so an all-32 sub-block gives exactly 0.
+__device__ __forceinline__ float q6k_unit(u32x4 ql0, u32x4 ql1, u32x4 qh, u32x4 scw, uint32_t dbits,
+                                          int h, int j, const float* xv, const float* X) {
+    const uint32_t L0[4] = {ql0.x, ql0.y, ql0.z, ql0.w};
+    const uint32_t L1[4] = {ql1.x, ql1.y, ql1.z, ql1.w};
+    const uint32_t H[4] = {qh.x, qh.y, qh.z, qh.w};
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t q1 = (L0[i] & 0x0F0F0F0Fu) | ((H[i] << 4) & 0x30303030u);
+        uint32_t q2 = (L1[i] & 0x0F0F0F0Fu) | ((H[i] << 2) & 0x30303030u);
+        uint32_t q3 = ((L0[i] >> 4) & 0x0F0F0F0Fu) | (H[i] & 0x30303030u);
+        uint32_t q4 = ((L1[i] >> 4) & 0x0F0F0F0Fu) | ((H[i] >> 2) & 0x30303030u);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            s[0] = fmaf(ubyte_f32(q1, k), xv[4 * i + k], s[0]);
+            s[1] = fmaf(ubyte_f32(q2, k), xv[16 + 4 * i + k], s[1]);
+            s[2] = fmaf(ubyte_f32(q3, k), xv[32 + 4 * i + k], s[2]);
+            s[3] = fmaf(ubyte_f32(q4, k), xv[48 + 4 * i + k], s[3]);
+        }
+    }
+    // scales sc[8h + j + 2k], k = 0..3 (signed bytes)
+    const uint32_t lo = h ? scw.z : scw.x, hi = h ? scw.w : scw.y;
+    const int sh = 8 * j;
+    float sc0 = (float)__builtin_amdgcn_sbfe(lo, sh, 8);
+    float sc1 = (float)__builtin_amdgcn_sbfe(lo, sh + 16, 8);
+    float sc2 = (float)__builtin_amdgcn_sbfe(hi, sh, 8);
+    float sc3 = (float)__builtin_amdgcn_sbfe(hi, sh + 16, 8);
+    float t = sc0 * (s[0] - 32.0f * X[0]);
+    t = fmaf(sc1, s[1] - 32.0f * X[1], t);
+    t = fmaf(sc2, s[2] - 32.0f * X[2], t);
+    t = fmaf(sc3, s[3] - 32.0f * X[3], t);
+    return t * half_bits_to_f32(dbits);
+}
+
+template <int LPR, int U, int PRO>
+__global__ void __launch_bounds__(kWG) gemv_q6k_kernel(const mivi::GemvArgs a) {
+    extern __shared__ float lds[];
+    stage_input<PRO, 16>(lds, a);
+    const int K = a.K, nb = K / 256;
+    const size_t row_bytes = (size_t)nb * 210;
+    const float* xsum = lds + K;
+    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    constexpr int RPG = 64 / LPR;
+    constexpr int RPT = RPG * U;
+    const int lane = threadIdx.x & 63, lr = lane % LPR, sub = lane / LPR;
+    const int units = nb * 4;
+    const int ntiles = (n + RPT - 1) / RPT;
+    const int nwaves = gridDim.x * (kWG / 64);
+    for (int tile = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); tile < ntiles; tile += nwaves) {
+        const uint8_t* rows[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) rows[k] = row_ptr(a, min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
+        float acc[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) acc[k] = 0.f;
+        for (int u = lr; u < units; u += LPR) {
+            const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+            u32x4 ql0[U], ql1[U], qh[U], scw[U];
+            uint32_t db[U];
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                const uint8_t* blk = rows[k] + (size_t)b * 210;
+                ql0[k] = ld16_a2(blk + 64 * h + 16 * j);
+                ql1[k] = ld16_a2(blk + 64 * h + 32 + 16 * j);
+                qh[k] = ld16_a2(blk + 128 + 32 * h + 16 * j);
+                scw[k] = ld16_a2(blk + 192);
+                db[k] = ld_u16(blk + 208);
+            }
+            float xv[64];
+            const int e0 = b * 256 + h * 128 + 16 * j;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    *(f32x4*)(xv + 16 * q + 4 * i) = *(const f32x4*)(lds + e0 + 32 * q + 4 * i);
+            float X[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) X[q] = xsum[(e0 + 32 * q) / 16];
+#pragma unroll
+            for (int k = 0; k < U; k++) acc[k] += q6k_unit(ql0[k], ql1[k], qh[k], scw[k], db[k], h, j, xv, X);
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            float s = group_sum<LPR>(acc[k]);
+            int r = tile * RPT + k * RPG + sub;
+            if (lr == 0 && r < n) store_row(a, r, s);
+        }
+    }
+}
+
+// ------------------------------------------------------------------- Q8_0
+
+template <int LPR, int U, int PRO>
+__global__ void __launch_bounds__(kWG) gemv_q80_kernel(const mivi::GemvArgs a) {
+    extern __shared__ float lds[];
+    stage_input<PRO, 0>(lds, a);
+    const int K = a.K, nb = K / 32;
+    const size_t row_bytes = (size_t)nb * 34;
+    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    constexpr int RPG = 64 / LPR;
+    constexpr int RPT = RPG * U;
+    const int lane = threadIdx.x & 63, lr = lane % LPR, sub = lane / LPR;
+    const int ntiles = (n + RPT - 1) / RPT;
+    const int nwaves = gridDim.x * (kWG / 64);
+    for (int tile = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); tile < ntiles; tile += nwaves) {
+        const uint8_t* rows[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) rows[k] = row_ptr(a, min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
+        float acc[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) acc[k] = 0.f;
+        for (int b = lr; b < nb; b += LPR) {
+            u32x4 qa[U], qb[U];
+            uint32_t db[U];
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                const uint8_t* blk = rows[k] + (size_t)b * 34;
+                db[k] = ld_u16(blk);
+                qa[k] = ld16_a2(blk + 2);
+                qb[k] = ld16_a2(blk + 18);
+            }
+            const float* xp = lds + b * 32;
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                const uint32_t q[8] = {qa[k].x, qa[k].y, qa[k].z, qa[k].w, qb[k].x, qb[k].y, qb[k].z, qb[k].w};
+                float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    s0 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 0, 8), xp[4 * i], s0);
+                    s1 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 8, 8), xp[4 * i + 1], s1);
+                    s0 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 16, 8), xp[4 * i + 2], s0);
+                    s1 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 24, 8), xp[4 * i + 3], s1);
+                }
+                acc[k] = fmaf(s0 + s1, half_bits_to_f32(db[k]), acc[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            float s = group_sum<LPR>(acc[k]);
+            int r = tile * RPT + k * RPG + sub;
+            if (lr == 0 && r < n) store_row(a, r, s);
+        }
+    }
+}
+
+// -------------------------------------------------- F16 / BF16 / F32 rows
+
+// KIND 0 f16, 1 bf16, 2 f32. One wave per row; rows of any alignment.
+template <int KIND, int PRO>
+__global__ void __launch_bounds__(kWG) gemv_dense_kernel(const mivi::GemvArgs a) {
+    extern __shared__ float lds[];
+    stage_input<PRO, 0>(lds, a);
+    const int d = a.K;
+    const size_t row_bytes = (size_t)d * (KIND == 2 ? 4 : 2);
+    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    const int lane = threadIdx.x & 63;
+    const int nwaves = gridDim.x * (kWG / 64);
+    for (int r = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); r < n; r += nwaves) {
+        const uint8_t* row = row_ptr(a, r, row_bytes);
+        float acc = 0.f;
+        for (int k = lane; k < d; k += 64) {
+            float w;
+            if (KIND == 2) {
+                const uint8_t* p = row + 4 * (size_t)k;
+                w = ((uintptr_t)p & 3) ? __uint_as_float(p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24))
+                                       : *(const float*)p;
+            } else {
+                uint32_t bits = ld_u16(row + 2 * (size_t)k);
+                w = KIND == 0 ? half_bits_to_f32(bits) : bf16_bits_to_f32(bits);
+            }
+            acc = fmaf(w, lds[k], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) store_row(a, r, acc);
+    }
+}
+
+// ------------------------------------------------------- Q8_0 quantize/dot
+
+// q8_0.rs:31-58, one wave per two blocks (32 lanes per block).
+__global__ void __launch_bounds__(kWG) quantize_q80_kernel(const float* __restrict__ src,
+                                                           uint8_t* __restrict__ dst, size_t nblocks) {
+    size_t t = (size_t)blockIdx.x * kWG + threadIdx.x;
+    size_t b = t >> 5;
+    int i = (int)(t & 31);
+    bool valid = b < nblocks;
+    float v = valid ? src[b * 32 + i] : 0.f;
+    float a = fabsf(v);
+#pragma unroll
+    for (int s = 16; s >= 1; s >>= 1) a = fmaxf(a, __shfl_xor(a, s, 32));
+    if (!valid) return;
+    float d = a / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    float q = roundf(v * id);
+    q = fminf(fmaxf(q, -128.0f), 127.0f);
+    uint8_t* blk = dst + b * 34;
+    blk[2 + i] = (uint8_t)(int8_t)q;
+    if (i == 0) {
+        uint32_t h = f32_to_half_bits(d);
+        blk[0] = (uint8_t)(h & 0xFF);
+        blk[1] = (uint8_t)(h >> 8);
+    }
+}
+
+// q8_0.rs:60-124: sum of q*k over 32 values, times d
+__global__ void __launch_bounds__(kWG) dot_q80_kernel(const float* __restrict__ q, const uint8_t* __restrict__ k,
+                                                      float* __restrict__ out, size_t n) {
+    size_t t = (size_t)blockIdx.x * kWG + threadIdx.x;
+    size_t b = t >> 5;
+    int i = (int)(t & 31);
+    bool valid = b < n;
+    float p = valid ? q[b * 32 + i] * (float)(int8_t)k[b * 34 + 2 + i] : 0.f;
+#pragma unroll
+    for (int s = 16; s >= 1; s >>= 1) p += __shfl_xor(p, s, 32);
+    if (valid && i == 0) out[b] = p * half_bits_to_f32(k[b * 34] | (k[b * 34 + 1] << 8));
+}
+
+int pow2_ceil(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+int grid_for(int waves) {
+    int wgs = (waves + 3) / 4;
+    int cap = mivi::num_cus() * 8;
+    return std::max(1, std::min(wgs, cap));
+}
+
+template <int PRO>
+int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
+    const int K = a.K;
+    const int U = n >= 16384 ? 4 : 2;
+#define L3(KER, LPR, UU) hipLaunchKernelGGL((KER<LPR, UU, PRO>), dim3(grid), dim3(kWG), lds, s, a)
+#define BY_U(KER, LPR) \
+    if (U == 4) L3(KER, LPR, 4); else L3(KER, LPR, 2)
+#define BY_LPR(KER)                          \
+    switch (lpr) {                           \
+    case 1: BY_U(KER, 1); break;             \
+    case 2: BY_U(KER, 2); break;             \
+    case 4: BY_U(KER, 4); break;             \
+    case 8: BY_U(KER, 8); break;             \
+    case 16: BY_U(KER, 16); break;           \
+    case 32: BY_U(KER, 32); break;           \
+    default: BY_U(KER, 64); break;           \
+    }
+    switch (t) {
+    case MIVI_GGML_Q4_K:
+    case MIVI_GGML_Q6_K: {
+        const int nb = K / 256;
+        const int lpr = std::min(64, pow2_ceil(nb * 4));
+        const size_t lds = (size_t)K * 4 + (size_t)K / (t == MIVI_GGML_Q4_K ? 32 : 16) * 4;
+        const int grid = grid_for((n + (64 / lpr) * U - 1) / ((64 / lpr) * U));
+        if (t == MIVI_GGML_Q4_K) {
+            BY_LPR(gemv_q4k_kernel)
+        } else {
+            BY_LPR(gemv_q6k_kernel)
+        }
+        break;
+    }
+    case MIVI_GGML_Q8_0: {
+        const int nb = K / 32;
+        const int lpr = std::min(64, pow2_ceil(nb));
+        const size_t lds = (size_t)K * 4;
+        const int grid = grid_for((n + (64 / lpr) * U - 1) / ((64 / lpr) * U));
+        BY_LPR(gemv_q80_kernel)
+        break;
+    }
+    case MIVI_GGML_F16:
+    case MIVI_GGML_BF16:
+    case MIVI_GGML_F32: {
+        const size_t lds = (size_t)K * 4;
+        const int grid = grid_for(n);
+        if (t == MIVI_GGML_F16) hipLaunchKernelGGL((gemv_dense_kernel<0, PRO>), dim3(grid), dim3(kWG), lds, s, a);
+        else if (t == MIVI_GGML_BF16) hipLaunchKernelGGL((gemv_dense_kernel<1, PRO>), dim3(grid), dim3(kWG), lds, s, a);
+        else hipLaunchKernelGGL((gemv_dense_kernel<2, PRO>), dim3(grid), dim3(kWG), lds, s, a);
+        break;
+    }
+    default: return mivi::err_unsupported(t);
+    }
+#undef BY_LPR
+#undef BY_U
+#undef L3
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ host launch
+
+namespace mivi {
+
+int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
+    int n = 0;
+    for (int i = 0; i < a.nseg; i++) n += a.seg[i].n;
+    if (n == 0 || a.K == 0) return MIVI_OK;
+    if ((size_t)a.K > kMaxLdsK)
+        return set_error(MIVI_ERR_UNSUPPORTED, "GEMV with d=%d exceeds the LDS staging limit %zu", a.K, kMaxLdsK);
+    switch (pro) {
+    case PRO_NONE: return launch_pro<PRO_NONE>(t, a, n, s);
+    case PRO_RMSNORM: return launch_pro<PRO_RMSNORM>(t, a, n, s);
+    case PRO_SWIGLU: return launch_pro<PRO_SWIGLU>(t, a, n, s);
+    default: return launch_pro<PRO_CONV>(t, a, n, s);
+    }
+}
+
+// Enqueues y[0..n) (=|+=) W[n, d] x for a validated problem.
+int32_t launch_gemv(int32_t t, const uint8_t* W, const float* x, float* y, size_t n, size_t d,
+                    bool accumulate, hipStream_t s) {
+    GemvArgs a = {};
+    a.seg[0] = {W, y, (int)n};
+    a.nseg = 1;
+    a.K = (int)d;
+    a.x = x;
+    a.accumulate = accumulate ? 1 : 0;
+    return launch_gemv_ex(t, PRO_NONE, a, s);
+}
+
+int32_t launch_dequant(int32_t t, const uint8_t* src, float* out, size_t count, hipStream_t s) {
+    // count = blocks (K-quants) or elements (dense)
+    if (count == 0) return MIVI_OK;
+    size_t threads;
+    switch (t) {
+    case MIVI_GGML_Q4_K:
+        threads = count * 128;
+        hipLaunchKernelGGL(dequant_q4k_kernel, dim3((threads + kWG - 1) / kWG), dim3(kWG), 0, s, src, out, count);
+        break;
+    case MIVI_GGML_Q6_K:
+        threads = count * 64;
+        hipLaunchKernelGGL(dequant_q6k_kernel, dim3((threads + kWG - 1) / kWG), dim3(kWG), 0, s, src, out, count);
+        break;
+    case MIVI_GGML_Q8_0:
+        threads = count * 32;
+        hipLaunchKernelGGL(dequant_q80_kernel, dim3((threads + kWG - 1) / kWG), dim3(kWG), 0, s, src, out, count);
+        break;
+    case MIVI_GGML_F16:
+    case MIVI_GGML_BF16:
+    case MIVI_GGML_F32:
+        hipLaunchKernelGGL(dequant_dense_kernel, dim3((count + kWG - 1) / kWG), dim3(kWG), 0, s, src, out, count,
+                           t == MIVI_GGML_F16 ? 0 : t == MIVI_GGML_BF16 ? 1 : 2);
+        break;
+    default: return err_unsupported(t);
+    }
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+int32_t launch_quantize_q80(const float* src, uint8_t* dst, size_t nblocks, hipStream_t s) {
+    if (nblocks == 0) return MIVI_OK;
+    size_t threads = nblocks * 32;
+    hipLaunchKernelGGL(quantize_q80_kernel, dim3((threads + kWG - 1) / kWG), dim3(kWG), 0, s, src, dst, nblocks);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+// Block size / type size of the formats this library runs
+// (types.rs:91-130); false for every other GgmlType.
+bool format_sizes(int32_t t, size_t* bs, size_t* ts) {
+    switch (t) {
+    case MIVI_GGML_Q4_K: *bs = 256; *ts = 144; return true;
+    case MIVI_GGML_Q6_K: *bs = 256; *ts = 210; return true;
+    case MIVI_GGML_Q8_0: *bs = 32; *ts = 34; return true;
+    case MIVI_GGML_F16:
+    case MIVI_GGML_BF16: *bs = 1; *ts = 2; return true;
+    case MIVI_GGML_F32: *bs = 1; *ts = 4; return true;
+    default: return false;
+    }
+}
+
+// Every GgmlType the reference's from_u32 accepts, with its block/type size
+// when it has one (types.rs:55-137).
+bool ggml_sizes(int32_t t, size_t* bs, size_t* ts) {
+    switch (t) {
+    case 0: case 26: *bs = 1; *ts = 4; return true;
+    case 1: case 30: case 25: *bs = 1; *ts = 2; return true;
+    case 24: *bs = 1; *ts = 1; return true;
+    case 27: case 28: *bs = 1; *ts = 8; return true;
+    case 2: *bs = 32; *ts = 18; return true;
+    case 3: *bs = 32; *ts = 20; return true;
+    case 6: *bs = 32; *ts = 22; return true;
+    case 7: *bs = 32; *ts = 24; return true;
+    case 8: *bs = 32; *ts = 34; return true;
+    case 9: *bs = 32; *ts = 36; return true;
+    case 10: *bs = 256; *ts = 84; return true;
+    case 11: *bs = 256; *ts = 110; return true;
+    case 12: *bs = 256; *ts = 144; return true;
+    case 13: *bs = 256; *ts = 176; return true;
+    case 14: *bs = 256; *ts = 210; return true;
+    case 15: *bs = 256; *ts = 292; return true;
+    default: return false;
+    }
+}
+
+// types.rs:146-181 validate_matvec_args, with the row-byte arithmetic of
+// each format's try_matvec_* (q4_k_m.rs:224-226, q6_k.rs:209-211,
+// q8_0.rs:134-136, f16.rs:49-52, lib.rs:90-93).
+int32_t validate_matvec(int32_t t, size_t out_len, size_t w_len, size_t x_len, size_t n, size_t d,
+                        size_t* row_bytes_out) {
+    size_t bs, ts, row_bytes;
+    if (!format_sizes(t, &bs, &ts)) return err_unsupported(t);
+    bool ovf = false;
+    if (bs == 1) {
+        if (__builtin_mul_overflow(d, ts, &row_bytes)) {
+            if (t != MIVI_GGML_F32) return err_overflow();  // f16.rs:49-51
+            ovf = true;                                    // lib.rs:90-93 maps it to BufferTooSmall
+        }
+    } else {
+        row_bytes = (d / bs) * ts;
+    }
+    if (d % bs != 0) return err_misaligned(d, bs);
+    if (out_len < n) return err_buffer_too_small(n, out_len);
+    if (x_len < d) return err_buffer_too_small(d, x_len);
+    size_t minw;
+    if (ovf || __builtin_mul_overflow(n, row_bytes, &minw)) return err_buffer_too_small(SIZE_MAX, w_len);
+    if (w_len < minw) return err_buffer_too_small(minw, w_len);
+    if (row_bytes_out) *row_bytes_out = row_bytes;
+    return MIVI_OK;
+}
+
+}  // namespace mivi
+
+// -------------------------------------------------------------------- C ABI
+
+using namespace mivi;
+
+static int32_t matvec_typed(int32_t t, float* out, size_t out_len, const uint8_t* w, size_t w_len,
+                            const float* x, size_t x_len, size_t n, size_t d, void* stream) {
+    int32_t rc = validate_matvec(t, out_len, w_len, x_len, n, d, nullptr);
+    if (rc) return rc;
+    if (n && (!out || !w || (d && !x))) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    clear_error();
+    return launch_gemv(t, w, x, out, n, d, false, (hipStream_t)stream);
+}
+
+extern "C" int32_t mivi_hip_quantized_matvec(float* out, size_t out_len, int32_t t, const uint8_t* w,
+                                             size_t w_len, const float* x, size_t x_len, size_t n, size_t d,
+                                             void* stream) {
+    return matvec_typed(t, out, out_len, w, w_len, x, x_len, n, d, stream);
+}
+
+#define TYPED_ENTRY(NAME, T)                                                                          \
+    extern "C" int32_t NAME(float* out, size_t out_len, const uint8_t* w, size_t w_len, const float* x, \
+                            size_t x_len, size_t n, size_t d, void* stream) {                        \
+        return matvec_typed(T, out, out_len, w, w_len, x, x_len, n, d, stream);                      \
+    }
+TYPED_ENTRY(mivi_hip_try_matvec_q4_k_m, MIVI_GGML_Q4_K)
+TYPED_ENTRY(mivi_hip_try_matvec_q6_k, MIVI_GGML_Q6_K)
+TYPED_ENTRY(mivi_hip_try_matvec_q8_0, MIVI_GGML_Q8_0)
+TYPED_ENTRY(mivi_hip_try_matvec_f16, MIVI_GGML_F16)
+TYPED_ENTRY(mivi_hip_try_matvec_bf16, MIVI_GGML_BF16)
+#undef TYPED_ENTRY
+
+extern "C" int32_t mivi_hip_dequantize_slice(int32_t t, const uint8_t* bytes, size_t bytes_len, float* out,
+                                             size_t out_len, void* stream) {
+    size_t bs, ts;
+    if (!format_sizes(t, &bs, &ts)) return err_unsupported(t);
+    size_t count;
+    if (bs == 1) {
+        count = bytes_len / ts;  // f16.rs:17-23, lib.rs:58-63
+        if (out_len < count) return err_buffer_too_small(count, out_len);
+    } else {
+        count = out_len / bs;    // types.rs:281-285
+        if (bytes_len < count * ts) return err_buffer_too_small(count * ts, bytes_len);
+    }
+    if (count && (!bytes || !out)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    clear_error();
+    return launch_dequant(t, bytes, out, count, (hipStream_t)stream);
+}
+
+extern "C" int32_t mivi_hip_quantize_q8_0(const float* src, size_t src_len, uint8_t* dst, size_t dst_len,
+                                          size_t n_blocks, void* stream) {
+    if (src_len < n_blocks * 32) return err_buffer_too_small(n_blocks * 32, src_len);
+    if (dst_len < n_blocks * 34) return err_buffer_too_small(n_blocks * 34, dst_len);
+    clear_error();
+    return launch_quantize_q80(src, dst, n_blocks, (hipStream_t)stream);
+}
+
+extern "C" int32_t mivi_hip_dot_q8_0_f32(const float* q, size_t q_len, const uint8_t* k, size_t k_len, float* out,
+                                         size_t out_len, size_t n, void* stream) {
+    if (q_len < n * 32) return err_buffer_too_small(n * 32, q_len);
+    if (k_len < n * 34) return err_buffer_too_small(n * 34, k_len);
+    if (out_len < n) return err_buffer_too_small(n, out_len);
+    clear_error();
+    if (n == 0) return MIVI_OK;
+    size_t threads = n * 32;
+    hipLaunchKernelGGL(dot_q80_kernel, dim3((threads + kWG - 1) / kWG), dim3(kWG), 0, (hipStream_t)stream, q, k, out, n);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}

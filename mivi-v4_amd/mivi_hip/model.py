@@ -1,0 +1,92 @@
+"""`Model`: the hybrid decode step resident on the GPU.
+
+Mirrors crates/mivi-model/src/model.rs: `forward(token, pos)` returns the
+logits (model.rs:488-491), `forward_step(..., compute_logits)` (model.rs:336),
+`reset_context()` (model.rs:494-497), plus the batched greedy loop and the
+state export/import used for state injection (cache.rs:682-914,
+arena.rs:110-123).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import KvPrecision, ModelError, MiviModelInfo, _check, _lib
+
+
+class Model:
+    def __init__(self, gguf: np.ndarray | bytes, max_ctx: int = 0, kv_precision=KvPrecision.F32,
+                 max_batch: int = 1):
+        img = np.frombuffer(gguf, np.uint8) if isinstance(gguf, (bytes, bytearray)) else \
+            np.ascontiguousarray(gguf, np.uint8)
+        h = C.c_void_p()
+        _check(_lib.mivi_hip_model_create(img.ctypes.data_as(C.c_void_p), img.nbytes, max_ctx,
+                                          int(kv_precision), max_batch, C.byref(h)), ModelError)
+        self._h = h
+        self.info = MiviModelInfo()
+        _lib.mivi_hip_model_info(self._h, C.byref(self.info))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.mivi_hip_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def vocab_size(self) -> int:
+        return self.info.vocab_size
+
+    def reset_context(self):
+        _check(_lib.mivi_hip_model_reset(self._h), ModelError)
+
+    def forward_step(self, token: int, pos: int, compute_logits: bool = True, seq: int = 0):
+        out = np.empty(self.info.vocab_size, np.float32) if compute_logits else None
+        ptr = out.ctypes.data_as(C.c_void_p) if out is not None else None
+        _check(_lib.mivi_hip_model_forward_step(self._h, seq, token, pos, 1 if compute_logits else 0, ptr),
+               ModelError)
+        return out
+
+    def forward(self, token: int, pos: int, seq: int = 0) -> np.ndarray:
+        return self.forward_step(token, pos, True, seq)
+
+    def prefill(self, tokens, pos0: int = 0, seq: int = 0):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        _check(_lib.mivi_hip_model_prefill(self._h, seq, t.ctypes.data_as(C.c_void_p), t.size, pos0), ModelError)
+
+    def generate_greedy(self, tokens, pos, n_steps: int) -> np.ndarray:
+        """tokens/pos: one entry per sequence. Returns [n_steps, batch] argmax tokens."""
+        t = np.ascontiguousarray(np.atleast_1d(tokens), np.uint32)
+        p = np.ascontiguousarray(np.atleast_1d(pos), np.uint64)
+        out = np.empty((n_steps, t.size), np.uint32)
+        _check(_lib.mivi_hip_model_generate_greedy(self._h, t.size, t.ctypes.data_as(C.c_void_p),
+                                                   p.ctypes.data_as(C.c_void_p), n_steps,
+                                                   out.ctypes.data_as(C.c_void_p)), ModelError)
+        return out
+
+    def kv_row_bytes(self) -> int:
+        kvd = self.info.kv_dim
+        return {0: 4 * kvd, 2: 2 * kvd, 1: kvd // 32 * 34}[self.info.kv_precision]
+
+    def conv_len(self) -> int:
+        return self.info.n_layers * self.info.dim * max(1, self.info.ssm_conv_kernel)
+
+    def export_state(self, tokens: int, seq: int = 0):
+        n = self.info.n_attn_layers * tokens * self.kv_row_bytes()
+        k = np.empty(n, np.uint8)
+        v = np.empty(n, np.uint8)
+        conv = np.empty(self.conv_len(), np.float32)
+        _check(_lib.mivi_hip_model_export_state(self._h, seq, tokens, k.ctypes.data_as(C.c_void_p),
+                                                v.ctypes.data_as(C.c_void_p), n, conv.ctypes.data_as(C.c_void_p),
+                                                conv.size), ModelError)
+        return k, v, conv
+
+    def import_state(self, tokens: int, k: np.ndarray, v: np.ndarray, conv: np.ndarray, seq: int = 0):
+        k = np.ascontiguousarray(k, np.uint8)
+        v = np.ascontiguousarray(v, np.uint8)
+        conv = np.ascontiguousarray(conv, np.float32)
+        _check(_lib.mivi_hip_model_import_state(self._h, seq, tokens, k.ctypes.data_as(C.c_void_p),
+                                                v.ctypes.data_as(C.c_void_p), min(k.nbytes, v.nbytes),
+                                                conv.ctypes.data_as(C.c_void_p), conv.size), ModelError)

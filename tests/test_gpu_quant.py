@@ -1,0 +1,238 @@
+"""GPU parity of the mivi-quant surface through the C ABI (HIP kernels) against
+the CPU oracle on identical packed bytes.
+
+Bars: dequantization bit-exact; GEMV/GEMM max |y - y_ref| <=
+1e-4 * ||w_row|| * ||x|| (fp32 accumulation), as the north star fixes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from test_oracle_quant import make_q6k_block, pattern_weights, random_blocks
+
+pytestmark = pytest.mark.gpu
+
+Q4_K, Q6_K, Q8_0, F16, BF16, F32 = 12, 14, 8, 1, 30, 0
+BS = {Q4_K: 256, Q6_K: 256, Q8_0: 32, F16: 1, BF16: 1, F32: 1}
+TS = {Q4_K: 144, Q6_K: 210, Q8_0: 34, F16: 2, BF16: 2, F32: 4}
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def dense_bytes(t, W):
+    if t == F32:
+        return W.astype(np.float32).view(np.uint8).reshape(-1)
+    if t == F16:
+        return W.astype(np.float16).view(np.uint8).reshape(-1)
+    return (W.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
+
+
+def weights(t, rows, cols, seed):
+    if t in (Q4_K, Q6_K, Q8_0):
+        return random_blocks(t, rows, cols, seed)
+    return dense_bytes(t, np.random.default_rng(seed).standard_normal((rows, cols)))
+
+
+def check_bound(oracle, t, w, x, y, rows, cols):
+    rc, deq, _ = oracle.dequantize_slice(t, w, rows * cols)
+    W = deq.reshape(rows, cols).astype(np.float64)
+    rc2, yref, _ = oracle.quantized_matvec(t, w, x, rows, cols)
+    assert rc == 0 and rc2 == 0
+    bound = 1e-4 * np.linalg.norm(W, axis=1) * np.linalg.norm(x.astype(np.float64))
+    err = np.abs(y.astype(np.float64) - yref.astype(np.float64))
+    assert np.all(err <= bound), (float(err.max()), float(bound.min()))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0, F16, BF16, F32])
+def test_dequantize_bit_exact(hip, oracle, torch_mod, t):
+    torch = torch_mod
+    rows, cols = 37, 512
+    w = weights(t, rows, cols, 100 + t)
+    n = rows * cols
+    out = torch.full((n + 3,), 7.5, dtype=torch.float32, device="cuda")
+    hip.dequantize_slice(t, dev(torch, w), out[:n])
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    rc, ref, _ = oracle.dequantize_slice(t, w, n)
+    assert rc == 0
+    assert np.array_equal(got[:n].view(np.uint32), ref.view(np.uint32))
+    assert np.all(got[n:] == 7.5)
+
+
+def test_dequantize_exhaustive_q4k_scales(hip, oracle, torch_mod):
+    # every 12-byte scale pattern position with all 256 byte values
+    torch = torch_mod
+    rng = np.random.default_rng(9)
+    blocks = np.tile(random_blocks(Q4_K, 1, 256, 1), 12 * 256).reshape(12 * 256, 144)
+    for p in range(12):
+        blocks[p * 256:(p + 1) * 256, 4 + p] = np.arange(256)
+    blocks[:, 16:] = rng.integers(0, 256, (12 * 256, 128))
+    w = blocks.reshape(-1)
+    n = 12 * 256 * 256
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    hip.dequantize_slice(Q4_K, dev(torch, w), out)
+    torch.cuda.synchronize()
+    rc, ref, _ = oracle.dequantize_slice(Q4_K, w, n)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+SHAPES = [(1, 256), (7, 512), (255, 2048), (257, 2048), (100, 768), (33, 4096), (64, 8192)]
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_gemv_matches_oracle(hip, oracle, torch_mod, t, shape):
+    torch = torch_mod
+    rows, cols = shape
+    w = weights(t, rows, cols, rows * 7 + cols + t)
+    x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
+    out = torch.full((rows + 5,), -3.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(out, t, dev(torch, w), dev(torch, x), rows, cols)
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    assert np.all(y[rows:] == -3.0)      # tail untouched (types.rs:312-328)
+    check_bound(oracle, t, w, x, y[:rows], rows, cols)
+
+
+@pytest.mark.parametrize("t", [F16, BF16, F32])
+def test_gemv_dense(hip, oracle, torch_mod, t):
+    torch = torch_mod
+    rows, cols = 129, 1000
+    w = weights(t, rows, cols, 5)
+    x = np.random.default_rng(6).standard_normal(cols).astype(np.float32)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(out, t, dev(torch, w), dev(torch, x), rows, cols)
+    torch.cuda.synchronize()
+    check_bound(oracle, t, w, x, out.cpu().numpy(), rows, cols)
+
+
+def test_gemv_unaligned_f32_rows(hip, oracle, torch_mod):
+    # lib.rs:95-129: F32 weights need not be 4-byte aligned
+    torch = torch_mod
+    rows, cols = 9, 50
+    W = np.random.default_rng(1).standard_normal((rows, cols)).astype(np.float32)
+    buf = np.zeros(rows * cols * 4 + 2, np.uint8)
+    buf[2:] = W.view(np.uint8).reshape(-1)
+    d = dev(torch, buf)
+    x = np.random.default_rng(2).standard_normal(cols).astype(np.float32)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(out, F32, d[2:], dev(torch, x), rows, cols)
+    torch.cuda.synchronize()
+    check_bound(oracle, F32, W.view(np.uint8).reshape(-1), x, out.cpu().numpy(), rows, cols)
+
+
+@pytest.mark.parametrize("fn,t", [("try_matvec_q4_k_m", Q4_K), ("try_matvec_q6_k", Q6_K), ("try_matvec_q8_0", Q8_0),
+                                  ("try_matvec_f16", F16), ("try_matvec_bf16", BF16)])
+def test_typed_entry_points(hip, oracle, torch_mod, fn, t):
+    torch = torch_mod
+    rows, cols = 40, 512
+    w = weights(t, rows, cols, 77)
+    x = np.random.default_rng(3).standard_normal(cols).astype(np.float32)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    getattr(hip, fn)(out, dev(torch, w), dev(torch, x), rows, cols)
+    torch.cuda.synchronize()
+    check_bound(oracle, t, w, x, out.cpu().numpy(), rows, cols)
+
+
+def test_q6k_all_offset_rows_are_exactly_zero(hip, torch_mod):
+    torch = torch_mod
+    blk = make_q6k_block(0.01, [100] * 16, [32] * 256)
+    w = np.frombuffer(blk * 8 * 16, np.uint8)   # 16 rows of 2048
+    x = np.random.default_rng(1).standard_normal(2048).astype(np.float32)
+    out = torch.full((16,), 5.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(out, Q6_K, dev(torch, w), dev(torch, x), 16, 2048)
+    torch.cuda.synchronize()
+    assert np.all(out.cpu().numpy() == 0.0)
+
+
+def test_errors_leave_output_untouched(hip, torch_mod):
+    # validation before any write (types.rs:146-235, lib.rs:152-169)
+    torch = torch_mod
+    w = torch.zeros(144 * 4, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(256, dtype=torch.float32, device="cuda")
+    out = torch.full((4,), 9.0, dtype=torch.float32, device="cuda")
+    for n, d, ww, xx, kind in ((4, 255, w, x, "DimensionMisaligned"), (5, 256, w, x, "BufferTooSmall"),
+                               (4, 256, w[:500], x, "BufferTooSmall"), (4, 256, w, x[:200], "BufferTooSmall")):
+        with pytest.raises(hip.QuantError) as ei:
+            hip.quantized_matvec(out, Q4_K, ww, xx, n, d)
+        assert ei.value.kind == kind
+    with pytest.raises(hip.QuantError) as ei:
+        hip.quantized_matvec(out, 2, w, x, 4, 256)
+    assert ei.value.kind == "UnsupportedType" and ei.value.type_id == 2
+    with pytest.raises(hip.QuantError):
+        hip.quantized_matmul_rows(out, Q4_K, w, x, 2, 2, 256)   # out too small for 2x2? (4 ok) -> inputs short
+    torch.cuda.synchronize()
+    assert np.all(out.cpu().numpy() == 9.0)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0, F32])
+@pytest.mark.parametrize("batch", [1, 2, 8, 9, 33])
+def test_matmul_rows_matches_oracle(hip, oracle, torch_mod, t, batch):
+    torch = torch_mod
+    rows, cols = 257, 512
+    w = pattern_weights(t, rows, cols) if t != F32 else weights(F32, rows, cols, 3)
+    inputs = ((np.arange(batch * cols) % 23).astype(np.float32) * np.float32(0.0625) - np.float32(0.75))
+    out = torch.full((batch * rows + 1,), 123.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matmul_rows(out[:batch * rows], t, dev(torch, w), dev(torch, inputs), batch, rows, cols)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert got[-1] == 123.0
+    rc, ref, _ = oracle.quantized_matmul_rows(t, w, inputs, batch, rows, cols)
+    rc2, deq, _ = oracle.dequantize_slice(t, w, rows * cols)
+    W = deq.reshape(rows, cols).astype(np.float64)
+    X = inputs.reshape(batch, cols).astype(np.float64)
+    bound = 1e-4 * np.linalg.norm(X, axis=1)[:, None] * np.linalg.norm(W, axis=1)[None, :]
+    assert np.all(np.abs(got[:-1].reshape(batch, rows) - ref.reshape(batch, rows)) <= bound)
+
+
+def test_quantize_q8_0_bit_exact_and_dot(hip, oracle, torch_mod):
+    torch = torch_mod
+    nb = 4096
+    src = (np.random.default_rng(4).standard_normal(nb * 32) * np.repeat(
+        np.random.default_rng(5).uniform(0.001, 50, nb), 32)).astype(np.float32)
+    src[:32] = 0.0                      # zero block
+    src[32:64] = np.arange(32) - 16.0   # reference test values
+    dst = torch.zeros(nb * 34, dtype=torch.uint8, device="cuda")
+    hip.quantize_f32_to_q8_0(dev(torch, src), dst, nb)
+    torch.cuda.synchronize()
+    got = dst.cpu().numpy()
+    ref = np.concatenate([oracle.quantize_q8_0_block(src[i * 32:(i + 1) * 32]) for i in range(nb)])
+    assert np.array_equal(got, ref)
+    q = np.random.default_rng(6).standard_normal(nb * 32).astype(np.float32)
+    out = torch.empty(nb, dtype=torch.float32, device="cuda")
+    hip.dot_q8_0_f32(dev(torch, q), dst, out, nb)
+    torch.cuda.synchronize()
+    d = out.cpu().numpy()
+    for i in range(0, nb, 97):
+        blk = ref[i * 34:(i + 1) * 34]
+        qi = q[i * 32:(i + 1) * 32]
+        r = oracle.dot_q8_0_f32(qi, blk)
+        kd = oracle.dequantize_slice(Q8_0, blk, 32)[1].astype(np.float64)
+        assert abs(d[i] - r) <= 1e-5 * np.abs(qi.astype(np.float64) * kd).sum() + 1e-30
+
+
+@pytest.mark.parametrize("t,rows", [(Q4_K, 8192), (Q6_K, 65536)])
+def test_config_shapes_match_oracle(hip, oracle, torch_mod, t, rows):
+    # BASELINE configs 1 and 2 at full size, synthetic N(0, 0.02) weights
+    torch = torch_mod
+    cols = 2048
+    w = hip.synth_random_weights(t, 42 + t, rows, cols, 0.02)
+    x = hip.synth_normal(43, cols)
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    dw, dx = dev(torch, w), dev(torch, x)
+    hip.quantized_matvec(out, t, dw, dx, rows, cols)
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    check_bound(oracle, t, w, x, y, rows, cols)
+    # size-independent property: linearity in x
+    x2 = hip.synth_normal(44, cols)
+    out2 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    out3 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(out2, t, dw, dev(torch, x2), rows, cols)
+    hip.quantized_matvec(out3, t, dw, dev(torch, (2.0 * x + x2).astype(np.float32)), rows, cols)
+    torch.cuda.synchronize()
+    lin = 2.0 * y + out2.cpu().numpy()
+    assert np.max(np.abs(out3.cpu().numpy() - lin)) <= 1e-4 * np.abs(lin).max() + 1e-4
