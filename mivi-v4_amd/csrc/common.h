@@ -85,6 +85,11 @@ __device__ __forceinline__ float ubyte_f32(uint32_t w, int k) {
     return (float)((w >> (8 * k)) & 0xFFu);
 }
 
+// byte k of w as a signed value (v_cvt_f32_i32 of the sign-extended byte)
+__device__ __forceinline__ float sbyte_f32(uint32_t w, int k) {
+    return (float)(int)(int8_t)(w >> (8 * k));
+}
+
 // Sum over groups of `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {

@@ -333,10 +333,10 @@ __device__ __forceinline__ float q6k_unit(u32x4 ql0, u32x4 ql1, u32x4 qh, u32x4 
     // scales sc[8h + j + 2k], k = 0..3 (signed bytes)
     const uint32_t lo = h ? scw.z : scw.x, hi = h ? scw.w : scw.y;
     const int sh = 8 * j;
-    float sc0 = (float)__builtin_amdgcn_sbfe(lo, sh, 8);
-    float sc1 = (float)__builtin_amdgcn_sbfe(lo, sh + 16, 8);
-    float sc2 = (float)__builtin_amdgcn_sbfe(hi, sh, 8);
-    float sc3 = (float)__builtin_amdgcn_sbfe(hi, sh + 16, 8);
+    float sc0 = sbyte_f32(lo >> sh, 0);
+    float sc1 = sbyte_f32(lo >> sh, 2);
+    float sc2 = sbyte_f32(hi >> sh, 0);
+    float sc3 = sbyte_f32(hi >> sh, 2);
     float t = sc0 * (s[0] - 32.0f * X[0]);
     t = fmaf(sc1, s[1] - 32.0f * X[1], t);
     t = fmaf(sc2, s[2] - 32.0f * X[2], t);
@@ -438,10 +438,10 @@ __global__ void __launch_bounds__(kWG) gemv_q80_kernel(const mivi::GemvArgs a) {
                 float s0 = 0.f, s1 = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    s0 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 0, 8), xp[4 * i], s0);
-                    s1 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 8, 8), xp[4 * i + 1], s1);
-                    s0 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 16, 8), xp[4 * i + 2], s0);
-                    s1 = fmaf((float)__builtin_amdgcn_sbfe(q[i], 24, 8), xp[4 * i + 3], s1);
+                    s0 = fmaf(sbyte_f32(q[i], 0), xp[4 * i], s0);
+                    s1 = fmaf(sbyte_f32(q[i], 1), xp[4 * i + 1], s1);
+                    s0 = fmaf(sbyte_f32(q[i], 2), xp[4 * i + 2], s0);
+                    s1 = fmaf(sbyte_f32(q[i], 3), xp[4 * i + 3], s1);
                 }
                 acc[k] = fmaf(s0 + s1, half_bits_to_f32(db[k]), acc[k]);
             }
