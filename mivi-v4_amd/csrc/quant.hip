@@ -15,6 +15,8 @@
 // reduced across the LPR lanes that share a row. Activations are staged once
 // per workgroup in LDS together with per-sub-block sums (the min term of
 // Q4_K and the -32 offset of Q6_K need sum(x) per sub-block).
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "common.h"
@@ -186,26 +188,58 @@ __device__ __forceinline__ void stage_input(float* lds, const mivi::GemvArgs& a)
     }
 }
 
-__device__ __forceinline__ int seg_of(const mivi::GemvArgs& a, int r, int* local) {
-    int n0 = a.seg[0].n;
-    if (r < n0 || a.nseg == 1) { *local = r; return 0; }
-    int n1 = a.seg[1].n;
-    if (r < n0 + n1 || a.nseg == 2) { *local = r - n0; return 1; }
-    *local = r - n0 - n1;
-    return 2;
-}
+// Segment table of a GemvArgs held in registers: the kernel-argument struct
+// is never indexed dynamically (that would turn every row lookup into a
+// dependent load from the kernarg segment).
+struct Segs {
+    // row r of the concatenated segments lives at
+    //   W0 + r * row_bytes + (r >= n0) * dW1 + (r >= n01) * dW2
+    // (and its output at y0 + r + ...): no per-row selects that the compiler
+    // could turn into an indexed table in scratch memory.
+    uintptr_t W0, y0;
+    int64_t dW1, dW2, dy1, dy2;
+    int n0, n01, n;
+    size_t rb;
+    __device__ __forceinline__ Segs(const mivi::GemvArgs& a, size_t row_bytes) : rb(row_bytes) {
+        n0 = a.seg[0].n;
+        n01 = n0 + (a.nseg > 1 ? a.seg[1].n : 0);
+        n = n01 + (a.nseg > 2 ? a.seg[2].n : 0);
+        W0 = (uintptr_t)a.seg[0].W;
+        y0 = (uintptr_t)a.seg[0].y;
+        const uintptr_t W1 = a.nseg > 1 ? (uintptr_t)a.seg[1].W : W0;
+        const uintptr_t W2 = a.nseg > 2 ? (uintptr_t)a.seg[2].W : W1;
+        const uintptr_t y1 = a.nseg > 1 ? (uintptr_t)a.seg[1].y : y0;
+        const uintptr_t y2 = a.nseg > 2 ? (uintptr_t)a.seg[2].y : y1;
+        // base of segment 1 minus where row n0 would be in segment 0, etc.
+        dW1 = (int64_t)(W1 - (uintptr_t)n0 * rb) - (int64_t)W0;
+        dW2 = (int64_t)(W2 - (uintptr_t)n01 * rb) - (int64_t)(W1 - (uintptr_t)n0 * rb);
+        dy1 = (int64_t)(y1 - (uintptr_t)n0 * 4) - (int64_t)y0;
+        dy2 = (int64_t)(y2 - (uintptr_t)n01 * 4) - (int64_t)(y1 - (uintptr_t)n0 * 4);
+    }
+    __device__ __forceinline__ const uint8_t* row(int r, size_t = 0) const {
+        uintptr_t p = W0 + (uintptr_t)r * rb;
+        p += (r >= n0 ? (uintptr_t)dW1 : 0) + (r >= n01 ? (uintptr_t)dW2 : 0);
+        return (const uint8_t*)p;
+    }
+    __device__ __forceinline__ float* out(int r) const {
+        uintptr_t p = y0 + (uintptr_t)r * 4;
+        p += (r >= n0 ? (uintptr_t)dy1 : 0) + (r >= n01 ? (uintptr_t)dy2 : 0);
+        return (float*)p;
+    }
+};
 
-__device__ __forceinline__ const uint8_t* row_ptr(const mivi::GemvArgs& a, int r, size_t row_bytes) {
-    int lr;
-    int s = seg_of(a, r, &lr);
-    return a.seg[s].W + (size_t)lr * row_bytes;
-}
+typedef __attribute__((address_space(1))) float gfloat;
 
-__device__ __forceinline__ void store_row(const mivi::GemvArgs& a, int r, float v) {
-    int lr;
-    int s = seg_of(a, r, &lr);
-    float* y = a.seg[s].y + lr;
-    *y = a.accumulate ? *y + v : v;
+// y[r] = v, or y[r] += v when accumulating. Each row has exactly one writer,
+// so the accumulate is a global atomic add without return: the same single
+// fp32 addition as a read-modify-write (up to denormal flushing in the atomic
+// unit), but with no load whose wait would drain the weight prefetch queue.
+__device__ __forceinline__ void store_out(const Segs& sg, int accumulate, int r, float v) {
+    gfloat* y = (gfloat*)sg.out(r);
+    if (accumulate)
+        __builtin_amdgcn_global_atomic_fadd_f32(y, v);
+    else
+        *y = v;
 }
 
 // ------------------------------------------------------------------- Q4_K
@@ -263,7 +297,8 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_kernel(const mivi::GemvArgs a) {
     const int K = a.K, nb = K / 256;
     const size_t row_bytes = (size_t)nb * 144;
     const float* xsum = lds + K;
-    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    const Segs sg(a, row_bytes);
+    const int n = sg.n;
     constexpr int RPG = 64 / LPR;   // rows per lane group
     constexpr int RPT = RPG * U;    // rows per wave tile
     const int lane = threadIdx.x & 63, lr = lane % LPR, sub = lane / LPR;
@@ -273,7 +308,7 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_kernel(const mivi::GemvArgs a) {
     for (int tile = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); tile < ntiles; tile += nwaves) {
         const uint8_t* rows[U];
 #pragma unroll
-        for (int k = 0; k < U; k++) rows[k] = row_ptr(a, min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
+        for (int k = 0; k < U; k++) rows[k] = sg.row(min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
         float acc[U];
 #pragma unroll
         for (int k = 0; k < U; k++) acc[k] = 0.f;
@@ -299,7 +334,7 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_kernel(const mivi::GemvArgs a) {
         for (int k = 0; k < U; k++) {
             float s = group_sum<LPR>(acc[k]);
             int r = tile * RPT + k * RPG + sub;
-            if (lr == 0 && r < n) store_row(a, r, s);
+            if (lr == 0 && r < n) store_out(sg, a.accumulate, r, s);
         }
     }
 }
@@ -351,7 +386,8 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_kernel(const mivi::GemvArgs a) {
     const int K = a.K, nb = K / 256;
     const size_t row_bytes = (size_t)nb * 210;
     const float* xsum = lds + K;
-    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    const Segs sg(a, row_bytes);
+    const int n = sg.n;
     constexpr int RPG = 64 / LPR;
     constexpr int RPT = RPG * U;
     const int lane = threadIdx.x & 63, lr = lane % LPR, sub = lane / LPR;
@@ -361,7 +397,7 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_kernel(const mivi::GemvArgs a) {
     for (int tile = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); tile < ntiles; tile += nwaves) {
         const uint8_t* rows[U];
 #pragma unroll
-        for (int k = 0; k < U; k++) rows[k] = row_ptr(a, min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
+        for (int k = 0; k < U; k++) rows[k] = sg.row(min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
         float acc[U];
 #pragma unroll
         for (int k = 0; k < U; k++) acc[k] = 0.f;
@@ -395,7 +431,7 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_kernel(const mivi::GemvArgs a) {
         for (int k = 0; k < U; k++) {
             float s = group_sum<LPR>(acc[k]);
             int r = tile * RPT + k * RPG + sub;
-            if (lr == 0 && r < n) store_row(a, r, s);
+            if (lr == 0 && r < n) store_out(sg, a.accumulate, r, s);
         }
     }
 }
@@ -408,7 +444,8 @@ __global__ void __launch_bounds__(kWG) gemv_q80_kernel(const mivi::GemvArgs a) {
     stage_input<PRO, 0>(lds, a);
     const int K = a.K, nb = K / 32;
     const size_t row_bytes = (size_t)nb * 34;
-    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    const Segs sg(a, row_bytes);
+    const int n = sg.n;
     constexpr int RPG = 64 / LPR;
     constexpr int RPT = RPG * U;
     const int lane = threadIdx.x & 63, lr = lane % LPR, sub = lane / LPR;
@@ -417,7 +454,7 @@ __global__ void __launch_bounds__(kWG) gemv_q80_kernel(const mivi::GemvArgs a) {
     for (int tile = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); tile < ntiles; tile += nwaves) {
         const uint8_t* rows[U];
 #pragma unroll
-        for (int k = 0; k < U; k++) rows[k] = row_ptr(a, min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
+        for (int k = 0; k < U; k++) rows[k] = sg.row(min(tile * RPT + k * RPG + sub, n - 1), row_bytes);
         float acc[U];
 #pragma unroll
         for (int k = 0; k < U; k++) acc[k] = 0.f;
@@ -450,7 +487,7 @@ __global__ void __launch_bounds__(kWG) gemv_q80_kernel(const mivi::GemvArgs a) {
         for (int k = 0; k < U; k++) {
             float s = group_sum<LPR>(acc[k]);
             int r = tile * RPT + k * RPG + sub;
-            if (lr == 0 && r < n) store_row(a, r, s);
+            if (lr == 0 && r < n) store_out(sg, a.accumulate, r, s);
         }
     }
 }
@@ -464,11 +501,12 @@ __global__ void __launch_bounds__(kWG) gemv_dense_kernel(const mivi::GemvArgs a)
     stage_input<PRO, 0>(lds, a);
     const int d = a.K;
     const size_t row_bytes = (size_t)d * (KIND == 2 ? 4 : 2);
-    const int n = a.seg[0].n + (a.nseg > 1 ? a.seg[1].n : 0) + (a.nseg > 2 ? a.seg[2].n : 0);
+    const Segs sg(a, row_bytes);
+    const int n = sg.n;
     const int lane = threadIdx.x & 63;
     const int nwaves = gridDim.x * (kWG / 64);
     for (int r = blockIdx.x * (kWG / 64) + (threadIdx.x >> 6); r < n; r += nwaves) {
-        const uint8_t* row = row_ptr(a, r, row_bytes);
+        const uint8_t* row = sg.row(r, row_bytes);
         float acc = 0.f;
         for (int k = lane; k < d; k += 64) {
             float w;
@@ -483,7 +521,191 @@ __global__ void __launch_bounds__(kWG) gemv_dense_kernel(const mivi::GemvArgs a)
             acc = fmaf(w, lds[k], acc);
         }
         acc = wave_sum(acc);
-        if (lane == 0) store_row(a, r, acc);
+        if (lane == 0) store_out(sg, a.accumulate, r, acc);
+    }
+}
+
+// ------------------------------------------------- tiled GEMV (Q4_K / Q6_K)
+//
+// Persistent workgroups stream tiles of RT whole rows: every thread copies
+// fixed 16-byte chunks of the tile (one contiguous 4 KB span per workgroup
+// instruction), holds the next tile in registers while the current one is
+// reduced out of LDS, then writes it to the other LDS buffer. The compute
+// layout is the per-quarter-superblock unit of the kernels above; each lane
+// keeps its activation slice and sub-block sums in registers for the whole
+// launch.
+
+enum { FMT_Q4K = 0, FMT_Q6K = 1 };
+
+template <int FMT> struct KQ;
+template <> struct KQ<FMT_Q4K> { static constexpr int bytes = 144, G = 32, CPT = 5; };
+template <> struct KQ<FMT_Q6K> { static constexpr int bytes = 210, G = 16, CPT = 7; };
+
+__device__ __forceinline__ u32x4 ldg16(const uint8_t* p) {
+    return *(const __attribute__((address_space(1))) u32x4*)p;
+}
+
+// 16 bytes at byte offset `off` (2-byte aligned) of an LDS region whose base
+// is 16-byte aligned: aligned dwords + alignbyte; reads [off - 2, off + 18).
+__device__ __forceinline__ u32x4 lds16_a2(const uint8_t* base16, int off) {
+    const uint32_t* w = (const uint32_t*)(base16 + (off & ~3));
+    const uint32_t sh = (uint32_t)(off & 3);
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    r.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    r.z = __builtin_amdgcn_alignbyte(w3, w2, sh);
+    r.w = __builtin_amdgcn_alignbyte(w4, w3, sh);
+    return r;
+}
+
+template <int FMT, int LPR, int NU, int UU, int PRO>
+__global__ void __launch_bounds__(kWG) gemv_kq_tiled_kernel(const mivi::GemvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int G = KQ<FMT>::G, CPT = KQ<FMT>::CPT;
+    constexpr int RPG = 64 / LPR, RW = RPG * UU, RT = 4 * RW;
+    const int K = a.K, nb = K / 256;
+    const int row_bytes = nb * KQ<FMT>::bytes;
+    const int row_chunks = row_bytes / 16, tile_chunks = RT * row_chunks;
+    const int tile_bytes = RT * row_bytes;
+    float* xs = (float*)smem;
+    const int xbytes = ((K + K / G) * 4 + 15) & ~15;
+    uint8_t* tb0 = smem + xbytes;
+    uint8_t* tb1 = tb0 + tile_bytes;
+    uint8_t* dummy = tb0 + 2 * tile_bytes;
+    const Segs sg(a, row_bytes);
+    const int n = sg.n;
+    const int ntiles = (n + RT - 1) / RT;
+    const int T0 = blockIdx.x, GS = gridDim.x;
+
+    // This thread's 16-byte chunks of a tile (row within the tile, byte
+    // offset, LDS destination). Copies are branch-free: chunks past the tile
+    // or rows past n re-read a valid row and land in a dummy LDS slot, so all
+    // loads of a tile stay in flight together.
+    int crow[CPT], coff[CPT], ldst[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+        const int c = threadIdx.x + k * kWG;
+        const bool ok = c < tile_chunks;
+        crow[k] = ok ? c / row_chunks : 0;
+        coff[k] = ok ? (c % row_chunks) * 16 : 0;
+        ldst[k] = ok ? crow[k] * row_bytes + coff[k] : -1;
+    }
+    // two register sets: tile j of this workgroup lives in set j % 2
+    u32x4 pa[CPT], pb[CPT];
+    auto load_tile = [&](u32x4 (&pf)[CPT], int t) {
+        t = t < ntiles ? t : ntiles - 1;
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            int r = t * RT + crow[k];
+            r = r < n ? r : n - 1;
+            pf[k] = ldg16(sg.row(r) + coff[k]);
+        }
+    };
+    auto store_tile = [&](const u32x4 (&pf)[CPT], uint8_t* buf) {
+#pragma unroll
+        for (int k = 0; k < CPT; k++) *(u32x4*)(ldst[k] >= 0 ? buf + ldst[k] : dummy) = pf[k];
+    };
+    if (T0 >= ntiles) return;  // workgroup-uniform
+    // the first two tiles' loads overlap the activation staging
+    load_tile(pa, T0);
+    load_tile(pb, T0 + GS);
+    stage_input<PRO, G>(xs, a);
+    const float* xsum = xs + K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane % LPR, sub = lane / LPR;
+    const int units = nb * 4;
+
+    // this lane's activation slices, fixed for the launch
+    float xv[NU][64];
+    float X[NU][4];
+#pragma unroll
+    for (int i = 0; i < NU; i++) {
+        const int u = min(lr + LPR * i, units - 1);
+        const int b = u >> 2;
+        if (FMT == FMT_Q4K) {
+            const int g = u & 3;
+#pragma unroll
+            for (int e = 0; e < 64; e++) xv[i][e] = xs[b * 256 + g * 64 + e];
+            X[i][0] = xsum[b * 8 + 2 * g];
+            X[i][1] = xsum[b * 8 + 2 * g + 1];
+            X[i][2] = X[i][3] = 0.f;
+        } else {
+            const int h = (u >> 1) & 1, j = u & 1;
+            const int e0 = b * 256 + h * 128 + 16 * j;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) xv[i][16 * q + e] = xs[e0 + 32 * q + e];
+                X[i][q] = xsum[(e0 + 32 * q) / 16];
+            }
+        }
+    }
+    store_tile(pa, tb0);
+    load_tile(pa, T0 + 2 * GS);
+    __syncthreads();
+
+    auto compute = [&](int tile, int boff) {
+        float acc[UU];
+#pragma unroll
+        for (int k = 0; k < UU; k++) {
+            acc[k] = 0.f;
+            const int roff = boff + (wave * RW + k * RPG + sub) * row_bytes;
+#pragma unroll
+            for (int i = 0; i < NU; i++) {
+                const int u = lr + LPR * i;
+                if (u >= units) continue;
+                const int b = u >> 2;
+                if (FMT == FMT_Q4K) {
+                    const int g = u & 3;
+                    const int bo = roff + b * 144;
+                    const u32x4 hdr = *(const u32x4*)(tb0 + bo);
+                    const u32x4 qa = *(const u32x4*)(tb0 + bo + 16 + 32 * g);
+                    const u32x4 qb = *(const u32x4*)(tb0 + bo + 32 + 32 * g);
+                    acc[k] += q4k_unit(hdr, qa, qb, g, xv[i], X[i][0], X[i][1]);
+                } else {
+                    const int h = (u >> 1) & 1, j = u & 1;
+                    const int bo = roff + b * 210;
+                    const u32x4 ql0 = lds16_a2(tb0, bo + 64 * h + 16 * j);
+                    const u32x4 ql1 = lds16_a2(tb0, bo + 64 * h + 32 + 16 * j);
+                    const u32x4 qh = lds16_a2(tb0, bo + 128 + 32 * h + 16 * j);
+                    const u32x4 scw = lds16_a2(tb0, bo + 192);
+                    const uint32_t db = *(const uint16_t*)(tb0 + bo + 208);
+                    acc[k] += q6k_unit(ql0, ql1, qh, scw, db, h, j, xv[i], X[i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < UU; k++) {
+            const float sum = group_sum<LPR>(acc[k]);
+            const int r = tile * RT + wave * RW + k * RPG + sub;
+            if (lr == 0 && r < n) store_out(sg, a.accumulate, r, sum);
+        }
+    };
+
+    // Tile i of this workgroup (T0 + i*GS) is computed from LDS buffer i % 2;
+    // before that buffer is reused, tile i+1 moves from its register set into
+    // the other buffer and the set is refilled with tile i+3. The loop runs
+    // whole pairs without early exits (exits merging into the loop header
+    // would make the compiler wait for every outstanding load), the tail
+    // handles the last one or two tiles.
+    const int cnt = (ntiles - T0 + GS - 1) / GS;
+    int i = 0;
+    for (; i + 2 < cnt; i += 2) {
+        const int t = T0 + i * GS;
+        compute(t, 0);
+        store_tile(pb, tb1);
+        load_tile(pb, t + 3 * GS);
+        __syncthreads();
+        compute(t + GS, tile_bytes);
+        store_tile(pa, tb0);
+        load_tile(pa, t + 4 * GS);
+        __syncthreads();
+    }
+    compute(T0 + i * GS, 0);
+    if (i + 1 < cnt) {
+        store_tile(pb, tb1);
+        __syncthreads();
+        compute(T0 + (i + 1) * GS, tile_bytes);
     }
 }
 
@@ -533,16 +755,25 @@ int pow2_ceil(int v) {
     return p;
 }
 
+// Launch-shape knobs (defaults tuned on MI355X; the environment variables
+// MIVI_GEMV_WG_PER_CU and MIVI_GEMV_U override them for sweeps).
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
 int grid_for(int waves) {
+    static const int per_cu = env_int("MIVI_GEMV_WG_PER_CU", 8);
     int wgs = (waves + 3) / 4;
-    int cap = mivi::num_cus() * 8;
+    int cap = mivi::num_cus() * per_cu;
     return std::max(1, std::min(wgs, cap));
 }
 
 template <int PRO>
 int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
     const int K = a.K;
-    const int U = n >= 16384 ? 4 : 2;
+    static const int u_env = env_int("MIVI_GEMV_U", 0);
+    const int U = u_env ? u_env : (n >= 16384 ? 4 : 2);
 #define L3(KER, LPR, UU) hipLaunchKernelGGL((KER<LPR, UU, PRO>), dim3(grid), dim3(kWG), lds, s, a)
 #define BY_U(KER, LPR) \
     if (U == 4) L3(KER, LPR, 4); else L3(KER, LPR, 2)
@@ -555,6 +786,33 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
     case 16: BY_U(KER, 16); break;           \
     case 32: BY_U(KER, 32); break;           \
     default: BY_U(KER, 64); break;           \
+    }
+    // tiled kernel for the shapes it covers (rows 16-byte multiples, 16-byte
+    // aligned matrices), the streaming kernel otherwise
+    if ((t == MIVI_GGML_Q4_K || t == MIVI_GGML_Q6_K) && (K == 2048 || K == 4096 || K == 8192) &&
+        !env_int("MIVI_GEMV_V1", 0)) {
+        bool aligned = true;
+        for (int i = 0; i < a.nseg; i++) aligned = aligned && ((uintptr_t)a.seg[i].W % 16 == 0);
+        const int rb = K / 256 * (t == MIVI_GGML_Q4_K ? 144 : 210);
+        if (aligned && rb % 16 == 0) {
+            const int G = t == MIVI_GGML_Q4_K ? 32 : 16;
+            const int lpr = K == 2048 ? 32 : 64, nu = K == 8192 ? 2 : 1, uu = K == 8192 ? 1 : 2;
+            const int rt = 4 * (64 / lpr) * uu;
+            const size_t lds = (((size_t)K + K / G) * 4 + 15) / 16 * 16 + 2 * (size_t)rt * rb + 32;
+            const int ntiles = (n + rt - 1) / rt;
+            static const int per_cu = env_int("MIVI_GEMV_TILED_WG_PER_CU", 2);
+            const int grid = std::max(1, std::min(ntiles, mivi::num_cus() * per_cu));
+#define LT(FMT, LPR, NU, UUV) \
+    hipLaunchKernelGGL((gemv_kq_tiled_kernel<FMT, LPR, NU, UUV, PRO>), dim3(grid), dim3(kWG), lds, s, a)
+            if (t == MIVI_GGML_Q4_K) {
+                if (K == 2048) LT(FMT_Q4K, 32, 1, 2); else if (K == 4096) LT(FMT_Q4K, 64, 1, 2); else LT(FMT_Q4K, 64, 2, 1);
+            } else {
+                if (K == 2048) LT(FMT_Q6K, 32, 1, 2); else if (K == 4096) LT(FMT_Q6K, 64, 1, 2); else LT(FMT_Q6K, 64, 2, 1);
+            }
+#undef LT
+            MIVI_HIP_CHECK(hipGetLastError());
+            return MIVI_OK;
+        }
     }
     switch (t) {
     case MIVI_GGML_Q4_K:
