@@ -539,174 +539,464 @@ enum { FMT_Q4K = 0, FMT_Q6K = 1 };
 
 template <int FMT> struct KQ;
 template <> struct KQ<FMT_Q4K> { static constexpr int bytes = 144, G = 32, CPT = 5; };
-template <> struct KQ<FMT_Q6K> { static constexpr int bytes = 210, G = 16, CPT = 7; };
+template <> struct KQ<FMT_Q6K> { static constexpr int bytes = 210, G = 0, CPT = 7; };
 
 __device__ __forceinline__ u32x4 ldg16(const uint8_t* p) {
     return *(const __attribute__((address_space(1))) u32x4*)p;
 }
 
-// 16 bytes at byte offset `off` (2-byte aligned) of an LDS region whose base
-// is 16-byte aligned: aligned dwords + alignbyte; reads [off - 2, off + 18).
-__device__ __forceinline__ u32x4 lds16_a2(const uint8_t* base16, int off) {
-    const uint32_t* w = (const uint32_t*)(base16 + (off & ~3));
-    const uint32_t sh = (uint32_t)(off & 3);
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
-    u32x4 r;
-    r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
-    r.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
-    r.z = __builtin_amdgcn_alignbyte(w3, w2, sh);
-    r.w = __builtin_amdgcn_alignbyte(w4, w3, sh);
-    return r;
+// Unaligned LDS/global vector types: the HSA runtime runs gfx9+ in unaligned
+// access mode, so these compile to single ds_read_b128 / ds_read_b64.
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2_a1 __attribute__((ext_vector_type(2), aligned(1)));
+
+// ------------------------------------------------ activations as int8 digits
+//
+// The tiled kernels multiply the weight codes by x in integer arithmetic.
+// x is represented against one scale per launch, s = max|x| / 127, as
+//     x ~= s * (d0 + d1 / 254 + d2 / 254^2),   d0, d1, d2 in [-127, 127],
+// with |x - x~| < 2.5e-7 * max|x|. A row's dot product is then
+//     s * sum_d 254^-d * sum_i w_i d_i,
+// where every sum of code * digit is exact in int32 (v_dot4_i32_i8) and the
+// per-sub-block scales are applied with exact 24-bit integer multiplies.
+// The error of the whole dot is below 2.5e-7 * ||w||_1 * max|x|, i.e.
+// 2.5e-7 * sqrt(K) * ||w|| * ||x|| (2.3e-5 of ||w|| ||x|| at K = 8192).
+constexpr float kDig1 = 1.0f / 254.0f, kDig2 = 1.0f / 64516.0f;
+
+__device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
+
+// Digit planes of the K floats staged at xs, written to dig[d * K / 4 + i]
+// (four values per dword, value 4i + e in byte e). Returns s (NaN when x
+// holds a NaN or an infinity, so the products come out NaN as in fp32).
+__device__ __forceinline__ float stage_digits(const float* xs, uint32_t* dig, int K) {
+    __shared__ float red[kWG / 64];
+    float m = 0.f;
+    for (int i = threadIdx.x; i < K; i += kWG) m = nanmax(m, fabsf(xs[i]));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = nanmax(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < kWG / 64; i++) m = nanmax(m, red[i]);
+    const bool finite = m > 0.f && m <= 3.40282347e38f;
+    const float inv = finite ? 127.0f / m : 0.0f;
+    const float sc = (m - m) + m / 127.0f;
+    for (int i = threadIdx.x; i < K / 4; i += kWG) {
+        const f32x4 v = *(const f32x4*)(xs + 4 * i);
+        uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float y = v[e] * inv;
+            const float d0 = rintf(y);
+            const float t1 = (y - d0) * 254.0f;
+            const float d1 = rintf(t1);
+            const float d2 = rintf((t1 - d1) * 254.0f);
+            w0 |= ((uint32_t)(int)d0 & 0xFFu) << (8 * e);
+            w1 |= ((uint32_t)(int)d1 & 0xFFu) << (8 * e);
+            w2 |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
+        }
+        dig[i] = w0;
+        dig[K / 4 + i] = w1;
+        dig[K / 2 + i] = w2;
+    }
+    return sc;
 }
 
-template <int FMT, int LPR, int NU, int UU, int PRO>
-__global__ void __launch_bounds__(kWG) gemv_kq_tiled_kernel(const mivi::GemvArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    constexpr int G = KQ<FMT>::G, CPT = KQ<FMT>::CPT;
-    constexpr int RPG = 64 / LPR, RW = RPG * UU, RT = 4 * RW;
-    const int K = a.K, nb = K / 256;
-    const int row_bytes = nb * KQ<FMT>::bytes;
-    const int row_chunks = row_bytes / 16, tile_chunks = RT * row_chunks;
-    const int tile_bytes = RT * row_bytes;
-    float* xs = (float*)smem;
-    const int xbytes = ((K + K / G) * 4 + 15) & ~15;
-    uint8_t* tb0 = smem + xbytes;
-    uint8_t* tb1 = tb0 + tile_bytes;
-    uint8_t* dummy = tb0 + 2 * tile_bytes;
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// a * b for |a| < 2^23 and 8-bit b: the explicit 24-bit sign extension lets
+// the compiler use the full-rate v_mad_i32_i24 instead of v_mul_lo_u32.
+__device__ __forceinline__ int mul24(int a, int b) { return (int)__builtin_amdgcn_sbfe(a, 0, 24) * b; }
+
+// One Q6_K unit (16 values of each of the sub-blocks l, l+32, l+64, l+96 of
+// half h, q6_k.rs:68-111): sum over the unit of sc * (q - 32) * digits, per
+// digit plane, in int32; off[k][d] = -32 * sum of the 16 digits of quad k.
+// Returns d * (A0 + A1/254 + A2/254^2) in units of s.
+__device__ __forceinline__ float q6k_unit_i8(u32x4 ql0, u32x4 ql1, u32x4 qh, u32x2 scw, uint32_t dbits,
+                                             const uint32_t (&xd)[3][16], const int (&off)[4][3]) {
+    const uint32_t L0[4] = {ql0.x, ql0.y, ql0.z, ql0.w};
+    const uint32_t L1[4] = {ql1.x, ql1.y, ql1.z, ql1.w};
+    const uint32_t H[4] = {qh.x, qh.y, qh.z, qh.w};
+    int D[4][3];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int d = 0; d < 3; d++) D[k][d] = off[k][d];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const uint32_t q1 = (L0[m] & 0x0F0F0F0Fu) | ((H[m] << 4) & 0x30303030u);
+        const uint32_t q2 = (L1[m] & 0x0F0F0F0Fu) | ((H[m] << 2) & 0x30303030u);
+        const uint32_t q3 = ((L0[m] >> 4) & 0x0F0F0F0Fu) | (H[m] & 0x30303030u);
+        const uint32_t q4 = ((L1[m] >> 4) & 0x0F0F0F0Fu) | ((H[m] >> 2) & 0x30303030u);
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            D[0][d] = sdot4(q1, xd[d][m], D[0][d]);
+            D[1][d] = sdot4(q2, xd[d][4 + m], D[1][d]);
+            D[2][d] = sdot4(q3, xd[d][8 + m], D[2][d]);
+            D[3][d] = sdot4(q4, xd[d][12 + m], D[3][d]);
+        }
+    }
+    // scales sc[8h + j + 2k], k = 0..3: bytes 0, 2, 4, 6 of scw
+    const int sc[4] = {(int)(int8_t)scw.x, (int)(int8_t)(scw.x >> 16), (int)(int8_t)scw.y,
+                       (int)(int8_t)(scw.y >> 16)};
+    int A[3];
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+        // |D| <= 16 * 32 * 127 < 2^17, |A| < 2^26: exact 24-bit multiplies
+        A[d] = mul24(D[0][d], sc[0]) + mul24(D[1][d], sc[1]) + mul24(D[2][d], sc[2]) + mul24(D[3][d], sc[3]);
+    }
+    const float f = fmaf((float)A[2], kDig2, fmaf((float)A[1], kDig1, (float)A[0]));
+    return half_bits_to_f32(dbits) * f;
+}
+
+// One Q4_K unit (sub-blocks 2g and 2g+1, q4_k_m.rs:144-214):
+// d * s * sum_d 254^-d (sc0 * sum(q xd) + sc1 * ...) - dmin * (m0 X0 + m1 X1),
+// X0, X1 the fp32 sums of x over the two sub-blocks.
+__device__ __forceinline__ float q4k_unit_i8(u32x4 hdr, u32x4 qa, u32x4 qb, int g, const uint32_t (&xd)[3][16],
+                                             float s, float X0, float X1) {
+    const float d = half_bits_to_f32(hdr.x), dmin = half_bits_to_f32(hdr.x >> 16);
+    uint32_t sc0, m0, sc1, m1;
+    q4k_scales(hdr.y, hdr.z, hdr.w, g, sc0, m0, sc1, m1);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    int Dl[3] = {0, 0, 0}, Dh[3] = {0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        const uint32_t lo = q[m] & 0x0F0F0F0Fu, hi = (q[m] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int e = 0; e < 3; e++) {
+            Dl[e] = sdot4(lo, xd[e][m], Dl[e]);       // values 64g + 4m + 0..3
+            Dh[e] = sdot4(hi, xd[e][8 + m], Dh[e]);   // values 64g + 32 + 4m + 0..3
+        }
+    }
+    int A[3];
+#pragma unroll
+    for (int e = 0; e < 3; e++) A[e] = mul24(Dl[e], (int)sc0) + mul24(Dh[e], (int)sc1);
+    const float f = fmaf((float)A[2], kDig2, fmaf((float)A[1], kDig1, (float)A[0]));
+    return (d * s) * f - dmin * fmaf((float)m0, X0, (float)m1 * X1);
+}
+
+// ------------------------------------------- activation staging (stream kernel)
+//
+// Each thread owns E = K / 256 consecutive activations. All of its input
+// loads are issued in one batch (before the weight prefetch, so waiting for
+// them never waits for weights), then one workgroup reduction (sum of
+// squares and max together) and one barrier publish the int8 digit planes
+// (and, for Q4_K, the fp32 sums of each 32-value sub-block) in LDS.
+
+typedef __attribute__((address_space(1))) const f32x4 gf32x4;
+
+constexpr int kConvKs = 3;  // conv window of the streaming prologue (LFM2 L_cache)
+
+template <int PRO, int E>
+struct StageIn {
+    static constexpr bool kConv = PRO == mivi::PRO_CONV;
+    f32x4 x[E / 4], y[E / 4];                 // NONE: x; RMSNORM: x, norm w; SWIGLU: gate, up; CONV: B, X
+    f32x4 c[kConv ? E / 4 : 1];               // CONV: C
+    f32x4 st[kConv ? E * kConvKs / 4 : 1];    // CONV: previous window of the E channels
+    f32x4 cw[kConv ? E * kConvKs / 4 : 1];    // CONV: per-channel weights (mode 0)
+
+    __device__ __forceinline__ void load(const mivi::GemvArgs& a) {
+        const int e0 = threadIdx.x * E;
+#pragma unroll
+        for (int i = 0; i < E / 4; i++) x[i] = *(gf32x4*)(a.x + e0 + 4 * i);
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) y[i] = *(gf32x4*)(a.norm_w + e0 + 4 * i);
+        } else if constexpr (PRO == mivi::PRO_SWIGLU) {
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) y[i] = *(gf32x4*)(a.x2 + e0 + 4 * i);
+        } else if constexpr (kConv) {
+            // a.x = [B | C | X], ssm.rs:80-140
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) {
+                c[i] = *(gf32x4*)(a.x + a.K + e0 + 4 * i);
+                y[i] = *(gf32x4*)(a.x + 2 * a.K + e0 + 4 * i);
+            }
+            const bool swap = a.phase && ((*a.phase) & 1);
+            const float* st_in = swap ? a.st_out : a.st_in;
+#pragma unroll
+            for (int i = 0; i < E * kConvKs / 4; i++) st[i] = *(gf32x4*)(st_in + e0 * kConvKs + 4 * i);
+            if (a.conv_mode == 0) {
+#pragma unroll
+                for (int i = 0; i < E * kConvKs / 4; i++) cw[i] = *(gf32x4*)(a.conv_w + e0 * kConvKs + 4 * i);
+            }
+        }
+    }
+
+    // Forms the activations, writes the digit planes dig[3][K/4] (and the
+    // Q4_K sub-block sums xsum[K/32] when SUMS) and returns the digit scale s.
+    template <bool SUMS>
+    __device__ __forceinline__ float finish(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
+        __shared__ float red[2][kWG / 64];
+        const int K = a.K, e0 = threadIdx.x * E;
+        float v[E];
+#pragma unroll
+        for (int i = 0; i < E; i++) v[i] = x[i / 4][i % 4];
+        float m = 0.f, ss = 0.f;
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+            // ss and max|x w| in one reduction; max|x * scale * w| = scale * max|x w|
+#pragma unroll
+            for (int i = 0; i < E; i++) {
+                ss = fmaf(v[i], v[i], ss);
+                m = nanmax(m, fabsf(v[i] * y[i / 4][i % 4]));
+            }
+        } else if constexpr (PRO == mivi::PRO_SWIGLU) {
+#pragma unroll
+            for (int i = 0; i < E; i++) v[i] = silu_f(v[i]) * y[i / 4][i % 4];  // math.rs:87-95
+        } else if constexpr (kConv) {
+            const bool writer = blockIdx.x == 0;
+            const bool swap = a.phase && ((*a.phase) & 1);
+            float* st_out = swap ? (float*)a.st_in : a.st_out;
+            float w[E * kConvKs];
+#pragma unroll
+            for (int i = 0; i < E * kConvKs; i++)
+                w[i] = a.conv_mode == 0 ? cw[i / 4][i % 4]
+                     : a.conv_mode == 1 ? a.conv_w[i % kConvKs] : 1.0f / (float)kConvKs;
+            float nst[E * kConvKs];
+#pragma unroll
+            for (int d = 0; d < E; d++) {
+                const float bx = v[d] * y[d / 4][d % 4];
+                float conv = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kConvKs; k++) {
+                    const int o = d * kConvKs + k;
+                    const float sv = k + 1 < kConvKs ? st[(o + 1) / 4][(o + 1) % 4] : bx;
+                    conv += w[o] * sv;
+                    nst[o] = sv;
+                }
+                v[d] = c[d / 4][d % 4] * conv;
+            }
+            if (writer) {
+#pragma unroll
+                for (int i = 0; i < E * kConvKs / 4; i++)
+                    *(f32x4*)(st_out + e0 * kConvKs + 4 * i) =
+                        f32x4{nst[4 * i], nst[4 * i + 1], nst[4 * i + 2], nst[4 * i + 3]};
+            }
+        }
+        if constexpr (PRO != mivi::PRO_RMSNORM) {
+#pragma unroll
+            for (int i = 0; i < E; i++) m = nanmax(m, fabsf(v[i]));
+        }
+        // one workgroup reduction of (ss, m)
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            if constexpr (PRO == mivi::PRO_RMSNORM) ss += __shfl_xor(ss, o, 64);
+            m = nanmax(m, __shfl_xor(m, o, 64));
+        }
+        if ((threadIdx.x & 63) == 0) {
+            red[0][threadIdx.x >> 6] = ss;
+            red[1][threadIdx.x >> 6] = m;
+        }
+        __syncthreads();
+        m = red[1][0];
+        ss = red[0][0];
+#pragma unroll
+        for (int i = 1; i < kWG / 64; i++) {
+            m = nanmax(m, red[1][i]);
+            ss += red[0][i];
+        }
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+            const float scale = 1.0f / sqrtf(ss / (float)K + a.eps);  // math.rs:7-22
+#pragma unroll
+            for (int i = 0; i < E; i++) v[i] = v[i] * scale * y[i / 4][i % 4];
+            m *= scale;
+        }
+        // digits (see the representation above)
+        const bool finite = m > 0.f && m <= 3.40282347e38f;
+        const float inv = finite ? 127.0f / m : 0.0f;
+        const float sc = (m - m) + m / 127.0f;
+        uint32_t w0[E / 4], w1[E / 4], w2[E / 4];
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            w0[q] = w1[q] = w2[q] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float yv = v[4 * q + e] * inv;
+                const float d0 = rintf(yv);
+                const float t1 = (yv - d0) * 254.0f;
+                const float d1 = rintf(t1);
+                const float d2 = rintf((t1 - d1) * 254.0f);
+                w0[q] |= ((uint32_t)(int)d0 & 0xFFu) << (8 * e);
+                w1[q] |= ((uint32_t)(int)d1 & 0xFFu) << (8 * e);
+                w2[q] |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            dig[e0 / 4 + q] = w0[q];
+            dig[K / 4 + e0 / 4 + q] = w1[q];
+            dig[K / 2 + e0 / 4 + q] = w2[q];
+        }
+        if constexpr (SUMS) {
+            // fp32 sums of each 32-value sub-block (32 / E threads share one)
+#pragma unroll
+            for (int b = 0; b < (E >= 32 ? E / 32 : 1); b++) {
+                float t = 0.f;
+#pragma unroll
+                for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[b * 32 + i];
+                if constexpr (E < 32) {
+#pragma unroll
+                    for (int o = 1; o < 32 / E; o <<= 1) t += __shfl_xor(t, o, 64);
+                }
+                if (E >= 32 || (threadIdx.x % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t;
+            }
+        }
+        __syncthreads();
+        return sc;
+    }
+};
+
+// Bytes of one 64-value unit of a row, as its lane loads them.
+template <int FMT> struct Unit;
+template <> struct Unit<FMT_Q6K> { u32x4 ql0, ql1, qh; u32x2 sc; uint32_t d; };
+template <> struct Unit<FMT_Q4K> { u32x4 hdr, qa, qb; };
+
+typedef __attribute__((address_space(1))) const u32x4_a2 gu32x4_a2;
+typedef __attribute__((address_space(1))) const u32x2_a1 gu32x2_a1;
+typedef __attribute__((address_space(1))) const uint16_t gu16;
+
+// Unit u of the row at `row`: Q6_K unit (b, h, j) = block u/4, half h,
+// l in [16j, 16j + 16); Q4_K unit (b, g) = block u/4, sub-blocks 2g, 2g+1.
+template <int FMT>
+__device__ __forceinline__ void load_unit(Unit<FMT>& U, const uint8_t* row, int u) {
+    const int b = u >> 2;
+    if constexpr (FMT == FMT_Q6K) {
+        const int h = (u >> 1) & 1, j = u & 1;
+        const uint8_t* p = row + b * 210;
+        U.ql0 = *(gu32x4_a2*)(p + 64 * h + 16 * j);
+        U.ql1 = *(gu32x4_a2*)(p + 64 * h + 32 + 16 * j);
+        U.qh = *(gu32x4_a2*)(p + 128 + 32 * h + 16 * j);
+        U.sc = *(gu32x2_a1*)(p + 192 + 8 * h + j);
+        U.d = *(gu16*)(p + 208);
+    } else {
+        const int g = u & 3;
+        const uint8_t* p = row + b * 144;
+        U.hdr = ldg16(p);
+        U.qa = ldg16(p + 16 + 32 * g);
+        U.qb = ldg16(p + 32 + 32 * g);
+    }
+}
+
+// K-quant GEMV for the decode shapes (K = 2048/4096/8192). A persistent grid
+// of waves walks groups of RPW = 64/LPR rows; in each group a row is covered
+// by LPR lanes, each owning NU fixed 64-value units, so a lane's activation
+// digits stay in registers for the whole launch. Every lane loads its own
+// units straight from HBM into a ring of PD row groups held in registers:
+// the loop has no LDS traffic and no barriers, so each wave streams at its
+// own pace. After the x staging the workgroup never synchronises again.
+template <int FMT, int KT, int LPR, int NU, int PD, int PRO>
+__global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArgs a) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int K = KT, nb = K / 256, units = nb * 4;
+    constexpr int row_bytes = nb * KQ<FMT>::bytes;
+    __shared__ __attribute__((aligned(16))) uint32_t dig[3 * K / 4];
+    __shared__ float xsum[FMT == FMT_Q4K ? K / 32 : 1];
     const Segs sg(a, row_bytes);
     const int n = sg.n;
-    const int ntiles = (n + RT - 1) / RT;
-    const int T0 = blockIdx.x, GS = gridDim.x;
-
-    // This thread's 16-byte chunks of a tile (row within the tile, byte
-    // offset, LDS destination). Copies are branch-free: chunks past the tile
-    // or rows past n re-read a valid row and land in a dummy LDS slot, so all
-    // loads of a tile stay in flight together.
-    int crow[CPT], coff[CPT], ldst[CPT];
-#pragma unroll
-    for (int k = 0; k < CPT; k++) {
-        const int c = threadIdx.x + k * kWG;
-        const bool ok = c < tile_chunks;
-        crow[k] = ok ? c / row_chunks : 0;
-        coff[k] = ok ? (c % row_chunks) * 16 : 0;
-        ldst[k] = ok ? crow[k] * row_bytes + coff[k] : -1;
-    }
-    // two register sets: tile j of this workgroup lives in set j % 2
-    u32x4 pa[CPT], pb[CPT];
-    auto load_tile = [&](u32x4 (&pf)[CPT], int t) {
-        t = t < ntiles ? t : ntiles - 1;
-#pragma unroll
-        for (int k = 0; k < CPT; k++) {
-            int r = t * RT + crow[k];
-            r = r < n ? r : n - 1;
-            pf[k] = ldg16(sg.row(r) + coff[k]);
-        }
-    };
-    auto store_tile = [&](const u32x4 (&pf)[CPT], uint8_t* buf) {
-#pragma unroll
-        for (int k = 0; k < CPT; k++) *(u32x4*)(ldst[k] >= 0 ? buf + ldst[k] : dummy) = pf[k];
-    };
-    if (T0 >= ntiles) return;  // workgroup-uniform
-    // the first two tiles' loads overlap the activation staging
-    load_tile(pa, T0);
-    load_tile(pb, T0 + GS);
-    stage_input<PRO, G>(xs, a);
-    const float* xsum = xs + K;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane % LPR, sub = lane / LPR;
-    const int units = nb * 4;
+    const int ngroups = (n + RPW - 1) / RPW;
+    const int nw = gridDim.x * (kWG / 64), wid = blockIdx.x * (kWG / 64) + wave;
+    const int cnt = wid < ngroups ? (ngroups - wid + nw - 1) / nw : 0;  // wave-uniform
 
-    // this lane's activation slices, fixed for the launch
-    float xv[NU][64];
-    float X[NU][4];
+    // row of this lane in step s of this wave (steps past the end re-read
+    // the wave's last row, which is then never stored)
+    auto row_of = [&](int st) {
+        st = st < cnt ? st : cnt - 1;
+        const int r = (wid + st * nw) * RPW + sub;
+        return r < n ? r : n - 1;
+    };
+    Unit<FMT> buf[PD][NU];
+    auto load_step = [&](Unit<FMT> (&B)[NU], int st) {
+        const uint8_t* row = sg.row(row_of(st));
+#pragma unroll
+        for (int i = 0; i < NU; i++) load_unit<FMT>(B[i], row, min(lr + LPR * i, units - 1));
+    };
+    // activation loads first, then the first PD row groups of weights, which
+    // stay in flight while x is staged
+    StageIn<PRO, K / kWG> in;
+    in.load(a);
+    if (cnt > 0) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) load_step(buf[p], p);
+    }
+    const float s = in.template finish<FMT == FMT_Q4K>(a, dig, xsum);
+
+    // this lane's activation digits (and their per-quad offsets / fp32
+    // sub-block sums), fixed for the launch
+    uint32_t xd[NU][3][16];
+    int off[NU][4][3];
+    float X[NU][2];
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = min(lr + LPR * i, units - 1);
         const int b = u >> 2;
         if (FMT == FMT_Q4K) {
             const int g = u & 3;
+            const int w0 = (b * 256 + g * 64) / 4;
 #pragma unroll
-            for (int e = 0; e < 64; e++) xv[i][e] = xs[b * 256 + g * 64 + e];
+            for (int e = 0; e < 3; e++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u32x4 v = *(const u32x4*)(dig + e * (K / 4) + w0 + 4 * q);
+                    xd[i][e][4 * q] = v.x; xd[i][e][4 * q + 1] = v.y;
+                    xd[i][e][4 * q + 2] = v.z; xd[i][e][4 * q + 3] = v.w;
+                }
             X[i][0] = xsum[b * 8 + 2 * g];
             X[i][1] = xsum[b * 8 + 2 * g + 1];
-            X[i][2] = X[i][3] = 0.f;
         } else {
             const int h = (u >> 1) & 1, j = u & 1;
             const int e0 = b * 256 + h * 128 + 16 * j;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
+            for (int e = 0; e < 3; e++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) xv[i][16 * q + e] = xs[e0 + 32 * q + e];
-                X[i][q] = xsum[(e0 + 32 * q) / 16];
-            }
-        }
-    }
-    store_tile(pa, tb0);
-    load_tile(pa, T0 + 2 * GS);
-    __syncthreads();
-
-    auto compute = [&](int tile, int boff) {
-        float acc[UU];
-#pragma unroll
-        for (int k = 0; k < UU; k++) {
-            acc[k] = 0.f;
-            const int roff = boff + (wave * RW + k * RPG + sub) * row_bytes;
-#pragma unroll
-            for (int i = 0; i < NU; i++) {
-                const int u = lr + LPR * i;
-                if (u >= units) continue;
-                const int b = u >> 2;
-                if (FMT == FMT_Q4K) {
-                    const int g = u & 3;
-                    const int bo = roff + b * 144;
-                    const u32x4 hdr = *(const u32x4*)(tb0 + bo);
-                    const u32x4 qa = *(const u32x4*)(tb0 + bo + 16 + 32 * g);
-                    const u32x4 qb = *(const u32x4*)(tb0 + bo + 32 + 32 * g);
-                    acc[k] += q4k_unit(hdr, qa, qb, g, xv[i], X[i][0], X[i][1]);
-                } else {
-                    const int h = (u >> 1) & 1, j = u & 1;
-                    const int bo = roff + b * 210;
-                    const u32x4 ql0 = lds16_a2(tb0, bo + 64 * h + 16 * j);
-                    const u32x4 ql1 = lds16_a2(tb0, bo + 64 * h + 32 + 16 * j);
-                    const u32x4 qh = lds16_a2(tb0, bo + 128 + 32 * h + 16 * j);
-                    const u32x4 scw = lds16_a2(tb0, bo + 192);
-                    const uint32_t db = *(const uint16_t*)(tb0 + bo + 208);
-                    acc[k] += q6k_unit(ql0, ql1, qh, scw, db, h, j, xv[i], X[i]);
+                for (int q = 0; q < 4; q++) {
+                    const u32x4 v = *(const u32x4*)(dig + e * (K / 4) + (e0 + 32 * q) / 4);
+                    xd[i][e][4 * q] = v.x; xd[i][e][4 * q + 1] = v.y;
+                    xd[i][e][4 * q + 2] = v.z; xd[i][e][4 * q + 3] = v.w;
+                    int t = 0;
+                    t = sdot4(v.x, 0x01010101u, t);
+                    t = sdot4(v.y, 0x01010101u, t);
+                    t = sdot4(v.z, 0x01010101u, t);
+                    t = sdot4(v.w, 0x01010101u, t);
+                    off[i][q][e] = -32 * t;
                 }
-            }
         }
-#pragma unroll
-        for (int k = 0; k < UU; k++) {
-            const float sum = group_sum<LPR>(acc[k]);
-            const int r = tile * RT + wave * RW + k * RPG + sub;
-            if (lr == 0 && r < n) store_out(sg, a.accumulate, r, sum);
-        }
-    };
+    }
+    if (cnt == 0) return;  // wave-uniform; no barrier follows
 
-    // Tile i of this workgroup (T0 + i*GS) is computed from LDS buffer i % 2;
-    // before that buffer is reused, tile i+1 moves from its register set into
-    // the other buffer and the set is refilled with tile i+3. The loop runs
-    // whole pairs without early exits (exits merging into the loop header
-    // would make the compiler wait for every outstanding load), the tail
-    // handles the last one or two tiles.
-    const int cnt = (ntiles - T0 + GS - 1) / GS;
-    int i = 0;
-    for (; i + 2 < cnt; i += 2) {
-        const int t = T0 + i * GS;
-        compute(t, 0);
-        store_tile(pb, tb1);
-        load_tile(pb, t + 3 * GS);
-        __syncthreads();
-        compute(t + GS, tile_bytes);
-        store_tile(pa, tb0);
-        load_tile(pa, t + 4 * GS);
-        __syncthreads();
+    auto compute = [&](const Unit<FMT> (&B)[NU], int st) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < NU; i++) {
+            if (lr + LPR * i >= units) continue;
+            if constexpr (FMT == FMT_Q4K)
+                acc += q4k_unit_i8(B[i].hdr, B[i].qa, B[i].qb, (lr + LPR * i) & 3, xd[i], s, X[i][0], X[i][1]);
+            else
+                acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, B[i].sc, B[i].d, xd[i], off[i]);
+        }
+        float sum = group_sum<LPR>(acc);
+        if (FMT == FMT_Q6K) sum *= s;
+        const int r = (wid + st * nw) * RPW + sub;
+        if (lr == 0 && r < n) store_out(sg, a.accumulate, r, sum);
+    };
+    // Step st is computed from ring slot st % PD, which is then refilled
+    // with step st + PD. Whole rounds of PD steps run without early exits
+    // (an exit merging into the loop header would make the compiler wait for
+    // every outstanding load); the tail computes the last < PD steps.
+    int st = 0;
+    for (; st + PD <= cnt; st += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(buf[p], st + p);
+            load_step(buf[p], st + p + PD);
+        }
     }
-    compute(T0 + i * GS, 0);
-    if (i + 1 < cnt) {
-        store_tile(pb, tb1);
-        __syncthreads();
-        compute(T0 + (i + 1) * GS, tile_bytes);
-    }
+#pragma unroll
+    for (int p = 0; p < PD; p++)
+        if (st + p < cnt) compute(buf[p], st + p);
 }
 
 // ------------------------------------------------------- Q8_0 quantize/dot
@@ -787,32 +1077,36 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
     case 32: BY_U(KER, 32); break;           \
     default: BY_U(KER, 64); break;           \
     }
-    // tiled kernel for the shapes it covers (rows 16-byte multiples, 16-byte
-    // aligned matrices), the streaming kernel otherwise
-    if ((t == MIVI_GGML_Q4_K || t == MIVI_GGML_Q6_K) && (K == 2048 || K == 4096 || K == 8192) &&
-        !env_int("MIVI_GEMV_V1", 0)) {
-        bool aligned = true;
-        for (int i = 0; i < a.nseg; i++) aligned = aligned && ((uintptr_t)a.seg[i].W % 16 == 0);
-        const int rb = K / 256 * (t == MIVI_GGML_Q4_K ? 144 : 210);
-        if (aligned && rb % 16 == 0) {
-            const int G = t == MIVI_GGML_Q4_K ? 32 : 16;
-            const int lpr = K == 2048 ? 32 : 64, nu = K == 8192 ? 2 : 1, uu = K == 8192 ? 1 : 2;
-            const int rt = 4 * (64 / lpr) * uu;
-            const size_t lds = (((size_t)K + K / G) * 4 + 15) / 16 * 16 + 2 * (size_t)rt * rb + 32;
-            const int ntiles = (n + rt - 1) / rt;
-            static const int per_cu = env_int("MIVI_GEMV_TILED_WG_PER_CU", 2);
-            const int grid = std::max(1, std::min(ntiles, mivi::num_cus() * per_cu));
-#define LT(FMT, LPR, NU, UUV) \
-    hipLaunchKernelGGL((gemv_kq_tiled_kernel<FMT, LPR, NU, UUV, PRO>), dim3(grid), dim3(kWG), lds, s, a)
-            if (t == MIVI_GGML_Q4_K) {
-                if (K == 2048) LT(FMT_Q4K, 32, 1, 2); else if (K == 4096) LT(FMT_Q4K, 64, 1, 2); else LT(FMT_Q4K, 64, 2, 1);
-            } else {
-                if (K == 2048) LT(FMT_Q6K, 32, 1, 2); else if (K == 4096) LT(FMT_Q6K, 64, 1, 2); else LT(FMT_Q6K, 64, 2, 1);
-            }
-#undef LT
-            MIVI_HIP_CHECK(hipGetLastError());
-            return MIVI_OK;
+    // streaming kernel for the decode shapes, the generic kernel otherwise
+    bool stream_ok = (t == MIVI_GGML_Q4_K || t == MIVI_GGML_Q6_K) && (K == 2048 || K == 4096 || K == 8192) &&
+                     !env_int("MIVI_GEMV_V1", 0);
+    // its staging loads activations as 16-byte vectors; the conv prologue is
+    // specialised for the 3-tap window
+    auto a16 = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
+    stream_ok = stream_ok && a16(a.x) && a16(a.x2) && a16(a.norm_w);
+    if (PRO == mivi::PRO_CONV)
+        stream_ok = stream_ok && K == 2048 && a.ksize == kConvKs && a16(a.st_in) && a16(a.st_out) &&
+                    (a.conv_mode != 0 || a16(a.conv_w));
+    if (stream_ok) {
+        const int lpr = K == 2048 ? 32 : 64;
+        const int ngroups = (n + 64 / lpr - 1) / (64 / lpr);
+        static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 3);
+        const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
+#define LS(FMT, KT, LPR, NU, PD) \
+    hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO>), dim3(grid), dim3(kWG), 0, s, a)
+        if (K == 2048) {
+            if (t == MIVI_GGML_Q4_K) LS(FMT_Q4K, 2048, 32, 1, 4); else LS(FMT_Q6K, 2048, 32, 1, 4);
         }
+        if constexpr (PRO != mivi::PRO_CONV) {  // the conv prologue only runs at K = 2048
+            if (K == 4096) {
+                if (t == MIVI_GGML_Q4_K) LS(FMT_Q4K, 4096, 64, 1, 4); else LS(FMT_Q6K, 4096, 64, 1, 4);
+            } else if (K == 8192) {
+                if (t == MIVI_GGML_Q4_K) LS(FMT_Q4K, 8192, 64, 2, 2); else LS(FMT_Q6K, 8192, 64, 2, 2);
+            }
+        }
+#undef LS
+        MIVI_HIP_CHECK(hipGetLastError());
+        return MIVI_OK;
     }
     switch (t) {
     case MIVI_GGML_Q4_K:
