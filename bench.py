@@ -139,6 +139,38 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
     return out
 
 
+def hbm_traffic():
+    """HBM bytes per launch of the config-2 kernel from the committed counter
+    profile (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by the same
+    counter on a kernel of known traffic); None when absent or when the kernel
+    source changed since it was measured."""
+    import hashlib
+    path = os.path.join(ROOT, "profiles", "q6k_head_gemv_traffic.json")
+    src = os.path.join(ROOT, "mivi-v4_amd", "csrc", "quant.hip")
+    try:
+        t = json.load(open(path))
+        if t.get("quant_hip_sha256") != hashlib.sha256(open(src, "rb").read()).hexdigest():
+            return None
+        return t["fetch_kib"] * 1024 / t["fetch_factor"] + t["write_kib"] * 1024 / t["write_factor"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_calibration(torch, mib, reps):
+    """Kernels of known HBM traffic for scaling the counters: a fill (writes
+    `mib` MiB), plain copies (read + write `mib` MiB each) and full reductions
+    (read `mib` MiB each)."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    for _ in range(reps):
+        src.sum()
+    torch.cuda.synchronize()
+    log(f"counter calibration: fill, {reps} copies and {reps} reductions of {n * 4} bytes")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +181,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-prefill", type=int, default=4096)
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--only-q6k", action="store_true", help="config 2 only (counter runs)")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="also run plain copies of MIB MiB (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -161,6 +196,10 @@ def main():
 
     q6 = gemv_bench(torch, hip, hip.GgmlType.Q6_K, 65536, 2048, a.steps, a.warmup, 100)
     log(f"Q6_K GEMV 65536x2048: {q6['ms_per_call'] * 1e3:.1f} us/call, {q6['gbs']:.0f} GB/s")
+    if a.copy_calib:
+        copy_calibration(torch, a.copy_calib, 10)
+    if a.only_q6k:
+        return
     q4 = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200)
     log(f"Q4_K GEMV 8192x2048: {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s")
     cpu = None
@@ -192,7 +231,7 @@ def main():
         "config": {"workload": "config2_q6k_head_gemv", "rows": 65536, "cols": 2048, "weight_type": "Q6_K",
                    "weight_copies": q6["copies"], "algo_bytes_per_call": q6["algo_bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(q6["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(q6["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(q6["gbs"] / HBM_PEAK_GBS, 4), "traffic": hbm_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }

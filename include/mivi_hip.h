@@ -103,7 +103,8 @@ int32_t mivi_hip_try_matvec_bf16(float* out, size_t out_len, const uint8_t* weig
 
 /* crates/mivi-quant/src/lib.rs:143-251 quantized_matmul_rows:
  * out[batch, rows] = inputs[batch, cols] * W[rows, cols]^T. batch == 1 is the
- * matvec path (lib.rs:173-182); batch >= 16 runs the MFMA tile kernel. */
+ * matvec path (lib.rs:173-182); larger batches currently run one GEMV per
+ * input row. */
 int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t ggml_type,
                                        const uint8_t* weights, size_t weights_len,
                                        const float* inputs, size_t inputs_len, size_t batch,
