@@ -41,9 +41,10 @@ using namespace mivi;
 namespace {
 
 constexpr int kWG = 256;
-constexpr int kChunk = 64;      // tokens per attention inner iteration
-constexpr int kMaxHd = 128;     // head_dim supported by the attention kernel
-constexpr int kMaxSplits = 512;
+constexpr int kMaxHd = 128;            // head_dim supported by the attention kernel
+constexpr int kMaxAttnSplits = 1024;   // 65536 tokens / 64 tokens per tile
+// tokens per attention workgroup (its LDS holds 8192 f32 of K and of V)
+inline int attn_tile_tokens(size_t head_dim) { return head_dim <= 64 ? 128 : 64; }
 
 // ------------------------------------------------------------------ GGUF
 
@@ -284,191 +285,301 @@ __device__ __forceinline__ void prep_head(float* dst, const float* src, const fl
     }
 }
 
-// Split-T GQA attention over one kv head (transformer.rs:112-301 with the KV
-// store of cache.rs:395-461). grid = (n_kv_heads, nsplit); each workgroup
-// scores a contiguous token range for the heads_per_kv query heads of its kv
-// head, one wave per query head, with an online softmax per 64-token chunk.
-// The workgroup whose range holds `pos` also quantizes the current K/V row
-// into the cache and uses that stored value for t = pos.
-template <int KVP>  // MIVI_KV_F32, MIVI_KV_Q8_0, MIVI_KV_F16
-__global__ void __launch_bounds__(kWG) attn_split_kernel(const AttnArgs a) {
-    __shared__ float kf[kChunk][kMaxHd + 1];
-    __shared__ float vf[kChunk][kMaxHd];
-    __shared__ float qs[4][kMaxHd];
-    __shared__ float ps[4][kChunk];
-    __shared__ float kcur[kMaxHd], vcur[kMaxHd];
-    __shared__ float red[4];
-    const int kvh = blockIdx.x, s = blockIdx.y;
-    const int hd = a.hd, half = hd / 2;
-    const int hpk = a.n_heads / a.n_kv_heads;
-    const int pos = *a.pos;
-    const int T = pos + 1;
-    const int per = (T + a.nsplit - 1) / a.nsplit;
-    const int t0 = s * per, t1 = min(T, t0 + per);
-    const float* cs = a.rope_cos + (size_t)pos * half;
-    const float* sn = a.rope_sin + (size_t)pos * half;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// ------------------------------------------------------------ attention
+//
+// GQA decode attention in two launches (transformer.rs:112-301):
+//  attn_tile_kernel    grid (n_kv_heads, nsplit): workgroup s takes tokens
+//                      [s*TT, s*TT + TT) of one kv head for its hpk query
+//                      heads and writes (max, sum, unnormalised output) per
+//                      query head;
+//  attn_combine_kernel grid n_heads: merges the splits.
+// The softmax is taken per tile and merged exactly (same value as the
+// reference's token-by-token online form, different rounding).
 
-    const bool owner = t0 <= pos && pos < t1;
-    if (owner) {
-        // current token: k rotated (and normed), v as is; store quantized
-        prep_head(kcur, a.k + kvh * hd, a.k_norm, a.eps, hd, cs, sn, red);
-        for (int i = threadIdx.x; i < hd; i += kWG) vcur[i] = a.v[kvh * hd + i];
-        __syncthreads();
-        uint8_t* krow = a.kc + (size_t)pos * a.row_bytes;
-        uint8_t* vrow = a.vc + (size_t)pos * a.row_bytes;
-        if (KVP == MIVI_KV_F32) {
-            for (int i = threadIdx.x; i < hd; i += kWG) {
+typedef __attribute__((address_space(1))) const u32x4 gau32x4;
+typedef uint32_t u32x4_a2m __attribute__((ext_vector_type(4), aligned(2)));
+typedef __attribute__((address_space(1))) const u32x4_a2m gau32x4_a2;
+
+// Head vector of the current token for this wave: optional per-head RMSNorm
+// (transformer.rs:81-96) then interleaved-pair RoPE (rope.rs:452-473). Lane l
+// holds the pair (2l, 2l+1); hd <= 128.
+__device__ __forceinline__ void wave_prep_head(float* dst, const float* src, const float* nw, float eps, int hd,
+                                               const float* cs, const float* sn) {
+    const int l = threadIdx.x & 63;
+    const bool on = 2 * l < hd;
+    float v0 = on ? src[2 * l] : 0.f, v1 = on ? src[2 * l + 1] : 0.f;
+    if (nw) {
+        const float ss = wave_sum(fmaf(v0, v0, v1 * v1));
+        const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
+        if (on) {
+            v0 = v0 * sc * nw[2 * l];
+            v1 = v1 * sc * nw[2 * l + 1];
+        }
+    }
+    if (on) {
+        const float c = cs[l], s = sn[l];
+        dst[2 * l] = v0 * c - v1 * s;
+        dst[2 * l + 1] = v0 * s + v1 * c;
+    }
+}
+
+template <int KVP, int HDM>  // cache precision; LDS sized for head_dim <= HDM (64 or 128)
+__global__ void __launch_bounds__(kWG) attn_tile_kernel(const AttnArgs a) {
+    constexpr int TT = 8192 / HDM;  // tokens per workgroup: 128 or 64
+    __shared__ float kt[TT][HDM + 1];
+    __shared__ float vt[TT][HDM];
+    __shared__ float qs[4][HDM];
+    __shared__ float sc[4][TT];
+    __shared__ float kcur[HDM], vcur[HDM];
+    const int kvh = blockIdx.x, split = blockIdx.y;
+    const int hd = a.hd, hpk = a.n_heads / a.n_kv_heads;
+    const int pos = *a.pos, T = pos + 1;
+    const int t0 = split * TT;
+    if (t0 >= T) return;  // workgroup-uniform: beyond the context
+    const int nt = min(TT, T - t0);
+    const bool owner = pos < t0 + TT;  // this tile holds the current token
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float* cs = a.rope_cos + (size_t)pos * (hd / 2);
+    const float* sn = a.rope_sin + (size_t)pos * (hd / 2);
+    const size_t rb = a.row_bytes;
+    const uint8_t* kbase = a.kc + (size_t)t0 * rb;
+    const uint8_t* vbase = a.vc + (size_t)t0 * rb;
+
+    // 1. issue the tile loads (rows past nt re-read row 0 and are dropped)
+    constexpr int CPT = KVP == MIVI_KV_F32 ? TT * HDM / 4 / kWG : KVP == MIVI_KV_F16 ? TT * HDM / 8 / kWG : 1;
+    u32x4 kr[CPT], vr[CPT];
+    uint32_t kd = 0, vd = 0;  // Q8_0 block scales
+    if constexpr (KVP == MIVI_KV_Q8_0) {
+        // one 32-value block per thread: t = tid / (hd/32), block bi
+        const int bpt = hd / 32;
+        const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
+        const bool ok = j < nt && threadIdx.x < TT * bpt;
+        const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)(kvh * bpt + bi) * 34;
+        kd = *(const __attribute__((address_space(1))) uint16_t*)(kbase + o);
+        vd = *(const __attribute__((address_space(1))) uint16_t*)(vbase + o);
+        kr[0] = *(gau32x4_a2*)(kbase + o + 2);
+        vr[0] = *(gau32x4_a2*)(vbase + o + 2);
+        // second half of the block in the upper registers of a 2-chunk array
+    } else {
+        constexpr int E = KVP == MIVI_KV_F32 ? 4 : 8;  // values per 16-byte chunk
+        const int cpr = hd / E;                        // chunks per row of this head
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            const int c = threadIdx.x + k * kWG;
+            const int j = c / cpr, part = c % cpr;
+            const bool ok = j < nt;
+            const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)kvh * hd * (16 / E) + (size_t)(ok ? part : 0) * 16;
+            kr[k] = *(gau32x4*)(kbase + o);
+            vr[k] = *(gau32x4*)(vbase + o);
+        }
+    }
+    u32x4 kr2 = {0, 0, 0, 0}, vr2 = {0, 0, 0, 0};
+    if constexpr (KVP == MIVI_KV_Q8_0) {
+        const int bpt = hd / 32;
+        const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
+        const bool ok = j < nt && threadIdx.x < TT * bpt;
+        const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)(kvh * bpt + bi) * 34;
+        kr2 = *(gau32x4_a2*)(kbase + o + 18);
+        vr2 = *(gau32x4_a2*)(vbase + o + 18);
+    }
+
+    // 2. query heads (one wave each) and, in the owner tile, the current K/V
+    if (wave < hpk) wave_prep_head(qs[wave], a.q + (size_t)(kvh * hpk + wave) * hd, a.q_norm, a.eps, hd, cs, sn);
+    if (owner && wave == 3) {
+        wave_prep_head(kcur, a.k + (size_t)kvh * hd, a.k_norm, a.eps, hd, cs, sn);
+        for (int i = lane; i < hd; i += 64) vcur[i] = a.v[(size_t)kvh * hd + i];
+        __builtin_amdgcn_wave_barrier();
+        uint8_t* krow = a.kc + (size_t)pos * rb;
+        uint8_t* vrow = a.vc + (size_t)pos * rb;
+        // store into the cache (cache.rs:395-461) and keep the stored value
+        if constexpr (KVP == MIVI_KV_F32) {
+            for (int i = lane; i < hd; i += 64) {
                 ((float*)krow)[kvh * hd + i] = kcur[i];
                 ((float*)vrow)[kvh * hd + i] = vcur[i];
             }
-        } else if (KVP == MIVI_KV_F16) {
-            for (int i = threadIdx.x; i < hd; i += kWG) {
-                uint32_t kb = f32_to_half_bits(kcur[i]), vb = f32_to_half_bits(vcur[i]);
+        } else if constexpr (KVP == MIVI_KV_F16) {
+            for (int i = lane; i < hd; i += 64) {
+                const uint32_t kb = f32_to_half_bits(kcur[i]), vb = f32_to_half_bits(vcur[i]);
                 ((uint16_t*)krow)[kvh * hd + i] = (uint16_t)kb;
                 ((uint16_t*)vrow)[kvh * hd + i] = (uint16_t)vb;
                 kcur[i] = half_bits_to_f32(kb);
                 vcur[i] = half_bits_to_f32(vb);
             }
         } else {
-            // q8_0.rs:31-58 per 32-value block; head kvh owns blocks
-            // [kvh*hd/32, (kvh+1)*hd/32) of the row (transformer.rs:170-171)
+            // q8_0.rs:31-58 per 32-value block: lanes 0-31 K, 32-63 V
             const int nbk = hd / 32;
-            if (threadIdx.x < 64 * 2 && (threadIdx.x >> 6) < 2) {
-                const bool isv = threadIdx.x >= 64;
-                float* cur = isv ? vcur : kcur;
-                uint8_t* row = isv ? vrow : krow;
-                for (int bi = 0; bi < nbk; bi++) {
-                    const int i = lane & 31;
-                    float xv = cur[bi * 32 + i];
-                    float am = fabsf(xv);
+            const bool isv = lane >= 32;
+            float* cur = isv ? vcur : kcur;
+            uint8_t* row = isv ? vrow : krow;
+            const int i = lane & 31;
+            for (int bi = 0; bi < nbk; bi++) {
+                const float xv = cur[bi * 32 + i];
+                float am = fabsf(xv);
 #pragma unroll
-                    for (int sh = 16; sh >= 1; sh >>= 1) am = fmaxf(am, __shfl_xor(am, sh, 32));
-                    float d = am / 127.0f;
-                    float id = d != 0.0f ? 1.0f / d : 0.0f;
-                    float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
-                    uint32_t dh = f32_to_half_bits(d);
-                    uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
-                    if (lane < 32) {
-                        blk[2 + i] = (uint8_t)(int8_t)q;
-                        if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
-                        cur[bi * 32 + i] = q * half_bits_to_f32(dh);
-                    }
-                }
+                for (int sh = 16; sh >= 1; sh >>= 1) am = fmaxf(am, __shfl_xor(am, sh, 32));
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
+                const uint32_t dh = f32_to_half_bits(d);
+                uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
+                blk[2 + i] = (uint8_t)(int8_t)q;
+                if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
+                cur[bi * 32 + i] = q * half_bits_to_f32(dh);
             }
         }
     }
-    // query heads of this kv head: normed, rotated
-    for (int w = 0; w < hpk && w < 4; w++)
-        prep_head(qs[w], a.q + (kvh * hpk + w) * hd, a.q_norm, a.eps, hd, cs, sn, red);
     __syncthreads();
 
-    float m_run = -INFINITY, l_run = 0.f;
-    float acc0 = 0.f, acc1 = 0.f;  // dims lane and lane + 64
-    const int h = kvh * hpk + wave;
-    for (int c0 = t0; c0 < t1; c0 += kChunk) {
-        const int nt = min(kChunk, t1 - c0);
-        // stage K/V rows [c0, c0+nt) of this kv head into LDS as f32
-        for (int idx = threadIdx.x; idx < nt * (hd / 4); idx += kWG) {
-            const int j = idx / (hd / 4), q4 = idx % (hd / 4);
-            const int t = c0 + j;
-            if (t == pos) {
+    // 3. tile to LDS as f32 (the current token from kcur/vcur)
+    if constexpr (KVP == MIVI_KV_Q8_0) {
+        const int bpt = hd / 32;
+        const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
+        if (j < nt && threadIdx.x < TT * bpt) {
+            const bool cur = t0 + j == pos;
+            const float dk = half_bits_to_f32(kd), dv = half_bits_to_f32(vd);
+            const uint32_t kw[8] = {kr[0].x, kr[0].y, kr[0].z, kr[0].w, kr2.x, kr2.y, kr2.z, kr2.w};
+            const uint32_t vw[8] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w, vr2.x, vr2.y, vr2.z, vr2.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    kf[j][4 * q4 + e] = kcur[4 * q4 + e];
-                    vf[j][4 * q4 + e] = vcur[4 * q4 + e];
-                }
-                continue;
-            }
-            const uint8_t* kr = a.kc + (size_t)t * a.row_bytes;
-            const uint8_t* vr = a.vc + (size_t)t * a.row_bytes;
-            if (KVP == MIVI_KV_F32) {
-                f32x4 kv = *(const f32x4*)((const float*)kr + kvh * hd + 4 * q4);
-                f32x4 vv = *(const f32x4*)((const float*)vr + kvh * hd + 4 * q4);
-                kf[j][4 * q4] = kv.x; kf[j][4 * q4 + 1] = kv.y; kf[j][4 * q4 + 2] = kv.z; kf[j][4 * q4 + 3] = kv.w;
-                vf[j][4 * q4] = vv.x; vf[j][4 * q4 + 1] = vv.y; vf[j][4 * q4 + 2] = vv.z; vf[j][4 * q4 + 3] = vv.w;
-            } else if (KVP == MIVI_KV_F16) {
-                uint2 kb = *(const uint2*)((const uint16_t*)kr + kvh * hd + 4 * q4);
-                uint2 vb = *(const uint2*)((const uint16_t*)vr + kvh * hd + 4 * q4);
-                kf[j][4 * q4] = half_bits_to_f32(kb.x); kf[j][4 * q4 + 1] = half_bits_to_f32(kb.x >> 16);
-                kf[j][4 * q4 + 2] = half_bits_to_f32(kb.y); kf[j][4 * q4 + 3] = half_bits_to_f32(kb.y >> 16);
-                vf[j][4 * q4] = half_bits_to_f32(vb.x); vf[j][4 * q4 + 1] = half_bits_to_f32(vb.x >> 16);
-                vf[j][4 * q4 + 2] = half_bits_to_f32(vb.y); vf[j][4 * q4 + 3] = half_bits_to_f32(vb.y >> 16);
-            } else {
-                const int e = 4 * q4, bi = e / 32, w8 = e % 32;
-                const uint8_t* kb = kr + (size_t)(kvh * (hd / 32) + bi) * 34;
-                const uint8_t* vb = vr + (size_t)(kvh * (hd / 32) + bi) * 34;
-                const float kd = half_bits_to_f32(ld_u16(kb)), vd = half_bits_to_f32(ld_u16(vb));
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    kf[j][e + u] = (float)(int8_t)kb[2 + w8 + u] * kd;
-                    vf[j][e + u] = (float)(int8_t)vb[2 + w8 + u] * vd;
-                }
+            for (int e = 0; e < 32; e++) {
+                const int d = bi * 32 + e;
+                kt[j][d] = cur ? kcur[d] : (float)(int8_t)(kw[e / 4] >> (8 * (e % 4))) * dk;
+                vt[j][d] = cur ? vcur[d] : (float)(int8_t)(vw[e / 4] >> (8 * (e % 4))) * dv;
             }
         }
-        __syncthreads();
-        if (wave < hpk) {
-            // scores: lane j <-> token c0 + j
-            float sc = -INFINITY;
-            if (lane < nt) {
+    } else {
+        constexpr int E = KVP == MIVI_KV_F32 ? 4 : 8;
+        const int cpr = hd / E;
+#pragma unroll
+        for (int k = 0; k < CPT; k++) {
+            const int c = threadIdx.x + k * kWG;
+            const int j = c / cpr, part = c % cpr;
+            if (j >= nt) continue;
+            const bool cur = t0 + j == pos;
+            const uint32_t kw[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
+            const uint32_t vw[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+                const int d = part * E + e;
+                float kvl, vvl;
+                if constexpr (KVP == MIVI_KV_F32) {
+                    kvl = __uint_as_float(kw[e]);
+                    vvl = __uint_as_float(vw[e]);
+                } else {
+                    kvl = half_bits_to_f32(kw[e / 2] >> (16 * (e % 2)));
+                    vvl = half_bits_to_f32(vw[e / 2] >> (16 * (e % 2)));
+                }
+                kt[j][d] = cur ? kcur[d] : kvl;
+                vt[j][d] = cur ? vcur[d] : vvl;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. scores: thread -> (token t, heads hg, hg + 256/TT, ...)
+    {
+        const int t = threadIdx.x % TT, hg = threadIdx.x / TT;
+        for (int h = hg; h < 4; h += kWG / TT) {
+            float s = -INFINITY;
+            if (h < hpk && t < nt) {
                 float d0 = 0.f, d1 = 0.f;
                 for (int i = 0; i < hd; i += 2) {
-                    d0 = fmaf(qs[wave][i], kf[lane][i], d0);
-                    d1 = fmaf(qs[wave][i + 1], kf[lane][i + 1], d1);
+                    d0 = fmaf(qs[h][i], kt[t][i], d0);
+                    d1 = fmaf(qs[h][i + 1], kt[t][i + 1], d1);
                 }
-                sc = (d0 + d1) * a.scale;
+                s = (d0 + d1) * a.scale;
             }
-            const float mc = wave_max(sc);
-            const float m_new = fmaxf(m_run, mc);
-            const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
-            const float p = lane < nt ? expf(sc - m_new) : 0.f;
-            l_run = l_run * alpha + wave_sum(p);
-            ps[wave][lane] = p;
-            m_run = m_new;
-            // ps[wave] is written and read by this wave only
-            __builtin_amdgcn_wave_barrier();
-            float o0 = 0.f, o1 = 0.f;
-            for (int j = 0; j < nt; j++) {
-                const float pj = ps[wave][j];
-                if (lane < hd) o0 = fmaf(pj, vf[j][lane], o0);
-                if (lane + 64 < hd) o1 = fmaf(pj, vf[j][lane + 64], o1);
-            }
-            acc0 = acc0 * alpha + o0;
-            acc1 = acc1 * alpha + o1;
+            sc[h][t] = s;
         }
-        __syncthreads();
     }
+    __syncthreads();
+
+    // 5. softmax of the tile and 6. P V, one wave per query head
     if (wave < hpk) {
-        const size_t pi = (size_t)h * a.nsplit + s;
-        if (lane == 0) {
-            a.part_m[pi] = m_run;
-            a.part_l[pi] = l_run;
+        float v[TT / 64];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < TT / 64; k++) {
+            v[k] = sc[wave][lane + 64 * k];
+            mx = fmaxf(mx, v[k]);
         }
-        if (lane < hd) a.part_acc[pi * hd + lane] = acc0;
-        if (lane + 64 < hd) a.part_acc[pi * hd + lane + 64] = acc1;
+        mx = wave_max(mx);
+        float l = 0.f;
+#pragma unroll
+        for (int k = 0; k < TT / 64; k++) {
+            const float p = lane + 64 * k < nt ? expf(v[k] - mx) : 0.f;
+            sc[wave][lane + 64 * k] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        __builtin_amdgcn_wave_barrier();  // sc[wave] is written and read by this wave only
+        float o0 = 0.f, o1 = 0.f;
+        for (int j = 0; j < nt; j++) {
+            const float pj = sc[wave][j];
+            if (lane < hd) o0 = fmaf(pj, vt[j][lane], o0);
+            if (HDM > 64 && lane + 64 < hd) o1 = fmaf(pj, vt[j][lane + 64], o1);
+        }
+        const int h = kvh * hpk + wave;
+        const size_t pi = (size_t)h * a.nsplit + split;
+        if (lane == 0) {
+            a.part_m[pi] = mx;
+            a.part_l[pi] = l;
+        }
+        if (lane < hd) a.part_acc[pi * hd + lane] = o0;
+        if (HDM > 64 && lane + 64 < hd) a.part_acc[pi * hd + lane + 64] = o1;
     }
 }
 
-// Merges the split partials of every query head: out = sum_s acc_s e^(m_s-M)
-// / sum_s l_s e^(m_s-M), multiplied by the reciprocal like transformer.rs:293-298.
-__global__ void __launch_bounds__(128) attn_combine_kernel(const float* part_m, const float* part_l,
-                                                           const float* part_acc, float* out, int nsplit, int hd) {
+// Merges the nv = ceil(T / TT) splits of query head blockIdx.x:
+// out = sum_s acc_s e^(m_s - M) * (1 / sum_s l_s e^(m_s - M)), the
+// reciprocal multiply of transformer.rs:293-298.
+__global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, const float* part_l,
+                                                           const float* part_acc, float* out, const int* posp,
+                                                           int nsplit, int tt, int hd) {
+    __shared__ float w[kMaxAttnSplits];
+    __shared__ float red[2][kWG / 64];
+    __shared__ float part[kWG];
     const int h = blockIdx.x;
+    const int nv = min(nsplit, (*posp + 1 + tt - 1) / tt);
     const float* pm = part_m + (size_t)h * nsplit;
     const float* pl = part_l + (size_t)h * nsplit;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pm[s]);
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        float L = 0.f, o = 0.f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < nsplit; s++) {
-                if (pm[s] == -INFINITY) continue;
-                const float w = expf(pm[s] - M);
-                L = fmaf(pl[s], w, L);
-                o = fmaf(part_acc[((size_t)h * nsplit + s) * hd + i], w, o);
-            }
+    for (int s = threadIdx.x; s < nv; s += kWG) M = fmaxf(M, pm[s]);
+    M = wave_max(M);
+    if ((threadIdx.x & 63) == 0) red[0][threadIdx.x >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float L = 0.f;
+    for (int s = threadIdx.x; s < nv; s += kWG) {
+        const float ws = expf(pm[s] - M);
+        w[s] = ws;
+        L = fmaf(pl[s], ws, L);
+    }
+    L = wave_sum(L);
+    if ((threadIdx.x & 63) == 0) red[1][threadIdx.x >> 6] = L;
+    __syncthreads();
+    L = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    // thread (g, d): dims d < hd, splits s = g, g + G, ...
+    const int hdp = hd <= 64 ? 64 : 128, G = kWG / hdp;
+    const int d = threadIdx.x % hdp, g = threadIdx.x / hdp;
+    float o = 0.f;
+    if (d < hd) {
+        const float* acc = part_acc + (size_t)h * nsplit * hd + d;
+        int s = g;
+        for (; s + 3 * G < nv; s += 4 * G) {
+            const float a0 = acc[(size_t)s * hd], a1 = acc[(size_t)(s + G) * hd];
+            const float a2 = acc[(size_t)(s + 2 * G) * hd], a3 = acc[(size_t)(s + 3 * G) * hd];
+            o = fmaf(a0, w[s], o);
+            o = fmaf(a1, w[s + G], o);
+            o = fmaf(a2, w[s + 2 * G], o);
+            o = fmaf(a3, w[s + 3 * G], o);
         }
-        out[(size_t)h * hd + i] = L > 0.f ? o * (1.0f / L) : 0.f;
+        for (; s < nv; s += G) o = fmaf(acc[(size_t)s * hd], w[s], o);
+    }
+    part[threadIdx.x] = o;
+    __syncthreads();
+    if (g == 0 && d < hd) {
+        for (int k = 1; k < G; k++) o += part[k * hdp + d];
+        out[(size_t)h * hd + d] = L > 0.f ? o * (1.0f / L) : 0.f;
     }
 }
 
@@ -657,11 +768,20 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
             a.scale = 1.0f / sqrtf((float)c.head_dim);
             a.part_m = st.part_m; a.part_l = st.part_l; a.part_acc = st.part_acc;
             dim3 grid((unsigned)c.n_kv_heads, (unsigned)m->nsplit);
-            if (c.kv_precision == MIVI_KV_F32) hipLaunchKernelGGL(attn_split_kernel<MIVI_KV_F32>, grid, dim3(kWG), 0, s, a);
-            else if (c.kv_precision == MIVI_KV_F16) hipLaunchKernelGGL(attn_split_kernel<MIVI_KV_F16>, grid, dim3(kWG), 0, s, a);
-            else hipLaunchKernelGGL(attn_split_kernel<MIVI_KV_Q8_0>, grid, dim3(kWG), 0, s, a);
-            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads), dim3(64), 0, s, st.part_m, st.part_l,
-                               st.part_acc, st.attn_out, m->nsplit, (int)c.head_dim);
+#define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
+            if (c.head_dim <= 64) {
+                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
+                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
+                else ATT(MIVI_KV_Q8_0, 64);
+            } else {
+                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
+                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
+                else ATT(MIVI_KV_Q8_0, 128);
+            }
+#undef ATT
+            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads), dim3(kWG), 0, s, st.part_m, st.part_l,
+                               st.part_acc, st.attn_out, &m->ctrl->pos[b], m->nsplit, attn_tile_tokens(c.head_dim),
+                               (int)c.head_dim);
             g = {};
             g.seg[0] = {L.wo.w, st.x, D};
             g.nseg = 1; g.K = D; g.x = st.attn_out; g.accumulate = 1;
@@ -814,8 +934,8 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
     c.max_seq_len = std::min(c.max_seq_len, cap);
     c.max_batch = max_batch;
     c.kv_precision = kv_precision;
-    if (c.head_dim > kMaxHd || c.head_dim % 4 != 0)
-        return model_error(MIVI_ERR_UNSUPPORTED, "head_dim %zu not supported (max %d, multiple of 4)", c.head_dim, kMaxHd);
+    if (c.head_dim > kMaxHd || c.head_dim % 8 != 0)
+        return model_error(MIVI_ERR_UNSUPPORTED, "head_dim %zu not supported (max %d, multiple of 8)", c.head_dim, kMaxHd);
     if (c.n_heads / c.n_kv_heads > 4)
         return model_error(MIVI_ERR_UNSUPPORTED, "more than 4 query heads per kv head");
     if (kv_precision == MIVI_KV_Q8_0 && c.head_dim % 32 != 0)
@@ -964,7 +1084,8 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
     // run state, KV caches
     m->kv_row_bytes = kv_precision == MIVI_KV_Q8_0 ? (c.kv_dim / 32) * 34
                     : kv_precision == MIVI_KV_F16 ? c.kv_dim * 2 : c.kv_dim * 4;
-    m->nsplit = (int)std::min<size_t>(kMaxSplits, std::max<size_t>(1, (c.max_seq_len + kChunk - 1) / kChunk));
+    const size_t tt = (size_t)attn_tile_tokens(c.head_dim);
+    m->nsplit = (int)std::max<size_t>(1, (c.max_seq_len + tt - 1) / tt);
     size_t ks = std::max<size_t>(1, c.ssm_conv_kernel);
     m->seqs.resize(max_batch);
     for (auto& st : m->seqs) {

@@ -902,11 +902,14 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     const int cnt = wid < ngroups ? (ngroups - wid + nw - 1) / nw : 0;  // wave-uniform
 
     // row of this lane in step s of this wave (steps past the end re-read
-    // the wave's last row, which is then never stored)
+    // the wave's last row, and waves without rows read row 0; such rows are
+    // never stored). Branch-free, so the waits for the activation loads stay
+    // precise: a branch around the prefetch would make the compiler wait for
+    // every outstanding weight load before staging x.
     auto row_of = [&](int st) {
         st = st < cnt ? st : cnt - 1;
         const int r = (wid + st * nw) * RPW + sub;
-        return r < n ? r : n - 1;
+        return r < 0 ? 0 : r < n ? r : n - 1;
     };
     Unit<FMT> buf[PD][NU];
     auto load_step = [&](Unit<FMT> (&B)[NU], int st) {
@@ -917,11 +920,13 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     // activation loads first, then the first PD row groups of weights, which
     // stay in flight while x is staged
     StageIn<PRO, K / kWG> in;
+    // (scheduling barriers keep this order: activation loads, weight loads,
+    // then the activation math, which then waits for the activations only)
     in.load(a);
-    if (cnt > 0) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < PD; p++) load_step(buf[p], p);
-    }
+    for (int p = 0; p < PD; p++) load_step(buf[p], p);
+    __builtin_amdgcn_sched_barrier(0);
     const float s = in.template finish<FMT == FMT_Q4K>(a, dig, xsum);
 
     // this lane's activation digits (and their per-quad offsets / fp32
