@@ -80,6 +80,30 @@ def cpu_gemv_baseline(t, w, x, rows, cols, budget_s):
                        f"{sec * 1e3:.2f} ms/call")
 
 
+def gemm_bench(torch, hip, steps, warmup):
+    """Config 3: X [512 x 2048] ~ N(0,1) times W [8192 x 2048]^T Q4_K on MFMA."""
+    rows, cols, batch = 8192, 2048, 512
+    w = torch.from_numpy(hip.synth_random_weights(hip.GgmlType.Q4_K, 300, rows, cols, 0.02)).cuda()
+    x = torch.from_numpy(hip.synth_normal(301, batch * cols)).cuda()
+    y = torch.empty(batch * rows, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        hip.quantized_matmul_rows(y, hip.GgmlType.Q4_K, w, x, batch, rows, cols, stream=stream)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        hip.quantized_matmul_rows(y, hip.GgmlType.Q4_K, w, x, batch, rows, cols, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flop = 2.0 * batch * rows * cols
+    return dict(batch=batch, rows=rows, cols=cols, algo_flop=flop, ms_per_call=ms,
+                tflops=flop / (ms * 1e-3) / 1e12, frac_of_fp16_mfma_peak=flop / (ms * 1e-3) / 2.5e15,
+                note="includes the activation split kernel (fp16 hi/lo + sub-block sums) run per call")
+
+
 def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
     from mivi_hip.synthmodel import LFM2_1B2, build_hybrid, weight_bytes_per_token
     t0 = time.perf_counter()
@@ -210,6 +234,9 @@ def main():
         "q4k_gemv_config1": {k: q4[k] for k in ("rows", "cols", "algo_bytes", "ms_per_call", "gbs", "copies")},
     }
     extra["q4k_gemv_config1"]["frac_of_peak"] = q4["gbs"] / HBM_PEAK_GBS
+    g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3)
+    log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s")
+    extra["q4k_gemm_config3"] = g3
     if not a.no_decode:
         dec = decode_bench(torch, hip, a.decode_prefill, a.decode_steps, 0 if a.no_cpu else a.cpu_seconds)
         log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['gbs']:.0f} GB/s)"

@@ -1,8 +1,26 @@
 // quantized_matmul_rows (crates/mivi-quant/src/lib.rs:143-357) for gfx950.
 //
-// batch == 1 is exactly the matvec path (lib.rs:171-182). Small batches run
-// the GEMV kernels once per input row; the weight rows stay hot in L2/MALL
-// across the launches.
+// batch == 1 is exactly the matvec path (lib.rs:171-182). Q4_K with at least
+// kMfmaMinBatch rows runs on the matrix cores:
+//
+//   gemm_prep_kernel   one workgroup per input row: scales the row by a power
+//                      of two 2^-e (so that |x| <= 1), splits it into fp16
+//                      hi + lo (x = hi + lo to about 2^-22 relative) and forms
+//                      the fp32 sums of each 32-value sub-block, also split;
+//   gemm_q4k_kernel    128 x 128 output tiles, v_mfma_f32_32x32x16_f16. The
+//                      B operand is sc*q of the Q4_K sub-block, an integer
+//                      <= 945 and so exact in fp16; one MFMA chain per 256-value
+//                      super-block gives sum(sc q x), folded into the fp32
+//                      accumulator as acc += d * C. The min term of
+//                      q4_k_m.rs:24-63, dmin * sum_sub m_sub * X_sub, runs on
+//                      the same MFMA shape with B = m (K = 8 sub-blocks padded
+//                      to 16) and is subtracted the same way. The row scale
+//                      2^e is applied at the store.
+//
+// Other formats, and Q4_K with fewer rows, run the GEMV once per input row.
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 
 namespace mivi {
@@ -13,6 +31,292 @@ bool ggml_sizes(int32_t t, size_t* bs, size_t* ts);
 }  // namespace mivi
 
 using namespace mivi;
+
+namespace {
+
+constexpr int kMfmaMinBatch = 16;
+constexpr int kTm = 128, kTn = 128, kTk = 64;  // output tile and k-tile
+constexpr int kXs = kTk + 8;                   // padded LDS row (halves) of an x tile
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------- prep
+// grid = Mp rows, 256 threads, K = 8 * 256 * r (thread t owns values
+// [8t, 8t + 8) of each 2048-value stretch). Row m < M: e = exponent with
+// max|x| * 2^-e <= 1; xh/xl = fp16 hi/lo of x * 2^-e; sh/sl = fp16 hi/lo of
+// each 32-value sub-block sum of x * 2^-e (fp32). Rows >= M are zero.
+typedef _Float16 half8p __attribute__((ext_vector_type(8)));
+__global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ X, int M, int K,
+                                                        _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                        _Float16* __restrict__ sh, _Float16* __restrict__ sl,
+                                                        float* __restrict__ rowscale) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const bool live = m < M;
+    const float* x = X + (size_t)m * K;
+    float mx = 0.f;
+    if (live)
+        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+            const f32x4 a = *(const f32x4*)(x + i), b = *(const f32x4*)(x + i + 4);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // 2^-e with max * 2^-e in [1/2, 1); e = 0 for an all-zero row
+    int e = 0;
+    if (mx > 0.f && mx <= 3.40282347e38f) frexpf(mx, &e);
+    const float inv = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.f;
+    for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+        if (live) {
+            a = *(const f32x4*)(x + i);
+            b = *(const f32x4*)(x + i + 4);
+        }
+        const float v[8] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv,
+                            b.x * inv, b.y * inv, b.z * inv, b.w * inv};  // exact: power-of-two scaling
+        half8p hv, lv;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            hv[q] = (_Float16)v[q];
+            lv[q] = (_Float16)(v[q] - (float)hv[q]);
+            sum += v[q];
+        }
+        *(half8p*)(xh + (size_t)m * K + i) = hv;
+        *(half8p*)(xl + (size_t)m * K + i) = lv;
+        // 4 consecutive threads hold one 32-value sub-block
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if ((threadIdx.x & 3) == 0) {
+            const _Float16 h = (_Float16)sum;
+            sh[(size_t)m * (K / 32) + i / 32] = h;
+            sl[(size_t)m * (K / 32) + i / 32] = (_Float16)(sum - (float)h);
+        }
+    }
+}
+
+// (scale, min) pair of sub-block j (0..7) from the 12 scale bytes held in
+// hdr dwords 1..3 (get_scale_min_k4, q4_k_m.rs:11-22)
+__device__ __forceinline__ void scale_min_k4(const uint8_t* q, int j, uint32_t& sc, uint32_t& m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// 8 nibbles (bytes of w0, w1; low or high nibble) times sc, as exact fp16
+__device__ __forceinline__ half8 nib8_times(uint32_t w0, uint32_t w1, bool high, _Float16 sc) {
+    uint32_t t0 = high ? (w0 >> 4) & 0x0F0F0F0Fu : w0 & 0x0F0F0F0Fu;
+    uint32_t t1 = high ? (w1 >> 4) & 0x0F0F0F0Fu : w1 & 0x0F0F0F0Fu;
+    // fp16 1024 + q has bit pattern 0x6400 | q: bytes [q, 0x64]
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, t0, 0x07010700u);  // q0, q1
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, t0, 0x07030702u);  // q2, q3
+    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, t1, 0x07010700u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, t1, 0x07030702u);
+    const half2v off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v s2 = {sc, sc};
+    half2v h0 = (__builtin_bit_cast(half2v, p0) + off) * s2;
+    half2v h1 = (__builtin_bit_cast(half2v, p1) + off) * s2;
+    half2v h2 = (__builtin_bit_cast(half2v, p2) + off) * s2;
+    half2v h3 = (__builtin_bit_cast(half2v, p3) + off) * s2;
+    return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
+}
+
+// grid = (ceil(N / 128), Mp / 128), 256 threads = 2 x 2 waves of 64 x 64.
+__global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict__ W, int N, int K,
+                                                       const _Float16* __restrict__ xh,
+                                                       const _Float16* __restrict__ xl,
+                                                       const _Float16* __restrict__ sh,
+                                                       const _Float16* __restrict__ sl,
+                                                       const float* __restrict__ rowscale, float* __restrict__ Y,
+                                                       int M) {
+    __shared__ __attribute__((aligned(16))) _Float16 Xh[kTm][kXs];
+    __shared__ __attribute__((aligned(16))) _Float16 Xl[kTm][kXs];
+    __shared__ __attribute__((aligned(16))) uint8_t Wq[kTn][32];   // qs bytes of the k-tile's group
+    __shared__ __attribute__((aligned(16))) uint8_t Wh[kTn][16];   // d, dmin, scales of the super-block
+    __shared__ __attribute__((aligned(16))) _Float16 Sh[kTm][8];   // sub-block sums of the super-block
+    __shared__ __attribute__((aligned(16))) _Float16 Sl[kTm][8];
+    const int n0 = blockIdx.x * kTn, m0 = blockIdx.y * kTm;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nb = K / 256;
+    const size_t rb = (size_t)nb * 144;
+    const int li = lane & 31, lh = lane >> 5;
+
+    // staging assignment: x chunks (8 halves) 8 per thread per plane pair
+    // (rows 0..127 x 8 chunks), one 16-byte qs chunk, one header chunk and
+    // one sub-sum chunk per thread
+    auto wrow = [&](int r) { const int n = n0 + r; return W + (size_t)(n < N ? n : N - 1) * rb; };
+
+    f32x16 acc[2][2], c1[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            acc[a][b] = f32x16{};
+            c1[a][b] = f32x16{};
+        }
+
+    const int ntiles = K / kTk;
+    u32x4 px[4], pxl[4], pq, ph, ps;
+    auto load_tile = [&](int t) {
+        const int k0 = t * kTk;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 256 * i;  // 0..1023: row c/8, chunk c%8
+            const int r = c >> 3, ch = c & 7;
+            const size_t o = (size_t)(m0 + r) * K + k0 + 8 * ch;
+            px[i] = *(const u32x4*)(xh + o);
+            pxl[i] = *(const u32x4*)(xl + o);
+        }
+        const int b = k0 / 256, g = (k0 % 256) / 64;
+        {
+            const int r = tid >> 1, ch = tid & 1;
+            pq = *(const u32x4*)(wrow(r) + (size_t)b * 144 + 16 + 32 * g + 16 * ch);
+        }
+        if (g == 0) {
+            const int r = tid & 127;
+            ph = *(const u32x4*)(wrow(r) + (size_t)b * 144);
+            const int rr = tid >> 1, half = tid & 1;
+            ps = half ? *(const u32x4*)(sl + (size_t)(m0 + rr) * (K / 32) + 8 * b)
+                      : *(const u32x4*)(sh + (size_t)(m0 + rr) * (K / 32) + 8 * b);
+        }
+    };
+    auto store_tile = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 256 * i;
+            const int r = c >> 3, ch = c & 7;
+            *(u32x4*)&Xh[r][8 * ch] = px[i];
+            *(u32x4*)&Xl[r][8 * ch] = pxl[i];
+        }
+        *(u32x4*)&Wq[tid >> 1][16 * (tid & 1)] = pq;
+        if (((t * kTk) % 256) == 0) {
+            if (tid < 128) *(u32x4*)&Wh[tid][0] = ph;
+            if (tid & 1) *(u32x4*)&Sl[tid >> 1][0] = ps;
+            else *(u32x4*)&Sh[tid >> 1][0] = ps;
+        }
+    };
+
+    load_tile(0);
+    for (int t = 0; t < ntiles; t++) {
+        __syncthreads();  // the previous tile's LDS reads are done
+        store_tile(t);
+        __syncthreads();
+        if (t + 1 < ntiles) load_tile(t + 1);
+        const int g = (t % 4);  // group of the super-block (sub-blocks 2g, 2g+1)
+        // this lane's rows (one per n-tile) and their scales for the group
+        _Float16 scv[2][2];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int r = wn * 64 + nt * 32 + li;
+            uint32_t s0, mm0, s1, mm1;
+            scale_min_k4(&Wh[r][4], 2 * g, s0, mm0);
+            scale_min_k4(&Wh[r][4], 2 * g + 1, s1, mm1);
+            scv[nt][0] = (_Float16)(float)s0;
+            scv[nt][1] = (_Float16)(float)s1;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            // k-step s: values 16s .. 16s+15 of the group; lane half lh holds 8 of them
+            half8 a_h[2], a_l[2], bq[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                const int r = wm * 64 + mt * 32 + li;
+                a_h[mt] = *(const half8*)&Xh[r][16 * s + 8 * lh];
+                a_l[mt] = *(const half8*)&Xl[r][16 * s + 8 * lh];
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                const int r = wn * 64 + nt * 32 + li;
+                // values 64g + 16s + 8lh + e: s < 2 low nibbles of qs[16s + 8lh + e],
+                // s >= 2 high nibbles of qs[16(s-2) + 8lh + e]
+                const u32x2 w = *(const u32x2*)&Wq[r][16 * (s & 1) + 8 * lh];
+                bq[nt] = nib8_times(w.x, w.y, s >= 2, scv[nt][s >> 1]);
+            }
+            // the four hi products, then the four lo products: no accumulator is
+            // used by two MFMAs in a row
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+                    c1[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h[mt], bq[nt], c1[mt][nt], 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+                    c1[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l[mt], bq[nt], c1[mt][nt], 0, 0, 0);
+        }
+        if (g == 3) {
+            // end of super-block: acc += d * C, then the min term
+            float d[2], dm[2];
+            half8 bm[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                const int r = wn * 64 + nt * 32 + li;
+                const uint32_t w0 = *(const uint32_t*)&Wh[r][0];
+                d[nt] = half_bits_to_f32(w0);
+                dm[nt] = half_bits_to_f32(w0 >> 16);
+                // B[k][n] = m of sub-block k for k < 8, 0 for k = 8..15 (lane half 1)
+                half8 v = {};
+                if (lh == 0) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        uint32_t sc, mm;
+                        scale_min_k4(&Wh[r][4], j, sc, mm);
+                        v[j] = (_Float16)(float)mm;
+                    }
+                }
+                bm[nt] = v;
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    acc[mt][nt] += d[nt] * c1[mt][nt];
+                    c1[mt][nt] = f32x16{};
+                }
+            half8 s_h[2], s_l[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                const int r = wm * 64 + mt * 32 + li;
+                s_h[mt] = lh == 0 ? *(const half8*)&Sh[r][0] : half8{};
+                s_l[mt] = lh == 0 ? *(const half8*)&Sl[r][0] : half8{};
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    f32x16 c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_h[mt], bm[nt], f32x16{}, 0, 0, 0);
+                    c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_l[mt], bm[nt], c2, 0, 0, 0);
+                    acc[mt][nt] -= dm[nt] * c2;
+                }
+        }
+    }
+    // store: D[i][j] in lane j + 32*((i/4)%2), register 4*(i/8) + i%4
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int n = n0 + wn * 64 + nt * 32 + li;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 64 + mt * 32 + 8 * (r / 4) + 4 * lh + (r % 4);
+                if (m < M && n < N) Y[(size_t)m * N + n] = acc[mt][nt][r] * rowscale[m];
+            }
+        }
+}
+
+}  // namespace
 
 // types.rs:188-235 validate_matmul_args after lib.rs:152-166
 static int32_t validate_matmul(int32_t t, size_t out_len, size_t w_len, size_t in_len, size_t batch, size_t rows,
@@ -30,6 +334,63 @@ static int32_t validate_matmul(int32_t t, size_t out_len, size_t w_len, size_t i
     return MIVI_OK;
 }
 
+// Device workspace of the MFMA path: one grow-only buffer per device, reused
+// across calls. Calls on different streams are ordered through an event
+// recorded after each use, so they never overwrite each other's activations.
+struct GemmWorkspace {
+    std::mutex mu;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+};
+
+static GemmWorkspace& gemm_workspace(int dev) {
+    static std::mutex mu;
+    static std::vector<GemmWorkspace*> all;
+    std::lock_guard<std::mutex> lk(mu);
+    if ((size_t)dev >= all.size()) all.resize(dev + 1, nullptr);
+    if (!all[dev]) all[dev] = new GemmWorkspace();  // lives until the process ends
+    return *all[dev];
+}
+
+static int32_t matmul_q4k_mfma(float* out, const uint8_t* w, const float* in, size_t batch, size_t rows,
+                               size_t cols, hipStream_t s) {
+    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || batch > (size_t)INT32_MAX - kTm)
+        return err_overflow();
+    const size_t mp = (batch + kTm - 1) / kTm * kTm, K = cols;
+    const size_t bx = mp * K * 2, bs = mp * (K / 32) * 2, bytes = 2 * bx + 2 * bs + mp * 4 + 256;
+    int dev = 0;
+    MIVI_HIP_CHECK(hipGetDevice(&dev));
+    GemmWorkspace& ws = gemm_workspace(dev);
+    std::lock_guard<std::mutex> lk(ws.mu);
+    if (!ws.done) MIVI_HIP_CHECK(hipEventCreateWithFlags(&ws.done, hipEventDisableTiming));
+    else MIVI_HIP_CHECK(hipStreamWaitEvent(s, ws.done, 0));  // the previous user is done with it
+    if (ws.bytes < bytes) {
+        if (ws.ptr) {
+            MIVI_HIP_CHECK(hipEventSynchronize(ws.done));
+            MIVI_HIP_CHECK(hipFree(ws.ptr));
+            ws.ptr = nullptr;
+            ws.bytes = 0;
+        }
+        MIVI_HIP_CHECK(hipMalloc(&ws.ptr, bytes));
+        ws.bytes = bytes;
+    }
+    uint8_t* p = (uint8_t*)ws.ptr;
+    _Float16* xh = (_Float16*)p;
+    _Float16* xl = (_Float16*)(p + bx);
+    _Float16* sh = (_Float16*)(p + 2 * bx);
+    _Float16* sl = (_Float16*)(p + 2 * bx + bs);
+    float* rs = (float*)(p + 2 * bx + 2 * bs);
+    hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)mp), dim3(256), 0, s, in, (int)batch, (int)K, xh, xl, sh, sl,
+                       rs);
+    dim3 grid((unsigned)((rows + kTn - 1) / kTn), (unsigned)(mp / kTm));
+    hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(256), 0, s, w, (int)rows, (int)K, xh, xl, sh, sl, rs, out,
+                       (int)batch);
+    MIVI_HIP_CHECK(hipGetLastError());
+    MIVI_HIP_CHECK(hipEventRecord(ws.done, s));
+    return MIVI_OK;
+}
+
 extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t t, const uint8_t* w,
                                                   size_t w_len, const float* in, size_t in_len, size_t batch,
                                                   size_t rows, size_t cols, void* stream) {
@@ -43,6 +404,8 @@ extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, in
     if (!out || !w || !in) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
     clear_error();
     hipStream_t s = (hipStream_t)stream;
+    if (t == MIVI_GGML_Q4_K && batch >= (size_t)kMfmaMinBatch && cols % 2048 == 0)
+        return matmul_q4k_mfma(out, w, in, batch, rows, cols, s);
     for (size_t b = 0; b < batch; b++) {
         rc = launch_gemv(t, w, in + b * cols, out + b * rows, rows, cols, false, s);
         if (rc) return rc;

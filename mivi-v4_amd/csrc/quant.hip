@@ -1095,7 +1095,8 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
     if (stream_ok) {
         const int lpr = K == 2048 ? 32 : 64;
         const int ngroups = (n + 64 / lpr - 1) / (64 / lpr);
-        static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 3);
+        // 2 workgroups per CU measured best for the head GEMV (24.7 us vs 26.2 at 3)
+        static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
         const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
 #define LS(FMT, KT, LPR, NU, PD) \
     hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO>), dim3(grid), dim3(kWG), 0, s, a)

@@ -236,3 +236,44 @@ def test_config_shapes_match_oracle(hip, oracle, torch_mod, t, rows):
     torch.cuda.synchronize()
     lin = 2.0 * y + out2.cpu().numpy()
     assert np.max(np.abs(out3.cpu().numpy() - lin)) <= 1e-4 * np.abs(lin).max() + 1e-4
+
+
+def _matmul_check(hip, oracle, torch, t, w, X, rows, cols):
+    batch = X.shape[0]
+    out = torch.full((batch * rows + 1,), 123.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matmul_rows(out[:batch * rows], t, dev(torch, w), dev(torch, X.reshape(-1)), batch, rows, cols)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert got[-1] == 123.0
+    rc, ref, _ = oracle.quantized_matmul_rows(t, w, X.reshape(-1), batch, rows, cols)
+    assert rc == 0
+    rc2, deq, _ = oracle.dequantize_slice(t, w, rows * cols)
+    wn = np.linalg.norm(deq.reshape(rows, cols).astype(np.float64), axis=1)
+    xn = np.linalg.norm(X.astype(np.float64), axis=1)
+    bound = 1e-4 * xn[:, None] * wn[None, :]
+    err = np.abs(got[:-1].reshape(batch, rows).astype(np.float64) - ref.reshape(batch, rows))
+    assert np.all(err <= bound), (float(err.max()), float((err / np.maximum(bound, 1e-30)).max()))
+
+
+def test_matmul_rows_config3_shape(hip, oracle, torch_mod):
+    # BASELINE config 3 at full size: X [512 x 2048] ~ N(0, 1), W [8192 x 2048] Q4_K (MFMA path)
+    torch = torch_mod
+    rows, cols, batch = 8192, 2048, 512
+    w = hip.synth_random_weights(Q4_K, 77, rows, cols, 0.02)
+    X = hip.synth_normal(78, batch * cols).reshape(batch, cols)
+    _matmul_check(hip, oracle, torch, Q4_K, w, X, rows, cols)
+
+
+@pytest.mark.parametrize("batch,rows", [(16, 128), (127, 200), (129, 384)])
+def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, rows):
+    # row magnitudes from 0 to 1e3 (the per-row power-of-two scaling), ragged M and N
+    torch = torch_mod
+    cols = 1024
+    w = hip.synth_random_weights(Q4_K, 80 + batch, rows, cols, 0.02)
+    X = hip.synth_normal(81 + batch, batch * cols).reshape(batch, cols).astype(np.float32)
+    X[0] = 0.0
+    X[1] *= np.float32(1e-3)
+    X[2] *= np.float32(1e3)
+    X[3] = 0.0
+    X[3, 5] = np.float32(7.5e3)      # one dominant value
+    _matmul_check(hip, oracle, torch, Q4_K, w, X, rows, cols)
