@@ -39,7 +39,21 @@ struct GemvArgs {
     float* st_out;         // PRO_CONV: next state, written by workgroup 0
     const int* phase;      // PRO_CONV: if set, st_in/st_out swap when *phase is odd
     int accumulate;        // 1: y += result (residual add, vec_add of ffn.rs:106)
+    int epilogue;          // GemvEpilogue
+    float* part_val;       // EPI_ARGMAX: per-wave maximum ...
+    int* part_idx;         // ... and the first row holding it
 };
+
+// What the GEMV does with its row results (streaming kernel, K = 2048).
+enum GemvEpilogue : int {
+    EPI_STORE = 0,    // y (=|+=) result
+    EPI_SWIGLU = 1,   // two segments gate|up of n rows each: y_gate[i] = silu(gate_i) * up_i (ffn.rs:84-95)
+    EPI_ARGMAX = 2,   // store, and each wave's (max, first row) into part_val/part_idx
+};
+
+// Number of per-wave argmax partials an EPI_ARGMAX launch of this shape
+// writes (0 when the shape cannot take the epilogue).
+int gemv_argmax_parts(int32_t ggml_type, int K, int n);
 
 int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
 

@@ -43,6 +43,7 @@ namespace {
 constexpr int kWG = 256;
 constexpr int kMaxHd = 128;            // head_dim supported by the attention kernel
 constexpr int kMaxAttnSplits = 1024;   // 65536 tokens / 64 tokens per tile
+constexpr int kMaxArgmaxParts = 16384; // per-wave argmax partials of the head GEMV
 // tokens per attention workgroup (its LDS holds 8192 f32 of K and of V)
 inline int attn_tile_tokens(size_t head_dim) { return head_dim <= 64 ? 128 : 64; }
 
@@ -586,17 +587,20 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
 // sampler.rs:305-316: index of the first strict maximum (NaN never wins).
 // Writes the token for the next step, records it, advances pos and the
 // ShortConv phase of the sequence.
-__global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, int n, uint32_t* tok, int* pos,
-                                                              int* phase, uint32_t* history, const int* step,
-                                                              int stride, int seq, int do_argmax) {
+// With part_idx set, `logits`/`n` are instead the per-wave (max, first row)
+// partials of the head GEMV's argmax epilogue.
+__global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, const int* part_idx, int n,
+                                                              uint32_t* tok, int* pos, int* phase, uint32_t* history,
+                                                              const int* step, int stride, int seq, int do_argmax) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     if (do_argmax) {
         float best = -INFINITY;
         int idx = 0x7FFFFFFF;
         for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            float v = logits[i];
-            if (v > best || (v == best && i < idx)) { best = v; idx = i; }
+            const float v = logits[i];
+            const int vi = part_idx ? part_idx[i] : i;
+            if (v > best || (v == best && vi < idx)) { best = v; idx = vi; }
         }
 #pragma unroll
         for (int sh = 32; sh >= 1; sh >>= 1) {
@@ -655,6 +659,8 @@ struct SeqState {
     float *x, *sc_in, *hb, *hb2, *q, *k, *v, *attn_out, *logits;
     float *conv_a, *conv_b;  // ping-pong [n_layers * dim * ksize]
     float *part_m, *part_l, *part_acc;
+    float* part_val;  // head GEMV argmax partials (kMaxArgmaxParts)
+    int* part_idx;
     uint8_t *kc, *vc;        // [n_attn * max_seq * row_bytes]
 };
 
@@ -792,7 +798,18 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
         g.seg[0] = {L.gate.w, st.hb, H};
         g.seg[1] = {L.up.w, st.hb2, H};
         g.nseg = 2; g.K = D; g.x = st.x; g.norm_w = L.ffn_norm; g.eps = c.rms_norm_eps;
+        bool fused = false;
         if (L.gate.type == L.up.type) {
+            // gate|up with the SwiGLU epilogue writes silu(gate) * up into hb
+            // directly where the streaming kernel takes the shape
+            g.epilogue = EPI_SWIGLU;
+            rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g, s);
+            fused = rc == MIVI_OK;
+            if (rc && rc != MIVI_ERR_UNSUPPORTED) return rc;
+            g.epilogue = EPI_STORE;
+        }
+        if (fused) {
+        } else if (L.gate.type == L.up.type) {
             if ((rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g, s))) return rc;
         } else {
             GemvArgs g1 = g;
@@ -804,18 +821,31 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
         g = {};
         g.seg[0] = {L.down.w, st.x, D};
         g.nseg = 1; g.K = H; g.x = st.hb; g.x2 = st.hb2; g.accumulate = 1;
-        if ((rc = launch_gemv_ex(L.down.type, PRO_SWIGLU, g, s))) return rc;
+        if ((rc = launch_gemv_ex(L.down.type, fused ? PRO_NONE : PRO_SWIGLU, g, s))) return rc;
     }
+    int parts = 0;  // > 0: the head GEMV reduced the argmax to per-wave partials
     if (logits) {
         // model.rs:435-473
         GemvArgs g = {};
         g.seg[0] = {m->head.w, st.logits, (int)c.vocab_size};
         g.nseg = 1; g.K = D; g.x = st.x; g.norm_w = m->out_norm; g.eps = c.rms_norm_eps;
-        if ((rc = launch_gemv_ex(m->head.type, m->out_norm ? PRO_RMSNORM : PRO_NONE, g, s))) return rc;
+        const int pro = m->out_norm ? PRO_RMSNORM : PRO_NONE;
+        const int np = argmax ? gemv_argmax_parts(m->head.type, D, (int)c.vocab_size) : 0;
+        if (np > 0 && np <= kMaxArgmaxParts) {
+            g.epilogue = EPI_ARGMAX;
+            g.part_val = st.part_val;
+            g.part_idx = st.part_idx;
+            rc = launch_gemv_ex(m->head.type, pro, g, s);
+            if (rc == MIVI_OK) parts = np;
+            else if (rc != MIVI_ERR_UNSUPPORTED) return rc;
+            g.epilogue = EPI_STORE;
+        }
+        if (!parts && (rc = launch_gemv_ex(m->head.type, pro, g, s))) return rc;
     }
-    hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, st.logits, (int)c.vocab_size,
-                       &m->ctrl->tok[b], &m->ctrl->pos[b], &m->ctrl->phase[b], argmax ? m->history : nullptr,
-                       &m->ctrl->step, (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
+    hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, parts ? st.part_val : st.logits,
+                       parts ? st.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b],
+                       &m->ctrl->pos[b], &m->ctrl->phase[b], argmax ? m->history : nullptr, &m->ctrl->step,
+                       (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
 }
@@ -1096,6 +1126,7 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
             (rc = m->alloc(&st.conv_a, c.n_layers * c.dim * ks)) || (rc = m->alloc(&st.conv_b, c.n_layers * c.dim * ks)) ||
             (rc = m->alloc(&st.part_m, c.n_heads * m->nsplit)) || (rc = m->alloc(&st.part_l, c.n_heads * m->nsplit)) ||
             (rc = m->alloc(&st.part_acc, c.n_heads * m->nsplit * c.head_dim)) ||
+            (rc = m->alloc(&st.part_val, kMaxArgmaxParts)) || (rc = m->alloc(&st.part_idx, kMaxArgmaxParts)) ||
             (rc = m->alloc(&st.kc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)) ||
             (rc = m->alloc(&st.vc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)))
             return fail(rc);

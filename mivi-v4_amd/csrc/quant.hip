@@ -887,9 +887,10 @@ __device__ __forceinline__ void load_unit(Unit<FMT>& U, const uint8_t* row, int 
 // units straight from HBM into a ring of PD row groups held in registers:
 // the loop has no LDS traffic and no barriers, so each wave streams at its
 // own pace. After the x staging the workgroup never synchronises again.
-template <int FMT, int KT, int LPR, int NU, int PD, int PRO>
+template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI>
 __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArgs a) {
     constexpr int RPW = 64 / LPR;
+    static_assert(EPI == mivi::EPI_STORE || LPR == 32, "pair and argmax epilogues take two rows per wave");
     constexpr int K = KT, nb = K / 256, units = nb * 4;
     constexpr int row_bytes = nb * KQ<FMT>::bytes;
     __shared__ __attribute__((aligned(16))) uint32_t dig[3 * K / 4];
@@ -897,7 +898,9 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     const Segs sg(a, row_bytes);
     const int n = sg.n;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane % LPR, sub = lane / LPR;
-    const int ngroups = (n + RPW - 1) / RPW;
+    // EPI_SWIGLU: group c is the row pair (gate c, up c) = rows c and n0 + c
+    const int n0 = a.seg[0].n;
+    const int ngroups = EPI == mivi::EPI_SWIGLU ? n0 : (n + RPW - 1) / RPW;
     const int nw = gridDim.x * (kWG / 64), wid = blockIdx.x * (kWG / 64) + wave;
     const int cnt = wid < ngroups ? (ngroups - wid + nw - 1) / nw : 0;  // wave-uniform
 
@@ -908,8 +911,14 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     // every outstanding weight load before staging x.
     auto row_of = [&](int st) {
         st = st < cnt ? st : cnt - 1;
-        const int r = (wid + st * nw) * RPW + sub;
-        return r < 0 ? 0 : r < n ? r : n - 1;
+        if constexpr (EPI == mivi::EPI_SWIGLU) {
+            int c = wid + st * nw;
+            c = c < 0 ? 0 : c < n0 ? c : n0 - 1;
+            return c + sub * n0;
+        } else {
+            const int r = (wid + st * nw) * RPW + sub;
+            return r < 0 ? 0 : r < n ? r : n - 1;
+        }
     };
     Unit<FMT> buf[PD][NU];
     auto load_step = [&](Unit<FMT> (&B)[NU], int st) {
@@ -970,7 +979,22 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
                 }
         }
     }
-    if (cnt == 0) return;  // wave-uniform; no barrier follows
+    float best = -INFINITY;  // EPI_ARGMAX: this lane's maximum and its first row
+    int bidx = 0x7FFFFFFF;
+    auto write_part = [&]() {
+        // the two row groups of the wave (lanes 0 and 32), then lane 0 writes
+        const float ov = __shfl(best, 32, 64);
+        const int oi = __shfl(bidx, 32, 64);
+        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+        if (lane == 0) {
+            a.part_val[wid] = best;
+            a.part_idx[wid] = bidx;
+        }
+    };
+    if (cnt == 0) {  // wave-uniform; no barrier follows
+        if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+        return;
+    }
 
     auto compute = [&](const Unit<FMT> (&B)[NU], int st) {
         float acc = 0.f;
@@ -984,8 +1008,20 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
         }
         float sum = group_sum<LPR>(acc);
         if (FMT == FMT_Q6K) sum *= s;
-        const int r = (wid + st * nw) * RPW + sub;
-        if (lr == 0 && r < n) store_out(sg, a.accumulate, r, sum);
+        if constexpr (EPI == mivi::EPI_SWIGLU) {
+            // lane 0 holds gate c, lane 32 up c (math.rs:87-95)
+            const float up = __shfl(sum, 32, 64);
+            const int c = wid + st * nw;
+            if (lane == 0 && c < n0) *(gfloat*)sg.out(c) = silu_f(sum) * up;
+        } else {
+            const int r = (wid + st * nw) * RPW + sub;
+            if (lr == 0 && r < n) {
+                store_out(sg, a.accumulate, r, sum);
+                // sampler.rs:305-316: strictly greater wins, so NaN never does
+                if constexpr (EPI == mivi::EPI_ARGMAX)
+                    if (sum > best) { best = sum; bidx = r; }
+            }
+        }
     };
     // Step st is computed from ring slot st % PD, which is then refilled
     // with step st + PD. Whole rounds of PD steps run without early exits
@@ -1002,6 +1038,7 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
 #pragma unroll
     for (int p = 0; p < PD; p++)
         if (st + p < cnt) compute(buf[p], st + p);
+    if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
 // ------------------------------------------------------- Q8_0 quantize/dot
@@ -1098,8 +1135,32 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
         // 2 workgroups per CU measured best for the head GEMV (24.7 us vs 26.2 at 3)
         static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
         const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
-#define LS(FMT, KT, LPR, NU, PD) \
-    hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO>), dim3(grid), dim3(kWG), 0, s, a)
+#define LSE(FMT, KT, LPR, NU, PD, EPI) \
+    hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO, EPI>), dim3(grid), dim3(kWG), 0, s, a)
+#define LS(FMT, KT, LPR, NU, PD) LSE(FMT, KT, LPR, NU, PD, mivi::EPI_STORE)
+        if (a.epilogue != mivi::EPI_STORE) {
+            // the fused epilogues run at K = 2048 (two rows per wave)
+            if (K != 2048 || PRO == mivi::PRO_SWIGLU || PRO == mivi::PRO_CONV)
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "GEMV epilogue %d needs K = 2048", a.epilogue);
+            if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
+                if (a.epilogue == mivi::EPI_SWIGLU) {
+                    if (a.nseg != 2 || a.seg[1].n != a.seg[0].n)
+                        return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "SwiGLU epilogue needs gate|up of equal rows");
+                    const int g1 = std::max(1, std::min((a.seg[0].n + 3) / 4, mivi::num_cus() * per_cu));
+                    if (t == MIVI_GGML_Q4_K)
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 2048, 32, 1, 4, PRO, mivi::EPI_SWIGLU>),
+                                           dim3(g1), dim3(kWG), 0, s, a);
+                    else
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, 2048, 32, 1, 4, PRO, mivi::EPI_SWIGLU>),
+                                           dim3(g1), dim3(kWG), 0, s, a);
+                } else {
+                    if (t == MIVI_GGML_Q4_K) LSE(FMT_Q4K, 2048, 32, 1, 4, mivi::EPI_ARGMAX);
+                    else LSE(FMT_Q6K, 2048, 32, 1, 4, mivi::EPI_ARGMAX);
+                }
+            }
+            MIVI_HIP_CHECK(hipGetLastError());
+            return MIVI_OK;
+        }
         if (K == 2048) {
             if (t == MIVI_GGML_Q4_K) LS(FMT_Q4K, 2048, 32, 1, 4); else LS(FMT_Q6K, 2048, 32, 1, 4);
         }
@@ -1111,9 +1172,12 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
             }
         }
 #undef LS
+#undef LSE
         MIVI_HIP_CHECK(hipGetLastError());
         return MIVI_OK;
     }
+    if (a.epilogue != mivi::EPI_STORE)
+        return mivi::set_error(MIVI_ERR_UNSUPPORTED, "GEMV epilogue %d needs the streaming kernel", a.epilogue);
     switch (t) {
     case MIVI_GGML_Q4_K:
     case MIVI_GGML_Q6_K: {
@@ -1160,6 +1224,13 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
 // ------------------------------------------------------------ host launch
 
 namespace mivi {
+
+int gemv_argmax_parts(int32_t t, int K, int n) {
+    if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || K != 2048 || env_int("MIVI_GEMV_V1", 0)) return 0;
+    static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
+    const int ngroups = (n + 1) / 2;
+    return 4 * std::max(1, std::min((ngroups + 3) / 4, num_cus() * per_cu));
+}
 
 int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     int n = 0;
