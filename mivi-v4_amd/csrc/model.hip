@@ -324,67 +324,128 @@ __device__ __forceinline__ void wave_prep_head(float* dst, const float* src, con
     }
 }
 
+// Tiles of TT tokens; split s of nsplit takes tiles [s * tps, s * tps + tps)
+// with tps = ceil(ntiles / nsplit), looping over them with an online softmax
+// (the tile max and sum merged into running ones) while the next tile's rows
+// are already being loaded.
 template <int KVP, int HDM>  // cache precision; LDS sized for head_dim <= HDM (64 or 128)
 __global__ void __launch_bounds__(kWG) attn_tile_kernel(const AttnArgs a) {
-    constexpr int TT = 8192 / HDM;  // tokens per workgroup: 128 or 64
-    __shared__ float kt[TT][HDM + 1];
-    __shared__ float vt[TT][HDM];
-    __shared__ float qs[4][HDM];
-    __shared__ float sc[4][TT];
-    __shared__ float kcur[HDM], vcur[HDM];
+    constexpr int TT = 8192 / HDM;  // tokens per tile: 128 or 64
+    __shared__ __attribute__((aligned(16))) float kt[TT][HDM + 4];
+    __shared__ __attribute__((aligned(16))) float vt[TT][HDM];
+    __shared__ __attribute__((aligned(16))) float qs[4][HDM];
+    __shared__ __attribute__((aligned(16))) float sc[4][TT];
+    __shared__ __attribute__((aligned(16))) float kcur[HDM], vcur[HDM];
     const int kvh = blockIdx.x, split = blockIdx.y;
     const int hd = a.hd, hpk = a.n_heads / a.n_kv_heads;
     const int pos = *a.pos, T = pos + 1;
-    const int t0 = split * TT;
-    if (t0 >= T) return;  // workgroup-uniform: beyond the context
-    const int nt = min(TT, T - t0);
-    const bool owner = pos < t0 + TT;  // this tile holds the current token
+    const int ntiles = (T + TT - 1) / TT;
+    const int tps = (ntiles + a.nsplit - 1) / a.nsplit;
+    const int tile0 = split * tps, tile1 = min(ntiles, tile0 + tps);
+    if (tile0 >= tile1) return;  // workgroup-uniform: beyond the context
+    const bool owner = tile1 == ntiles;  // the last tile holds the current token
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const float* cs = a.rope_cos + (size_t)pos * (hd / 2);
     const float* sn = a.rope_sin + (size_t)pos * (hd / 2);
     const size_t rb = a.row_bytes;
-    const uint8_t* kbase = a.kc + (size_t)t0 * rb;
-    const uint8_t* vbase = a.vc + (size_t)t0 * rb;
 
-    // 1. issue the tile loads (rows past nt re-read row 0 and are dropped)
-    constexpr int CPT = KVP == MIVI_KV_F32 ? TT * HDM / 4 / kWG : KVP == MIVI_KV_F16 ? TT * HDM / 8 / kWG : 1;
+    // tile loads into registers (rows past the tile re-read its row 0 and are dropped)
+    constexpr bool Q8 = KVP == MIVI_KV_Q8_0;
+    constexpr int E = KVP == MIVI_KV_F32 ? 4 : 8;  // values per 16-byte chunk (f32/f16)
+    constexpr int CPT = Q8 ? 2 : TT * HDM / E / kWG;
     u32x4 kr[CPT], vr[CPT];
-    uint32_t kd = 0, vd = 0;  // Q8_0 block scales
-    if constexpr (KVP == MIVI_KV_Q8_0) {
-        // one 32-value block per thread: t = tid / (hd/32), block bi
-        const int bpt = hd / 32;
-        const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
-        const bool ok = j < nt && threadIdx.x < TT * bpt;
-        const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)(kvh * bpt + bi) * 34;
-        kd = *(const __attribute__((address_space(1))) uint16_t*)(kbase + o);
-        vd = *(const __attribute__((address_space(1))) uint16_t*)(vbase + o);
-        kr[0] = *(gau32x4_a2*)(kbase + o + 2);
-        vr[0] = *(gau32x4_a2*)(vbase + o + 2);
-        // second half of the block in the upper registers of a 2-chunk array
-    } else {
-        constexpr int E = KVP == MIVI_KV_F32 ? 4 : 8;  // values per 16-byte chunk
-        const int cpr = hd / E;                        // chunks per row of this head
+    uint32_t kd = 0, vd = 0;  // Q8_0 block scales (thread = one 32-value block)
+    auto load_tile = [&](int t) {
+        const int t0 = t * TT, nt = min(TT, T - t0);
+        const uint8_t* kb = a.kc + (size_t)t0 * rb;
+        const uint8_t* vb = a.vc + (size_t)t0 * rb;
+        if constexpr (Q8) {
+            const int bpt = hd / 32;
+            const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
+            const bool ok = j < nt && threadIdx.x < TT * bpt;
+            const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)(kvh * bpt + bi) * 34;
+            kd = *(const __attribute__((address_space(1))) uint16_t*)(kb + o);
+            vd = *(const __attribute__((address_space(1))) uint16_t*)(vb + o);
+            kr[0] = *(gau32x4_a2*)(kb + o + 2);
+            kr[1] = *(gau32x4_a2*)(kb + o + 18);
+            vr[0] = *(gau32x4_a2*)(vb + o + 2);
+            vr[1] = *(gau32x4_a2*)(vb + o + 18);
+        } else {
+            const int cpr = hd / E;
 #pragma unroll
-        for (int k = 0; k < CPT; k++) {
-            const int c = threadIdx.x + k * kWG;
-            const int j = c / cpr, part = c % cpr;
-            const bool ok = j < nt;
-            const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)kvh * hd * (16 / E) + (size_t)(ok ? part : 0) * 16;
-            kr[k] = *(gau32x4*)(kbase + o);
-            vr[k] = *(gau32x4*)(vbase + o);
+            for (int k = 0; k < CPT; k++) {
+                const int c = threadIdx.x + k * kWG;
+                const int j = c / cpr, part = c % cpr;
+                const bool ok = j < nt;
+                const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)kvh * hd * (16 / E) + (size_t)(ok ? part : 0) * 16;
+                kr[k] = *(gau32x4*)(kb + o);
+                vr[k] = *(gau32x4*)(vb + o);
+            }
         }
-    }
-    u32x4 kr2 = {0, 0, 0, 0}, vr2 = {0, 0, 0, 0};
-    if constexpr (KVP == MIVI_KV_Q8_0) {
-        const int bpt = hd / 32;
-        const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
-        const bool ok = j < nt && threadIdx.x < TT * bpt;
-        const size_t o = (ok ? (size_t)j * rb : 0) + (size_t)(kvh * bpt + bi) * 34;
-        kr2 = *(gau32x4_a2*)(kbase + o + 18);
-        vr2 = *(gau32x4_a2*)(vbase + o + 18);
-    }
+    };
+    // registers -> LDS as f32 (the current token from kcur/vcur)
+    auto store_tile = [&](int t) {
+        const int t0 = t * TT, nt = min(TT, T - t0);
+        if constexpr (Q8) {
+            const int bpt = hd / 32;
+            const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
+            if (j < nt && threadIdx.x < TT * bpt) {
+                const bool cur = t0 + j == pos;
+                const float dk = half_bits_to_f32(kd), dv = half_bits_to_f32(vd);
+                const uint32_t kw[8] = {kr[0].x, kr[0].y, kr[0].z, kr[0].w, kr[1].x, kr[1].y, kr[1].z, kr[1].w};
+                const uint32_t vw[8] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w, vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int d = bi * 32 + 4 * q;
+                    f32x4 kk = {sbyte_f32(kw[q], 0) * dk, sbyte_f32(kw[q], 1) * dk, sbyte_f32(kw[q], 2) * dk,
+                                sbyte_f32(kw[q], 3) * dk};
+                    f32x4 vv = {sbyte_f32(vw[q], 0) * dv, sbyte_f32(vw[q], 1) * dv, sbyte_f32(vw[q], 2) * dv,
+                                sbyte_f32(vw[q], 3) * dv};
+                    if (cur) {
+                        kk = *(const f32x4*)&kcur[d];
+                        vv = *(const f32x4*)&vcur[d];
+                    }
+                    *(f32x4*)&kt[j][d] = kk;
+                    *(f32x4*)&vt[j][d] = vv;
+                }
+            }
+        } else {
+            const int cpr = hd / E;
+#pragma unroll
+            for (int k = 0; k < CPT; k++) {
+                const int c = threadIdx.x + k * kWG;
+                const int j = c / cpr, part = c % cpr;
+                if (j >= nt) continue;
+                const bool cur = t0 + j == pos;
+                const uint32_t kw[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
+                const uint32_t vw[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
+#pragma unroll
+                for (int q = 0; q < E / 4; q++) {
+                    const int d = part * E + 4 * q;
+                    f32x4 kk, vv;
+                    if constexpr (KVP == MIVI_KV_F32) {
+                        kk = __builtin_bit_cast(f32x4, kr[k]);
+                        vv = __builtin_bit_cast(f32x4, vr[k]);
+                    } else {
+                        kk = {half_bits_to_f32(kw[2 * q]), half_bits_to_f32(kw[2 * q] >> 16),
+                              half_bits_to_f32(kw[2 * q + 1]), half_bits_to_f32(kw[2 * q + 1] >> 16)};
+                        vv = {half_bits_to_f32(vw[2 * q]), half_bits_to_f32(vw[2 * q] >> 16),
+                              half_bits_to_f32(vw[2 * q + 1]), half_bits_to_f32(vw[2 * q + 1] >> 16)};
+                    }
+                    if (cur) {
+                        kk = *(const f32x4*)&kcur[d];
+                        vv = *(const f32x4*)&vcur[d];
+                    }
+                    *(f32x4*)&kt[j][d] = kk;
+                    *(f32x4*)&vt[j][d] = vv;
+                }
+            }
+        }
+    };
 
-    // 2. query heads (one wave each) and, in the owner tile, the current K/V
+    // 1. the first tile's loads, then 2. query heads (one wave each) and, in
+    // the owner split, the current K/V
+    load_tile(tile0);
     if (wave < hpk) wave_prep_head(qs[wave], a.q + (size_t)(kvh * hpk + wave) * hd, a.q_norm, a.eps, hd, cs, sn);
     if (owner && wave == 3) {
         wave_prep_head(kcur, a.k + (size_t)kvh * hd, a.k_norm, a.eps, hd, cs, sn);
@@ -429,101 +490,92 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(const AttnArgs a) {
             }
         }
     }
-    __syncthreads();
 
-    // 3. tile to LDS as f32 (the current token from kcur/vcur)
-    if constexpr (KVP == MIVI_KV_Q8_0) {
-        const int bpt = hd / 32;
-        const int j = threadIdx.x / bpt, bi = threadIdx.x % bpt;
-        if (j < nt && threadIdx.x < TT * bpt) {
-            const bool cur = t0 + j == pos;
-            const float dk = half_bits_to_f32(kd), dv = half_bits_to_f32(vd);
-            const uint32_t kw[8] = {kr[0].x, kr[0].y, kr[0].z, kr[0].w, kr2.x, kr2.y, kr2.z, kr2.w};
-            const uint32_t vw[8] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w, vr2.x, vr2.y, vr2.z, vr2.w};
-#pragma unroll
-            for (int e = 0; e < 32; e++) {
-                const int d = bi * 32 + e;
-                kt[j][d] = cur ? kcur[d] : (float)(int8_t)(kw[e / 4] >> (8 * (e % 4))) * dk;
-                vt[j][d] = cur ? vcur[d] : (float)(int8_t)(vw[e / 4] >> (8 * (e % 4))) * dv;
+    // running softmax state of query head `wave`: lane holds dims lane, lane + 64
+    float m_run = -INFINITY, l_run = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int t = tile0; t < tile1; t++) {
+        const int nt = min(TT, T - t * TT);
+        __syncthreads();  // previous tile's LDS reads (and the query prep) are done
+        store_tile(t);
+        __syncthreads();
+        if (t + 1 < tile1) load_tile(t + 1);
+        // scores: thread -> (token j, heads hg, hg + 256/TT, ...)
+        {
+            const int j = threadIdx.x % TT, hg = threadIdx.x / TT;
+            for (int h = hg; h < 4; h += kWG / TT) {
+                float sv = -INFINITY;
+                if (h < hpk && j < nt) {
+                    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                    for (int i = 0; i < hd; i += 4) {
+                        const f32x4 kk = *(const f32x4*)&kt[j][i];
+                        const f32x4 qq = *(const f32x4*)&qs[h][i];
+                        d.x = fmaf(qq.x, kk.x, d.x);
+                        d.y = fmaf(qq.y, kk.y, d.y);
+                        d.z = fmaf(qq.z, kk.z, d.z);
+                        d.w = fmaf(qq.w, kk.w, d.w);
+                    }
+                    sv = ((d.x + d.y) + (d.z + d.w)) * a.scale;
+                }
+                sc[h][j] = sv;
             }
         }
-    } else {
-        constexpr int E = KVP == MIVI_KV_F32 ? 4 : 8;
-        const int cpr = hd / E;
+        __syncthreads();
+        if (wave < hpk) {
+            float v[TT / 64];
+            float mx = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < CPT; k++) {
-            const int c = threadIdx.x + k * kWG;
-            const int j = c / cpr, part = c % cpr;
-            if (j >= nt) continue;
-            const bool cur = t0 + j == pos;
-            const uint32_t kw[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
-            const uint32_t vw[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
-#pragma unroll
-            for (int e = 0; e < E; e++) {
-                const int d = part * E + e;
-                float kvl, vvl;
-                if constexpr (KVP == MIVI_KV_F32) {
-                    kvl = __uint_as_float(kw[e]);
-                    vvl = __uint_as_float(vw[e]);
-                } else {
-                    kvl = half_bits_to_f32(kw[e / 2] >> (16 * (e % 2)));
-                    vvl = half_bits_to_f32(vw[e / 2] >> (16 * (e % 2)));
-                }
-                kt[j][d] = cur ? kcur[d] : kvl;
-                vt[j][d] = cur ? vcur[d] : vvl;
+            for (int k = 0; k < TT / 64; k++) {
+                v[k] = sc[wave][lane + 64 * k];
+                mx = fmaxf(mx, v[k]);
             }
+            mx = wave_max(mx);
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+            float l = 0.f;
+#pragma unroll
+            for (int k = 0; k < TT / 64; k++) {
+                const float p = lane + 64 * k < nt ? expf(v[k] - m_new) : 0.f;
+                sc[wave][lane + 64 * k] = p;
+                l += p;
+            }
+            l = wave_sum(l);
+            __builtin_amdgcn_wave_barrier();  // sc[wave] is written and read by this wave only
+            // whole groups of 4 tokens, then the rest (rows past nt are never
+            // read: they may hold anything)
+            float a0 = 0.f, a1 = 0.f;
+            const int dl = lane < hd ? lane : 0;
+            const int dh = lane + 64 < hd ? lane + 64 : 0;
+            int j = 0;
+            for (; j + 4 <= nt; j += 4) {
+                const f32x4 pj = *(const f32x4*)&sc[wave][j];
+                a0 = fmaf(pj.x, vt[j][dl], a0);
+                a0 = fmaf(pj.y, vt[j + 1][dl], a0);
+                a0 = fmaf(pj.z, vt[j + 2][dl], a0);
+                a0 = fmaf(pj.w, vt[j + 3][dl], a0);
+                if (HDM > 64) {
+                    a1 = fmaf(pj.x, vt[j][dh], a1);
+                    a1 = fmaf(pj.y, vt[j + 1][dh], a1);
+                    a1 = fmaf(pj.z, vt[j + 2][dh], a1);
+                    a1 = fmaf(pj.w, vt[j + 3][dh], a1);
+                }
+            }
+            for (; j < nt; j++) {
+                const float pj = sc[wave][j];
+                a0 = fmaf(pj, vt[j][dl], a0);
+                if (HDM > 64) a1 = fmaf(pj, vt[j][dh], a1);
+            }
+            o0 = o0 * alpha + a0;
+            o1 = o1 * alpha + a1;
+            l_run = l_run * alpha + l;
+            m_run = m_new;
         }
     }
-    __syncthreads();
-
-    // 4. scores: thread -> (token t, heads hg, hg + 256/TT, ...)
-    {
-        const int t = threadIdx.x % TT, hg = threadIdx.x / TT;
-        for (int h = hg; h < 4; h += kWG / TT) {
-            float s = -INFINITY;
-            if (h < hpk && t < nt) {
-                float d0 = 0.f, d1 = 0.f;
-                for (int i = 0; i < hd; i += 2) {
-                    d0 = fmaf(qs[h][i], kt[t][i], d0);
-                    d1 = fmaf(qs[h][i + 1], kt[t][i + 1], d1);
-                }
-                s = (d0 + d1) * a.scale;
-            }
-            sc[h][t] = s;
-        }
-    }
-    __syncthreads();
-
-    // 5. softmax of the tile and 6. P V, one wave per query head
     if (wave < hpk) {
-        float v[TT / 64];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < TT / 64; k++) {
-            v[k] = sc[wave][lane + 64 * k];
-            mx = fmaxf(mx, v[k]);
-        }
-        mx = wave_max(mx);
-        float l = 0.f;
-#pragma unroll
-        for (int k = 0; k < TT / 64; k++) {
-            const float p = lane + 64 * k < nt ? expf(v[k] - mx) : 0.f;
-            sc[wave][lane + 64 * k] = p;
-            l += p;
-        }
-        l = wave_sum(l);
-        __builtin_amdgcn_wave_barrier();  // sc[wave] is written and read by this wave only
-        float o0 = 0.f, o1 = 0.f;
-        for (int j = 0; j < nt; j++) {
-            const float pj = sc[wave][j];
-            if (lane < hd) o0 = fmaf(pj, vt[j][lane], o0);
-            if (HDM > 64 && lane + 64 < hd) o1 = fmaf(pj, vt[j][lane + 64], o1);
-        }
         const int h = kvh * hpk + wave;
         const size_t pi = (size_t)h * a.nsplit + split;
         if (lane == 0) {
-            a.part_m[pi] = mx;
-            a.part_l[pi] = l;
+            a.part_m[pi] = m_run;
+            a.part_l[pi] = l_run;
         }
         if (lane < hd) a.part_acc[pi * hd + lane] = o0;
         if (HDM > 64 && lane + 64 < hd) a.part_acc[pi * hd + lane + 64] = o1;
@@ -540,7 +592,9 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
     __shared__ float red[2][kWG / 64];
     __shared__ float part[kWG];
     const int h = blockIdx.x;
-    const int nv = min(nsplit, (*posp + 1 + tt - 1) / tt);
+    const int ntiles = (*posp + 1 + tt - 1) / tt;
+    const int tps = (ntiles + nsplit - 1) / nsplit;
+    const int nv = (ntiles + tps - 1) / tps;  // splits that hold tiles
     const float* pm = part_m + (size_t)h * nsplit;
     const float* pl = part_l + (size_t)h * nsplit;
     float M = -INFINITY;
@@ -710,19 +764,22 @@ struct mivi_model {
 
 namespace {
 
-int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s) {
+// Enqueues part of one decode step of sequence b: the embedding (do_embed),
+// layers [l0, l1), then the head, argmax and position advance (do_head).
+int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s, bool do_embed, size_t l0,
+                     size_t l1, bool do_head) {
     const mivi_model_info& c = m->info;
     SeqState& st = m->seqs[b];
     int32_t rc;
     const int D = (int)c.dim, H = (int)c.hidden_dim, KV = (int)c.kv_dim;
-    {
+    if (do_embed) {
         size_t bs, ts;
         format_sizes(m->embd.type, &bs, &ts);
         size_t row_bytes = (c.dim * ts) / bs;  // model.rs:358-360
         hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kWG), 0, s, m->embd.type, m->embd.w, row_bytes,
                            &m->ctrl->tok[b], st.x, D);
     }
-    for (size_t l = 0; l < c.n_layers; l++) {
+    for (size_t l = l0; l < l1 && l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
         GemvArgs g = {};
         if (!L.attn) {
@@ -823,6 +880,10 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
         g.nseg = 1; g.K = H; g.x = st.hb; g.x2 = st.hb2; g.accumulate = 1;
         if ((rc = launch_gemv_ex(L.down.type, fused ? PRO_NONE : PRO_SWIGLU, g, s))) return rc;
     }
+    if (!do_head) {
+        MIVI_HIP_CHECK(hipGetLastError());
+        return MIVI_OK;
+    }
     int parts = 0;  // > 0: the head GEMV reduced the argmax to per-wave partials
     if (logits) {
         // model.rs:435-473
@@ -848,6 +909,22 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
                        (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
+}
+
+int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s) {
+    return enqueue_step(m, b, logits, argmax, s, true, 0, m->info.n_layers, true);
+}
+
+// One greedy step of sequences 0..batch-1, layer by layer across the
+// sequences, so that each layer's weights are reused from the Infinity Cache
+// by every sequence after the first.
+int32_t enqueue_batch_step(mivi_model* m, size_t batch, hipStream_t s) {
+    int32_t rc = MIVI_OK;
+    for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, s, true, 0, 0, false);
+    for (size_t l = 0; l < m->info.n_layers && !rc; l++)
+        for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, s, false, l, l + 1, false);
+    for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, s, false, 0, 0, true);
+    return rc;
 }
 
 void host_rope_table(std::vector<float>& cs, std::vector<float>& sn, size_t hd, size_t max_seq, float base,
@@ -1114,8 +1191,11 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
     // run state, KV caches
     m->kv_row_bytes = kv_precision == MIVI_KV_Q8_0 ? (c.kv_dim / 32) * 34
                     : kv_precision == MIVI_KV_F16 ? c.kv_dim * 2 : c.kv_dim * 4;
+    // about two workgroups per CU over all kv heads (each split loops over
+    // ceil(tiles / nsplit) tiles)
     const size_t tt = (size_t)attn_tile_tokens(c.head_dim);
-    m->nsplit = (int)std::max<size_t>(1, (c.max_seq_len + tt - 1) / tt);
+    const size_t want = std::max<size_t>(1, 2 * (size_t)num_cus() / std::max<size_t>(1, c.n_kv_heads));
+    m->nsplit = (int)std::max<size_t>(1, std::min((c.max_seq_len + tt - 1) / tt, want));
     size_t ks = std::max<size_t>(1, c.ssm_conv_kernel);
     m->seqs.resize(max_batch);
     for (auto& st : m->seqs) {
@@ -1240,7 +1320,7 @@ extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, c
         hipGraph_t gr;
         MIVI_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
         int32_t rc = MIVI_OK;
-        for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, m->stream);
+        rc = enqueue_batch_step(m, batch, m->stream);
         if (!rc) hipLaunchKernelGGL(step_counter_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step);
         hipError_t e = hipStreamEndCapture(m->stream, &gr);
         if (rc) return rc;

@@ -128,3 +128,55 @@ def test_state_export_import_into_oracle(hip, oracle, small_img, prec, oprec):
     m3.prefill(prompt)
     t0 = int(prompt[0])
     assert np.array_equal(m2.forward(t0, len(prompt)), m3.forward(t0, len(prompt)))
+
+
+def test_batched_q8_kv_greedy_matches_oracle(hip, oracle, small_img):
+    # config-5 semantics at small size: independent sequences, Q8_0 KV,
+    # per-sequence ShortConv state; each sequence against its own oracle run
+    B = 3
+    m = hip.Model(small_img, max_ctx=512, kv_precision=1, max_batch=B)
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, SMALL["vocab"], 20 + 7 * b) for b in range(B)]
+    for b, pr in enumerate(prompts):
+        m.prefill(pr[:-1], seq=b)
+    n = 24
+    got = m.generate_greedy([int(p[-1]) for p in prompts], [len(p) - 1 for p in prompts], n)
+    for b, pr in enumerate(prompts):
+        o = oracle.Model(small_img, max_ctx=512, kv_precision=1)
+        for p, t in enumerate(pr[:-1]):
+            o.forward_step(int(t), p, False)
+        tok, want = int(pr[-1]), []
+        for i in range(n):
+            lo = o.forward(tok, len(pr) - 1 + i)
+            tok = oracle.argmax(lo)
+            want.append(tok)
+        assert list(got[:, b]) == want
+
+
+def test_long_context_q8_kv_matches_oracle(hip, oracle):
+    # 6000 cached tokens (many attention splits), working context 8192 (YaRN
+    # active): the same synthetic Q8_0 cache and conv state in both
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(**SMALL, ctx_len=16384, seed=7)
+    T, ctx = 6000, 8192
+    m = hip.Model(img, max_ctx=ctx, kv_precision=1)
+    o = oracle.Model(img, max_ctx=ctx, kv_precision=1)
+    assert m.info.yarn == 1
+    L, kvd = m.info.n_attn_layers, m.info.kv_dim
+    k = hip.synth_random_weights(hip.GgmlType.Q8_0, 70, L * T, kvd, 1.0)
+    v = hip.synth_random_weights(hip.GgmlType.Q8_0, 71, L * T, kvd, 1.0)
+    conv = hip.synth_normal(72, m.conv_len(), std=0.1)
+    m.import_state(T, k, v, conv)
+    ok, ov = o.kv_views()
+    row = m.kv_row_bytes()
+    per = ok.size // L
+    for l in range(L):
+        ok[l * per: l * per + T * row] = k[l * T * row:(l + 1) * T * row]
+        ov[l * per: l * per + T * row] = v[l * T * row:(l + 1) * T * row]
+    o.conv_view()[:] = conv
+    tok = 17
+    for i in range(6):
+        lg = m.forward(tok, T + i)
+        lo = o.forward(tok, T + i)
+        assert rel_err(lg, lo) <= 1e-3
+        tok = int(np.argmax(lo))
