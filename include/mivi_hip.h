@@ -103,12 +103,29 @@ int32_t mivi_hip_try_matvec_bf16(float* out, size_t out_len, const uint8_t* weig
 
 /* crates/mivi-quant/src/lib.rs:143-251 quantized_matmul_rows:
  * out[batch, rows] = inputs[batch, cols] * W[rows, cols]^T. batch == 1 is the
- * matvec path (lib.rs:173-182); larger batches currently run one GEMV per
- * input row. */
+ * matvec path (lib.rs:173-182); Q4_K with batch >= 16 and cols a multiple of
+ * 2048 runs on the matrix cores, other cases one GEMV per input row. */
 int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t ggml_type,
                                        const uint8_t* weights, size_t weights_len,
                                        const float* inputs, size_t inputs_len, size_t batch,
                                        size_t rows, size_t cols, void* stream);
+
+/* No counterpart in the reference (its Rust kernels read the GGUF layout):
+ * rewrites rows x cols Q6_K weights (cols 2048, 4096 or 8192) into the
+ * unit-plane layout of the packed GEMV, a byte permutation of each row that
+ * keeps its size. dst must not overlap src. Other types/shapes return
+ * MIVI_ERR_UNSUPPORTED. For callers that keep weights resident (the model
+ * loader does this once for the Q6_K head). */
+int32_t mivi_hip_pack_weights(int32_t ggml_type, const uint8_t* src, size_t src_len, uint8_t* dst,
+                              size_t dst_len, size_t rows, size_t cols, void* stream);
+
+/* quantized_matvec (lib.rs:75-134) over weights packed by
+ * mivi_hip_pack_weights (16-byte aligned): the same result as
+ * mivi_hip_quantized_matvec on the unpacked bytes, bit for bit; validation,
+ * sizes and errors as there. No counterpart in the reference. */
+int32_t mivi_hip_quantized_matvec_packed(float* out, size_t out_len, int32_t ggml_type,
+                                         const uint8_t* packed, size_t packed_len, const float* x,
+                                         size_t x_len, size_t n, size_t d, void* stream);
 
 /* crates/mivi-quant/src/lib.rs:35-72 dequantize_slice: bit-exact decode of
  * out_len / block_size blocks (Q4_K, Q6_K, Q8_0) or of bytes_len / type_size

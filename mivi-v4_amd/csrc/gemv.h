@@ -40,6 +40,7 @@ struct GemvArgs {
     const int* phase;      // PRO_CONV: if set, st_in/st_out swap when *phase is odd
     int accumulate;        // 1: y += result (residual add, vec_add of ffn.rs:106)
     int epilogue;          // GemvEpilogue
+    int packed;            // 1: Q6_K rows in the unit-plane layout of mivi_hip_pack_weights
     float* part_val;       // EPI_ARGMAX: per-wave maximum ...
     int* part_idx;         // ... and the first row holding it
 };
@@ -56,5 +57,8 @@ enum GemvEpilogue : int {
 int gemv_argmax_parts(int32_t ggml_type, int K, int n);
 
 int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
+
+// rows x cols Q6_K (cols 2048/4096/8192) into the packed unit-plane layout
+int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
 
 }  // namespace mivi

@@ -733,6 +733,7 @@ struct mivi_model {
     uint8_t* d_weights = nullptr;
     float* d_aux = nullptr;  // decoded f32 vectors
     Mat embd, head;
+    uint8_t* head_packed = nullptr;  // Q6_K head in the packed unit-plane layout (else null)
     const float* out_norm = nullptr;
     std::vector<Layer> layers;
     float *rope_cos = nullptr, *rope_sin = nullptr;
@@ -888,8 +889,9 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
     if (logits) {
         // model.rs:435-473
         GemvArgs g = {};
-        g.seg[0] = {m->head.w, st.logits, (int)c.vocab_size};
+        g.seg[0] = {m->head_packed ? m->head_packed : m->head.w, st.logits, (int)c.vocab_size};
         g.nseg = 1; g.K = D; g.x = st.x; g.norm_w = m->out_norm; g.eps = c.rms_norm_eps;
+        g.packed = m->head_packed ? 1 : 0;
         const int pro = m->out_norm ? PRO_RMSNORM : PRO_NONE;
         const int np = argmax ? gemv_argmax_parts(m->head.type, D, (int)c.vocab_size) : 0;
         if (np > 0 && np <= kMaxArgmaxParts) {
@@ -1152,6 +1154,15 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
             return fail(rc);
     }
     if ((rc = check(m->head, c.vocab_size, c.dim, "head"))) return fail(rc);
+    // the head GEMV streams the largest matrix: keep a packed copy of a Q6_K
+    // head (the GGUF copy stays for the embedding lookup)
+    if (m->head.type == MIVI_GGML_Q6_K && (c.dim == 2048 || c.dim == 4096 || c.dim == 8192) &&
+        ((uintptr_t)m->head.w % 16) == 0 && !getenv("MIVI_NO_PACK")) {
+        const size_t bytes = c.vocab_size * (c.dim / 256) * 210;
+        if ((rc = m->alloc(&m->head_packed, bytes))) return fail(rc);
+        if ((rc = launch_pack_q6k(m->head.w, m->head_packed, c.vocab_size, c.dim, nullptr))) return fail(rc);
+        if (hipDeviceSynchronize() != hipSuccess) return fail(set_error(MIVI_ERR_HIP, "packing the head failed"));
+    }
     {
         size_t bs, ts;
         if (!format_sizes(m->embd.type, &bs, &ts) || c.dim % bs) return fail(err_unsupported(m->embd.type));

@@ -858,6 +858,30 @@ typedef __attribute__((address_space(1))) const u32x4_a2 gu32x4_a2;
 typedef __attribute__((address_space(1))) const u32x2_a1 gu32x2_a1;
 typedef __attribute__((address_space(1))) const uint16_t gu16;
 
+// Packed Q6_K row of U = K/64 units (mivi_hip_pack_weights): the same bytes
+// as the GGUF row, regrouped so that each load of a wave is contiguous:
+//   [0, 16U)      ql bytes 64h + 16j .. +16 of unit u = (b, h, j) at 16u
+//   [16U, 32U)    ql bytes 64h + 32 + 16j .. +16
+//   [32U, 48U)    qh bytes 128 + 32h + 16j .. +16
+//   [48U, 52U)    the unit's four scales sc[8h + j + 2k], k = 0..3, at 4u
+//   [52U, 52.5U)  d of block b at 52U + 2b
+__device__ __forceinline__ void load_unit_q6k_packed(Unit<FMT_Q6K>& U, const uint8_t* row, int u, int nu) {
+    U.ql0 = ldg16(row + 16 * u);
+    U.ql1 = ldg16(row + 16 * nu + 16 * u);
+    U.qh = ldg16(row + 32 * nu + 16 * u);
+    // the four scale bytes, spread by packed_q6k_scales at compute time (doing
+    // it here would make the wave wait for this load as soon as it is issued)
+    U.sc.x = *(const __attribute__((address_space(1))) uint32_t*)(row + 48 * nu + 4 * u);
+    U.sc.y = 0;
+    U.d = *(gu16*)(row + 52 * nu + 2 * (u >> 2));
+}
+
+// The packed unit's scale dword (sc[k] in byte k) as the GGUF layout's two
+// dwords hold them (sc[k] in byte 2k).
+__device__ __forceinline__ u32x2 packed_q6k_scales(uint32_t w) {
+    return u32x2{(w & 0xFFu) | ((w & 0xFF00u) << 8), ((w >> 16) & 0xFFu) | ((w >> 24) << 16)};
+}
+
 // Unit u of the row at `row`: Q6_K unit (b, h, j) = block u/4, half h,
 // l in [16j, 16j + 16); Q4_K unit (b, g) = block u/4, sub-blocks 2g, 2g+1.
 template <int FMT>
@@ -887,8 +911,9 @@ __device__ __forceinline__ void load_unit(Unit<FMT>& U, const uint8_t* row, int 
 // units straight from HBM into a ring of PD row groups held in registers:
 // the loop has no LDS traffic and no barriers, so each wave streams at its
 // own pace. After the x staging the workgroup never synchronises again.
-template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI>
+template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI, bool PACK = false>
 __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArgs a) {
+    static_assert(!PACK || FMT == FMT_Q6K, "only Q6_K has a packed layout");
     constexpr int RPW = 64 / LPR;
     static_assert(EPI == mivi::EPI_STORE || LPR == 32, "pair and argmax epilogues take two rows per wave");
     constexpr int K = KT, nb = K / 256, units = nb * 4;
@@ -924,7 +949,10 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     auto load_step = [&](Unit<FMT> (&B)[NU], int st) {
         const uint8_t* row = sg.row(row_of(st));
 #pragma unroll
-        for (int i = 0; i < NU; i++) load_unit<FMT>(B[i], row, min(lr + LPR * i, units - 1));
+        for (int i = 0; i < NU; i++) {
+            if constexpr (PACK) load_unit_q6k_packed(B[i], row, min(lr + LPR * i, units - 1), units);
+            else load_unit<FMT>(B[i], row, min(lr + LPR * i, units - 1));
+        }
     };
     // activation loads first, then the first PD row groups of weights, which
     // stay in flight while x is staged
@@ -1004,7 +1032,8 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
             if constexpr (FMT == FMT_Q4K)
                 acc += q4k_unit_i8(B[i].hdr, B[i].qa, B[i].qb, (lr + LPR * i) & 3, xd[i], s, X[i][0], X[i][1]);
             else
-                acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, B[i].sc, B[i].d, xd[i], off[i]);
+                acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, PACK ? packed_q6k_scales(B[i].sc.x) : B[i].sc,
+                                   B[i].d, xd[i], off[i]);
         }
         float sum = group_sum<LPR>(acc);
         if (FMT == FMT_Q6K) sum *= s;
@@ -1138,6 +1167,26 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
 #define LSE(FMT, KT, LPR, NU, PD, EPI) \
     hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO, EPI>), dim3(grid), dim3(kWG), 0, s, a)
 #define LS(FMT, KT, LPR, NU, PD) LSE(FMT, KT, LPR, NU, PD, mivi::EPI_STORE)
+#define LSP(KT, LPR, NU, PD, EPI) \
+    hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, KT, LPR, NU, PD, PRO, EPI, true>), dim3(grid), dim3(kWG), 0, s, a)
+        if (a.packed) {
+            // packed Q6_K rows (store or argmax epilogue, no conv/SwiGLU prologue)
+            if (t != MIVI_GGML_Q6_K || a.epilogue == mivi::EPI_SWIGLU)
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows are Q6_K with the store or argmax epilogue");
+            if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
+                if (a.epilogue == mivi::EPI_ARGMAX) {
+                    if (K != 2048) return mivi::set_error(MIVI_ERR_UNSUPPORTED, "argmax epilogue needs K = 2048");
+                    LSP(2048, 32, 1, 4, mivi::EPI_ARGMAX);
+                } else if (K == 2048) LSP(2048, 32, 1, 4, mivi::EPI_STORE);
+                else if (K == 4096) LSP(4096, 64, 1, 4, mivi::EPI_STORE);
+                else LSP(8192, 64, 2, 2, mivi::EPI_STORE);
+                MIVI_HIP_CHECK(hipGetLastError());
+                return MIVI_OK;
+            } else {
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows take no conv or SwiGLU prologue");
+            }
+        }
+#undef LSP
         if (a.epilogue != mivi::EPI_STORE) {
             // the fused epilogues run at K = 2048 (two rows per wave)
             if (K != 2048 || PRO == mivi::PRO_SWIGLU || PRO == mivi::PRO_CONV)
@@ -1178,6 +1227,7 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
     }
     if (a.epilogue != mivi::EPI_STORE)
         return mivi::set_error(MIVI_ERR_UNSUPPORTED, "GEMV epilogue %d needs the streaming kernel", a.epilogue);
+    if (a.packed) return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows need the streaming kernel (K = 2048/4096/8192)");
     switch (t) {
     case MIVI_GGML_Q4_K:
     case MIVI_GGML_Q6_K: {
@@ -1361,9 +1411,88 @@ int32_t validate_matvec(int32_t t, size_t out_len, size_t w_len, size_t x_len, s
 
 }  // namespace mivi
 
+// ------------------------------------------------------------ Q6_K packing
+
+namespace {
+// one thread per (row, unit): moves the unit's bytes into the plane layout
+// of load_unit_q6k_packed (a permutation of the row's bytes)
+__global__ void __launch_bounds__(kWG) pack_q6k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                       size_t rows, int nu, size_t row_bytes) {
+    const size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= rows * (size_t)nu) return;
+    const size_t r = i / nu;
+    const int u = (int)(i % nu), b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+    const uint8_t* p = src + r * row_bytes + (size_t)b * 210;
+    uint8_t* q = dst + r * row_bytes;
+    for (int k = 0; k < 16; k++) {
+        q[16 * u + k] = p[64 * h + 16 * j + k];
+        q[16 * nu + 16 * u + k] = p[64 * h + 32 + 16 * j + k];
+        q[32 * nu + 16 * u + k] = p[128 + 32 * h + 16 * j + k];
+    }
+    for (int k = 0; k < 4; k++) q[48 * nu + 4 * u + k] = p[192 + 8 * h + j + 2 * k];
+    if ((u & 3) == 0) {
+        q[52 * nu + 2 * b] = p[208];
+        q[52 * nu + 2 * b + 1] = p[209];
+    }
+}
+}  // namespace
+
+namespace mivi {
+int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s) {
+    const int nu = (int)(cols / 64);
+    const size_t threads = rows * (size_t)nu;
+    if (threads == 0) return MIVI_OK;
+    hipLaunchKernelGGL(pack_q6k_kernel, dim3((unsigned)((threads + kWG - 1) / kWG)), dim3(kWG), 0, s, src, dst, rows,
+                       nu, (cols / 256) * 210);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+}  // namespace mivi
+
 // -------------------------------------------------------------------- C ABI
 
 using namespace mivi;
+
+// Packed rows: Q6_K with d in {2048, 4096, 8192} (the streaming kernel's shapes).
+static bool packable(int32_t t, size_t d) { return t == MIVI_GGML_Q6_K && (d == 2048 || d == 4096 || d == 8192); }
+
+extern "C" int32_t mivi_hip_pack_weights(int32_t t, const uint8_t* src, size_t src_len, uint8_t* dst,
+                                         size_t dst_len, size_t rows, size_t cols, void* stream) {
+    size_t bs, ts;
+    if (!format_sizes(t, &bs, &ts)) return err_unsupported(t);
+    if (cols % bs != 0) return err_misaligned(cols, bs);
+    size_t need;
+    if (__builtin_mul_overflow(rows, (cols / bs) * ts, &need)) return err_overflow();
+    if (src_len < need) return err_buffer_too_small(need, src_len);
+    if (dst_len < need) return err_buffer_too_small(need, dst_len);
+    if (!packable(t, cols))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu columns", t, cols);
+    if (rows && (!src || !dst)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    if (src == dst && rows) return set_error(MIVI_ERR_INVALID_ARGUMENT, "packing needs distinct buffers");
+    clear_error();
+    return launch_pack_q6k(src, dst, rows, cols, (hipStream_t)stream);
+}
+
+extern "C" int32_t mivi_hip_quantized_matvec_packed(float* out, size_t out_len, int32_t t, const uint8_t* packed,
+                                                    size_t packed_len, const float* x, size_t x_len, size_t n,
+                                                    size_t d, void* stream) {
+    int32_t rc = validate_matvec(t, out_len, packed_len, x_len, n, d, nullptr);
+    if (rc) return rc;
+    if (!packable(t, d))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu columns", t, d);
+    if (n && (!out || !packed || !x)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    if ((uintptr_t)packed % 16) return set_error(MIVI_ERR_INVALID_ARGUMENT, "packed rows must be 16-byte aligned");
+    if (n > (size_t)INT32_MAX) return err_overflow();
+    clear_error();
+    if (n == 0) return MIVI_OK;
+    GemvArgs a = {};
+    a.seg[0] = {packed, out, (int)n};
+    a.nseg = 1;
+    a.K = (int)d;
+    a.x = x;
+    a.packed = 1;
+    return launch_gemv_ex(t, PRO_NONE, a, (hipStream_t)stream);
+}
 
 static int32_t matvec_typed(int32_t t, float* out, size_t out_len, const uint8_t* w, size_t w_len,
                             const float* x, size_t x_len, size_t n, size_t d, void* stream) {

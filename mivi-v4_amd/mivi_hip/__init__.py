@@ -103,6 +103,8 @@ _sig = {
     "mivi_hip_try_matvec_f16": ([_P, _S, _P, _S, _P, _S, _S, _S, _P], _I),
     "mivi_hip_try_matvec_bf16": ([_P, _S, _P, _S, _P, _S, _S, _S, _P], _I),
     "mivi_hip_quantized_matmul_rows": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _S, _P], _I),
+    "mivi_hip_pack_weights": ([_I, _P, _S, _P, _S, _S, _S, _P], _I),
+    "mivi_hip_quantized_matvec_packed": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _P], _I),
     "mivi_hip_dequantize_slice": ([_I, _P, _S, _P, _S, _P], _I),
     "mivi_hip_quantize_q8_0": ([_P, _S, _P, _S, _S, _P], _I),
     "mivi_hip_dot_q8_0_f32": ([_P, _S, _P, _S, _P, _S, _S, _P], _I),
@@ -193,6 +195,20 @@ try_matvec_q6_k = _typed(_lib.mivi_hip_try_matvec_q6_k)       # q6_k.rs:202
 try_matvec_q8_0 = _typed(_lib.mivi_hip_try_matvec_q8_0)       # q8_0.rs:127
 try_matvec_f16 = _typed(_lib.mivi_hip_try_matvec_f16)         # f16.rs:42
 try_matvec_bf16 = _typed(_lib.mivi_hip_try_matvec_bf16)       # f16.rs:75
+
+
+def pack_weights(ggml_type, src, dst, rows: int, cols: int, stream=None):
+    """Q6_K rows into the packed unit-plane layout (u8 GPU tensors of equal size)."""
+    _check(_lib.mivi_hip_pack_weights(int(ggml_type), C.c_void_p(src.data_ptr()), _nbytes(src),
+                                      C.c_void_p(dst.data_ptr()), _nbytes(dst), rows, cols, _stream(stream)))
+
+
+def quantized_matvec_packed(out, ggml_type, packed, x, n: int, d: int, stream=None):
+    """quantized_matvec over rows packed by pack_weights."""
+    po, lo = _dev(out)
+    px, lx = _dev(x)
+    _check(_lib.mivi_hip_quantized_matvec_packed(po, lo, int(ggml_type), C.c_void_p(packed.data_ptr()),
+                                                 _nbytes(packed), px, lx, n, d, _stream(stream)))
 
 
 def quantized_matmul_rows(out, ggml_type, weights, inputs, batch: int, rows: int, cols: int, stream=None):

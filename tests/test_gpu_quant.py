@@ -277,3 +277,44 @@ def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, 
     X[3] = 0.0
     X[3, 5] = np.float32(7.5e3)      # one dominant value
     _matmul_check(hip, oracle, torch, Q4_K, w, X, rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (1000, 4096), (130, 8192), (65536, 2048)])
+def test_packed_q6k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols):
+    # the packed layout is a byte permutation: the packed GEMV must give the
+    # raw GEMV's result bit for bit, and both meet the oracle bound
+    torch = torch_mod
+    w = hip.synth_random_weights(Q6_K, 90 + cols, rows, cols, 0.02)
+    x = hip.synth_normal(91, cols)
+    dw, dx = dev(torch, w), dev(torch, x)
+    packed = torch.empty_like(dw)
+    hip.pack_weights(Q6_K, dw, packed, rows, cols)
+    y_raw = torch.empty(rows, dtype=torch.float32, device="cuda")
+    y_pk = torch.full((rows + 1,), 7.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(y_raw, Q6_K, dw, dx, rows, cols)
+    hip.quantized_matvec_packed(y_pk[:rows], Q6_K, packed, dx, rows, cols)
+    torch.cuda.synchronize()
+    a, b = y_raw.cpu().numpy(), y_pk.cpu().numpy()
+    assert b[-1] == 7.0
+    assert np.array_equal(a.view(np.uint32), b[:-1].view(np.uint32))
+    # the packed bytes are a permutation of each row
+    pw = packed.cpu().numpy().reshape(rows, -1)
+    assert np.array_equal(np.sort(pw[:3], axis=1), np.sort(w.reshape(rows, -1)[:3], axis=1))
+    if rows <= 1000:
+        check_bound(oracle, Q6_K, w, x, a, rows, cols)
+
+
+def test_packed_rejects_other_types_and_shapes(hip, torch_mod):
+    torch = torch_mod
+    w = torch.zeros(144 * 8 * 4, dtype=torch.uint8, device="cuda")
+    dst = torch.zeros_like(w)
+    with pytest.raises(hip.QuantError):
+        hip.pack_weights(Q4_K, w, dst, 4, 2048)
+    w6 = torch.zeros(210 * 4 * 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(hip.QuantError):
+        hip.pack_weights(Q6_K, w6, torch.zeros_like(w6), 4, 1024)   # no packed layout for d = 1024
+    out = torch.zeros(4, dtype=torch.float32, device="cuda")
+    x = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    with pytest.raises(hip.QuantError):
+        hip.quantized_matvec_packed(out, Q6_K, w6, x, 4, 1024)
+    assert hip.last_error().code == 116
