@@ -17,15 +17,15 @@
 //                      to 16) and is subtracted the same way. The row scale
 //                      2^e is applied at the store.
 //
-// Other formats, and Q4_K with fewer rows, run the GEMV once per input row.
+// Other formats, and Q4_K with fewer rows, run the batched GEMV (the inputs
+// as its columns).
 #include <mutex>
 #include <vector>
 
 #include "common.h"
+#include "gemv.h"
 
 namespace mivi {
-int32_t launch_gemv(int32_t t, const uint8_t* W, const float* x, float* y, size_t n, size_t d, bool accumulate,
-                    hipStream_t s);
 bool format_sizes(int32_t t, size_t* bs, size_t* ts);
 bool ggml_sizes(int32_t t, size_t* bs, size_t* ts);
 }  // namespace mivi
@@ -406,9 +406,17 @@ extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, in
     hipStream_t s = (hipStream_t)stream;
     if (t == MIVI_GGML_Q4_K && batch >= (size_t)kMfmaMinBatch && cols % 2048 == 0)
         return matmul_q4k_mfma(out, w, in, batch, rows, cols, s);
-    for (size_t b = 0; b < batch; b++) {
-        rc = launch_gemv(t, w, in + b * cols, out + b * rows, rows, cols, false, s);
-        if (rc) return rc;
-    }
-    return MIVI_OK;
+    // one GEMV over the batch's input rows as columns: the streaming kernel
+    // reads each weight row once per two inputs, with every input's result
+    // bit-identical to its own matvec (lib.rs:404-457); other shapes run one
+    // launch per input row
+    mivi::GemvArgs a = {};
+    a.seg[0] = {w, out, (int)rows};
+    a.nseg = 1;
+    a.K = (int)cols;
+    a.x = in;
+    a.ncol = (int)batch;
+    a.xs = (int64_t)cols;
+    a.ys = (int64_t)rows;
+    return mivi::launch_gemv_ex(t, mivi::PRO_NONE, a, s);
 }

@@ -43,7 +43,17 @@ struct GemvArgs {
     int packed;            // 1: Q6_K rows in the unit-plane layout of mivi_hip_pack_weights
     float* part_val;       // EPI_ARGMAX: per-wave maximum ...
     int* part_idx;         // ... and the first row holding it
+    // Batched columns: ncol > 1 activation vectors (one per sequence) against
+    // the same rows. Column c reads x + c*xs (x2 + c*xs; st_in / st_out +
+    // c*sts; phase + c) and writes every segment's outputs at + c*ys (the
+    // argmax partials at + c*ps). ncol 0 or 1: one column.
+    int ncol;
+    int64_t xs, sts, ys, ps;
 };
+
+// Most columns one batched streaming launch takes (more are split into
+// launches of at most this many).
+constexpr int kMaxGemvCols = 2;
 
 // What the GEMV does with its row results (streaming kernel, K = 2048).
 enum GemvEpilogue : int {

@@ -718,6 +718,12 @@ struct SeqState {
     uint8_t *kc, *vc;        // [n_attn * max_seq * row_bytes]
 };
 
+// Element strides between consecutive sequences' vectors in the per-kind
+// arenas (SeqState pointers of sequence b = arena + b * stride).
+struct SeqStrides {
+    size_t x = 0, sc_in = 0, hb = 0, qkv = 0, logits = 0, conv = 0, parts = 0;
+};
+
 struct Ctrl {  // device control block
     uint32_t tok[64];
     int pos[64];
@@ -738,6 +744,7 @@ struct mivi_model {
     std::vector<Layer> layers;
     float *rope_cos = nullptr, *rope_sin = nullptr;
     std::vector<SeqState> seqs;
+    SeqStrides strides;
     std::vector<void*> allocs;
     Ctrl* ctrl = nullptr;
     uint32_t* history = nullptr;  // [max_seq * max_batch]
@@ -765,20 +772,26 @@ struct mivi_model {
 
 namespace {
 
-// Enqueues part of one decode step of sequence b: the embedding (do_embed),
-// layers [l0, l1), then the head, argmax and position advance (do_head).
-int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s, bool do_embed, size_t l0,
-                     size_t l1, bool do_head) {
+// Enqueues part of one decode step of sequences b0 .. b0+nb-1: the
+// embeddings (do_embed), layers [l0, l1), then the head, argmax and position
+// advance (do_head). Each projection is one GEMV over the nb sequences'
+// activation columns (weights read once for all of them); attention runs per
+// sequence.
+int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argmax, hipStream_t s, bool do_embed,
+                     size_t l0, size_t l1, bool do_head) {
     const mivi_model_info& c = m->info;
-    SeqState& st = m->seqs[b];
+    const SeqStrides& z = m->strides;
+    SeqState& s0 = m->seqs[b0];
     int32_t rc;
     const int D = (int)c.dim, H = (int)c.hidden_dim, KV = (int)c.kv_dim;
+    const int ncol = (int)nb;
     if (do_embed) {
         size_t bs, ts;
         format_sizes(m->embd.type, &bs, &ts);
         size_t row_bytes = (c.dim * ts) / bs;  // model.rs:358-360
-        hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kWG), 0, s, m->embd.type, m->embd.w, row_bytes,
-                           &m->ctrl->tok[b], st.x, D);
+        for (size_t b = b0; b < b0 + nb; b++)
+            hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kWG), 0, s, m->embd.type, m->embd.w, row_bytes,
+                               &m->ctrl->tok[b], m->seqs[b].x, D);
     }
     for (size_t l = l0; l < l1 && l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
@@ -786,27 +799,30 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
         if (!L.attn) {
             if (c.ssm_conv_kernel == 0) continue;  // ssm.rs:60-62
             // in_proj on rms_norm(x, ssm_norm)
-            g.seg[0] = {L.in_proj.w, st.sc_in, 3 * D};
-            g.nseg = 1; g.K = D; g.x = st.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            g.seg[0] = {L.in_proj.w, s0.sc_in, 3 * D};
+            g.nseg = 1; g.K = D; g.x = s0.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            g.ncol = ncol; g.xs = z.x; g.ys = z.sc_in;
             if ((rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
             // out_proj on the gated conv, residual add into x
             const size_t ks = c.ssm_conv_kernel;
             g = {};
-            g.seg[0] = {L.out_proj.w, st.x, D};
-            g.nseg = 1; g.K = D; g.x = st.sc_in;
+            g.seg[0] = {L.out_proj.w, s0.x, D};
+            g.nseg = 1; g.K = D; g.x = s0.sc_in;
             g.conv_w = L.conv;
             g.conv_mode = (L.conv && L.conv_len >= (size_t)D * ks) ? 0 : (L.conv && L.conv_len >= ks) ? 1 : 2;
             g.ksize = (int)ks;
-            g.st_in = st.conv_a + l * (size_t)D * ks;
-            g.st_out = st.conv_b + l * (size_t)D * ks;
-            g.phase = &m->ctrl->phase[b];
+            g.st_in = s0.conv_a + l * (size_t)D * ks;
+            g.st_out = s0.conv_b + l * (size_t)D * ks;
+            g.phase = &m->ctrl->phase[b0];
             g.accumulate = 1;
+            g.ncol = ncol; g.xs = z.sc_in; g.sts = z.conv; g.ys = z.x;
             if ((rc = launch_gemv_ex(L.out_proj.type, PRO_CONV, g, s))) return rc;
         } else {
-            g.seg[0] = {L.wq.w, st.q, D};
-            g.seg[1] = {L.wk.w, st.k, KV};
-            g.seg[2] = {L.wv.w, st.v, KV};
-            g.nseg = 3; g.K = D; g.x = st.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            g.seg[0] = {L.wq.w, s0.q, D};
+            g.seg[1] = {L.wk.w, s0.k, KV};
+            g.seg[2] = {L.wv.w, s0.v, KV};
+            g.nseg = 3; g.K = D; g.x = s0.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            g.ncol = ncol; g.xs = z.x; g.ys = z.qkv;
             if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
                 if ((rc = launch_gemv_ex(L.wq.type, PRO_RMSNORM, g, s))) return rc;
             } else {
@@ -818,44 +834,49 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
                     if ((rc = launch_gemv_ex(ms[i]->type, PRO_RMSNORM, g1, s))) return rc;
                 }
             }
-            AttnArgs a = {};
-            a.q = st.q; a.k = st.k; a.v = st.v;
-            a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
-            a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-            size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
-            a.kc = st.kc + (size_t)L.cache_idx * layer_bytes;
-            a.vc = st.vc + (size_t)L.cache_idx * layer_bytes;
-            a.row_bytes = m->kv_row_bytes;
-            a.pos = &m->ctrl->pos[b];
-            a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
-            a.nsplit = m->nsplit;
-            a.scale = 1.0f / sqrtf((float)c.head_dim);
-            a.part_m = st.part_m; a.part_l = st.part_l; a.part_acc = st.part_acc;
-            dim3 grid((unsigned)c.n_kv_heads, (unsigned)m->nsplit);
+            for (size_t b = b0; b < b0 + nb; b++) {
+                SeqState& st = m->seqs[b];
+                AttnArgs a = {};
+                a.q = st.q; a.k = st.k; a.v = st.v;
+                a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
+                a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
+                size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
+                a.kc = st.kc + (size_t)L.cache_idx * layer_bytes;
+                a.vc = st.vc + (size_t)L.cache_idx * layer_bytes;
+                a.row_bytes = m->kv_row_bytes;
+                a.pos = &m->ctrl->pos[b];
+                a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
+                a.nsplit = m->nsplit;
+                a.scale = 1.0f / sqrtf((float)c.head_dim);
+                a.part_m = st.part_m; a.part_l = st.part_l; a.part_acc = st.part_acc;
+                dim3 grid((unsigned)c.n_kv_heads, (unsigned)m->nsplit);
 #define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
-            if (c.head_dim <= 64) {
-                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
-                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
-                else ATT(MIVI_KV_Q8_0, 64);
-            } else {
-                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
-                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
-                else ATT(MIVI_KV_Q8_0, 128);
-            }
+                if (c.head_dim <= 64) {
+                    if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
+                    else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
+                    else ATT(MIVI_KV_Q8_0, 64);
+                } else {
+                    if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
+                    else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
+                    else ATT(MIVI_KV_Q8_0, 128);
+                }
 #undef ATT
-            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads), dim3(kWG), 0, s, st.part_m, st.part_l,
-                               st.part_acc, st.attn_out, &m->ctrl->pos[b], m->nsplit, attn_tile_tokens(c.head_dim),
-                               (int)c.head_dim);
+                hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads), dim3(kWG), 0, s, st.part_m,
+                                   st.part_l, st.part_acc, st.attn_out, &m->ctrl->pos[b], m->nsplit,
+                                   attn_tile_tokens(c.head_dim), (int)c.head_dim);
+            }
             g = {};
-            g.seg[0] = {L.wo.w, st.x, D};
-            g.nseg = 1; g.K = D; g.x = st.attn_out; g.accumulate = 1;
+            g.seg[0] = {L.wo.w, s0.x, D};
+            g.nseg = 1; g.K = D; g.x = s0.attn_out; g.accumulate = 1;
+            g.ncol = ncol; g.xs = z.x; g.ys = z.x;
             if ((rc = launch_gemv_ex(L.wo.type, PRO_NONE, g, s))) return rc;
         }
         // ffn.rs:56-108
         g = {};
-        g.seg[0] = {L.gate.w, st.hb, H};
-        g.seg[1] = {L.up.w, st.hb2, H};
-        g.nseg = 2; g.K = D; g.x = st.x; g.norm_w = L.ffn_norm; g.eps = c.rms_norm_eps;
+        g.seg[0] = {L.gate.w, s0.hb, H};
+        g.seg[1] = {L.up.w, s0.hb2, H};
+        g.nseg = 2; g.K = D; g.x = s0.x; g.norm_w = L.ffn_norm; g.eps = c.rms_norm_eps;
+        g.ncol = ncol; g.xs = z.x; g.ys = z.hb;
         bool fused = false;
         if (L.gate.type == L.up.type) {
             // gate|up with the SwiGLU epilogue writes silu(gate) * up into hb
@@ -877,8 +898,9 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
             if ((rc = launch_gemv_ex(L.up.type, PRO_RMSNORM, g1, s))) return rc;
         }
         g = {};
-        g.seg[0] = {L.down.w, st.x, D};
-        g.nseg = 1; g.K = H; g.x = st.hb; g.x2 = st.hb2; g.accumulate = 1;
+        g.seg[0] = {L.down.w, s0.x, D};
+        g.nseg = 1; g.K = H; g.x = s0.hb; g.x2 = s0.hb2; g.accumulate = 1;
+        g.ncol = ncol; g.xs = z.hb; g.ys = z.x;
         if ((rc = launch_gemv_ex(L.down.type, fused ? PRO_NONE : PRO_SWIGLU, g, s))) return rc;
     }
     if (!do_head) {
@@ -889,15 +911,17 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
     if (logits) {
         // model.rs:435-473
         GemvArgs g = {};
-        g.seg[0] = {m->head_packed ? m->head_packed : m->head.w, st.logits, (int)c.vocab_size};
-        g.nseg = 1; g.K = D; g.x = st.x; g.norm_w = m->out_norm; g.eps = c.rms_norm_eps;
+        g.seg[0] = {m->head_packed ? m->head_packed : m->head.w, s0.logits, (int)c.vocab_size};
+        g.nseg = 1; g.K = D; g.x = s0.x; g.norm_w = m->out_norm; g.eps = c.rms_norm_eps;
         g.packed = m->head_packed ? 1 : 0;
+        g.ncol = ncol; g.xs = z.x; g.ys = z.logits;
         const int pro = m->out_norm ? PRO_RMSNORM : PRO_NONE;
         const int np = argmax ? gemv_argmax_parts(m->head.type, D, (int)c.vocab_size) : 0;
         if (np > 0 && np <= kMaxArgmaxParts) {
             g.epilogue = EPI_ARGMAX;
-            g.part_val = st.part_val;
-            g.part_idx = st.part_idx;
+            g.part_val = s0.part_val;
+            g.part_idx = s0.part_idx;
+            g.ps = z.parts;
             rc = launch_gemv_ex(m->head.type, pro, g, s);
             if (rc == MIVI_OK) parts = np;
             else if (rc != MIVI_ERR_UNSUPPORTED) return rc;
@@ -905,28 +929,25 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
         }
         if (!parts && (rc = launch_gemv_ex(m->head.type, pro, g, s))) return rc;
     }
-    hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, parts ? st.part_val : st.logits,
-                       parts ? st.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b],
-                       &m->ctrl->pos[b], &m->ctrl->phase[b], argmax ? m->history : nullptr, &m->ctrl->step,
-                       (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
+    for (size_t b = b0; b < b0 + nb; b++) {
+        SeqState& st = m->seqs[b];
+        hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, parts ? st.part_val : st.logits,
+                           parts ? st.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b],
+                           &m->ctrl->pos[b], &m->ctrl->phase[b], argmax ? m->history : nullptr, &m->ctrl->step,
+                           (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
+    }
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
 }
 
 int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s) {
-    return enqueue_step(m, b, logits, argmax, s, true, 0, m->info.n_layers, true);
+    return enqueue_step(m, b, 1, logits, argmax, s, true, 0, m->info.n_layers, true);
 }
 
 // One greedy step of sequences 0..batch-1, layer by layer across the
-// sequences, so that each layer's weights are reused from the Infinity Cache
-// by every sequence after the first.
+// sequences: every projection is one GEMV over all the sequences' columns.
 int32_t enqueue_batch_step(mivi_model* m, size_t batch, hipStream_t s) {
-    int32_t rc = MIVI_OK;
-    for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, s, true, 0, 0, false);
-    for (size_t l = 0; l < m->info.n_layers && !rc; l++)
-        for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, s, false, l, l + 1, false);
-    for (size_t b = 0; b < batch && !rc; b++) rc = enqueue_step(m, b, true, true, s, false, 0, 0, true);
-    return rc;
+    return enqueue_step(m, 0, batch, true, true, s, true, 0, m->info.n_layers, true);
 }
 
 void host_rope_table(std::vector<float>& cs, std::vector<float>& sn, size_t hd, size_t max_seq, float base,
@@ -1208,16 +1229,35 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
     const size_t want = std::max<size_t>(1, 2 * (size_t)num_cus() / std::max<size_t>(1, c.n_kv_heads));
     m->nsplit = (int)std::max<size_t>(1, std::min((c.max_seq_len + tt - 1) / tt, want));
     size_t ks = std::max<size_t>(1, c.ssm_conv_kernel);
+    // Per-sequence vectors live in one arena per kind, sequence b at
+    // base + b * stride, so a batched GEMV addresses every sequence's
+    // activations and outputs with one stride (q|k|v share one slot).
     m->seqs.resize(max_batch);
+    {
+        SeqStrides& z = m->strides;
+        z.x = c.dim; z.sc_in = 3 * c.dim; z.hb = c.hidden_dim; z.qkv = c.dim + 2 * c.kv_dim;
+        z.logits = c.vocab_size; z.conv = c.n_layers * c.dim * ks; z.parts = kMaxArgmaxParts;
+        const size_t B = max_batch;
+        float *x, *sc_in, *hb, *hb2, *qkv, *ao, *lg, *ca, *cb, *pv;
+        int* pi;
+        if ((rc = m->alloc(&x, B * z.x)) || (rc = m->alloc(&sc_in, B * z.sc_in)) || (rc = m->alloc(&hb, B * z.hb)) ||
+            (rc = m->alloc(&hb2, B * z.hb)) || (rc = m->alloc(&qkv, B * z.qkv)) || (rc = m->alloc(&ao, B * z.x)) ||
+            (rc = m->alloc(&lg, B * z.logits)) || (rc = m->alloc(&ca, B * z.conv)) || (rc = m->alloc(&cb, B * z.conv)) ||
+            (rc = m->alloc(&pv, B * z.parts)) || (rc = m->alloc(&pi, B * z.parts)))
+            return fail(rc);
+        for (size_t b = 0; b < B; b++) {
+            SeqState& st = m->seqs[b];
+            st.x = x + b * z.x; st.sc_in = sc_in + b * z.sc_in;
+            st.hb = hb + b * z.hb; st.hb2 = hb2 + b * z.hb;
+            st.q = qkv + b * z.qkv; st.k = st.q + c.dim; st.v = st.k + c.kv_dim;
+            st.attn_out = ao + b * z.x; st.logits = lg + b * z.logits;
+            st.conv_a = ca + b * z.conv; st.conv_b = cb + b * z.conv;
+            st.part_val = pv + b * z.parts; st.part_idx = pi + b * z.parts;
+        }
+    }
     for (auto& st : m->seqs) {
-        if ((rc = m->alloc(&st.x, c.dim)) || (rc = m->alloc(&st.sc_in, 3 * c.dim)) ||
-            (rc = m->alloc(&st.hb, c.hidden_dim)) || (rc = m->alloc(&st.hb2, c.hidden_dim)) ||
-            (rc = m->alloc(&st.q, c.dim)) || (rc = m->alloc(&st.k, c.kv_dim)) || (rc = m->alloc(&st.v, c.kv_dim)) ||
-            (rc = m->alloc(&st.attn_out, c.dim)) || (rc = m->alloc(&st.logits, c.vocab_size)) ||
-            (rc = m->alloc(&st.conv_a, c.n_layers * c.dim * ks)) || (rc = m->alloc(&st.conv_b, c.n_layers * c.dim * ks)) ||
-            (rc = m->alloc(&st.part_m, c.n_heads * m->nsplit)) || (rc = m->alloc(&st.part_l, c.n_heads * m->nsplit)) ||
+        if ((rc = m->alloc(&st.part_m, c.n_heads * m->nsplit)) || (rc = m->alloc(&st.part_l, c.n_heads * m->nsplit)) ||
             (rc = m->alloc(&st.part_acc, c.n_heads * m->nsplit * c.head_dim)) ||
-            (rc = m->alloc(&st.part_val, kMaxArgmaxParts)) || (rc = m->alloc(&st.part_idx, kMaxArgmaxParts)) ||
             (rc = m->alloc(&st.kc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)) ||
             (rc = m->alloc(&st.vc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)))
             return fail(rc);

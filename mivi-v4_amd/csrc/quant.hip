@@ -904,6 +904,18 @@ __device__ __forceinline__ void load_unit(Unit<FMT>& U, const uint8_t* row, int 
     }
 }
 
+// Column c of a batched launch (a.ncol > 1): the same weights against the
+// c-th activation vector, written to the c-th outputs (pointer + c * stride).
+__device__ __forceinline__ mivi::GemvArgs gemv_column(const mivi::GemvArgs& a, int c) {
+    mivi::GemvArgs v = a;
+    v.x = a.x + c * a.xs;
+    if (a.x2) v.x2 = a.x2 + c * a.xs;
+    if (a.st_in) v.st_in = a.st_in + c * a.sts;
+    if (a.st_out) v.st_out = a.st_out + c * a.sts;
+    if (a.phase) v.phase = a.phase + c;
+    return v;
+}
+
 // K-quant GEMV for the decode shapes (K = 2048/4096/8192). A persistent grid
 // of waves walks groups of RPW = 64/LPR rows; in each group a row is covered
 // by LPR lanes, each owning NU fixed 64-value units, so a lane's activation
@@ -911,17 +923,23 @@ __device__ __forceinline__ void load_unit(Unit<FMT>& U, const uint8_t* row, int 
 // units straight from HBM into a ring of PD row groups held in registers:
 // the loop has no LDS traffic and no barriers, so each wave streams at its
 // own pace. After the x staging the workgroup never synchronises again.
-template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI, bool PACK = false>
+// NC > 1: up to NC activation columns (sequences of a batched decode step)
+// against the same rows. Each row is loaded once and its units are dotted
+// with every column's digits (also held in registers), in the same order as
+// the one-column kernel, so every column's result is bit-identical to a
+// one-column launch on that column.
+template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI, bool PACK = false, int NC = 1>
 __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArgs a) {
     static_assert(!PACK || FMT == FMT_Q6K, "only Q6_K has a packed layout");
     constexpr int RPW = 64 / LPR;
     static_assert(EPI != mivi::EPI_SWIGLU || LPR == 32, "the pair epilogue takes two rows per wave");
     constexpr int K = KT, nb = K / 256, units = nb * 4;
     constexpr int row_bytes = nb * KQ<FMT>::bytes;
-    __shared__ __attribute__((aligned(16))) uint32_t dig[3 * K / 4];
-    __shared__ float xsum[FMT == FMT_Q4K ? K / 32 : 1];
+    __shared__ __attribute__((aligned(16))) uint32_t dig[NC][3 * K / 4];
+    __shared__ float xsum[NC][FMT == FMT_Q4K ? K / 32 : 1];
     const Segs sg(a, row_bytes);
     const int n = sg.n;
+    const int ncol = NC == 1 ? 1 : a.ncol;  // workgroup-uniform, <= NC
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane % LPR, sub = lane / LPR;
     // EPI_SWIGLU: group c is the row pair (gate c, up c) = rows c and n0 + c
     const int n0 = a.seg[0].n;
@@ -955,22 +973,35 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
         }
     };
     // activation loads first, then the first PD row groups of weights, which
-    // stay in flight while x is staged
-    StageIn<PRO, K / kWG> in;
+    // stay in flight while x is staged; with several columns the next
+    // column's activations load while the current one is staged
+    StageIn<PRO, K / kWG> in[NC > 1 ? 2 : 1];
+    float s[NC];
     // (scheduling barriers keep this order: activation loads, weight loads,
     // then the activation math, which then waits for the activations only)
-    in.load(a);
+    in[0].load(NC == 1 ? a : gemv_column(a, 0));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < PD; p++) load_step(buf[p], p);
     __builtin_amdgcn_sched_barrier(0);
-    const float s = in.template finish<FMT == FMT_Q4K>(a, dig, xsum);
+    if constexpr (NC == 1) {
+        s[0] = in[0].template finish<FMT == FMT_Q4K>(a, dig[0], xsum[0]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            if (c + 1 < ncol) in[(c + 1) & 1].load(gemv_column(a, c + 1));
+            if (c < ncol) s[c] = in[c & 1].template finish<FMT == FMT_Q4K>(gemv_column(a, c), dig[c], xsum[c]);
+            else s[c] = 0.0f;
+        }
+    }
 
     // this lane's activation digits (and their per-quad offsets / fp32
-    // sub-block sums), fixed for the launch
-    uint32_t xd[NU][3][16];
-    int off[NU][4][3];
-    float X[NU][2];
+    // sub-block sums), per column, fixed for the launch
+    uint32_t xd[NC][NU][3][16];
+    int off[NC][NU][4][3];
+    float X[NC][NU][2];
+#pragma unroll
+    for (int cc = 0; cc < NC; cc++)
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = min(lr + LPR * i, units - 1);
@@ -982,12 +1013,12 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
             for (int e = 0; e < 3; e++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const u32x4 v = *(const u32x4*)(dig + e * (K / 4) + w0 + 4 * q);
-                    xd[i][e][4 * q] = v.x; xd[i][e][4 * q + 1] = v.y;
-                    xd[i][e][4 * q + 2] = v.z; xd[i][e][4 * q + 3] = v.w;
+                    const u32x4 v = *(const u32x4*)(dig[cc] + e * (K / 4) + w0 + 4 * q);
+                    xd[cc][i][e][4 * q] = v.x; xd[cc][i][e][4 * q + 1] = v.y;
+                    xd[cc][i][e][4 * q + 2] = v.z; xd[cc][i][e][4 * q + 3] = v.w;
                 }
-            X[i][0] = xsum[b * 8 + 2 * g];
-            X[i][1] = xsum[b * 8 + 2 * g + 1];
+            X[cc][i][0] = xsum[cc][b * 8 + 2 * g];
+            X[cc][i][1] = xsum[cc][b * 8 + 2 * g + 1];
         } else {
             const int h = (u >> 1) & 1, j = u & 1;
             const int e0 = b * 256 + h * 128 + 16 * j;
@@ -995,32 +1026,41 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
             for (int e = 0; e < 3; e++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const u32x4 v = *(const u32x4*)(dig + e * (K / 4) + (e0 + 32 * q) / 4);
-                    xd[i][e][4 * q] = v.x; xd[i][e][4 * q + 1] = v.y;
-                    xd[i][e][4 * q + 2] = v.z; xd[i][e][4 * q + 3] = v.w;
+                    const u32x4 v = *(const u32x4*)(dig[cc] + e * (K / 4) + (e0 + 32 * q) / 4);
+                    xd[cc][i][e][4 * q] = v.x; xd[cc][i][e][4 * q + 1] = v.y;
+                    xd[cc][i][e][4 * q + 2] = v.z; xd[cc][i][e][4 * q + 3] = v.w;
                     int t = 0;
                     t = sdot4(v.x, 0x01010101u, t);
                     t = sdot4(v.y, 0x01010101u, t);
                     t = sdot4(v.z, 0x01010101u, t);
                     t = sdot4(v.w, 0x01010101u, t);
-                    off[i][q][e] = -32 * t;
+                    off[cc][i][q][e] = -32 * t;
                 }
         }
     }
-    float best = -INFINITY;  // EPI_ARGMAX: this lane's maximum and its first row
-    int bidx = 0x7FFFFFFF;
-    auto write_part = [&]() {
-        // merge the RPW row groups of the wave (lanes 0, LPR, ...), then
-        // lane 0 writes; lanes that hold no row carry (-inf, INT_MAX)
+    // EPI_ARGMAX: per column, this lane's maximum and its first row
+    float best[NC];
+    int bidx[NC];
 #pragma unroll
-        for (int o = LPR; o < 64; o <<= 1) {
-            const float ov = __shfl_xor(best, o, 64);
-            const int oi = __shfl_xor(bidx, o, 64);
-            if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
-        }
-        if (lane == 0) {
-            a.part_val[wid] = best;
-            a.part_idx[wid] = bidx;
+    for (int c = 0; c < NC; c++) { best[c] = -INFINITY; bidx[c] = 0x7FFFFFFF; }
+    auto write_part = [&]() {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            if (c >= ncol) break;
+            // merge the RPW row groups of the wave (lanes 0, LPR, ...), then
+            // lane 0 writes; lanes that hold no row carry (-inf, INT_MAX)
+            float bv = best[c];
+            int bi = bidx[c];
+#pragma unroll
+            for (int o = LPR; o < 64; o <<= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) {
+                a.part_val[c * a.ps + wid] = bv;
+                a.part_idx[c * a.ps + wid] = bi;
+            }
         }
     };
     if (cnt == 0) {  // wave-uniform; no barrier follows
@@ -1029,30 +1069,37 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     }
 
     auto compute = [&](const Unit<FMT> (&B)[NU], int st) {
-        float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < NU; i++) {
-            if (lr + LPR * i >= units) continue;
-            if constexpr (FMT == FMT_Q4K)
-                acc += q4k_unit_i8(B[i].hdr, B[i].qa, B[i].qb, (lr + LPR * i) & 3, xd[i], s, X[i][0], X[i][1]);
-            else
-                acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, PACK ? packed_q6k_scales(B[i].sc.x) : B[i].sc,
-                                   B[i].d, xd[i], off[i]);
-        }
-        float sum = group_sum<LPR>(acc);
-        if (FMT == FMT_Q6K) sum *= s;
-        if constexpr (EPI == mivi::EPI_SWIGLU) {
-            // lane 0 holds gate c, lane 32 up c (math.rs:87-95)
-            const float up = __shfl(sum, 32, 64);
-            const int c = wid + st * nw;
-            if (lane == 0 && c < n0) *(gfloat*)sg.out(c) = silu_f(sum) * up;
-        } else {
-            const int r = (wid + st * nw) * RPW + sub;
-            if (lr == 0 && r < n) {
-                store_out(sg, a.accumulate, r, sum);
-                // sampler.rs:305-316: strictly greater wins, so NaN never does
-                if constexpr (EPI == mivi::EPI_ARGMAX)
-                    if (sum > best) { best = sum; bidx = r; }
+        for (int cc = 0; cc < NC; cc++) {
+            if (cc >= ncol) break;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < NU; i++) {
+                if (lr + LPR * i >= units) continue;
+                if constexpr (FMT == FMT_Q4K)
+                    acc += q4k_unit_i8(B[i].hdr, B[i].qa, B[i].qb, (lr + LPR * i) & 3, xd[cc][i], s[cc], X[cc][i][0],
+                                       X[cc][i][1]);
+                else
+                    acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, PACK ? packed_q6k_scales(B[i].sc.x) : B[i].sc,
+                                       B[i].d, xd[cc][i], off[cc][i]);
+            }
+            float sum = group_sum<LPR>(acc);
+            if (FMT == FMT_Q6K) sum *= s[cc];
+            if constexpr (EPI == mivi::EPI_SWIGLU) {
+                // lane 0 holds gate c, lane 32 up c (math.rs:87-95)
+                const float up = __shfl(sum, 32, 64);
+                const int c = wid + st * nw;
+                if (lane == 0 && c < n0) *(gfloat*)(sg.out(c) + cc * a.ys) = silu_f(sum) * up;
+            } else {
+                const int r = (wid + st * nw) * RPW + sub;
+                if (lr == 0 && r < n) {
+                    gfloat* y = (gfloat*)(sg.out(r) + cc * a.ys);
+                    if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(y, sum);
+                    else *y = sum;
+                    // sampler.rs:305-316: strictly greater wins, so NaN never does
+                    if constexpr (EPI == mivi::EPI_ARGMAX)
+                        if (sum > best[cc]) { best[cc] = sum; bidx[cc] = r; }
+                }
             }
         }
     };
@@ -1162,6 +1209,7 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
     if (PRO == mivi::PRO_CONV)
         stream_ok = stream_ok && K == 2048 && a.ksize == kConvKs && a16(a.st_in) && a16(a.st_out) &&
                     (a.conv_mode != 0 || a16(a.conv_w));
+    if (a.ncol > 1 && !stream_ok) return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no batched GEMV for this shape");
     if (stream_ok) {
         const int lpr = K == 2048 ? 32 : 64;
         const int ngroups = (n + 64 / lpr - 1) / (64 / lpr);
@@ -1173,6 +1221,50 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
 #define LS(FMT, KT, LPR, NU, PD) LSE(FMT, KT, LPR, NU, PD, mivi::EPI_STORE)
 #define LSP(KT, LPR, NU, PD, EPI) \
     hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, KT, LPR, NU, PD, PRO, EPI, true>), dim3(grid), dim3(kWG), 0, s, a)
+        if (a.ncol > 1) {
+            // batched columns (launch_cols passes at most gemv_max_cols):
+            // the one-column kernel's mapping, so each column's result is
+            // bit-identical to a one-column launch; PD 2 leaves registers for
+            // the columns' digits
+#define LB(FMT, KT, LPR, NU, PD, EPI, PACK, NC)                                                                 \
+    hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO, EPI, PACK, NC>), dim3(grid), dim3(kWG), 0, \
+                       s, a)
+            const int ep = a.epilogue;
+            if (K == 2048) {
+                if (ep == mivi::EPI_STORE) {
+                    if (a.packed) {
+                        if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM)
+                            LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_STORE, true, 2);
+                        else
+                            return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows take no conv or SwiGLU prologue");
+                    } else if (t == MIVI_GGML_Q4_K) LB(FMT_Q4K, 2048, 32, 1, 2, mivi::EPI_STORE, false, 2);
+                    else LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_STORE, false, 2);
+                } else if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
+                    if (ep == mivi::EPI_SWIGLU) {
+                        if (a.nseg != 2 || a.seg[1].n != a.seg[0].n)
+                            return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "SwiGLU epilogue needs gate|up of equal rows");
+                        const int g1 = std::max(1, std::min((a.seg[0].n + 3) / 4, mivi::num_cus() * per_cu));
+                        if (t == MIVI_GGML_Q4_K)
+                            hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 2048, 32, 1, 2, PRO, mivi::EPI_SWIGLU, false, 2>),
+                                               dim3(g1), dim3(kWG), 0, s, a);
+                        else
+                            hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, 2048, 32, 1, 2, PRO, mivi::EPI_SWIGLU, false, 2>),
+                                               dim3(g1), dim3(kWG), 0, s, a);
+                    } else {
+                        if (a.packed) LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, true, 2);
+                        else if (t == MIVI_GGML_Q4_K) LB(FMT_Q4K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, false, 2);
+                        else LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, false, 2);
+                    }
+                } else {
+                    return mivi::set_error(MIVI_ERR_UNSUPPORTED, "batched GEMV epilogue %d with this prologue", ep);
+                }
+            } else {
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no batched GEMV for d=%d", K);
+            }
+#undef LB
+            MIVI_HIP_CHECK(hipGetLastError());
+            return MIVI_OK;
+        }
         if (a.packed) {
             // packed Q6_K rows (store or argmax epilogue, no conv/SwiGLU prologue)
             if (t != MIVI_GGML_Q6_K || a.epilogue == mivi::EPI_SWIGLU)
@@ -1293,18 +1385,65 @@ int gemv_argmax_parts(int32_t t, int K, int n) {
     return 4 * std::max(1, std::min((ngroups + 3) / 4, num_cus() * per_cu));
 }
 
-int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
-    int n = 0;
-    for (int i = 0; i < a.nseg; i++) n += a.seg[i].n;
-    if (n == 0 || a.K == 0) return MIVI_OK;
-    if ((size_t)a.K > kMaxLdsK)
-        return set_error(MIVI_ERR_UNSUPPORTED, "GEMV with d=%d exceeds the LDS staging limit %zu", a.K, kMaxLdsK);
+// Most columns one batched streaming launch takes at depth K, 1 where there
+// is no batched kernel. Its lanes hold every column's digits in registers:
+// two columns at K = 2048 fit in 164-198 VGPRs; at K = 8192 (two units per
+// lane) two columns would spill.
+static int gemv_max_cols(int32_t t, int K) {
+    if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
+    return K == 2048 ? kMaxGemvCols : 1;
+}
+
+// Columns [c0, c0 + nc) of a batched GEMV as one launch's arguments.
+static GemvArgs column_args(const GemvArgs& a, int c0, int nc) {
+    GemvArgs v = a;
+    v.x = a.x + c0 * a.xs;
+    if (a.x2) v.x2 = a.x2 + c0 * a.xs;
+    if (a.st_in) v.st_in = a.st_in + c0 * a.sts;
+    if (a.st_out) v.st_out = a.st_out + c0 * a.sts;
+    if (a.phase) v.phase = a.phase + c0;
+    for (int i = 0; i < a.nseg; i++) v.seg[i].y = a.seg[i].y + c0 * a.ys;
+    if (a.part_val) v.part_val = a.part_val + c0 * a.ps;
+    if (a.part_idx) v.part_idx = a.part_idx + c0 * a.ps;
+    v.ncol = nc;
+    return v;
+}
+
+static int32_t launch_by_pro(int32_t t, int pro, const GemvArgs& a, int n, hipStream_t s) {
     switch (pro) {
     case PRO_NONE: return launch_pro<PRO_NONE>(t, a, n, s);
     case PRO_RMSNORM: return launch_pro<PRO_RMSNORM>(t, a, n, s);
     case PRO_SWIGLU: return launch_pro<PRO_SWIGLU>(t, a, n, s);
     default: return launch_pro<PRO_CONV>(t, a, n, s);
     }
+}
+
+int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
+    int n = 0;
+    for (int i = 0; i < a.nseg; i++) n += a.seg[i].n;
+    if (n == 0 || a.K == 0) return MIVI_OK;
+    if (a.ncol > 1) {
+        // column groups of the batched kernel; columns it cannot take run
+        // one launch each
+        const int cap = gemv_max_cols(t, a.K);
+        for (int c0 = 0; c0 < a.ncol;) {
+            const int nc = std::min(cap, a.ncol - c0);
+            int32_t rc = nc > 1 ? launch_by_pro(t, pro, column_args(a, c0, nc), n, s) : MIVI_ERR_UNSUPPORTED;
+            if (rc == MIVI_ERR_UNSUPPORTED) {
+                for (int c = c0; c < c0 + nc; c++)
+                    if ((rc = launch_gemv_ex(t, pro, column_args(a, c, 1), s))) return rc;
+            } else if (rc) {
+                return rc;
+            }
+            c0 += nc;
+        }
+        return MIVI_OK;
+    }
+    if ((size_t)a.K > kMaxLdsK)
+        return set_error(MIVI_ERR_UNSUPPORTED, "GEMV with d=%d exceeds the LDS staging limit %zu", a.K, kMaxLdsK);
+    GemvArgs one = a;
+    one.ncol = 1;
+    return launch_by_pro(t, pro, one, n, s);
 }
 
 // Enqueues y[0..n) (=|+=) W[n, d] x for a validated problem.

@@ -97,6 +97,28 @@ def test_batched_sequences_are_independent(hip, small_img):
         assert np.array_equal(out[:, b], one)
 
 
+def test_batched_full_width_matches_single_sequences(hip):
+    # dim 2048 (the decode shapes): the packed Q6_K head, two-column GEMV
+    # launches, the d = 8192 per-column fallback, and an odd batch (3 = 2 + 1
+    # columns); every sequence's greedy tokens and final logits equal its own
+    # single-sequence run bit for bit
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
+                       ctx_len=1024, seed=11)
+    B = 3
+    mb = hip.Model(img, max_ctx=256, max_batch=B)
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, 4096, 6 + 3 * b) for b in range(B)]
+    for b, pr in enumerate(prompts):
+        mb.prefill(pr[:-1], seq=b)
+    out = mb.generate_greedy([int(p[-1]) for p in prompts], [len(p) - 1 for p in prompts], 12)
+    for b, pr in enumerate(prompts):
+        m1 = hip.Model(img, max_ctx=256)
+        m1.prefill(pr[:-1])
+        one = m1.generate_greedy([int(pr[-1])], [len(pr) - 1], 12)[:, 0]
+        assert np.array_equal(out[:, b], one), (b, out[:, b], one)
+
+
 @pytest.mark.parametrize("prec,oprec", [(0, 0), (1, 1)])
 def test_state_export_import_into_oracle(hip, oracle, small_img, prec, oprec):
     # cache.rs:682-914 / arena.rs:110-123 semantics: GPU-built state injected

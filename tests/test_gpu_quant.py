@@ -279,6 +279,35 @@ def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, 
     _matmul_check(hip, oracle, torch, Q4_K, w, X, rows, cols)
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("batch,rows,cols", [(2, 64, 2048), (3, 1001, 2048), (5, 6144, 2048), (4, 65536, 2048),
+                                             (3, 300, 8192), (2, 130, 4096)])
+def test_batched_gemv_columns_bit_exact_with_matvec(hip, oracle, torch_mod, t, batch, rows, cols):
+    # matmul_rows below the MFMA threshold runs the batched streaming GEMV
+    # (inputs as columns, two per launch at d = 2048; one launch per input
+    # otherwise): every input's row of outputs equals its own matvec bit for
+    # bit (lib.rs:404-457), and meets the oracle bound
+    torch = torch_mod
+    w = hip.synth_random_weights(t, 70 + batch, rows, cols, 0.02)
+    X = np.stack([hip.synth_normal(80 + b, cols) for b in range(batch)])
+    dw, dX = dev(torch, w), dev(torch, X.reshape(-1))
+    out = torch.full((batch * rows + 1,), 5.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matmul_rows(out[:batch * rows], t, dw, dX, batch, rows, cols)
+    ones = []
+    for b in range(batch):
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        hip.quantized_matvec(y, t, dw, dX[b * cols:(b + 1) * cols], rows, cols)
+        ones.append(y)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert got[-1] == 5.0
+    for b in range(batch):
+        assert np.array_equal(got[b * rows:(b + 1) * rows].view(np.uint32), ones[b].cpu().numpy().view(np.uint32))
+    if rows <= 1001:
+        for b in range(batch):
+            check_bound(oracle, t, w, X[b], got[b * rows:(b + 1) * rows], rows, cols)
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 2048), (1000, 4096), (130, 8192), (65536, 2048)])
 def test_packed_q6k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols):
     # the packed layout is a byte permutation: the packed GEMV must give the
