@@ -45,7 +45,7 @@ constexpr int kMaxHd = 128;            // head_dim supported by the attention ke
 constexpr int kMaxAttnSplits = 1024;   // 65536 tokens / 64 tokens per tile
 constexpr int kMaxArgmaxParts = 16384; // per-wave argmax partials of the head GEMV
 // tokens per attention workgroup (its LDS holds 8192 f32 of K and of V)
-inline int attn_tile_tokens(size_t head_dim) { return head_dim <= 64 ? 128 : 64; }
+inline int attn_tile_tokens(size_t) { return 64; }
 
 // ------------------------------------------------------------------ GGUF
 
@@ -208,6 +208,10 @@ struct AttnArgs {
     float* part_m;         // [n_heads * nsplit]
     float* part_l;
     float* part_acc;       // [n_heads * nsplit * hd]
+    // sequence b of a batched launch (blockIdx.y): q/k/v + b*qkv_s,
+    // kc/vc + b*kv_s bytes, pos + b, part_m/part_l + b*part_s,
+    // part_acc + b*part_s*hd
+    int64_t qkv_s, kv_s, part_s;
 };
 
 __device__ __forceinline__ float block_sum256(float v, float* red) {
@@ -289,11 +293,12 @@ __device__ __forceinline__ void prep_head(float* dst, const float* src, const fl
 // ------------------------------------------------------------ attention
 //
 // GQA decode attention in two launches (transformer.rs:112-301):
-//  attn_tile_kernel    grid (n_kv_heads, nsplit): workgroup s takes tokens
-//                      [s*TT, s*TT + TT) of one kv head for its hpk query
+//  attn_tile_kernel    grid (8 * ceil(nsplit / 8) * n_kv_heads, sequences):
+//                      one workgroup per (kv head, split) of a sequence takes
+//                      the split's tiles of that kv head for its hpk query
 //                      heads and writes (max, sum, unnormalised output) per
 //                      query head;
-//  attn_combine_kernel grid n_heads: merges the splits.
+//  attn_combine_kernel grid (n_heads, sequences): merges the splits.
 // The softmax is taken per tile and merged exactly (same value as the
 // reference's token-by-token online form, different rounding).
 
@@ -328,15 +333,38 @@ __device__ __forceinline__ void wave_prep_head(float* dst, const float* src, con
 // with tps = ceil(ntiles / nsplit), looping over them with an online softmax
 // (the tile max and sum merged into running ones) while the next tile's rows
 // are already being loaded.
+// Workgroup id -> (kv head, split): dispatch deals workgroups to the 8 XCDs
+// round robin by id, and each XCD has its own L2. A cache row holds every kv
+// head of its token, so the n_kv_heads workgroups of one split are placed on
+// the same XCD (id % 8 = split % 8) and each row's lines come from HBM once.
+__device__ __forceinline__ bool attn_tile_of(int n_kv, int nsplit, int* kvh, int* split) {
+    const int id = blockIdx.x, slot = id >> 3;
+    *kvh = slot % n_kv;
+    *split = (slot / n_kv) * 8 + (id & 7);
+    return *split < nsplit;
+}
+
+// Workgroups of one attention launch: 8 * ceil(nsplit / 8) * n_kv per
+// sequence (the last ones idle when nsplit is not a multiple of 8).
+inline unsigned attn_tile_grid(int n_kv, int nsplit) { return (unsigned)(8 * ((nsplit + 7) / 8) * n_kv); }
+
 template <int KVP, int HDM>  // cache precision; LDS sized for head_dim <= HDM (64 or 128)
-__global__ void __launch_bounds__(kWG) attn_tile_kernel(const AttnArgs a) {
-    constexpr int TT = 8192 / HDM;  // tokens per tile: 128 or 64
+__global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
+    constexpr int TT = 64;  // tokens per tile (LDS 36-67 KB: four or two workgroups per CU)
     __shared__ __attribute__((aligned(16))) float kt[TT][HDM + 4];
     __shared__ __attribute__((aligned(16))) float vt[TT][HDM];
     __shared__ __attribute__((aligned(16))) float qs[4][HDM];
     __shared__ __attribute__((aligned(16))) float sc[4][TT];
     __shared__ __attribute__((aligned(16))) float kcur[HDM], vcur[HDM];
-    const int kvh = blockIdx.x, split = blockIdx.y;
+    int kvh, split;
+    if (!attn_tile_of(a.n_kv_heads, a.nsplit, &kvh, &split)) return;  // workgroup-uniform
+    {
+        const int b = blockIdx.y;  // sequence of a batched launch
+        a.q += b * a.qkv_s; a.k += b * a.qkv_s; a.v += b * a.qkv_s;
+        a.kc += b * a.kv_s; a.vc += b * a.kv_s;
+        a.pos += b;
+        a.part_m += b * a.part_s; a.part_l += b * a.part_s; a.part_acc += b * a.part_s * a.hd;
+    }
     const int hd = a.hd, hpk = a.n_heads / a.n_kv_heads;
     const int pos = *a.pos, T = pos + 1;
     const int ntiles = (T + TT - 1) / TT;
@@ -585,13 +613,19 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(const AttnArgs a) {
 // Merges the nv = ceil(T / TT) splits of query head blockIdx.x:
 // out = sum_s acc_s e^(m_s - M) * (1 / sum_s l_s e^(m_s - M)), the
 // reciprocal multiply of transformer.rs:293-298.
+// blockIdx.y: sequence of a batched launch (partials + b * part_s (m, l) and
+// + b * part_s * hd (acc), out + b * out_s, position posp[b]).
 __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, const float* part_l,
                                                            const float* part_acc, float* out, const int* posp,
-                                                           int nsplit, int tt, int hd) {
+                                                           int nsplit, int tt, int hd, int64_t part_s,
+                                                           int64_t out_s) {
     __shared__ float w[kMaxAttnSplits];
     __shared__ float red[2][kWG / 64];
     __shared__ float part[kWG];
-    const int h = blockIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y;
+    part_m += b * part_s; part_l += b * part_s; part_acc += b * part_s * hd;
+    out += b * out_s;
+    posp += b;
     const int ntiles = (*posp + 1 + tt - 1) / tt;
     const int tps = (ntiles + nsplit - 1) / nsplit;
     const int nv = (ntiles + tps - 1) / tps;  // splits that hold tiles
@@ -722,6 +756,8 @@ struct SeqState {
 // arenas (SeqState pointers of sequence b = arena + b * stride).
 struct SeqStrides {
     size_t x = 0, sc_in = 0, hb = 0, qkv = 0, logits = 0, conv = 0, parts = 0;
+    size_t kv = 0;    // bytes: one sequence's K (or V) cache
+    size_t part = 0;  // attention split partials (m, l) per sequence; acc: part * head_dim
 };
 
 struct Ctrl {  // device control block
@@ -834,22 +870,23 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
                     if ((rc = launch_gemv_ex(ms[i]->type, PRO_RMSNORM, g1, s))) return rc;
                 }
             }
-            for (size_t b = b0; b < b0 + nb; b++) {
-                SeqState& st = m->seqs[b];
+            {
+                // one launch for the nb sequences (blockIdx.y = sequence)
                 AttnArgs a = {};
-                a.q = st.q; a.k = st.k; a.v = st.v;
+                a.q = s0.q; a.k = s0.k; a.v = s0.v;
                 a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
                 a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
                 size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
-                a.kc = st.kc + (size_t)L.cache_idx * layer_bytes;
-                a.vc = st.vc + (size_t)L.cache_idx * layer_bytes;
+                a.kc = s0.kc + (size_t)L.cache_idx * layer_bytes;
+                a.vc = s0.vc + (size_t)L.cache_idx * layer_bytes;
                 a.row_bytes = m->kv_row_bytes;
-                a.pos = &m->ctrl->pos[b];
+                a.pos = &m->ctrl->pos[b0];
                 a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
                 a.nsplit = m->nsplit;
                 a.scale = 1.0f / sqrtf((float)c.head_dim);
-                a.part_m = st.part_m; a.part_l = st.part_l; a.part_acc = st.part_acc;
-                dim3 grid((unsigned)c.n_kv_heads, (unsigned)m->nsplit);
+                a.part_m = s0.part_m; a.part_l = s0.part_l; a.part_acc = s0.part_acc;
+                a.qkv_s = (int64_t)z.qkv; a.kv_s = (int64_t)z.kv; a.part_s = (int64_t)z.part;
+                dim3 grid(attn_tile_grid((int)c.n_kv_heads, m->nsplit), (unsigned)nb);
 #define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
                 if (c.head_dim <= 64) {
                     if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
@@ -861,9 +898,9 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
                     else ATT(MIVI_KV_Q8_0, 128);
                 }
 #undef ATT
-                hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads), dim3(kWG), 0, s, st.part_m,
-                                   st.part_l, st.part_acc, st.attn_out, &m->ctrl->pos[b], m->nsplit,
-                                   attn_tile_tokens(c.head_dim), (int)c.head_dim);
+                hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads, (unsigned)nb), dim3(kWG), 0, s,
+                                   s0.part_m, s0.part_l, s0.part_acc, s0.attn_out, &m->ctrl->pos[b0], m->nsplit,
+                                   attn_tile_tokens(c.head_dim), (int)c.head_dim, (int64_t)z.part, (int64_t)z.x);
             }
             g = {};
             g.seg[0] = {L.wo.w, s0.x, D};
@@ -1255,12 +1292,22 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
             st.part_val = pv + b * z.parts; st.part_idx = pi + b * z.parts;
         }
     }
-    for (auto& st : m->seqs) {
-        if ((rc = m->alloc(&st.part_m, c.n_heads * m->nsplit)) || (rc = m->alloc(&st.part_l, c.n_heads * m->nsplit)) ||
-            (rc = m->alloc(&st.part_acc, c.n_heads * m->nsplit * c.head_dim)) ||
-            (rc = m->alloc(&st.kc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)) ||
-            (rc = m->alloc(&st.vc, c.n_attn_layers * c.max_seq_len * m->kv_row_bytes)))
+    {
+        SeqStrides& z = m->strides;
+        z.kv = c.n_attn_layers * c.max_seq_len * m->kv_row_bytes;
+        z.part = c.n_heads * m->nsplit;
+        const size_t B = max_batch;
+        float *pm, *pl, *pa;
+        uint8_t *kc, *vc;
+        if ((rc = m->alloc(&pm, B * z.part)) || (rc = m->alloc(&pl, B * z.part)) ||
+            (rc = m->alloc(&pa, B * z.part * c.head_dim)) || (rc = m->alloc(&kc, B * z.kv)) ||
+            (rc = m->alloc(&vc, B * z.kv)))
             return fail(rc);
+        for (size_t b = 0; b < B; b++) {
+            SeqState& st = m->seqs[b];
+            st.part_m = pm + b * z.part; st.part_l = pl + b * z.part; st.part_acc = pa + b * z.part * c.head_dim;
+            st.kc = kc + b * z.kv; st.vc = vc + b * z.kv;
+        }
     }
     c.kv_bytes = 2 * max_batch * c.n_attn_layers * c.max_seq_len * m->kv_row_bytes;
     if ((rc = m->alloc(&m->ctrl, 1)) || (rc = m->alloc(&m->history, c.max_seq_len * max_batch))) return fail(rc);
