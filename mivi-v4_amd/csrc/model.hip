@@ -224,8 +224,11 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 
 // Embedding row of token tok (model.rs:355-366): bit-exact dequantization of
 // one row, generic over the stored format.
+// blockIdx.x = b: token tok[b] into x + b * x_stride.
 __global__ void __launch_bounds__(kWG) embed_kernel(int32_t type, const uint8_t* table, size_t row_bytes,
-                                                    const uint32_t* tok, float* x, int dim) {
+                                                    const uint32_t* tok, float* x, int dim, int64_t x_stride) {
+    tok += blockIdx.x;
+    x += blockIdx.x * x_stride;
     const uint8_t* row = table + (size_t)(*tok) * row_bytes;
     for (int i = threadIdx.x; i < dim; i += kWG) {
         float y = 0.f;
@@ -677,11 +680,21 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
 // ShortConv phase of the sequence.
 // With part_idx set, `logits`/`n` are instead the per-wave (max, first row)
 // partials of the head GEMV's argmax epilogue.
+// blockIdx.x = b: sequence seq + b of a batched launch (values and indices
+// + b * vstride; tok, pos, phase + b).
 __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, const int* part_idx, int n,
                                                               uint32_t* tok, int* pos, int* phase, uint32_t* history,
-                                                              const int* step, int stride, int seq, int do_argmax) {
+                                                              const int* step, int stride, int seq, int do_argmax,
+                                                              int64_t vstride) {
     __shared__ float bv[16];
     __shared__ int bi[16];
+    {
+        const int b = blockIdx.x;
+        logits += b * vstride;
+        if (part_idx) part_idx += b * vstride;
+        tok += b; pos += b; phase += b;
+        seq += b;
+    }
     if (do_argmax) {
         float best = -INFINITY;
         int idx = 0x7FFFFFFF;
@@ -825,9 +838,8 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
         size_t bs, ts;
         format_sizes(m->embd.type, &bs, &ts);
         size_t row_bytes = (c.dim * ts) / bs;  // model.rs:358-360
-        for (size_t b = b0; b < b0 + nb; b++)
-            hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kWG), 0, s, m->embd.type, m->embd.w, row_bytes,
-                               &m->ctrl->tok[b], m->seqs[b].x, D);
+        hipLaunchKernelGGL(embed_kernel, dim3((unsigned)nb), dim3(kWG), 0, s, m->embd.type, m->embd.w, row_bytes,
+                           &m->ctrl->tok[b0], s0.x, D, (int64_t)z.x);
     }
     for (size_t l = l0; l < l1 && l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
@@ -966,13 +978,11 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
         }
         if (!parts && (rc = launch_gemv_ex(m->head.type, pro, g, s))) return rc;
     }
-    for (size_t b = b0; b < b0 + nb; b++) {
-        SeqState& st = m->seqs[b];
-        hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, parts ? st.part_val : st.logits,
-                           parts ? st.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b],
-                           &m->ctrl->pos[b], &m->ctrl->phase[b], argmax ? m->history : nullptr, &m->ctrl->step,
-                           (int)c.max_batch, (int)b, (argmax && logits) ? 1 : 0);
-    }
+    hipLaunchKernelGGL(argmax_advance_kernel, dim3((unsigned)nb), dim3(1024), 0, s, parts ? s0.part_val : s0.logits,
+                       parts ? s0.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b0],
+                       &m->ctrl->pos[b0], &m->ctrl->phase[b0], argmax ? m->history : nullptr, &m->ctrl->step,
+                       (int)c.max_batch, (int)b0, (argmax && logits) ? 1 : 0,
+                       (int64_t)(parts ? z.parts : z.logits));
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
 }

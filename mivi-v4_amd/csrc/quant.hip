@@ -928,7 +928,9 @@ __device__ __forceinline__ mivi::GemvArgs gemv_column(const mivi::GemvArgs& a, i
 // with every column's digits (also held in registers), in the same order as
 // the one-column kernel, so every column's result is bit-identical to a
 // one-column launch on that column.
-template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI, bool PACK = false, int NC = 1>
+// XL: the digits stay in LDS and each step reads its units' digits there
+// (for column counts whose digits would not fit in registers).
+template <int FMT, int KT, int LPR, int NU, int PD, int PRO, int EPI, bool PACK = false, int NC = 1, bool XL = false>
 __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArgs a) {
     static_assert(!PACK || FMT == FMT_Q6K, "only Q6_K has a packed layout");
     constexpr int RPW = 64 / LPR;
@@ -997,13 +999,48 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
 
     // this lane's activation digits (and their per-quad offsets / fp32
     // sub-block sums), per column, fixed for the launch
-    uint32_t xd[NC][NU][3][16];
-    int off[NC][NU][4][3];
-    float X[NC][NU][2];
+    constexpr int NCR = XL ? 1 : NC;  // columns held in registers
+    uint32_t xd[NCR][NU][3][16];
+    int off[NCR][NU][4][3];
+    float X[NCR][NU][2];
+    auto fetch_digits = [&](int cc, int i, uint32_t (&d)[3][16], int (&o)[4][3], float (&xs)[2]) {
+        const int u = min(lr + LPR * i, units - 1);
+        const int b = u >> 2;
+        if (FMT == FMT_Q4K) {
+            const int g = u & 3;
+            const int w0 = (b * 256 + g * 64) / 4;
 #pragma unroll
-    for (int cc = 0; cc < NC; cc++)
+            for (int e = 0; e < 3; e++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u32x4 v = *(const u32x4*)(dig[cc] + e * (K / 4) + w0 + 4 * q);
+                    d[e][4 * q] = v.x; d[e][4 * q + 1] = v.y; d[e][4 * q + 2] = v.z; d[e][4 * q + 3] = v.w;
+                }
+            xs[0] = xsum[cc][b * 8 + 2 * g];
+            xs[1] = xsum[cc][b * 8 + 2 * g + 1];
+        } else {
+            const int h = (u >> 1) & 1, j = u & 1;
+            const int e0 = b * 256 + h * 128 + 16 * j;
+#pragma unroll
+            for (int e = 0; e < 3; e++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u32x4 v = *(const u32x4*)(dig[cc] + e * (K / 4) + (e0 + 32 * q) / 4);
+                    d[e][4 * q] = v.x; d[e][4 * q + 1] = v.y; d[e][4 * q + 2] = v.z; d[e][4 * q + 3] = v.w;
+                    int t = 0;
+                    t = sdot4(v.x, 0x01010101u, t);
+                    t = sdot4(v.y, 0x01010101u, t);
+                    t = sdot4(v.z, 0x01010101u, t);
+                    t = sdot4(v.w, 0x01010101u, t);
+                    o[q][e] = -32 * t;
+                }
+        }
+    };
+#pragma unroll
+    for (int cc = 0; cc < NCR; cc++)
 #pragma unroll
     for (int i = 0; i < NU; i++) {
+        if constexpr (XL) break;
         const int u = min(lr + LPR * i, units - 1);
         const int b = u >> 2;
         if (FMT == FMT_Q4K) {
@@ -1076,12 +1113,14 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
 #pragma unroll
             for (int i = 0; i < NU; i++) {
                 if (lr + LPR * i >= units) continue;
+                const int cr = XL ? 0 : cc;
+                if constexpr (XL) fetch_digits(cc, i, xd[0][i], off[0][i], X[0][i]);
                 if constexpr (FMT == FMT_Q4K)
-                    acc += q4k_unit_i8(B[i].hdr, B[i].qa, B[i].qb, (lr + LPR * i) & 3, xd[cc][i], s[cc], X[cc][i][0],
-                                       X[cc][i][1]);
+                    acc += q4k_unit_i8(B[i].hdr, B[i].qa, B[i].qb, (lr + LPR * i) & 3, xd[cr][i], s[cc], X[cr][i][0],
+                                       X[cr][i][1]);
                 else
                     acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, PACK ? packed_q6k_scales(B[i].sc.x) : B[i].sc,
-                                       B[i].d, xd[cc][i], off[cc][i]);
+                                       B[i].d, xd[cr][i], off[cr][i]);
             }
             float sum = group_sum<LPR>(acc);
             if (FMT == FMT_Q6K) sum *= s[cc];
@@ -1258,6 +1297,18 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                 } else {
                     return mivi::set_error(MIVI_ERR_UNSUPPORTED, "batched GEMV epilogue %d with this prologue", ep);
                 }
+            } else if (K == 8192 && ep == mivi::EPI_STORE && !a.packed) {
+                // two units per lane: the columns' digits stay in LDS
+                if constexpr (PRO == mivi::PRO_NONE) {
+                    if (t == MIVI_GGML_Q4_K)
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 8192, 64, 2, 2, PRO, mivi::EPI_STORE, false, 2, true>),
+                                           dim3(grid), dim3(kWG), 0, s, a);
+                    else
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, 8192, 64, 2, 2, PRO, mivi::EPI_STORE, false, 2, true>),
+                                           dim3(grid), dim3(kWG), 0, s, a);
+                } else {
+                    return mivi::set_error(MIVI_ERR_UNSUPPORTED, "batched d=8192 GEMV takes no prologue");
+                }
             } else {
                 return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no batched GEMV for d=%d", K);
             }
@@ -1386,12 +1437,12 @@ int gemv_argmax_parts(int32_t t, int K, int n) {
 }
 
 // Most columns one batched streaming launch takes at depth K, 1 where there
-// is no batched kernel. Its lanes hold every column's digits in registers:
-// two columns at K = 2048 fit in 164-198 VGPRs; at K = 8192 (two units per
-// lane) two columns would spill.
+// is no batched kernel. At K = 2048 its lanes hold every column's digits in
+// registers (two columns fit in 164-198 VGPRs); at K = 8192 (two units per
+// lane) they would spill, so that kernel reads them from LDS each step.
 static int gemv_max_cols(int32_t t, int K) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
-    return K == 2048 ? kMaxGemvCols : 1;
+    return K == 2048 || K == 8192 ? kMaxGemvCols : 1;
 }
 
 // Columns [c0, c0 + nc) of a batched GEMV as one launch's arguments.
