@@ -35,8 +35,9 @@ using namespace mivi;
 namespace {
 
 constexpr int kMfmaMinBatch = 16;
-constexpr int kTm = 128, kTn = 128, kTk = 64;  // output tile and k-tile
-constexpr int kXs = kTk + 8;                   // padded LDS row (halves) of an x tile
+constexpr int kTm = 64, kTn = 128;  // output tile (m = input rows, n = weight rows)
+constexpr int kTk = 64;             // k-tile: one Q4_K group (a sub-block pair)
+constexpr int kXs = kTk + 8;        // padded LDS row (halves) of an x or B tile
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -113,6 +114,16 @@ __device__ __forceinline__ void scale_min_k4(const uint8_t* q, int j, uint32_t& 
     }
 }
 
+// The 6-bit scale of sub-block j (0..7) from a block header held in
+// registers (dwords 1..3 = the 12 scale bytes), get_scale_min_k4 of
+// q4_k_m.rs:11-22 with byte selects by shifts, so j may vary at run time.
+__device__ __forceinline__ uint32_t scale_k4(const u32x4& hdr, int j) {
+    const int sh = 8 * (j & 3);
+    const uint32_t a = (hdr.y >> sh) & 0xFFu;  // q[j & 3]
+    const uint32_t c = (hdr.w >> sh) & 0xFFu;  // q[8 + (j & 3)]
+    return j < 4 ? (a & 63u) : ((c & 0xFu) | ((a >> 6) << 4));
+}
+
 // 8 nibbles (bytes of w0, w1; low or high nibble) times sc, as exact fp16
 __device__ __forceinline__ half8 nib8_times(uint32_t w0, uint32_t w1, bool high, _Float16 sc) {
     uint32_t t0 = high ? (w0 >> 4) & 0x0F0F0F0Fu : w0 & 0x0F0F0F0Fu;
@@ -131,7 +142,19 @@ __device__ __forceinline__ half8 nib8_times(uint32_t w0, uint32_t w1, bool high,
     return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
 }
 
-// grid = (ceil(N / 128), Mp / 128), 256 threads = 2 x 2 waves of 64 x 64.
+// grid = (ceil(N / 128), Mp / 64), 256 threads = 2 x 2 waves of 32 input
+// rows x 64 weight rows (two 32 x 32 MFMA tiles each). Per 64-value k-tile
+// the workgroup stages x (fp16 hi and lo, 16 KB) and builds the fp16 B
+// operand sc*q once into LDS (two threads per weight row, from qs bytes and
+// scales held in registers), so no wave repeats another's conversion. The
+// loop is bound by load latency, not by the matrix cores: each tile's bytes
+// are loaded three tiles ahead into one of three register stages. About
+// 41 KB of LDS: two workgroups (eight waves) per CU.
+struct GemmStage {
+    u32x4 xh[2], xl[2];  // x chunks: rows c/8, chunk c%8 for c = tid, tid + 256
+    u32x4 qs, hdr, ps;    // 16 qs bytes of weight row tid/2; its block header; sub-block sums
+};
+
 __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict__ W, int N, int K,
                                                        const _Float16* __restrict__ xh,
                                                        const _Float16* __restrict__ xl,
@@ -141,9 +164,9 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
                                                        int M) {
     __shared__ __attribute__((aligned(16))) _Float16 Xh[kTm][kXs];
     __shared__ __attribute__((aligned(16))) _Float16 Xl[kTm][kXs];
-    __shared__ __attribute__((aligned(16))) uint8_t Wq[kTn][32];   // qs bytes of the k-tile's group
-    __shared__ __attribute__((aligned(16))) uint8_t Wh[kTn][16];   // d, dmin, scales of the super-block
-    __shared__ __attribute__((aligned(16))) _Float16 Sh[kTm][8];   // sub-block sums of the super-block
+    __shared__ __attribute__((aligned(16))) _Float16 Bt[kTn][kXs];  // sc * q of the k-tile, weight-row major
+    __shared__ __attribute__((aligned(16))) uint8_t Wh[kTn][16];     // d, dmin, scales of the super-block
+    __shared__ __attribute__((aligned(16))) _Float16 Sh[kTm][8];     // sub-block sums of the super-block
     __shared__ __attribute__((aligned(16))) _Float16 Sl[kTm][8];
     const int n0 = blockIdx.x * kTn, m0 = blockIdx.y * kTm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -151,118 +174,88 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
     const int nb = K / 256;
     const size_t rb = (size_t)nb * 144;
     const int li = lane & 31, lh = lane >> 5;
+    // B building: weight row bn = tid / 2 of the tile, qs bytes [16 bc, 16 bc + 16) of the group
+    const int bn = tid >> 1, bc = tid & 1;
+    const uint8_t* brow = W + (size_t)(n0 + bn < N ? n0 + bn : N - 1) * rb;
 
-    // staging assignment: x chunks (8 halves) 8 per thread per plane pair
-    // (rows 0..127 x 8 chunks), one 16-byte qs chunk, one header chunk and
-    // one sub-sum chunk per thread
-    auto wrow = [&](int r) { const int n = n0 + r; return W + (size_t)(n < N ? n : N - 1) * rb; };
-
-    f32x16 acc[2][2], c1[2][2];
+    f32x16 acc[2], c1[2];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            acc[a][b] = f32x16{};
-            c1[a][b] = f32x16{};
-        }
+    for (int nt = 0; nt < 2; nt++) {
+        acc[nt] = f32x16{};
+        c1[nt] = f32x16{};
+    }
 
     const int ntiles = K / kTk;
-    u32x4 px[4], pxl[4], pq, ph, ps;
-    auto load_tile = [&](int t) {
+    auto load_tile = [&](GemmStage& S, int t) {
         const int k0 = t * kTk;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i;  // 0..1023: row c/8, chunk c%8
+        for (int i = 0; i < 2; i++) {
+            const int c = tid + 256 * i;  // 0..511: row c/8, chunk c%8
             const int r = c >> 3, ch = c & 7;
             const size_t o = (size_t)(m0 + r) * K + k0 + 8 * ch;
-            px[i] = *(const u32x4*)(xh + o);
-            pxl[i] = *(const u32x4*)(xl + o);
+            S.xh[i] = *(const u32x4*)(xh + o);
+            S.xl[i] = *(const u32x4*)(xl + o);
         }
         const int b = k0 / 256, g = (k0 % 256) / 64;
-        {
-            const int r = tid >> 1, ch = tid & 1;
-            pq = *(const u32x4*)(wrow(r) + (size_t)b * 144 + 16 + 32 * g + 16 * ch);
-        }
+        S.qs = *(const u32x4*)(brow + (size_t)b * 144 + 16 + 32 * g + 16 * bc);
         if (g == 0) {
-            const int r = tid & 127;
-            ph = *(const u32x4*)(wrow(r) + (size_t)b * 144);
-            const int rr = tid >> 1, half = tid & 1;
-            ps = half ? *(const u32x4*)(sl + (size_t)(m0 + rr) * (K / 32) + 8 * b)
-                      : *(const u32x4*)(sh + (size_t)(m0 + rr) * (K / 32) + 8 * b);
+            S.hdr = *(const u32x4*)(brow + (size_t)b * 144);
+            if (tid < 2 * kTm) {
+                const int rr = tid >> 1, half = tid & 1;
+                S.ps = half ? *(const u32x4*)(sl + (size_t)(m0 + rr) * (K / 32) + 8 * b)
+                            : *(const u32x4*)(sh + (size_t)(m0 + rr) * (K / 32) + 8 * b);
+            }
         }
     };
-    auto store_tile = [&](int t) {
+    u32x4 hdr = {};  // this thread's weight row header of the current super-block
+    auto store_tile = [&](const GemmStage& S, int t) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 2; i++) {
             const int c = tid + 256 * i;
             const int r = c >> 3, ch = c & 7;
-            *(u32x4*)&Xh[r][8 * ch] = px[i];
-            *(u32x4*)&Xl[r][8 * ch] = pxl[i];
+            *(u32x4*)&Xh[r][8 * ch] = S.xh[i];
+            *(u32x4*)&Xl[r][8 * ch] = S.xl[i];
         }
-        *(u32x4*)&Wq[tid >> 1][16 * (tid & 1)] = pq;
-        if (((t * kTk) % 256) == 0) {
-            if (tid < 128) *(u32x4*)&Wh[tid][0] = ph;
-            if (tid & 1) *(u32x4*)&Sl[tid >> 1][0] = ps;
-            else *(u32x4*)&Sh[tid >> 1][0] = ps;
+        const int g = t & 3;
+        if (g == 0) {
+            hdr = S.hdr;
+            if (bc == 0) *(u32x4*)&Wh[bn][0] = S.hdr;
+            if (tid < 2 * kTm) {
+                if (tid & 1) *(u32x4*)&Sl[tid >> 1][0] = S.ps;
+                else *(u32x4*)&Sh[tid >> 1][0] = S.ps;
+            }
         }
+        // values 16bc .. 16bc+15 of sub-blocks 2g (low nibbles) and 2g+1 (high)
+        const _Float16 s0 = (_Float16)(float)scale_k4(hdr, 2 * g), s1 = (_Float16)(float)scale_k4(hdr, 2 * g + 1);
+        *(half8*)&Bt[bn][16 * bc] = nib8_times(S.qs.x, S.qs.y, false, s0);
+        *(half8*)&Bt[bn][16 * bc + 8] = nib8_times(S.qs.z, S.qs.w, false, s0);
+        *(half8*)&Bt[bn][32 + 16 * bc] = nib8_times(S.qs.x, S.qs.y, true, s1);
+        *(half8*)&Bt[bn][32 + 16 * bc + 8] = nib8_times(S.qs.z, S.qs.w, true, s1);
     };
 
-    load_tile(0);
-    for (int t = 0; t < ntiles; t++) {
-        __syncthreads();  // the previous tile's LDS reads are done
-        store_tile(t);
-        __syncthreads();
-        if (t + 1 < ntiles) load_tile(t + 1);
-        const int g = (t % 4);  // group of the super-block (sub-blocks 2g, 2g+1)
-        // this lane's rows (one per n-tile) and their scales for the group
-        _Float16 scv[2][2];
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int r = wn * 64 + nt * 32 + li;
-            uint32_t s0, mm0, s1, mm1;
-            scale_min_k4(&Wh[r][4], 2 * g, s0, mm0);
-            scale_min_k4(&Wh[r][4], 2 * g + 1, s1, mm1);
-            scv[nt][0] = (_Float16)(float)s0;
-            scv[nt][1] = (_Float16)(float)s1;
-        }
+    const int ar = 32 * wm + li;  // this lane's A row (input row of the tile)
+    auto compute = [&](int t) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             // k-step s: values 16s .. 16s+15 of the group; lane half lh holds 8 of them
-            half8 a_h[2], a_l[2], bq[2];
+            const half8 a_h = *(const half8*)&Xh[ar][16 * s + 8 * lh];
+            const half8 a_l = *(const half8*)&Xl[ar][16 * s + 8 * lh];
+            half8 bq[2];
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const int r = wm * 64 + mt * 32 + li;
-                a_h[mt] = *(const half8*)&Xh[r][16 * s + 8 * lh];
-                a_l[mt] = *(const half8*)&Xl[r][16 * s + 8 * lh];
-            }
+            for (int nt = 0; nt < 2; nt++) bq[nt] = *(const half8*)&Bt[64 * wn + 32 * nt + li][16 * s + 8 * lh];
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const int r = wn * 64 + nt * 32 + li;
-                // values 64g + 16s + 8lh + e: s < 2 low nibbles of qs[16s + 8lh + e],
-                // s >= 2 high nibbles of qs[16(s-2) + 8lh + e]
-                const u32x2 w = *(const u32x2*)&Wq[r][16 * (s & 1) + 8 * lh];
-                bq[nt] = nib8_times(w.x, w.y, s >= 2, scv[nt][s >> 1]);
-            }
-            // the four hi products, then the four lo products: no accumulator is
-            // used by two MFMAs in a row
+            for (int nt = 0; nt < 2; nt++) c1[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, bq[nt], c1[nt], 0, 0, 0);
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-                    c1[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h[mt], bq[nt], c1[mt][nt], 0, 0, 0);
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-                    c1[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l[mt], bq[nt], c1[mt][nt], 0, 0, 0);
+            for (int nt = 0; nt < 2; nt++) c1[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, bq[nt], c1[nt], 0, 0, 0);
         }
-        if (g == 3) {
+        if ((t & 3) == 3) {
             // end of super-block: acc += d * C, then the min term
+            // dmin * sum_sub m_sub * X_sub on the same MFMA shape
             float d[2], dm[2];
             half8 bm[2];
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) {
-                const int r = wn * 64 + nt * 32 + li;
+                const int r = 64 * wn + 32 * nt + li;
                 const uint32_t w0 = *(const uint32_t*)&Wh[r][0];
                 d[nt] = half_bits_to_f32(w0);
                 dm[nt] = half_bits_to_f32(w0 >> 16);
@@ -279,41 +272,47 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
                 bm[nt] = v;
             }
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    acc[mt][nt] += d[nt] * c1[mt][nt];
-                    c1[mt][nt] = f32x16{};
-                }
-            half8 s_h[2], s_l[2];
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const int r = wm * 64 + mt * 32 + li;
-                s_h[mt] = lh == 0 ? *(const half8*)&Sh[r][0] : half8{};
-                s_l[mt] = lh == 0 ? *(const half8*)&Sl[r][0] : half8{};
+            for (int nt = 0; nt < 2; nt++) {
+                acc[nt] += d[nt] * c1[nt];
+                c1[nt] = f32x16{};
             }
+            const half8 s_h = lh == 0 ? *(const half8*)&Sh[ar][0] : half8{};
+            const half8 s_l = lh == 0 ? *(const half8*)&Sl[ar][0] : half8{};
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    f32x16 c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_h[mt], bm[nt], f32x16{}, 0, 0, 0);
-                    c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_l[mt], bm[nt], c2, 0, 0, 0);
-                    acc[mt][nt] -= dm[nt] * c2;
-                }
+            for (int nt = 0; nt < 2; nt++) {
+                f32x16 c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_h, bm[nt], f32x16{}, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_l, bm[nt], c2, 0, 0, 0);
+                acc[nt] -= dm[nt] * c2;
+            }
         }
+    };
+    // three register stages with fixed roles (no dynamic indexing)
+    GemmStage S0, S1, S2;
+    auto step = [&](GemmStage& S, int t) {
+        __syncthreads();  // the previous tile's LDS reads are done
+        store_tile(S, t);
+        __syncthreads();
+        if (t + 3 < ntiles) load_tile(S, t + 3);
+        compute(t);
+    };
+    load_tile(S0, 0);
+    if (1 < ntiles) load_tile(S1, 1);
+    if (2 < ntiles) load_tile(S2, 2);
+    for (int t = 0; t < ntiles; t += 3) {
+        step(S0, t);
+        if (t + 1 < ntiles) step(S1, t + 1);
+        if (t + 2 < ntiles) step(S2, t + 2);
     }
     // store: D[i][j] in lane j + 32*((i/4)%2), register 4*(i/8) + i%4
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int nt = 0; nt < 2; nt++) {
+        const int n = n0 + 64 * wn + 32 * nt + li;
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int n = n0 + wn * 64 + nt * 32 + li;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * 64 + mt * 32 + 8 * (r / 4) + 4 * lh + (r % 4);
-                if (m < M && n < N) Y[(size_t)m * N + n] = acc[mt][nt][r] * rowscale[m];
-            }
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4);
+            if (m < M && n < N) Y[(size_t)m * N + n] = acc[nt][r] * rowscale[m];
         }
+    }
 }
 
 }  // namespace

@@ -332,6 +332,56 @@ __device__ __forceinline__ void wave_prep_head(float* dst, const float* src, con
     }
 }
 
+// The current token's K (per-head RMSNorm, RoPE) and V of kv head kvh into
+// the cache in its precision (cache.rs:395-461); kcur/vcur keep the values
+// as stored, which is what attention reads back. One wave.
+template <int KVP>
+__device__ __forceinline__ void attn_store_current(const AttnArgs& a, int kvh, int pos, const float* cs,
+                                                   const float* sn, float* kcur, float* vcur) {
+    const int hd = a.hd, lane = threadIdx.x & 63;
+    const size_t rb = a.row_bytes;
+    wave_prep_head(kcur, a.k + (size_t)kvh * hd, a.k_norm, a.eps, hd, cs, sn);
+    for (int i = lane; i < hd; i += 64) vcur[i] = a.v[(size_t)kvh * hd + i];
+    __builtin_amdgcn_wave_barrier();
+    uint8_t* krow = a.kc + (size_t)pos * rb;
+    uint8_t* vrow = a.vc + (size_t)pos * rb;
+    if constexpr (KVP == MIVI_KV_F32) {
+        for (int i = lane; i < hd; i += 64) {
+            ((float*)krow)[kvh * hd + i] = kcur[i];
+            ((float*)vrow)[kvh * hd + i] = vcur[i];
+        }
+    } else if constexpr (KVP == MIVI_KV_F16) {
+        for (int i = lane; i < hd; i += 64) {
+            const uint32_t kb = f32_to_half_bits(kcur[i]), vb = f32_to_half_bits(vcur[i]);
+            ((uint16_t*)krow)[kvh * hd + i] = (uint16_t)kb;
+            ((uint16_t*)vrow)[kvh * hd + i] = (uint16_t)vb;
+            kcur[i] = half_bits_to_f32(kb);
+            vcur[i] = half_bits_to_f32(vb);
+        }
+    } else {
+        // q8_0.rs:31-58 per 32-value block: lanes 0-31 K, 32-63 V
+        const int nbk = hd / 32;
+        const bool isv = lane >= 32;
+        float* cur = isv ? vcur : kcur;
+        uint8_t* row = isv ? vrow : krow;
+        const int i = lane & 31;
+        for (int bi = 0; bi < nbk; bi++) {
+            const float xv = cur[bi * 32 + i];
+            float am = fabsf(xv);
+#pragma unroll
+            for (int sh = 16; sh >= 1; sh >>= 1) am = fmaxf(am, __shfl_xor(am, sh, 32));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
+            const uint32_t dh = f32_to_half_bits(d);
+            uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
+            blk[2 + i] = (uint8_t)(int8_t)q;
+            if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
+            cur[bi * 32 + i] = q * half_bits_to_f32(dh);
+        }
+    }
+}
+
 // Tiles of TT tokens; split s of nsplit takes tiles [s * tps, s * tps + tps)
 // with tps = ceil(ntiles / nsplit), looping over them with an online softmax
 // (the tile max and sum merged into running ones) while the next tile's rows
@@ -478,49 +528,7 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
     // the owner split, the current K/V
     load_tile(tile0);
     if (wave < hpk) wave_prep_head(qs[wave], a.q + (size_t)(kvh * hpk + wave) * hd, a.q_norm, a.eps, hd, cs, sn);
-    if (owner && wave == 3) {
-        wave_prep_head(kcur, a.k + (size_t)kvh * hd, a.k_norm, a.eps, hd, cs, sn);
-        for (int i = lane; i < hd; i += 64) vcur[i] = a.v[(size_t)kvh * hd + i];
-        __builtin_amdgcn_wave_barrier();
-        uint8_t* krow = a.kc + (size_t)pos * rb;
-        uint8_t* vrow = a.vc + (size_t)pos * rb;
-        // store into the cache (cache.rs:395-461) and keep the stored value
-        if constexpr (KVP == MIVI_KV_F32) {
-            for (int i = lane; i < hd; i += 64) {
-                ((float*)krow)[kvh * hd + i] = kcur[i];
-                ((float*)vrow)[kvh * hd + i] = vcur[i];
-            }
-        } else if constexpr (KVP == MIVI_KV_F16) {
-            for (int i = lane; i < hd; i += 64) {
-                const uint32_t kb = f32_to_half_bits(kcur[i]), vb = f32_to_half_bits(vcur[i]);
-                ((uint16_t*)krow)[kvh * hd + i] = (uint16_t)kb;
-                ((uint16_t*)vrow)[kvh * hd + i] = (uint16_t)vb;
-                kcur[i] = half_bits_to_f32(kb);
-                vcur[i] = half_bits_to_f32(vb);
-            }
-        } else {
-            // q8_0.rs:31-58 per 32-value block: lanes 0-31 K, 32-63 V
-            const int nbk = hd / 32;
-            const bool isv = lane >= 32;
-            float* cur = isv ? vcur : kcur;
-            uint8_t* row = isv ? vrow : krow;
-            const int i = lane & 31;
-            for (int bi = 0; bi < nbk; bi++) {
-                const float xv = cur[bi * 32 + i];
-                float am = fabsf(xv);
-#pragma unroll
-                for (int sh = 16; sh >= 1; sh >>= 1) am = fmaxf(am, __shfl_xor(am, sh, 32));
-                const float d = am / 127.0f;
-                const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                const float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
-                const uint32_t dh = f32_to_half_bits(d);
-                uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
-                blk[2 + i] = (uint8_t)(int8_t)q;
-                if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
-                cur[bi * 32 + i] = q * half_bits_to_f32(dh);
-            }
-        }
-    }
+    if (owner && wave == 3) attn_store_current<KVP>(a, kvh, pos, cs, sn, kcur, vcur);
 
     // running softmax state of query head `wave`: lane holds dims lane, lane + 64
     float m_run = -INFINITY, l_run = 0.f, o0 = 0.f, o1 = 0.f;
