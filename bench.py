@@ -120,12 +120,23 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
     m = hip.Model(img, max_ctx=ctx, kv_precision=hip.KvPrecision.F16)
     rng = __import__("numpy").random.default_rng(11)
     prompt = rng.integers(0, LFM2_1B2["vocab"], prefill + 1)
+    # prompt prefill: token by token once, then chunked (tiles of 512 rows,
+    # PrefillStrategy::Chunked) warmed up and timed; the decode below runs
+    # from the chunked prefill's state
     t1 = time.perf_counter()
     m.prefill(prompt[:-1])
-    log(f"decode: prefill {prefill} tokens in {time.perf_counter() - t1:.1f}s")
+    t_token = time.perf_counter() - t1
     m.generate_greedy([int(prompt[-1])], [prefill], 8)   # warm-up + graph capture (re-prefills below)
     m.reset_context()
+    m.set_prefill_strategy(512)
     m.prefill(prompt[:-1])
+    m.reset_context()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    m.prefill(prompt[:-1])
+    t_chunked = time.perf_counter() - t1
+    log(f"decode: prefill {prefill} tokens in {t_chunked * 1e3:.0f} ms chunked (tiles of 512), "
+        f"{t_token:.2f} s token by token")
     state = m.export_state(prefill) if cpu_budget_s > 0 else None
     torch.cuda.synchronize()
     t2 = time.perf_counter()
@@ -135,6 +146,7 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
     kv_per_tok = 2 * 6 * 512 * 2  # fp16 K+V bytes per cached token (6 attention layers)
     mean_t = prefill + (steps + 1) / 2
     out = dict(tok_s=steps / dt, ms_per_token=1e3 * dt / steps, prefill=prefill, steps=steps,
+               prefill_tok_s=prefill / t_chunked, prefill_tile=512, prefill_token_path_tok_s=prefill / t_token,
                bytes_per_token=wb + kv_per_tok * mean_t, weight_bytes_per_token=wb, kv_precision="f16",
                working_ctx=ctx, first_tokens=[int(v) for v in toks[:8, 0]])
     out["gbs"] = out["bytes_per_token"] * out["tok_s"] / 1e9

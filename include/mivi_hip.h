@@ -197,10 +197,20 @@ int32_t mivi_hip_model_forward(mivi_model* m, size_t seq, uint32_t token, size_t
 int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, const uint32_t* tokens,
                                        const size_t* pos, size_t n_steps, uint32_t* tokens_out);
 
-/* Token-by-token prompt prefill of one sequence (model.rs:499-606 with
- * PrefillStrategy::Token): forward_step(tokens[i], pos0 + i, false). */
+/* Prompt prefill of one sequence (model.rs:499-606): with the default
+ * PrefillStrategy::Token, forward_step(tokens[i], pos0 + i, false) per token;
+ * after mivi_hip_model_set_prefill_tile(m, t > 1), PrefillStrategy::Chunked:
+ * tiles of t tokens through every layer at once (model.rs:676-831,
+ * attention_forward_tile transformer.rs:356-559, ssm_forward_tile
+ * ssm.rs:174-387): row-batch products (matrix cores for Q4_K), K/V and the
+ * ShortConv state left as the token path leaves them. Synchronous. */
 int32_t mivi_hip_model_prefill(mivi_model* m, size_t seq, const uint32_t* tokens, size_t n,
                                size_t pos0);
+
+/* Model::set_prefill_strategy (model.rs:260-266): tile_tokens 0 or 1 =
+ * Token, t > 1 = Chunked { tile_tokens: t } (at most 4096). Tile buffers are
+ * allocated by the first chunked prefill. */
+int32_t mivi_hip_model_set_prefill_tile(mivi_model* m, size_t tile_tokens);
 
 /* State export/import for one sequence (cache.rs:682-914, arena.rs:110-123
  * semantics with raw layouts): K and V are [n_attn_layers, tokens, row] with

@@ -51,6 +51,9 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
 }
 
+// silu(g) = g / (1 + exp(-g)), 0 for g <= -50 (math.rs:76-82)
+__device__ __forceinline__ float silu_f(float g) { return g <= -50.0f ? 0.0f : g / (1.0f + expf(-g)); }
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
     return __uint_as_float((bits & 0xFFFFu) << 16);
 }

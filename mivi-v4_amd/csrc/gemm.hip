@@ -45,42 +45,60 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------- prep
 // grid = Mp rows, 256 threads, K = 8 * 256 * r (thread t owns values
-// [8t, 8t + 8) of each 2048-value stretch). Row m < M: e = exponent with
-// max|x| * 2^-e <= 1; xh/xl = fp16 hi/lo of x * 2^-e; sh/sl = fp16 hi/lo of
-// each 32-value sub-block sum of x * 2^-e (fp32). Rows >= M are zero.
+// [8t, 8t + 8) of each 2048-value stretch). Row m < M is v = pro(X row m)
+// with X row m at X + m * ldx: PRO_NONE v = x; PRO_RMSNORM v = (x * s) * w,
+// s = 1/sqrt(mean(x^2) + eps) (norm.rs:38-72); PRO_SWIGLU v = silu(x) * x2
+// (math.rs:87-95, X2 row m at X2 + m * ldx). Then e = exponent with
+// max|v| * 2^-e <= 1; xh/xl = fp16 hi/lo of v * 2^-e; sh/sl = fp16 hi/lo of
+// each 32-value sub-block sum of v * 2^-e (fp32). Rows >= M are zero.
 typedef _Float16 half8p __attribute__((ext_vector_type(8)));
-__global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ X, int M, int K,
-                                                        _Float16* __restrict__ xh, _Float16* __restrict__ xl,
-                                                        _Float16* __restrict__ sh, _Float16* __restrict__ sl,
-                                                        float* __restrict__ rowscale) {
+__global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ X, const float* __restrict__ X2,
+                                                        const float* __restrict__ norm_w, float eps, int pro,
+                                                        int64_t ldx, int M, int K, _Float16* __restrict__ xh,
+                                                        _Float16* __restrict__ xl, _Float16* __restrict__ sh,
+                                                        _Float16* __restrict__ sl, float* __restrict__ rowscale) {
     __shared__ float red[4];
     const int m = blockIdx.x;
     const bool live = m < M;
-    const float* x = X + (size_t)m * K;
+    const float* x = X + (live ? m : 0) * ldx;
+    const float* x2 = pro == PRO_SWIGLU ? X2 + (live ? m : 0) * ldx : nullptr;
+    auto block_red = [&](float v, bool is_max) {
+        v = is_max ? wave_max(v) : wave_sum(v);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
+    };
+    float scale = 1.0f;
+    if (pro == PRO_RMSNORM) {
+        float ss = 0.f;
+        if (live)
+            for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+#pragma unroll
+                for (int q = 0; q < 8; q++) ss = fmaf(x[i + q], x[i + q], ss);
+        ss = block_red(ss, false);
+        scale = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    auto value = [&](int i) {  // pro(x)[i]
+        if (pro == PRO_RMSNORM) return x[i] * scale * norm_w[i];
+        if (pro == PRO_SWIGLU) return silu_f(x[i]) * x2[i];
+        return x[i];
+    };
     float mx = 0.f;
     if (live)
-        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
-            const f32x4 a = *(const f32x4*)(x + i), b = *(const f32x4*)(x + i + 4);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
-        }
-    mx = wave_max(mx);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+#pragma unroll
+            for (int q = 0; q < 8; q++) mx = fmaxf(mx, fabsf(value(i + q)));
+    mx = block_red(mx, true);
     // 2^-e with max * 2^-e in [1/2, 1); e = 0 for an all-zero row
     int e = 0;
     if (mx > 0.f && mx <= 3.40282347e38f) frexpf(mx, &e);
     const float inv = ldexpf(1.0f, -e);
     if (threadIdx.x == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.f;
     for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-        if (live) {
-            a = *(const f32x4*)(x + i);
-            b = *(const f32x4*)(x + i + 4);
-        }
-        const float v[8] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv,
-                            b.x * inv, b.y * inv, b.z * inv, b.w * inv};  // exact: power-of-two scaling
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = live ? value(i + q) * inv : 0.f;  // exact: power-of-two scaling
         half8p hv, lv;
         float sum = 0.f;
 #pragma unroll
@@ -161,7 +179,7 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
                                                        const _Float16* __restrict__ sh,
                                                        const _Float16* __restrict__ sl,
                                                        const float* __restrict__ rowscale, float* __restrict__ Y,
-                                                       int M) {
+                                                       int M, int64_t ldy, int accumulate) {
     __shared__ __attribute__((aligned(16))) _Float16 Xh[kTm][kXs];
     __shared__ __attribute__((aligned(16))) _Float16 Xl[kTm][kXs];
     __shared__ __attribute__((aligned(16))) _Float16 Bt[kTn][kXs];  // sc * q of the k-tile, weight-row major
@@ -310,7 +328,11 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int m = m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4);
-            if (m < M && n < N) Y[(size_t)m * N + n] = acc[nt][r] * rowscale[m];
+            if (m < M && n < N) {
+                float* y = Y + m * ldy + n;
+                const float v = acc[nt][r] * rowscale[m];
+                *y = accumulate ? *y + v : v;  // one writer per output
+            }
         }
     }
 }
@@ -352,11 +374,12 @@ static GemmWorkspace& gemm_workspace(int dev) {
     return *all[dev];
 }
 
-static int32_t matmul_q4k_mfma(float* out, const uint8_t* w, const float* in, size_t batch, size_t rows,
-                               size_t cols, hipStream_t s) {
-    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || batch > (size_t)INT32_MAX - kTm)
-        return err_overflow();
-    const size_t mp = (batch + kTm - 1) / kTm * kTm, K = cols;
+// Y_s[m * ys + n] (=|+=) sum_k W_s[n, k] * pro(X)[m, k] for the segments s
+// of a (Q4_K, K % 2048 == 0): one activation split, one GEMM per segment.
+static int32_t rows_q4k_mfma(int pro, const GemvArgs& a, hipStream_t s) {
+    const size_t batch = (size_t)a.ncol;
+    if (batch > (size_t)INT32_MAX - kTm) return err_overflow();
+    const size_t mp = (batch + kTm - 1) / kTm * kTm, K = (size_t)a.K;
     const size_t bx = mp * K * 2, bs = mp * (K / 32) * 2, bytes = 2 * bx + 2 * bs + mp * 4 + 256;
     int dev = 0;
     MIVI_HIP_CHECK(hipGetDevice(&dev));
@@ -380,15 +403,28 @@ static int32_t matmul_q4k_mfma(float* out, const uint8_t* w, const float* in, si
     _Float16* sh = (_Float16*)(p + 2 * bx);
     _Float16* sl = (_Float16*)(p + 2 * bx + bs);
     float* rs = (float*)(p + 2 * bx + 2 * bs);
-    hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)mp), dim3(256), 0, s, in, (int)batch, (int)K, xh, xl, sh, sl,
-                       rs);
-    dim3 grid((unsigned)((rows + kTn - 1) / kTn), (unsigned)(mp / kTm));
-    hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(256), 0, s, w, (int)rows, (int)K, xh, xl, sh, sl, rs, out,
-                       (int)batch);
+    hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)mp), dim3(256), 0, s, a.x, a.x2, a.norm_w, a.eps, pro, a.xs,
+                       (int)batch, (int)K, xh, xl, sh, sl, rs);
+    for (int i = 0; i < a.nseg; i++) {
+        const int rows = a.seg[i].n;
+        if (rows == 0) continue;
+        dim3 grid((unsigned)((rows + kTn - 1) / kTn), (unsigned)(mp / kTm));
+        hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(256), 0, s, a.seg[i].W, rows, (int)K, xh, xl, sh, sl, rs,
+                           a.seg[i].y, (int)batch, a.ys, a.accumulate);
+    }
     MIVI_HIP_CHECK(hipGetLastError());
     MIVI_HIP_CHECK(hipEventRecord(ws.done, s));
     return MIVI_OK;
 }
+
+namespace mivi {
+int32_t launch_rows(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
+    if (pro == PRO_CONV || a.epilogue != EPI_STORE)
+        return set_error(MIVI_ERR_UNSUPPORTED, "row products take no conv prologue or fused epilogue");
+    if (t == MIVI_GGML_Q4_K && a.ncol >= kMfmaMinBatch && a.K % 2048 == 0) return rows_q4k_mfma(pro, a, s);
+    return launch_gemv_ex(t, pro, a, s);
+}
+}  // namespace mivi
 
 extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t t, const uint8_t* w,
                                                   size_t w_len, const float* in, size_t in_len, size_t batch,
@@ -403,12 +439,12 @@ extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, in
     if (!out || !w || !in) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
     clear_error();
     hipStream_t s = (hipStream_t)stream;
-    if (t == MIVI_GGML_Q4_K && batch >= (size_t)kMfmaMinBatch && cols % 2048 == 0)
-        return matmul_q4k_mfma(out, w, in, batch, rows, cols, s);
-    // one GEMV over the batch's input rows as columns: the streaming kernel
-    // reads each weight row once per two inputs, with every input's result
-    // bit-identical to its own matvec (lib.rs:404-457); other shapes run one
-    // launch per input row
+    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || batch > (size_t)INT32_MAX - kTm) return err_overflow();
+    // Q4_K with batch >= kMfmaMinBatch and cols % 2048 == 0: the matrix cores;
+    // otherwise one GEMV over the batch's input rows as columns: the streaming
+    // kernel reads each weight row once per two inputs, with every input's
+    // result bit-identical to its own matvec (lib.rs:404-457); other shapes
+    // run one launch per input row
     mivi::GemvArgs a = {};
     a.seg[0] = {w, out, (int)rows};
     a.nseg = 1;
@@ -417,5 +453,5 @@ extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, in
     a.ncol = (int)batch;
     a.xs = (int64_t)cols;
     a.ys = (int64_t)rows;
-    return mivi::launch_gemv_ex(t, mivi::PRO_NONE, a, s);
+    return mivi::launch_rows(t, mivi::PRO_NONE, a, s);
 }

@@ -68,6 +68,14 @@ int gemv_argmax_parts(int32_t ggml_type, int K, int n);
 
 int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
 
+// Row-batch product: the a.ncol activation rows (row m at a.x + m * a.xs,
+// after the prologue) against each segment's weight rows, output row m of
+// segment s at a.seg[s].y + m * a.ys (=|+= with a.accumulate). Q4_K with at
+// least 16 rows and K % 2048 == 0 runs on the matrix cores (fp16 hi/lo
+// activations), anything else as a batched GEMV. No conv prologue, store
+// epilogue only.
+int32_t launch_rows(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
+
 // rows x cols Q6_K (cols 2048/4096/8192) into the packed unit-plane layout
 int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
 

@@ -212,6 +212,7 @@ struct AttnArgs {
     // kc/vc + b*kv_s bytes, pos + b, part_m/part_l + b*part_s,
     // part_acc + b*part_s*hd
     int64_t qkv_s, kv_s, part_s;
+    int keep_cache;        // 1: the current token's K/V are already in the cache (not stored again)
 };
 
 __device__ __forceinline__ float block_sum256(float v, float* red) {
@@ -334,10 +335,11 @@ __device__ __forceinline__ void wave_prep_head(float* dst, const float* src, con
 
 // The current token's K (per-head RMSNorm, RoPE) and V of kv head kvh into
 // the cache in its precision (cache.rs:395-461); kcur/vcur keep the values
-// as stored, which is what attention reads back. One wave.
+// as stored, which is what attention reads back (with write false only those
+// values are formed, the cache is left alone). One wave.
 template <int KVP>
 __device__ __forceinline__ void attn_store_current(const AttnArgs& a, int kvh, int pos, const float* cs,
-                                                   const float* sn, float* kcur, float* vcur) {
+                                                   const float* sn, float* kcur, float* vcur, bool write = true) {
     const int hd = a.hd, lane = threadIdx.x & 63;
     const size_t rb = a.row_bytes;
     wave_prep_head(kcur, a.k + (size_t)kvh * hd, a.k_norm, a.eps, hd, cs, sn);
@@ -346,15 +348,17 @@ __device__ __forceinline__ void attn_store_current(const AttnArgs& a, int kvh, i
     uint8_t* krow = a.kc + (size_t)pos * rb;
     uint8_t* vrow = a.vc + (size_t)pos * rb;
     if constexpr (KVP == MIVI_KV_F32) {
-        for (int i = lane; i < hd; i += 64) {
+        for (int i = lane; i < hd && write; i += 64) {
             ((float*)krow)[kvh * hd + i] = kcur[i];
             ((float*)vrow)[kvh * hd + i] = vcur[i];
         }
     } else if constexpr (KVP == MIVI_KV_F16) {
         for (int i = lane; i < hd; i += 64) {
             const uint32_t kb = f32_to_half_bits(kcur[i]), vb = f32_to_half_bits(vcur[i]);
-            ((uint16_t*)krow)[kvh * hd + i] = (uint16_t)kb;
-            ((uint16_t*)vrow)[kvh * hd + i] = (uint16_t)vb;
+            if (write) {
+                ((uint16_t*)krow)[kvh * hd + i] = (uint16_t)kb;
+                ((uint16_t*)vrow)[kvh * hd + i] = (uint16_t)vb;
+            }
             kcur[i] = half_bits_to_f32(kb);
             vcur[i] = half_bits_to_f32(vb);
         }
@@ -375,8 +379,10 @@ __device__ __forceinline__ void attn_store_current(const AttnArgs& a, int kvh, i
             const float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
             const uint32_t dh = f32_to_half_bits(d);
             uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
-            blk[2 + i] = (uint8_t)(int8_t)q;
-            if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
+            if (write) {
+                blk[2 + i] = (uint8_t)(int8_t)q;
+                if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
+            }
             cur[bi * 32 + i] = q * half_bits_to_f32(dh);
         }
     }
@@ -528,7 +534,7 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
     // the owner split, the current K/V
     load_tile(tile0);
     if (wave < hpk) wave_prep_head(qs[wave], a.q + (size_t)(kvh * hpk + wave) * hd, a.q_norm, a.eps, hd, cs, sn);
-    if (owner && wave == 3) attn_store_current<KVP>(a, kvh, pos, cs, sn, kcur, vcur);
+    if (owner && wave == 3) attn_store_current<KVP>(a, kvh, pos, cs, sn, kcur, vcur, !a.keep_cache);
 
     // running softmax state of query head `wave`: lane holds dims lane, lane + 64
     float m_run = -INFINITY, l_run = 0.f, o0 = 0.f, o1 = 0.f;
@@ -619,6 +625,57 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
         if (lane < hd) a.part_acc[pi * hd + lane] = o0;
         if (HDM > 64 && lane + 64 < hd) a.part_acc[pi * hd + lane + 64] = o1;
     }
+}
+
+// Prefill tile: K/V of tile row blockIdx.x (position pos0 + row, k/v at
+// a.k/a.v + row * qkv_s) for kv head blockIdx.y into the cache, as the decode
+// step stores its current token. One wave per (row, kv head).
+template <int KVP>
+__global__ void __launch_bounds__(64) kv_store_rows_kernel(AttnArgs a, int pos0) {
+    __shared__ __attribute__((aligned(16))) float kcur[kMaxHd], vcur[kMaxHd];
+    const int r = blockIdx.x, kvh = blockIdx.y, pos = pos0 + r;
+    a.k += r * a.qkv_s;
+    a.v += r * a.qkv_s;
+    const float* cs = a.rope_cos + (size_t)pos * (a.hd / 2);
+    const float* sn = a.rope_sin + (size_t)pos * (a.hd / 2);
+    attn_store_current<KVP>(a, kvh, pos, cs, sn, kcur, vcur, true);
+}
+
+// Prefill tile ShortConv (ssm.rs:174-300, kernel size ks <= 8): channel d
+// walks the tile's rows in order, r = 0..rows-1, with the window of the
+// sequence's current state (the phase's buffer, updated in place): bx =
+// B*X, window shift, conv = sum_k w_k s_k, out = C * conv. proj rows are
+// [B | C | X] (3 * dim), out rows dim.
+__global__ void __launch_bounds__(256) conv_rows_kernel(const float* proj, float* out, int rows, int dim, int ks,
+                                                        const float* conv_w, int conv_mode, float* st_a, float* st_b,
+                                                        const int* phase) {
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= dim) return;
+    float* st = ((*phase) & 1 ? st_b : st_a) + (size_t)d * ks;
+    float s[8], w[8];
+    for (int k = 0; k < ks; k++) {
+        s[k] = st[k];
+        w[k] = conv_mode == 0 ? conv_w[(size_t)d * ks + k] : conv_mode == 1 ? conv_w[k] : 1.0f / (float)ks;
+    }
+    for (int r = 0; r < rows; r++) {
+        const float* p = proj + (size_t)r * 3 * dim;
+        const float bx = p[d] * p[2 * dim + d];
+        for (int k = 0; k + 1 < ks; k++) s[k] = s[k + 1];
+        s[ks - 1] = bx;
+        float conv = 0.f;
+        if (ks == 3) {
+            conv = w[0] * s[0] + w[1] * s[1] + w[2] * s[2];  // ssm.rs:250-252
+        } else {
+            for (int k = 0; k < ks; k++) conv += w[k] * s[k];
+        }
+        out[(size_t)r * dim + d] = p[dim + d] * conv;
+    }
+    for (int k = 0; k < ks; k++) st[k] = s[k];
+}
+
+__global__ void iota_kernel(int* dst, int base, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = base + i;
 }
 
 // Merges the nv = ceil(T / TT) splits of query head blockIdx.x:
@@ -809,6 +866,13 @@ struct mivi_model {
     int nsplit = 1;
     hipGraphExec_t graph = nullptr;
     size_t graph_batch = 0;
+    // chunked prefill (PrefillStrategy::Chunked, model.rs:519-536): rows per
+    // tile (0 = token by token) and the tile buffers, allocated on first use
+    size_t prefill_tile = 0, pf_cap = 0;
+    float *pf_x = nullptr, *pf_p1 = nullptr, *pf_p2 = nullptr, *pf_ao = nullptr;
+    float *pf_pm = nullptr, *pf_pl = nullptr, *pf_pa = nullptr;
+    int* pf_pos = nullptr;
+    uint32_t* pf_tok = nullptr;
 
     ~mivi_model() {
         if (graph) hipGraphExecDestroy(graph);
@@ -1003,6 +1067,152 @@ int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStrea
 // sequences: every projection is one GEMV over all the sequences' columns.
 int32_t enqueue_batch_step(mivi_model* m, size_t batch, hipStream_t s) {
     return enqueue_step(m, 0, batch, true, true, s, true, 0, m->info.n_layers, true);
+}
+
+constexpr int kPrefillSplits = 16;  // attention splits per tile row, at most
+
+// Tile buffers for `rows` rows (grow-only).
+int32_t prefill_buffers(mivi_model* m, size_t rows) {
+    if (m->pf_cap >= rows) return MIVI_OK;
+    const mivi_model_info& c = m->info;
+    const size_t D = c.dim, H = c.hidden_dim, KV = c.kv_dim;
+    const size_t p1 = std::max({3 * D, D + 2 * KV, H});
+    const size_t parts = rows * c.n_heads * kPrefillSplits;
+    int32_t rc;
+    if ((rc = m->alloc(&m->pf_x, rows * D)) || (rc = m->alloc(&m->pf_p1, rows * p1)) ||
+        (rc = m->alloc(&m->pf_p2, rows * H)) || (rc = m->alloc(&m->pf_ao, rows * D)) ||
+        (rc = m->alloc(&m->pf_pm, parts)) || (rc = m->alloc(&m->pf_pl, parts)) ||
+        (rc = m->alloc(&m->pf_pa, parts * c.head_dim)) || (rc = m->alloc(&m->pf_pos, rows)) ||
+        (rc = m->alloc(&m->pf_tok, rows)))
+        return rc;
+    m->pf_cap = rows;
+    return MIVI_OK;
+}
+
+// One prefill tile of sequence b: tokens (device) at positions p0 .. p0+rows-1
+// through every layer (model.rs:608-831 with attention_forward_tile and
+// ssm_forward_tile): row-batch products for the projections (matrix cores
+// for Q4_K), the tile's K/V stored before attention, attention per row over
+// the cache, the ShortConv window walked over the rows. Leaves the caches and
+// the conv state as the token-by-token path would; the residual rows are
+// dropped at the end (the next decode step embeds its own token).
+int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hipStream_t s) {
+    const mivi_model_info& c = m->info;
+    SeqState& st = m->seqs[b];
+    const int D = (int)c.dim, H = (int)c.hidden_dim, KV = (int)c.kv_dim, R = (int)rows;
+    const size_t ldq = (size_t)D + 2 * KV;
+    int32_t rc;
+    size_t bs, ts;
+    format_sizes(m->embd.type, &bs, &ts);
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)R), dim3(kWG), 0, s, m->embd.type, m->embd.w,
+                       (c.dim * ts) / bs, m->pf_tok, m->pf_x, D, (int64_t)D);
+    hipLaunchKernelGGL(iota_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, s, m->pf_pos, (int)p0, R);
+    for (size_t l = 0; l < c.n_layers; l++) {
+        const Layer& L = m->layers[l];
+        GemvArgs g = {};
+        if (!L.attn) {
+            if (c.ssm_conv_kernel == 0) continue;  // ssm.rs:60-62
+            g.seg[0] = {L.in_proj.w, m->pf_p1, 3 * D};
+            g.nseg = 1; g.K = D; g.x = m->pf_x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            g.ncol = R; g.xs = D; g.ys = 3 * D;
+            if ((rc = launch_rows(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
+            const size_t ks = c.ssm_conv_kernel;
+            const int mode = (L.conv && L.conv_len >= (size_t)D * ks) ? 0 : (L.conv && L.conv_len >= ks) ? 1 : 2;
+            hipLaunchKernelGGL(conv_rows_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, m->pf_p1,
+                               m->pf_ao, R, D, (int)ks, L.conv, mode, st.conv_a + l * (size_t)D * ks,
+                               st.conv_b + l * (size_t)D * ks, &m->ctrl->phase[b]);
+            g = {};
+            g.seg[0] = {L.out_proj.w, m->pf_x, D};
+            g.nseg = 1; g.K = D; g.x = m->pf_ao; g.accumulate = 1;
+            g.ncol = R; g.xs = D; g.ys = D;
+            if ((rc = launch_rows(L.out_proj.type, PRO_NONE, g, s))) return rc;
+        } else {
+            g.seg[0] = {L.wq.w, m->pf_p1, D};
+            g.seg[1] = {L.wk.w, m->pf_p1 + D, KV};
+            g.seg[2] = {L.wv.w, m->pf_p1 + D + KV, KV};
+            g.nseg = 3; g.K = D; g.x = m->pf_x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
+            g.ncol = R; g.xs = D; g.ys = (int64_t)ldq;
+            if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
+                if ((rc = launch_rows(L.wq.type, PRO_RMSNORM, g, s))) return rc;
+            } else {
+                const Mat* ms[3] = {&L.wq, &L.wk, &L.wv};
+                for (int i = 0; i < 3; i++) {
+                    GemvArgs g1 = g;
+                    g1.seg[0] = g.seg[i];
+                    g1.nseg = 1;
+                    if ((rc = launch_rows(ms[i]->type, PRO_RMSNORM, g1, s))) return rc;
+                }
+            }
+            AttnArgs a = {};
+            a.q = m->pf_p1; a.k = m->pf_p1 + D; a.v = m->pf_p1 + D + KV;
+            a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
+            a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
+            const size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
+            a.kc = st.kc + (size_t)L.cache_idx * layer_bytes;
+            a.vc = st.vc + (size_t)L.cache_idx * layer_bytes;
+            a.row_bytes = m->kv_row_bytes;
+            a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
+            a.scale = 1.0f / sqrtf((float)c.head_dim);
+            a.qkv_s = (int64_t)ldq; a.kv_s = 0;
+            // 1. the tile's K/V rows into the cache
+            dim3 sgrid((unsigned)R, (unsigned)c.n_kv_heads);
+#define KVS(KVP) hipLaunchKernelGGL((kv_store_rows_kernel<KVP>), sgrid, dim3(64), 0, s, a, (int)p0)
+            if (c.kv_precision == MIVI_KV_F32) KVS(MIVI_KV_F32);
+            else if (c.kv_precision == MIVI_KV_F16) KVS(MIVI_KV_F16);
+            else KVS(MIVI_KV_Q8_0);
+#undef KVS
+            // 2. attention of every row over the cache up to its position
+            const size_t tt = (size_t)attn_tile_tokens(c.head_dim);
+            const int nsplit = (int)std::max<size_t>(1, std::min<size_t>(kPrefillSplits, (p0 + rows + 8 * tt - 1) / (8 * tt)));
+            a.pos = m->pf_pos;
+            a.nsplit = nsplit;
+            a.part_m = m->pf_pm; a.part_l = m->pf_pl; a.part_acc = m->pf_pa;
+            a.part_s = (int64_t)c.n_heads * nsplit;
+            a.keep_cache = 1;
+            dim3 grid(attn_tile_grid((int)c.n_kv_heads, nsplit), (unsigned)R);
+#define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
+            if (c.head_dim <= 64) {
+                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
+                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
+                else ATT(MIVI_KV_Q8_0, 64);
+            } else {
+                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
+                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
+                else ATT(MIVI_KV_Q8_0, 128);
+            }
+#undef ATT
+            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads, (unsigned)R), dim3(kWG), 0, s, m->pf_pm,
+                               m->pf_pl, m->pf_pa, m->pf_ao, m->pf_pos, nsplit, (int)tt, (int)c.head_dim,
+                               (int64_t)c.n_heads * nsplit, (int64_t)D);
+            g = {};
+            g.seg[0] = {L.wo.w, m->pf_x, D};
+            g.nseg = 1; g.K = D; g.x = m->pf_ao; g.accumulate = 1;
+            g.ncol = R; g.xs = D; g.ys = D;
+            if ((rc = launch_rows(L.wo.type, PRO_NONE, g, s))) return rc;
+        }
+        // ffn.rs:56-108 on the rows
+        g = {};
+        g.seg[0] = {L.gate.w, m->pf_p1, H};
+        g.seg[1] = {L.up.w, m->pf_p2, H};
+        g.nseg = 2; g.K = D; g.x = m->pf_x; g.norm_w = L.ffn_norm; g.eps = c.rms_norm_eps;
+        g.ncol = R; g.xs = D; g.ys = H;
+        if (L.gate.type == L.up.type) {
+            if ((rc = launch_rows(L.gate.type, PRO_RMSNORM, g, s))) return rc;
+        } else {
+            GemvArgs g1 = g;
+            g1.nseg = 1;
+            if ((rc = launch_rows(L.gate.type, PRO_RMSNORM, g1, s))) return rc;
+            g1.seg[0] = g.seg[1];
+            if ((rc = launch_rows(L.up.type, PRO_RMSNORM, g1, s))) return rc;
+        }
+        g = {};
+        g.seg[0] = {L.down.w, m->pf_x, D};
+        g.nseg = 1; g.K = H; g.x = m->pf_p1; g.x2 = m->pf_p2; g.accumulate = 1;
+        g.ncol = R; g.xs = H; g.ys = D;
+        if ((rc = launch_rows(L.down.type, PRO_SWIGLU, g, s))) return rc;
+    }
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
 }
 
 void host_rope_table(std::vector<float>& cs, std::vector<float>& sn, size_t hd, size_t max_seq, float base,
@@ -1395,11 +1605,33 @@ extern "C" int32_t mivi_hip_model_forward(mivi_model* m, size_t seq, uint32_t to
     return mivi_hip_model_forward_step(m, seq, token, pos, 1, logits);
 }
 
+extern "C" int32_t mivi_hip_model_set_prefill_tile(mivi_model* m, size_t tile_tokens) {
+    if (!m) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null model");
+    if (tile_tokens > 4096) return set_error(MIVI_ERR_INVALID_ARGUMENT, "prefill tile of %zu tokens (at most 4096)", tile_tokens);
+    // ssm.rs:174-300 walks windows of at most 8 taps here
+    m->prefill_tile = m->info.ssm_conv_kernel > 8 ? 0 : tile_tokens;
+    return clear_error();
+}
+
 extern "C" int32_t mivi_hip_model_prefill(mivi_model* m, size_t seq, const uint32_t* tokens, size_t n, size_t pos0) {
     if (!m || seq >= m->info.max_batch || (n && !tokens)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
     for (size_t i = 0; i < n; i++) {
         int32_t rc = check_tok_pos(m, tokens[i], pos0 + i);
         if (rc) return rc;
+    }
+    if (m->prefill_tile > 1 && n > 1) {
+        // chunked: tiles of prefill_tile rows (model.rs:676-831)
+        const size_t tile = std::min(m->prefill_tile, n);
+        int32_t rc = prefill_buffers(m, tile);
+        if (rc) return rc;
+        for (size_t c0 = 0; c0 < n; c0 += tile) {
+            const size_t rows = std::min(tile, n - c0);
+            MIVI_HIP_CHECK(hipMemcpyAsync(m->pf_tok, tokens + c0, rows * 4, hipMemcpyHostToDevice, m->stream));
+            if ((rc = enqueue_prefill_tile(m, seq, pos0 + c0, rows, m->stream))) return rc;
+            // the host token array is read by the copy above before it returns
+            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+        }
+        return clear_error();
     }
     for (size_t i = 0; i < n; i++) {
         int32_t rc = set_ctrl(m, seq, tokens[i], pos0 + i);

@@ -111,11 +111,6 @@ __global__ void __launch_bounds__(kWG) dequant_dense_kernel(const uint8_t* __res
 
 // -------------------------------------------------------------- x staging
 
-__device__ __forceinline__ float silu_f(float g) {
-    // math.rs:76-82
-    return g <= -50.0f ? 0.0f : g / (1.0f + expf(-g));
-}
-
 // Workgroup-wide sum (all threads get the result). `red` holds >= 4 floats.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);

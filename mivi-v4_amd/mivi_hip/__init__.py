@@ -116,6 +116,7 @@ _sig = {
     "mivi_hip_model_forward": ([_P, _S, C.c_uint32, _S, _P], _I),
     "mivi_hip_model_generate_greedy": ([_P, _S, _P, _P, _S, _P], _I),
     "mivi_hip_model_prefill": ([_P, _S, _P, _S, _S], _I),
+    "mivi_hip_model_set_prefill_tile": ([_P, _S], _I),
     "mivi_hip_model_export_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_model_import_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_synth_normal": ([C.c_uint64, C.c_float, C.c_float, _P, _S], None),

@@ -56,6 +56,11 @@ class Model:
         t = np.ascontiguousarray(tokens, np.uint32)
         _check(_lib.mivi_hip_model_prefill(self._h, seq, t.ctypes.data_as(C.c_void_p), t.size, pos0), ModelError)
 
+    def set_prefill_strategy(self, tile_tokens: int = 0):
+        """Model::set_prefill_strategy (model.rs:260-266): 0/1 = Token,
+        t > 1 = Chunked { tile_tokens: t }."""
+        _check(_lib.mivi_hip_model_set_prefill_tile(self._h, tile_tokens), ModelError)
+
     def generate_greedy(self, tokens, pos, n_steps: int) -> np.ndarray:
         """tokens/pos: one entry per sequence. Returns [n_steps, batch] argmax tokens."""
         t = np.ascontiguousarray(np.atleast_1d(tokens), np.uint32)

@@ -119,6 +119,59 @@ def test_batched_full_width_matches_single_sequences(hip):
         assert np.array_equal(out[:, b], one), (b, out[:, b], one)
 
 
+@pytest.mark.parametrize("prec,oprec", [(0, 0), (2, 100), (1, 1)])
+def test_chunked_prefill_matches_token_prefill_and_oracle(hip, oracle, small_img, prec, oprec):
+    # PrefillStrategy::Chunked vs ::Token (model.rs:2110 tile == token): 149
+    # prompt tokens in tiles of 32 (the last one ragged), then the next token's
+    # logits against the token-path model and the oracle, and greedy tokens
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, SMALL["vocab"], 150)
+    mt = hip.Model(small_img, max_ctx=512, kv_precision=prec)
+    mt.prefill(prompt[:-1])
+    mc = hip.Model(small_img, max_ctx=512, kv_precision=prec)
+    mc.set_prefill_strategy(32)
+    mc.prefill(prompt[:-1])
+    o = oracle.Model(small_img, max_ctx=512, kv_precision=oprec)
+    for p, t in enumerate(prompt[:-1]):
+        o.forward(int(t), p)
+    n = len(prompt) - 1
+    lt, lc, lo = mt.forward(int(prompt[-1]), n), mc.forward(int(prompt[-1]), n), o.forward(int(prompt[-1]), n)
+    assert rel_err(lc, lt) <= 1e-3
+    assert rel_err(lc, lo) <= 1e-3
+    tok = int(np.argmax(lo))
+    gt = mt.generate_greedy([tok], [n + 1], 8)[:, 0]
+    gc = mc.generate_greedy([tok], [n + 1], 8)[:, 0]
+    assert np.array_equal(gt, gc)
+    # the caches and the conv state the tiles leave match the token path's
+    kt, vt, ct = mt.export_state(n)
+    kc, vc, cc = mc.export_state(n)
+    assert np.allclose(ct, cc, rtol=1e-3, atol=1e-5)
+    if prec != 1:  # float caches; Q8_0 bytes may differ where a value sits on a rounding boundary
+        dt = np.float32 if prec == 0 else np.float16
+        a, b = kt.view(dt).astype(np.float64), kc.view(dt).astype(np.float64)
+        assert np.max(np.abs(a - b)) <= 1e-3 * np.max(np.abs(a))
+
+
+def test_chunked_prefill_full_width_matrix_cores(hip):
+    # dim 2048: tiles of 64 rows run the projections on the MFMA GEMM (RMSNorm
+    # and SwiGLU in the activation split, residual adds in its store); the
+    # ragged last tile (8 rows) the batched GEMV
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
+                       ctx_len=1024, seed=11)
+    prompt = np.random.default_rng(22).integers(0, 4096, 201)
+    n = len(prompt) - 1
+    mt = hip.Model(img, max_ctx=512)
+    mt.prefill(prompt[:-1])
+    mc = hip.Model(img, max_ctx=512)
+    mc.set_prefill_strategy(64)
+    mc.prefill(prompt[:-1])
+    lt, lc = mt.forward(int(prompt[-1]), n), mc.forward(int(prompt[-1]), n)
+    assert rel_err(lc, lt) <= 1e-3
+    tok = int(np.argmax(lt))
+    assert np.array_equal(mt.generate_greedy([tok], [n + 1], 8)[:, 0], mc.generate_greedy([tok], [n + 1], 8)[:, 0])
+
+
 @pytest.mark.parametrize("prec,oprec", [(0, 0), (1, 1)])
 def test_state_export_import_into_oracle(hip, oracle, small_img, prec, oprec):
     # cache.rs:682-914 / arena.rs:110-123 semantics: GPU-built state injected
