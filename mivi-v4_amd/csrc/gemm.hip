@@ -69,26 +69,46 @@ __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict_
         __syncthreads();
         return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
     };
+    // the 8 values [i, i + 8) of a row as two 16-byte loads
+    auto load8 = [&](const float* p, int i, float (&v)[8]) {
+        const f32x4 a = *(const f32x4*)(p + i), b = *(const f32x4*)(p + i + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    };
     float scale = 1.0f;
     if (pro == PRO_RMSNORM) {
         float ss = 0.f;
         if (live)
-            for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+            for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+                float v[8];
+                load8(x, i, v);
 #pragma unroll
-                for (int q = 0; q < 8; q++) ss = fmaf(x[i + q], x[i + q], ss);
+                for (int q = 0; q < 8; q++) ss = fmaf(v[q], v[q], ss);
+            }
         ss = block_red(ss, false);
         scale = 1.0f / sqrtf(ss / (float)K + eps);
     }
-    auto value = [&](int i) {  // pro(x)[i]
-        if (pro == PRO_RMSNORM) return x[i] * scale * norm_w[i];
-        if (pro == PRO_SWIGLU) return silu_f(x[i]) * x2[i];
-        return x[i];
+    auto values = [&](int i, float (&v)[8]) {  // pro(x)[i .. i + 8)
+        load8(x, i, v);
+        if (pro == PRO_RMSNORM) {
+            float w[8];
+            load8(norm_w, i, w);
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[q] = v[q] * scale * w[q];
+        } else if (pro == PRO_SWIGLU) {
+            float u[8];
+            load8(x2, i, u);
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[q] = silu_f(v[q]) * u[q];
+        }
     };
     float mx = 0.f;
     if (live)
-        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256)
+        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+            float v[8];
+            values(i, v);
 #pragma unroll
-            for (int q = 0; q < 8; q++) mx = fmaxf(mx, fabsf(value(i + q)));
+            for (int q = 0; q < 8; q++) mx = fmaxf(mx, fabsf(v[q]));
+        }
     mx = block_red(mx, true);
     // 2^-e with max * 2^-e in [1/2, 1); e = 0 for an all-zero row
     int e = 0;
@@ -96,9 +116,10 @@ __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict_
     const float inv = ldexpf(1.0f, -e);
     if (threadIdx.x == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.f;
     for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
-        float v[8];
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (live) values(i, v);
 #pragma unroll
-        for (int q = 0; q < 8; q++) v[q] = live ? value(i + q) * inv : 0.f;  // exact: power-of-two scaling
+        for (int q = 0; q < 8; q++) v[q] *= inv;  // exact: power-of-two scaling
         half8p hv, lv;
         float sum = 0.f;
 #pragma unroll
@@ -421,7 +442,10 @@ namespace mivi {
 int32_t launch_rows(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     if (pro == PRO_CONV || a.epilogue != EPI_STORE)
         return set_error(MIVI_ERR_UNSUPPORTED, "row products take no conv prologue or fused epilogue");
-    if (t == MIVI_GGML_Q4_K && a.ncol >= kMfmaMinBatch && a.K % 2048 == 0) return rows_q4k_mfma(pro, a, s);
+    // the activation split reads 16-byte vectors of every row
+    auto a16 = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
+    const bool aligned = a16(a.x) && a16(a.x2) && a16(a.norm_w) && a.xs % 4 == 0;
+    if (t == MIVI_GGML_Q4_K && a.ncol >= kMfmaMinBatch && a.K % 2048 == 0 && aligned) return rows_q4k_mfma(pro, a, s);
     return launch_gemv_ex(t, pro, a, s);
 }
 }  // namespace mivi
