@@ -213,7 +213,28 @@ struct AttnArgs {
     // part_acc + b*part_s*hd
     int64_t qkv_s, kv_s, part_s;
     int keep_cache;        // 1: the current token's K/V are already in the cache (not stored again)
+    int packed;            // 1: Q8_0 caches in 16-token groups (q8g_* layout below)
 };
+
+// Q8_0 caches with head_dim 64 in 16-token groups, the layout the matrix-core
+// attention reads with one aligned 16-byte load per lane: group g (tokens
+// 16g..16g+15) of kv head h sits at (g * n_kv + h) * 1088 bytes and holds,
+// for token t of the group and lane l = t + 16c,
+//   bytes 16l..16l+15   K: quants 8c..8c+7 of block 0, then of block 1
+//                       V: dims 16c..16c+15
+//   bytes 1024 + 4t + 2b  the f16 scale of block b of token t.
+// Same bytes as the reference's rows (cache.rs: 68 per kv head and token),
+// rearranged; state export/import converts at the boundary.
+constexpr int kQ8GroupBytes = 1088;
+__host__ __device__ inline size_t q8g_base(size_t pos, int kvh, int n_kv) {
+    return ((pos / 16) * (size_t)n_kv + kvh) * kQ8GroupBytes;
+}
+__host__ __device__ inline int q8g_k_off(int t, int d) {
+    const int b = d / 32, i = d % 32;
+    return 16 * (t + 16 * (i / 8)) + 8 * b + i % 8;
+}
+__host__ __device__ inline int q8g_v_off(int t, int d) { return 16 * (t + 16 * (d / 16)) + d % 16; }
+__host__ __device__ inline int q8g_d_off(int t, int b) { return 1024 + 4 * t + 2 * b; }
 
 __device__ __forceinline__ float block_sum256(float v, float* red) {
     v = wave_sum(v);
@@ -378,8 +399,13 @@ __device__ __forceinline__ void attn_store_current(const AttnArgs& a, int kvh, i
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             const float q = fminf(fmaxf(roundf(xv * id), -128.0f), 127.0f);
             const uint32_t dh = f32_to_half_bits(d);
-            uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
-            if (write) {
+            if (write && a.packed) {
+                uint8_t* g = (isv ? a.vc : a.kc) + q8g_base((size_t)pos, kvh, a.n_kv_heads);
+                const int t = pos & 15, dd = bi * 32 + i;
+                g[isv ? q8g_v_off(t, dd) : q8g_k_off(t, dd)] = (uint8_t)(int8_t)q;
+                if (i == 0) { g[q8g_d_off(t, bi)] = (uint8_t)dh; g[q8g_d_off(t, bi) + 1] = (uint8_t)(dh >> 8); }
+            } else if (write) {
+                uint8_t* blk = row + (size_t)(kvh * nbk + bi) * 34;
                 blk[2 + i] = (uint8_t)(int8_t)q;
                 if (i == 0) { blk[0] = (uint8_t)dh; blk[1] = (uint8_t)(dh >> 8); }
             }
@@ -627,6 +653,254 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
     }
 }
 
+// ------------------------------------------- Q8_0 attention on the matrix cores
+//
+// Q8_0 caches (q8g_* group layout) with head_dim 64 and at most 4 query heads
+// per kv head. One wave per (kv head, split), a workgroup = 4 kv heads of one
+// split (placed as attn_tile_of places its workgroups). Each wave walks its
+// split's 16-token groups (1088 contiguous bytes of K and of V each, one
+// 16-byte load per lane) with an online softmax of its own; no workgroup
+// barriers.
+//  scores  S[h][t] = q_h . k_t on v_mfma_i32_16x16x32_i8, one instruction per
+//          32-value block: the query of each head as four int8 digit planes,
+//          q = s_h (d0 + d1/254 + d2/254^2) (A rows 4h + p), the
+//          cache's int8 K quants as stored (B operand), the block scales and
+//          plane weights applied to the int32 sums (lane t + 16h, reg p);
+//  values  O[h][d] += p_h(t) dv(t) v(t, d) in f32 on the VALU, lane t + 16c
+//          owning token t and dims 16c..16c+15 for all four heads (the p of
+//          the other heads' lanes by permlane row swaps).
+// The softmax reference point moves only when a group's maximum exceeds it by
+// 2^8 (p <= 256); the lane partials are summed over the 16 token lanes at the
+// end. Tokens of the last group past the position get p = 0 (their bytes are
+// never used).
+constexpr int kQ8GroupTokens = 16;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// sum / max over each row of 16 lanes, result in every lane of the row
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_a2m __attribute__((ext_vector_type(2), aligned(2)));
+typedef __attribute__((address_space(1))) const u32x2_a2m gau32x2_a2;
+typedef __attribute__((address_space(1))) const uint16_t gau16;
+typedef __attribute__((address_space(1))) const uint32_t gau32;
+
+struct Q8Group {
+    u32x4 k;       // B operands: 8 K quants of block 0 (xy) and of block 1 (zw), token lane & 15
+    uint32_t dk;   // its block scales (f16 | f16 << 16)
+    u32x4 v;       // V dims 16c..16c+15 of token lane & 15 (c = lane >> 4)
+    uint32_t dv;   // their block scale (f16)
+};
+
+inline bool attn_q8_mfma_ok(int kv_precision, int hd, int n_heads, int n_kv) {
+    return kv_precision == MIVI_KV_Q8_0 && hd == 64 && n_kv > 0 && n_heads % n_kv == 0 && n_heads / n_kv <= 4;
+}
+
+// x of the four lanes t, t + 16, t + 32, t + 48 (rows 0..3 at the lane's
+// position t) into every lane of that position: one v_permlane16_swap
+// (odd rows of one copy with even rows of the other) gives rows {2r, 2r + 1}
+// of the lane's half, two v_permlane32_swap (upper half of one copy with the
+// lower half of the other) spread each over both halves.
+__device__ __forceinline__ void rows_all(float x, float& r0, float& r1, float& r2, float& r3) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const auto e = __builtin_amdgcn_permlane32_swap(a[0], a[0], false, false);  // a[0]: row 2(c >> 1)
+    const auto o = __builtin_amdgcn_permlane32_swap(a[1], a[1], false, false);  // a[1]: row 2(c >> 1) + 1
+    r0 = __uint_as_float(e[0]); r2 = __uint_as_float(e[1]);
+    r1 = __uint_as_float(o[0]); r3 = __uint_as_float(o[1]);
+}
+
+template <int PD>  // groups in flight per wave
+__global__ void __launch_bounds__(kWG, 4) attn_q8_mfma_kernel(AttnArgs a) {
+    constexpr int HD = 64, G = kQ8GroupTokens;
+    __shared__ __attribute__((aligned(16))) float qs[4][4][HD];   // [wave][head][dim]
+    __shared__ __attribute__((aligned(16))) float cur[4][2][HD];  // owner: current K/V as stored
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    int kvg, split;
+    if (!attn_tile_of((a.n_kv_heads + 3) >> 2, a.nsplit, &kvg, &split)) return;  // workgroup-uniform
+    const int kvh = kvg * 4 + wave;
+    if (kvh >= a.n_kv_heads) return;  // wave-uniform (no workgroup barrier below)
+    {
+        const int b = blockIdx.y;
+        a.q += b * a.qkv_s; a.k += b * a.qkv_s; a.v += b * a.qkv_s;
+        a.kc += b * a.kv_s; a.vc += b * a.kv_s;
+        a.pos += b;
+        a.part_m += b * a.part_s; a.part_l += b * a.part_s; a.part_acc += b * a.part_s * HD;
+    }
+    const int hpk = a.n_heads / a.n_kv_heads;
+    const int pos = *a.pos;
+    const int ng = (pos + G) / G;
+    const int gps = (ng + a.nsplit - 1) / a.nsplit;
+    const int g0 = split * gps, g1 = min(ng, g0 + gps);
+    if (g0 >= g1) return;  // beyond the context
+    const float* cs = a.rope_cos + (size_t)pos * (HD / 2);
+    const float* sn = a.rope_sin + (size_t)pos * (HD / 2);
+
+    // 1. the split holding the current token stores its K/V first (then reads
+    //    it back like any cached token)
+    if (g1 == ng && !a.keep_cache) {
+        attn_store_current<MIVI_KV_Q8_0>(a, kvh, pos, cs, sn, cur[wave][0], cur[wave][1], true);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+
+    // 2. group loads, q8g_* layout: a wave-uniform group address plus fixed
+    //    lane offsets (branch free: past the split's end the last group is re-read)
+    const int t = lane & 15, c = lane >> 4;
+    const size_t gstride = (size_t)a.n_kv_heads * kQ8GroupBytes;
+    const uint8_t* kc = a.kc + (size_t)kvh * kQ8GroupBytes;
+    const uint8_t* vc = a.vc + (size_t)kvh * kQ8GroupBytes;
+    const int o_kv = 16 * lane, o_dk = q8g_d_off(t, 0), o_dv = q8g_d_off(t, c >> 1);
+    auto load = [&](Q8Group& q, int g) {
+        g = min(g, g1 - 1);
+        const uint8_t* kg = kc + (size_t)g * gstride;
+        const uint8_t* vg = vc + (size_t)g * gstride;
+        q.k = *(gau32x4*)(kg + o_kv);
+        q.dk = *(gau32*)(kg + o_dk);
+        q.v = *(gau32x4*)(vg + o_kv);
+        q.dv = *(gau16*)(vg + o_dv);
+    };
+    Q8Group ring[PD];
+#pragma unroll
+    for (int i = 0; i < PD; i++) load(ring[i], g0 + i);
+
+    // 3. query heads (QK-norm, RoPE) and their digit planes: A row 4h + p
+    //    (p < 3; row 4h + 3 zero), lane = row + 16 * (k / 8)
+    for (int h = 0; h < hpk; h++)
+        wave_prep_head(qs[wave][h], a.q + (size_t)(kvh * hpk + h) * HD, a.q_norm, a.eps, HD, cs, sn);
+    __builtin_amdgcn_wave_barrier();
+    float amax[4];
+#pragma unroll
+    for (int h = 0; h < 4; h++) amax[h] = h < hpk ? wave_max(fabsf(qs[wave][h][lane])) : 0.f;
+    long qa[2];
+    {
+        const int qh = t >> 2, qp = t & 3;
+        const float am = qh == 0 ? amax[0] : qh == 1 ? amax[1] : qh == 2 ? amax[2] : amax[3];
+        const float inv = am > 0.f ? 127.0f / am : 0.f;
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float y = qh < hpk && qp < 3 ? qs[wave][qh][32 * b + 8 * c + e] * inv : 0.f;
+                float dg = rintf(y);
+                for (int k = 0; k < qp; k++) {
+                    y = (y - dg) * 254.0f;  // exact: |y - dg| <= 1/2
+                    dg = rintf(y);
+                }
+                w[e >> 2] |= ((uint32_t)(int)dg & 0xFFu) << (8 * (e & 3));
+            }
+            qa[b] = (long)(((uint64_t)w[1] << 32) | w[0]);
+        }
+    }
+    // score of lane (t, h = c) in log2 units: scale * s_h * log2(e) / 254 * sum
+    const float am_c = c == 0 ? amax[0] : c == 1 ? amax[1] : c == 2 ? amax[2] : amax[3];
+    const float qscale = a.scale * (am_c / 127.0f) * (1.4426950408889634f / 254.0f);
+
+    float m_run = -INFINITY, l_run = 0.f;  // head c (lane t + 16c)
+    float acc[4][16];                      // head h, dim 16c + i (lane t + 16c)
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[k][i] = 0.f;
+
+    auto scores = [&](const Q8Group& q, i32x4* s) {
+        const i32x4 z = {0, 0, 0, 0};
+        const long kb0 = (long)(((uint64_t)q.k.y << 32) | q.k.x), kb1 = (long)(((uint64_t)q.k.w << 32) | q.k.z);
+        s[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[0], kb0, z, 0, 0, 0);
+        s[1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[1], kb1, z, 0, 0, 0);
+    };
+    auto step = [&](const Q8Group& q, const i32x4* sa, int g) {
+        // 254 * (d0 + d1/254 + d2/254^2) sums per block: (254 a0 + a1) + a2/254
+        const float u0 = fmaf((float)sa[0].z, 1.0f / 254.0f, (float)(254 * sa[0].x + sa[0].y));
+        const float u1 = fmaf((float)sa[1].z, 1.0f / 254.0f, (float)(254 * sa[1].x + sa[1].y));
+        const bool valid = g * G + t <= pos;  // bytes of tokens past the position may hold anything
+        float s = fmaf(half_bits_to_f32(q.dk >> 16), u1, half_bits_to_f32(q.dk) * u0) * qscale;
+        s = valid ? s : -INFINITY;
+        if (__builtin_amdgcn_ballot_w64(s > m_run + 8.0f)) {  // wave-uniform, rare after the first group
+            const float m_new = fmaxf(m_run, row_max16(s));
+            const float al = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
+            m_run = m_new;
+            l_run *= al;
+            float a0, a1, a2, a3;
+            rows_all(al, a0, a1, a2, a3);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                acc[0][i] *= a0; acc[1][i] *= a1; acc[2][i] *= a2; acc[3][i] *= a3;
+            }
+        }
+        const float p = __builtin_amdgcn_exp2f(s - m_run);  // v_exp_f32 (p <= 256)
+        l_run += p;
+        float p0, p1, p2, p3;  // p of token t for heads 0..3
+        rows_all(p, p0, p1, p2, p3);
+        const float dv = valid ? half_bits_to_f32(q.dv) : 0.f;
+        const float w0 = p0 * dv, w1 = p1 * dv, w2 = p2 * dv, w3 = p3 * dv;
+        const uint32_t vw[4] = {q.v.x, q.v.y, q.v.z, q.v.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float vf = sbyte_f32(vw[i >> 2], i & 3);
+            acc[0][i] = fmaf(w0, vf, acc[0][i]);
+            acc[1][i] = fmaf(w1, vf, acc[1][i]);
+            acc[2][i] = fmaf(w2, vf, acc[2][i]);
+            acc[3][i] = fmaf(w3, vf, acc[3][i]);
+        }
+    };
+
+    // the score products of a group are issued one group ahead
+    i32x4 sa[2];
+    scores(ring[0], sa);
+    for (int base = g0; base < g1; base += PD) {
+#pragma unroll
+        for (int i = 0; i < PD; i++) {
+            if (base + i < g1) {  // wave-uniform
+                const i32x4 cur_s[2] = {sa[0], sa[1]};
+                scores(ring[(i + 1) % PD], sa);
+                step(ring[i], cur_s, base + i);
+            }
+            load(ring[i], base + i + PD);
+        }
+    }
+
+    // 4. sums over the token lanes; lane 16c writes head c's (m, l) and dims
+    //    16c..16c+15 of every head
+    l_run = row_sum16(l_run);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[k][i] = row_sum16(acc[k][i]);
+    if (t == 0) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            if (h >= hpk) break;
+            const size_t pi = (size_t)(kvh * hpk + h) * a.nsplit + split;
+            float* dst = a.part_acc + pi * HD + 16 * c;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *(f32x4*)(dst + i) = f32x4{acc[h][i], acc[h][i + 1], acc[h][i + 2], acc[h][i + 3]};
+        }
+        if (c < hpk) {
+            const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
+            a.part_m[pi] = m_run * 0.69314718055994531f;  // natural-log units for the combine
+            a.part_l[pi] = l_run;
+        }
+    }
+}
+
 // Prefill tile: K/V of tile row blockIdx.x (position pos0 + row, k/v at
 // a.k/a.v + row * qkv_s) for kv head blockIdx.y into the cache, as the decode
 // step stores its current token. One wave per (row, kv head).
@@ -847,6 +1121,34 @@ struct Ctrl {  // device control block
 
 }  // namespace
 
+// Attention of nseq sequences (tile rows) over their caches, then the merge of
+// the splits into out (+ b * out_s).
+void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nseq, float* out, int64_t out_s,
+                       hipStream_t s) {
+    int tt;
+    if (a.packed) {  // Q8_0 group layout (attn_q8_mfma_ok shapes)
+        dim3 grid(attn_tile_grid(((int)c.n_kv_heads + 3) / 4, a.nsplit), nseq);
+        hipLaunchKernelGGL(attn_q8_mfma_kernel<3>, grid, dim3(kWG), 0, s, a);
+        tt = kQ8GroupTokens;
+    } else {
+        dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
+#define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
+        if (c.head_dim <= 64) {
+            if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
+            else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
+            else ATT(MIVI_KV_Q8_0, 64);
+        } else {
+            if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
+            else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
+            else ATT(MIVI_KV_Q8_0, 128);
+        }
+#undef ATT
+        tt = attn_tile_tokens(c.head_dim);
+    }
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads, nseq), dim3(kWG), 0, s, a.part_m, a.part_l,
+                       a.part_acc, out, a.pos, a.nsplit, tt, (int)c.head_dim, a.part_s, out_s);
+}
+
 struct mivi_model {
     mivi_model_info info{};
     hipStream_t stream = nullptr;
@@ -863,6 +1165,8 @@ struct mivi_model {
     Ctrl* ctrl = nullptr;
     uint32_t* history = nullptr;  // [max_seq * max_batch]
     size_t kv_row_bytes = 0;
+    bool kv_packed = false;    // Q8_0 caches in the q8g_* group layout
+    size_t kv_layer_bytes = 0; // one attention layer's K (or V) cache of one sequence
     int nsplit = 1;
     hipGraphExec_t graph = nullptr;
     size_t graph_batch = 0;
@@ -960,31 +1264,17 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
                 a.q = s0.q; a.k = s0.k; a.v = s0.v;
                 a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
                 a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-                size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
-                a.kc = s0.kc + (size_t)L.cache_idx * layer_bytes;
-                a.vc = s0.vc + (size_t)L.cache_idx * layer_bytes;
+                a.kc = s0.kc + (size_t)L.cache_idx * m->kv_layer_bytes;
+                a.vc = s0.vc + (size_t)L.cache_idx * m->kv_layer_bytes;
                 a.row_bytes = m->kv_row_bytes;
+                a.packed = m->kv_packed;
                 a.pos = &m->ctrl->pos[b0];
                 a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
                 a.nsplit = m->nsplit;
                 a.scale = 1.0f / sqrtf((float)c.head_dim);
                 a.part_m = s0.part_m; a.part_l = s0.part_l; a.part_acc = s0.part_acc;
                 a.qkv_s = (int64_t)z.qkv; a.kv_s = (int64_t)z.kv; a.part_s = (int64_t)z.part;
-                dim3 grid(attn_tile_grid((int)c.n_kv_heads, m->nsplit), (unsigned)nb);
-#define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
-                if (c.head_dim <= 64) {
-                    if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
-                    else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
-                    else ATT(MIVI_KV_Q8_0, 64);
-                } else {
-                    if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
-                    else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
-                    else ATT(MIVI_KV_Q8_0, 128);
-                }
-#undef ATT
-                hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads, (unsigned)nb), dim3(kWG), 0, s,
-                                   s0.part_m, s0.part_l, s0.part_acc, s0.attn_out, &m->ctrl->pos[b0], m->nsplit,
-                                   attn_tile_tokens(c.head_dim), (int)c.head_dim, (int64_t)z.part, (int64_t)z.x);
+                enqueue_attention(c, a, (unsigned)nb, s0.attn_out, (int64_t)z.x, s);
             }
             g = {};
             g.seg[0] = {L.wo.w, s0.x, D};
@@ -1147,10 +1437,10 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
             a.q = m->pf_p1; a.k = m->pf_p1 + D; a.v = m->pf_p1 + D + KV;
             a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
             a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin;
-            const size_t layer_bytes = c.max_seq_len * m->kv_row_bytes;
-            a.kc = st.kc + (size_t)L.cache_idx * layer_bytes;
-            a.vc = st.vc + (size_t)L.cache_idx * layer_bytes;
+            a.kc = st.kc + (size_t)L.cache_idx * m->kv_layer_bytes;
+            a.vc = st.vc + (size_t)L.cache_idx * m->kv_layer_bytes;
             a.row_bytes = m->kv_row_bytes;
+            a.packed = m->kv_packed;
             a.n_heads = (int)c.n_heads; a.n_kv_heads = (int)c.n_kv_heads; a.hd = (int)c.head_dim;
             a.scale = 1.0f / sqrtf((float)c.head_dim);
             a.qkv_s = (int64_t)ldq; a.kv_s = 0;
@@ -1169,21 +1459,7 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
             a.part_m = m->pf_pm; a.part_l = m->pf_pl; a.part_acc = m->pf_pa;
             a.part_s = (int64_t)c.n_heads * nsplit;
             a.keep_cache = 1;
-            dim3 grid(attn_tile_grid((int)c.n_kv_heads, nsplit), (unsigned)R);
-#define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
-            if (c.head_dim <= 64) {
-                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 64);
-                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 64);
-                else ATT(MIVI_KV_Q8_0, 64);
-            } else {
-                if (c.kv_precision == MIVI_KV_F32) ATT(MIVI_KV_F32, 128);
-                else if (c.kv_precision == MIVI_KV_F16) ATT(MIVI_KV_F16, 128);
-                else ATT(MIVI_KV_Q8_0, 128);
-            }
-#undef ATT
-            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads, (unsigned)R), dim3(kWG), 0, s, m->pf_pm,
-                               m->pf_pl, m->pf_pa, m->pf_ao, m->pf_pos, nsplit, (int)tt, (int)c.head_dim,
-                               (int64_t)c.n_heads * nsplit, (int64_t)D);
+            enqueue_attention(c, a, (unsigned)R, m->pf_ao, (int64_t)D, s);
             g = {};
             g.seg[0] = {L.wo.w, m->pf_x, D};
             g.nseg = 1; g.K = D; g.x = m->pf_ao; g.accumulate = 1;
@@ -1488,6 +1764,9 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
     // run state, KV caches
     m->kv_row_bytes = kv_precision == MIVI_KV_Q8_0 ? (c.kv_dim / 32) * 34
                     : kv_precision == MIVI_KV_F16 ? c.kv_dim * 2 : c.kv_dim * 4;
+    m->kv_packed = attn_q8_mfma_ok(kv_precision, (int)c.head_dim, (int)c.n_heads, (int)c.n_kv_heads);
+    // the group layout holds whole 16-token groups
+    m->kv_layer_bytes = (m->kv_packed ? (c.max_seq_len + 15) / 16 * 16 : c.max_seq_len) * m->kv_row_bytes;
     // about two workgroups per CU over all kv heads (each split loops over
     // ceil(tiles / nsplit) tiles)
     const size_t tt = (size_t)attn_tile_tokens(c.head_dim);
@@ -1522,7 +1801,7 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
     }
     {
         SeqStrides& z = m->strides;
-        z.kv = c.n_attn_layers * c.max_seq_len * m->kv_row_bytes;
+        z.kv = c.n_attn_layers * m->kv_layer_bytes;
         z.part = c.n_heads * m->nsplit;
         const size_t B = max_batch;
         float *pm, *pl, *pa;
@@ -1537,7 +1816,7 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
             st.kc = kc + b * z.kv; st.vc = vc + b * z.kv;
         }
     }
-    c.kv_bytes = 2 * max_batch * c.n_attn_layers * c.max_seq_len * m->kv_row_bytes;
+    c.kv_bytes = 2 * max_batch * m->strides.kv;
     if ((rc = m->alloc(&m->ctrl, 1)) || (rc = m->alloc(&m->history, c.max_seq_len * max_batch))) return fail(rc);
     if (hipStreamSynchronize(m->stream) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
         return fail(set_error(MIVI_ERR_HIP, "model setup failed"));
@@ -1687,6 +1966,38 @@ extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, c
     return clear_error();
 }
 
+// One layer's Q8_0 cache between the reference's rows (tokens x n_kv x 68
+// bytes: per kv head two blocks of f16 scale + 32 quants) and the q8g_* group
+// layout (whole groups; bytes of tokens past `tokens` left as they are).
+static void q8_rows_to_groups(const uint8_t* rows, size_t tokens, int n_kv, bool is_v, uint8_t* groups) {
+    const size_t rb = (size_t)n_kv * 68;
+    for (size_t p = 0; p < tokens; p++) {
+        const int t = (int)(p % 16);
+        for (int h = 0; h < n_kv; h++) {
+            const uint8_t* src = rows + p * rb + (size_t)h * 68;
+            uint8_t* g = groups + q8g_base(p, h, n_kv);
+            for (int b = 0; b < 2; b++) {
+                memcpy(g + q8g_d_off(t, b), src + 34 * b, 2);
+                for (int i = 0; i < 32; i++) g[is_v ? q8g_v_off(t, 32 * b + i) : q8g_k_off(t, 32 * b + i)] = src[34 * b + 2 + i];
+            }
+        }
+    }
+}
+static void q8_groups_to_rows(const uint8_t* groups, size_t tokens, int n_kv, bool is_v, uint8_t* rows) {
+    const size_t rb = (size_t)n_kv * 68;
+    for (size_t p = 0; p < tokens; p++) {
+        const int t = (int)(p % 16);
+        for (int h = 0; h < n_kv; h++) {
+            uint8_t* dst = rows + p * rb + (size_t)h * 68;
+            const uint8_t* g = groups + q8g_base(p, h, n_kv);
+            for (int b = 0; b < 2; b++) {
+                memcpy(dst + 34 * b, g + q8g_d_off(t, b), 2);
+                for (int i = 0; i < 32; i++) dst[34 * b + 2 + i] = g[is_v ? q8g_v_off(t, 32 * b + i) : q8g_k_off(t, 32 * b + i)];
+            }
+        }
+    }
+}
+
 static int32_t state_sizes(mivi_model* m, size_t seq, size_t tokens, size_t kv_len, size_t conv_len) {
     if (!m || seq >= m->info.max_batch) return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad model or sequence");
     if (tokens > m->info.max_seq_len)
@@ -1705,10 +2016,23 @@ extern "C" int32_t mivi_hip_model_export_state(mivi_model* m, size_t seq, size_t
     if (rc) return rc;
     const mivi_model_info& c = m->info;
     SeqState& st = m->seqs[seq];
-    size_t lb = c.max_seq_len * m->kv_row_bytes, tb = tokens * m->kv_row_bytes;
-    for (size_t l = 0; l < c.n_attn_layers; l++) {
-        MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)k_out + l * tb, st.kc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
-        MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)v_out + l * tb, st.vc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
+    size_t lb = m->kv_layer_bytes, tb = tokens * m->kv_row_bytes;
+    if (m->kv_packed) {  // whole groups to the host, then the reference's rows
+        const int nkv = (int)c.n_kv_heads;
+        const size_t gb = (tokens + 15) / 16 * 16 * m->kv_row_bytes;
+        std::vector<uint8_t> kg(gb), vg(gb);
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            MIVI_HIP_CHECK(hipMemcpyAsync(kg.data(), st.kc + l * lb, gb, hipMemcpyDeviceToHost, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync(vg.data(), st.vc + l * lb, gb, hipMemcpyDeviceToHost, m->stream));
+            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+            q8_groups_to_rows(kg.data(), tokens, nkv, false, (uint8_t*)k_out + l * tb);
+            q8_groups_to_rows(vg.data(), tokens, nkv, true, (uint8_t*)v_out + l * tb);
+        }
+    } else {
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)k_out + l * tb, st.kc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)v_out + l * tb, st.vc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
+        }
     }
     Ctrl ctl;
     MIVI_HIP_CHECK(hipMemcpyAsync(&ctl, m->ctrl, sizeof(Ctrl), hipMemcpyDeviceToHost, m->stream));
@@ -1726,10 +2050,23 @@ extern "C" int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t
     if (rc) return rc;
     const mivi_model_info& c = m->info;
     SeqState& st = m->seqs[seq];
-    size_t lb = c.max_seq_len * m->kv_row_bytes, tb = tokens * m->kv_row_bytes;
-    for (size_t l = 0; l < c.n_attn_layers; l++) {
-        MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb, (const uint8_t*)k_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
-        MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb, (const uint8_t*)v_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
+    size_t lb = m->kv_layer_bytes, tb = tokens * m->kv_row_bytes;
+    if (m->kv_packed) {  // the reference's rows into whole groups on the host, then to the device
+        const int nkv = (int)c.n_kv_heads;
+        const size_t gb = (tokens + 15) / 16 * 16 * m->kv_row_bytes;
+        std::vector<uint8_t> kg(gb, 0), vg(gb, 0);
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));  // the previous layer's copies have read kg/vg
+            q8_rows_to_groups((const uint8_t*)k_in + l * tb, tokens, nkv, false, kg.data());
+            q8_rows_to_groups((const uint8_t*)v_in + l * tb, tokens, nkv, true, vg.data());
+            MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb, kg.data(), gb, hipMemcpyHostToDevice, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb, vg.data(), gb, hipMemcpyHostToDevice, m->stream));
+        }
+    } else {
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb, (const uint8_t*)k_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb, (const uint8_t*)v_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
+        }
     }
     size_t cl = c.n_layers * c.dim * std::max<size_t>(1, c.ssm_conv_kernel);
     // the imported state becomes phase 0's input buffer

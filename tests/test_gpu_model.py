@@ -255,3 +255,46 @@ def test_long_context_q8_kv_matches_oracle(hip, oracle):
         lo = o.forward(tok, T + i)
         assert rel_err(lg, lo) <= 1e-3
         tok = int(np.argmax(lo))
+
+
+def test_full_width_q8_kv_matrix_core_attention_matches_oracle(hip, oracle):
+    # 32 query heads over 8 kv heads (four per kv head: every row of the int8
+    # score tile in use), Q8_0 caches of 2777 and 1000 tokens (ragged 16-token
+    # groups, several splits), two sequences in one batched launch; logits of
+    # each sequence against its own oracle run, then batched greedy tokens
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=2048, hidden=8192, n_layers=2, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
+                       ctx_len=4096, seed=31)
+    lens = [2777, 1000]
+    m = hip.Model(img, max_ctx=4096, kv_precision=1, max_batch=2)
+    L, kvd, row = m.info.n_attn_layers, m.info.kv_dim, m.kv_row_bytes()
+    orc = []
+    for b, T in enumerate(lens):
+        k = hip.synth_random_weights(hip.GgmlType.Q8_0, 80 + 2 * b, L * T, kvd, 1.0)
+        v = hip.synth_random_weights(hip.GgmlType.Q8_0, 81 + 2 * b, L * T, kvd, 1.0)
+        conv = hip.synth_normal(90 + b, m.conv_len(), std=0.1)
+        m.import_state(T, k, v, conv, seq=b)
+        k2, v2, _ = m.export_state(T, seq=b)  # group layout on the device, the reference's rows outside
+        assert np.array_equal(k2, k) and np.array_equal(v2, v)
+        o = oracle.Model(img, max_ctx=4096, kv_precision=1)
+        ok, ov = o.kv_views()
+        per = ok.size // L
+        for l in range(L):
+            ok[l * per: l * per + T * row] = k[l * T * row:(l + 1) * T * row]
+            ov[l * per: l * per + T * row] = v[l * T * row:(l + 1) * T * row]
+        o.conv_view()[:] = conv
+        orc.append(o)
+    toks = [101, 2020]
+    for b, T in enumerate(lens):
+        lg = m.forward(toks[b], T, seq=b)
+        lo = orc[b].forward(toks[b], T)
+        assert rel_err(lg, lo) <= 1e-3, (b, rel_err(lg, lo))
+        toks[b] = int(np.argmax(lo))
+    n = 4
+    got = m.generate_greedy(toks, [T + 1 for T in lens], n)
+    for b, T in enumerate(lens):
+        tok, want = toks[b], []
+        for i in range(n):
+            tok = oracle.argmax(orc[b].forward(tok, T + 1 + i))
+            want.append(tok)
+        assert list(got[:, b]) == want, (b, list(got[:, b]), want)
