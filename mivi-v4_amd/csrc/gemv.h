@@ -63,8 +63,16 @@ enum GemvEpilogue : int {
 };
 
 // Number of per-wave argmax partials an EPI_ARGMAX launch of this shape
-// writes (0 when the shape cannot take the epilogue).
-int gemv_argmax_parts(int32_t ggml_type, int K, int n);
+// writes (0 when the shape cannot take the epilogue); packed: the rows are in
+// the layout of launch_pack_q6k.
+int gemv_argmax_parts(int32_t ggml_type, int K, int n, bool packed = false);
+
+// Packed Q6_K matrices of K = 2048 columns and a multiple of 4 rows use the
+// row-quad layout (matrix-core GEMV); other packed shapes the unit-plane one.
+inline bool quad_layout(size_t rows, size_t cols) { return cols == 2048 && rows % 4 == 0; }
+
+// Workgroups of a row-quad GEMV over n rows.
+int quad_grid(int n);
 
 int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
 
@@ -76,7 +84,8 @@ int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipSt
 // epilogue only.
 int32_t launch_rows(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
 
-// rows x cols Q6_K (cols 2048/4096/8192) into the packed unit-plane layout
+// rows x cols Q6_K (cols 2048/4096/8192) into the packed layout: row quads
+// when quad_layout(rows, cols), unit planes otherwise
 int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
 
 }  // namespace mivi

@@ -1327,7 +1327,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
         g.packed = m->head_packed ? 1 : 0;
         g.ncol = ncol; g.xs = z.x; g.ys = z.logits;
         const int pro = m->out_norm ? PRO_RMSNORM : PRO_NONE;
-        const int np = argmax ? gemv_argmax_parts(m->head.type, D, (int)c.vocab_size) : 0;
+        const int np = argmax ? gemv_argmax_parts(m->head.type, D, (int)c.vocab_size, m->head_packed != nullptr) : 0;
         if (np > 0 && np <= kMaxArgmaxParts) {
             g.epilogue = EPI_ARGMAX;
             g.part_val = s0.part_val;

@@ -1155,6 +1155,266 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
+// ------------------------------------------ Q6_K row quads on the matrix cores
+//
+// Packed Q6_K matrices with K = 2048 and a multiple of 4 rows
+// (mivi_hip_pack_weights) are stored as row quads: quad Q (rows 4Q .. 4Q+3)
+// is 6720 contiguous bytes laid out for the 64 lanes l = 4b + j of one wave
+// (j = row of the quad, b = 0..15). Lane (b, j) owns units b and b + 16 of row
+// j, the units a lane of the unit-plane kernel owns at 16 lanes per row (unit
+// u: superblock u/4, half (u/2)&1, values 16(u&1) .. +16 of each quarter
+// q = 0..3 of the half, q6_k.rs:8-43). Slot g = 4i + q is quarter q of the
+// lane's unit i: sixteen 6-bit codes c_0..c_15 with scale sc[8h + (u&1) + 2q].
+//   [0, 6144)     codes, 16 B per lane at 1024 k + 16 l (k = 0..5). Slot g is
+//                 dwords 3g .. 3g+2 of the lane's 24: byte e of dword 3g+m
+//                 holds c_{4m+e} in bits 0-5 and bits 2m, 2m+1 of c_{12+e} in
+//                 bits 6-7, so the four dwords of codes unpack in 9 operations.
+//   [6144, 6656)  8 B per lane at 6144 + 8 l: the scale of slot g in byte g
+//   [6656, 6720)  4 B per (row j, superblock s < 4) at 6656 + 4 (4 j + s): the
+//                 fp16 d of superblock s, then of superblock s + 4
+// Every wave load of codes reads 1 KB of contiguous bytes, and a quad is
+// 4 x 1680 bytes, so a packed matrix keeps the GGUF matrix's size.
+//
+// The products run on v_mfma_i32_4x4x4_16b_i8 (16 independent 4 x 4 x 4
+// blocks; block b is lanes 4b .. 4b+3): lane 4b+v supplies row v of A, the
+// digit plane v of x (v = 0..2; zeros for v = 3) at the block's four k, and
+// lane 4b+j supplies column j of B, four codes of row j, so lane 4b+j
+// receives D[v] = sum over k of digit_v * code for its own row. Four
+// instructions cover a slot; the chain starts from T = -32 * (sum of the
+// slot's digits of plane v), the Q6_K offset. The integer sums are those of
+// the sdot4 kernel, the per-unit float steps and the cross-lane reduction run
+// in the same order, so the result equals the unit-plane kernel's bit for bit.
+
+constexpr int kQuadBytes = 6720;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4 mfma4x4(uint32_t a, uint32_t b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 ldg16_nt(const uint8_t* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+
+// the 6-bit code of value 128h + 32q + l of the Q6_K superblock at blk (q6_k.rs:8-43, before the -32)
+__device__ __forceinline__ uint32_t q6_code(const uint8_t* blk, int h, int q, int l) {
+    const uint8_t* ql = blk + 64 * h;
+    const uint8_t* qh = blk + 128 + 32 * h;
+    uint32_t lo = (q & 1) ? ql[l + 32] : ql[l];
+    lo = (q & 2) ? (lo >> 4) : (lo & 0xFu);
+    return lo | (((uint32_t)(qh[l] >> (2 * q)) & 3u) << 4);
+}
+
+// NC columns (sequences) against the same quads, as the stream kernel's
+// batched columns; PD row quads in flight per wave.
+template <int PRO, int EPI, int NC, int PD>
+__global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs a) {
+    constexpr int K = 2048;
+    __shared__ __attribute__((aligned(16))) uint32_t dig[NC][3 * K / 4];
+    __shared__ i32x4 tl[NC > 1 ? NC : 1][8][16];  // NC > 1: offset tuples per column, slot, block
+    const int nquads = a.seg[0].n / 4;
+    const uint8_t* W = a.seg[0].W;
+    const int ncol = NC == 1 ? 1 : a.ncol;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = lane >> 2, jv = lane & 3;
+    const int nw = gridDim.x * (kWG / 64), wid = blockIdx.x * (kWG / 64) + wave;
+    const int cnt = wid < nquads ? (nquads - wid + nw - 1) / nw : 0;  // wave-uniform
+
+    u32x4 w[PD][6];
+    u32x2 scw[PD];
+    uint32_t dw[PD];
+    // quad of step st (steps past the end re-read the wave's last quad and
+    // waves without quads read quad 0; nothing is stored for them)
+    auto load = [&](int p, int st) {
+        st = st < cnt ? st : cnt - 1;
+        int q = wid + st * nw;
+        q = q < 0 ? 0 : q < nquads ? q : nquads - 1;
+        const uint8_t* base = W + (size_t)q * kQuadBytes;
+#pragma unroll
+        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(base + 1024 * k + 16 * lane);
+        scw[p] = *(const __attribute__((address_space(1))) u32x2*)(base + 6144 + 8 * lane);
+        dw[p] = *(const __attribute__((address_space(1))) uint32_t*)(base + 6656 + 4 * (4 * jv + (b >> 2)));
+    };
+    // activation loads, then the first PD quads, then the activation math
+    StageIn<PRO, K / kWG> in[NC > 1 ? 2 : 1];
+    float s[NC];
+    in[0].load(NC == 1 ? a : gemv_column(a, 0));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PD; p++) load(p, p);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NC == 1) {
+        s[0] = in[0].template finish<false>(a, dig[0], nullptr);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            if (c + 1 < ncol) in[(c + 1) & 1].load(gemv_column(a, c + 1));
+            if (c < ncol) s[c] = in[c & 1].template finish<false>(gemv_column(a, c), dig[c], nullptr);
+            else s[c] = 0.0f;
+        }
+    }
+    // A operands: plane jv of the digits at the slot's k (lanes jv = 3: zeros)
+    uint32_t A[NC][32];
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int u = b + 16 * (g >> 2), q = g & 3;
+            const int base = 64 * (u >> 2) + 32 * ((u >> 1) & 1) + 8 * q + 4 * (u & 1);
+            u32x4 t = *(const u32x4*)(dig[c] + (jv < 3 ? jv : 0) * (K / 4) + base);
+            if (jv == 3) t = u32x4{0, 0, 0, 0};
+            A[c][4 * g] = t.x; A[c][4 * g + 1] = t.y; A[c][4 * g + 2] = t.z; A[c][4 * g + 3] = t.w;
+        }
+    // offset tuples T[g] = -32 * (sum of the slot's 16 digits of plane v), by
+    // the same instruction against codes of -32 (0xE0)
+    i32x4 T[NC == 1 ? 8 : 1];
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            i32x4 t = {0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < 4; m++) t = mfma4x4(A[c][4 * g + m], 0xE0E0E0E0u, t);
+            if constexpr (NC == 1) T[g] = t;
+            else if (wave == 0 && jv == 0) tl[c][g][b] = t;
+        }
+    if constexpr (NC > 1) __syncthreads();
+
+    float best[NC];
+    int bidx[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) { best[c] = -INFINITY; bidx[c] = 0x7FFFFFFF; }
+    auto write_part = [&]() {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            if (c >= ncol) break;
+            // rows of the wave's steps sit in lanes 0..3; others carry (-inf, INT_MAX)
+            float bv = best[c];
+            int bi = bidx[c];
+#pragma unroll
+            for (int o = 1; o < 4; o <<= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) {
+                a.part_val[c * a.ps + wid] = bv;
+                a.part_idx[c * a.ps + wid] = bi;
+            }
+        }
+    };
+    if (cnt == 0) {  // wave-uniform; no barrier follows
+        if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+        return;
+    }
+
+    auto compute = [&](int p, int st) {
+        int acc[NC][2][3];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int D0 = 3 * g;
+            const uint32_t W0 = w[p][D0 >> 2][D0 & 3];
+            const uint32_t W1 = w[p][(D0 + 1) >> 2][(D0 + 1) & 3];
+            const uint32_t W2 = w[p][(D0 + 2) >> 2][(D0 + 2) & 3];
+            const uint32_t B0 = W0 & 0x3F3F3F3Fu, B1 = W1 & 0x3F3F3F3Fu, B2 = W2 & 0x3F3F3F3Fu;
+            const uint32_t B3 = ((W0 >> 6) & 0x03030303u) | ((W1 >> 4) & 0x0C0C0C0Cu) | ((W2 >> 2) & 0x30303030u);
+            const int scv = __builtin_amdgcn_sbfe((int)(g < 4 ? scw[p].x : scw[p].y), 8 * (g & 3), 8);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                if (c >= ncol) break;
+                i32x4 D;
+                if constexpr (NC == 1) D = T[g];
+                else D = tl[c][g][b];
+                D = mfma4x4(A[c][4 * g], B0, D);
+                D = mfma4x4(A[c][4 * g + 1], B1, D);
+                D = mfma4x4(A[c][4 * g + 2], B2, D);
+                D = mfma4x4(A[c][4 * g + 3], B3, D);
+                // |D| < 2^18, |A| < 2^26: exact 24-bit multiplies (as q6k_unit_i8)
+                const int i = g >> 2;
+                if ((g & 3) == 0) {
+                    acc[c][i][0] = mul24(D[0], scv);
+                    acc[c][i][1] = mul24(D[1], scv);
+                    acc[c][i][2] = mul24(D[2], scv);
+                } else {
+                    acc[c][i][0] += mul24(D[0], scv);
+                    acc[c][i][1] += mul24(D[1], scv);
+                    acc[c][i][2] += mul24(D[2], scv);
+                }
+            }
+        }
+        const int r = 4 * (wid + st * nw) + jv;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            if (c >= ncol) break;
+            // per unit d * s-less value, units b then b + 16, as the unit-plane kernel sums them
+            float v = 0.f;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const float f = fmaf((float)acc[c][i][2], kDig2, fmaf((float)acc[c][i][1], kDig1, (float)acc[c][i][0]));
+                v += half_bits_to_f32(i ? dw[p] >> 16 : dw[p]) * f;
+            }
+            // sum over the row's 16 lanes (b), in group_sum<16>'s order
+            v += __shfl_xor(v, 32, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 4, 64);
+            v *= s[c];
+            if (lane < 4) {
+                gfloat* y = (gfloat*)(a.seg[0].y + r + c * a.ys);
+                if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(y, v);
+                else *y = v;
+                // sampler.rs:305-316: strictly greater wins, so NaN never does
+                if constexpr (EPI == mivi::EPI_ARGMAX)
+                    if (v > best[c]) { best[c] = v; bidx[c] = r; }
+            }
+        }
+    };
+    int st = 0;
+    for (; st + PD <= cnt; st += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, st + p);
+            load(p, st + p + PD);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < PD; p++)
+        if (st + p < cnt) compute(p, st + p);
+    if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+}
+
+// One thread per (quad, lane): writes the lane's codes, scales and (lanes
+// with b % 4 == 0) the d pair of its row.
+__global__ void __launch_bounds__(kWG) pack_q6k_quad_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                            size_t nquads) {
+    const size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= nquads * 64) return;
+    const size_t Q = i >> 6;
+    const int l = (int)(i & 63), b = l >> 2, j = l & 3;
+    const uint8_t* row = src + (4 * Q + j) * 1680;
+    uint8_t* o = dst + Q * kQuadBytes;
+    for (int g = 0; g < 8; g++) {
+        const int u = b + 16 * (g >> 2), q = g & 3, h = (u >> 1) & 1, jj = u & 1;
+        const uint8_t* blk = row + (u >> 2) * 210;
+        uint32_t c[16];
+        for (int e = 0; e < 16; e++) c[e] = q6_code(blk, h, q, 16 * jj + e);
+        for (int m = 0; m < 3; m++) {
+            uint32_t word = 0;
+            for (int e = 0; e < 4; e++) word |= (c[4 * m + e] | (((c[12 + e] >> (2 * m)) & 3u) << 6)) << (8 * e);
+            const int D = 3 * g + m;
+            *(uint32_t*)(o + 1024 * (D >> 2) + 16 * l + 4 * (D & 3)) = word;
+        }
+        o[6144 + 8 * l + g] = blk[192 + 8 * h + jj + 2 * q];
+    }
+    if ((b & 3) == 0) {
+        const int s = b >> 2;
+        uint8_t* dp = o + 6656 + 4 * (4 * j + s);
+        dp[0] = row[s * 210 + 208];
+        dp[1] = row[s * 210 + 209];
+        dp[2] = row[(s + 4) * 210 + 208];
+        dp[3] = row[(s + 4) * 210 + 209];
+    }
+}
+
 // ------------------------------------------------------- Q8_0 quantize/dot
 
 // q8_0.rs:31-58, one wave per two blocks (32 lanes per block).
@@ -1250,6 +1510,25 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
         // 2 workgroups per CU measured best for the head GEMV (24.7 us vs 26.2 at 3)
         static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
         const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
+        if (a.packed && mivi::quad_layout(n, K)) {
+            // packed Q6_K row quads on the matrix cores (one segment: the quads span the matrix)
+            if (t != MIVI_GGML_Q6_K || a.nseg != 1 || a.epilogue == mivi::EPI_SWIGLU)
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed row quads take one Q6_K segment, store or argmax");
+            if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
+                const int qgrid = mivi::quad_grid(n);
+#define LQ(EPI, NC, PD) hipLaunchKernelGGL((gemv_q6k_quad_kernel<PRO, EPI, NC, PD>), dim3(qgrid), dim3(kWG), 0, s, a)
+                if (a.epilogue == mivi::EPI_ARGMAX) {
+                    if (a.ncol > 1) LQ(mivi::EPI_ARGMAX, 2, 2); else LQ(mivi::EPI_ARGMAX, 1, 3);
+                } else {
+                    if (a.ncol > 1) LQ(mivi::EPI_STORE, 2, 2); else LQ(mivi::EPI_STORE, 1, 3);
+                }
+#undef LQ
+                MIVI_HIP_CHECK(hipGetLastError());
+                return MIVI_OK;
+            } else {
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows take no conv or SwiGLU prologue");
+            }
+        }
 #define LSE(FMT, KT, LPR, NU, PD, EPI) \
     hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO, EPI>), dim3(grid), dim3(kWG), 0, s, a)
 #define LS(FMT, KT, LPR, NU, PD) LSE(FMT, KT, LPR, NU, PD, mivi::EPI_STORE)
@@ -1424,8 +1703,14 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
 
 namespace mivi {
 
-int gemv_argmax_parts(int32_t t, int K, int n) {
+int quad_grid(int n) {
+    static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
+    return std::max(1, std::min((n / 4 + 3) / 4, num_cus() * per_cu));
+}
+
+int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || K != 2048 || env_int("MIVI_GEMV_V1", 0)) return 0;
+    if (packed && t == MIVI_GGML_Q6_K && quad_layout(n, K)) return 4 * quad_grid(n);
     static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
     const int ngroups = (n + 1) / 2;
     return 4 * std::max(1, std::min((ngroups + 3) / 4, num_cus() * per_cu));
@@ -1635,6 +1920,14 @@ __global__ void __launch_bounds__(kWG) pack_q6k_kernel(const uint8_t* __restrict
 
 namespace mivi {
 int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s) {
+    if (quad_layout(rows, cols)) {
+        const size_t threads = rows / 4 * 64;
+        if (threads == 0) return MIVI_OK;
+        hipLaunchKernelGGL(pack_q6k_quad_kernel, dim3((unsigned)((threads + kWG - 1) / kWG)), dim3(kWG), 0, s, src, dst,
+                           rows / 4);
+        MIVI_HIP_CHECK(hipGetLastError());
+        return MIVI_OK;
+    }
     const int nu = (int)(cols / 64);
     const size_t threads = rows * (size_t)nu;
     if (threads == 0) return MIVI_OK;

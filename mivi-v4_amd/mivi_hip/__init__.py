@@ -199,7 +199,8 @@ try_matvec_bf16 = _typed(_lib.mivi_hip_try_matvec_bf16)       # f16.rs:75
 
 
 def pack_weights(ggml_type, src, dst, rows: int, cols: int, stream=None):
-    """Q6_K rows into the packed unit-plane layout (u8 GPU tensors of equal size)."""
+    """Q6_K rows into the packed layout (row quads at 2048 columns and rows % 4 == 0, unit planes
+    otherwise; u8 GPU tensors of equal size)."""
     _check(_lib.mivi_hip_pack_weights(int(ggml_type), C.c_void_p(src.data_ptr()), _nbytes(src),
                                       C.c_void_p(dst.data_ptr()), _nbytes(dst), rows, cols, _stream(stream)))
 

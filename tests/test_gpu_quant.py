@@ -308,10 +308,56 @@ def test_batched_gemv_columns_bit_exact_with_matvec(hip, oracle, torch_mod, t, b
             check_bound(oracle, t, w, X[b], got[b * rows:(b + 1) * rows], rows, cols)
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 2048), (1000, 4096), (130, 8192), (65536, 2048)])
+def q6k_codes(w, rows, cols):
+    """6-bit codes [rows, cols] of GGUF Q6_K rows (q6_k.rs:8-43, before the -32)."""
+    B = w.reshape(rows, cols // 256, 210).astype(np.uint32)
+    ql, qh = B[:, :, :128], B[:, :, 128:192]
+    out = np.zeros((rows, cols // 256, 256), np.uint32)
+    for h in range(2):
+        for q in range(4):
+            lo = ql[:, :, 64 * h + 32 * (q & 1):64 * h + 32 * (q & 1) + 32]
+            lo = (lo >> 4) if q & 2 else (lo & 0xF)
+            hi = (qh[:, :, 32 * h:32 * h + 32] >> (2 * q)) & 3
+            out[:, :, 128 * h + 32 * q:128 * h + 32 * q + 32] = lo | (hi << 4)
+    return out.reshape(rows, cols)
+
+
+def quad_pack_ref(w, rows):
+    """The row-quad packed layout of a Q6_K matrix with 2048 columns, restated
+    from its definition: quad Q holds rows 4Q..4Q+3 in 6720 bytes; lane
+    l = 4b + j owns units b and b + 16 of row j; slot g = 4i + q (quarter q of
+    unit i) is dwords 3g..3g+2 of the lane's codes, byte e of dword 3g+m being
+    c[4m+e] | (bits 2m..2m+1 of c[12+e]) << 6; then the slot scales, then the
+    d pairs (superblock s, s + 4) per (row, s < 4)."""
+    nq = rows // 4
+    codes = q6k_codes(w, rows, 2048).reshape(nq, 4, 8, 256)
+    B = w.reshape(nq, 4, 8, 210)
+    out = np.zeros((nq, 6720), np.uint8)
+    for l in range(64):
+        b, j = l >> 2, l & 3
+        for g in range(8):
+            u, q = b + 16 * (g >> 2), g & 3
+            sb, h, jj = u >> 2, (u >> 1) & 1, u & 1
+            c = codes[:, j, sb, 128 * h + 32 * q + 16 * jj:128 * h + 32 * q + 16 * jj + 16]
+            for m in range(3):
+                byte = c[:, 4 * m:4 * m + 4] | (((c[:, 12:16] >> (2 * m)) & 3) << 6)
+                D = 3 * g + m
+                o = 1024 * (D >> 2) + 16 * l + 4 * (D & 3)
+                out[:, o:o + 4] = byte.astype(np.uint8)
+            out[:, 6144 + 8 * l + g] = B[:, j, sb, 192 + 8 * h + jj + 2 * q]
+    for j in range(4):
+        for s4 in range(4):
+            o = 6656 + 4 * (4 * j + s4)
+            out[:, o:o + 2] = B[:, j, s4, 208:210]
+            out[:, o + 2:o + 4] = B[:, j, s4 + 4, 208:210]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (66, 2048), (1000, 4096), (130, 8192), (65536, 2048)])
 def test_packed_q6k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols):
-    # the packed layout is a byte permutation: the packed GEMV must give the
-    # raw GEMV's result bit for bit, and both meet the oracle bound
+    # the packed GEMV must give the raw GEMV's result bit for bit, and both
+    # meet the oracle bound; 2048 columns with rows % 4 == 0 use the row-quad
+    # layout (matrix cores), other shapes the unit-plane byte permutation
     torch = torch_mod
     w = hip.synth_random_weights(Q6_K, 90 + cols, rows, cols, 0.02)
     x = hip.synth_normal(91, cols)
@@ -326,9 +372,14 @@ def test_packed_q6k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols
     a, b = y_raw.cpu().numpy(), y_pk.cpu().numpy()
     assert b[-1] == 7.0
     assert np.array_equal(a.view(np.uint32), b[:-1].view(np.uint32))
-    # the packed bytes are a permutation of each row
-    pw = packed.cpu().numpy().reshape(rows, -1)
-    assert np.array_equal(np.sort(pw[:3], axis=1), np.sort(w.reshape(rows, -1)[:3], axis=1))
+    pw = packed.cpu().numpy()
+    if cols == 2048 and rows % 4 == 0:
+        n = min(rows, 256)  # the layout restated on the first quads
+        assert np.array_equal(pw[:n * 1680], quad_pack_ref(w[:n * 1680], n))
+    else:
+        # the unit-plane bytes are a permutation of each row
+        pw = pw.reshape(rows, -1)
+        assert np.array_equal(np.sort(pw[:3], axis=1), np.sort(w.reshape(rows, -1)[:3], axis=1))
     if rows <= 1000:
         check_bound(oracle, Q6_K, w, x, a, rows, cols)
 
