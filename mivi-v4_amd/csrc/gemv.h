@@ -74,6 +74,9 @@ inline bool quad_layout(size_t rows, size_t cols) { return cols == 2048 && rows 
 // Workgroups of a row-quad GEMV over n rows.
 int quad_grid(int n);
 
+// Workgroups per CU of a streaming GEMV over n rows (all segments).
+int stream_wg_per_cu(int n);
+
 int32_t launch_gemv_ex(int32_t ggml_type, int prologue, const GemvArgs& a, hipStream_t s);
 
 // Row-batch product: the a.ncol activation rows (row m at a.x + m * a.xs,

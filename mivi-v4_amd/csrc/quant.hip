@@ -1165,15 +1165,18 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
 // u: superblock u/4, half (u/2)&1, values 16(u&1) .. +16 of each quarter
 // q = 0..3 of the half, q6_k.rs:8-43). Slot g = 4i + q is quarter q of the
 // lane's unit i: sixteen 6-bit codes c_0..c_15 with scale sc[8h + (u&1) + 2q].
+// Offsets below are from o = 64 for odd Q (0 for even Q):
 //   [0, 6144)     codes, 16 B per lane at 1024 k + 16 l (k = 0..5). Slot g is
 //                 dwords 3g .. 3g+2 of the lane's 24: byte e of dword 3g+m
 //                 holds c_{4m+e} in bits 0-5 and bits 2m, 2m+1 of c_{12+e} in
 //                 bits 6-7, so the four dwords of codes unpack in 9 operations.
 //   [6144, 6656)  8 B per lane at 6144 + 8 l: the scale of slot g in byte g
-//   [6656, 6720)  4 B per (row j, superblock s < 4) at 6656 + 4 (4 j + s): the
-//                 fp16 d of superblock s, then of superblock s + 4
-// Every wave load of codes reads 1 KB of contiguous bytes, and a quad is
-// 4 x 1680 bytes, so a packed matrix keeps the GGUF matrix's size.
+// and the 64 bytes of d, 4 B per (row j, superblock s < 4) at 4 (4 j + s) (the
+// fp16 d of superblock s, then of superblock s + 4), follow at 6656 for even
+// Q and lead at 0 for odd Q. A quad is 4 x 1680 = 52.5 lines of 128 B, so the
+// odd quads start half a line in; with their d first, every 1 KB wave load of
+// codes and every scale load is line-aligned, and the d regions of quads 2P
+// and 2P + 1 share one line. A packed matrix keeps the GGUF matrix's size.
 //
 // The products run on v_mfma_i32_4x4x4_16b_i8 (16 independent 4 x 4 x 4
 // blocks; block b is lanes 4b .. 4b+3): lane 4b+v supplies row v of A, the
@@ -1229,10 +1232,12 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs
         int q = wid + st * nw;
         q = q < 0 ? 0 : q < nquads ? q : nquads - 1;
         const uint8_t* base = W + (size_t)q * kQuadBytes;
+        const uint8_t* cb = base + 64 * (q & 1);  // codes and scales
+        const uint8_t* db = base + ((q & 1) ? 0 : 6656);
 #pragma unroll
-        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(base + 1024 * k + 16 * lane);
-        scw[p] = *(const __attribute__((address_space(1))) u32x2*)(base + 6144 + 8 * lane);
-        dw[p] = *(const __attribute__((address_space(1))) uint32_t*)(base + 6656 + 4 * (4 * jv + (b >> 2)));
+        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(cb + 1024 * k + 16 * lane);
+        scw[p] = *(const __attribute__((address_space(1))) u32x2*)(cb + 6144 + 8 * lane);
+        dw[p] = *(const __attribute__((address_space(1))) uint32_t*)(db + 4 * (4 * jv + (b >> 2)));
     };
     // activation loads, then the first PD quads, then the activation math
     StageIn<PRO, K / kWG> in[NC > 1 ? 2 : 1];
@@ -1368,13 +1373,25 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs
             }
         }
     };
+    // Rounds whose refills all stay in range run branch-free; the last full
+    // round refills only the steps that exist (a refill of an earlier quad
+    // would go back to memory: the code loads are non-temporal), and the
+    // tail computes the last < PD steps.
     int st = 0;
-    for (; st + PD <= cnt; st += PD) {
+    for (; st + 2 * PD <= cnt; st += PD) {
 #pragma unroll
         for (int p = 0; p < PD; p++) {
             compute(p, st + p);
             load(p, st + p + PD);
         }
+    }
+    if (st + PD <= cnt) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, st + p);
+            if (st + p + PD < cnt) load(p, st + p + PD);
+        }
+        st += PD;
     }
 #pragma unroll
     for (int p = 0; p < PD; p++)
@@ -1391,7 +1408,8 @@ __global__ void __launch_bounds__(kWG) pack_q6k_quad_kernel(const uint8_t* __res
     const size_t Q = i >> 6;
     const int l = (int)(i & 63), b = l >> 2, j = l & 3;
     const uint8_t* row = src + (4 * Q + j) * 1680;
-    uint8_t* o = dst + Q * kQuadBytes;
+    uint8_t* o = dst + Q * kQuadBytes + 64 * (Q & 1);  // codes and scales
+    uint8_t* od = dst + Q * kQuadBytes + ((Q & 1) ? 0 : 6656);
     for (int g = 0; g < 8; g++) {
         const int u = b + 16 * (g >> 2), q = g & 3, h = (u >> 1) & 1, jj = u & 1;
         const uint8_t* blk = row + (u >> 2) * 210;
@@ -1407,7 +1425,7 @@ __global__ void __launch_bounds__(kWG) pack_q6k_quad_kernel(const uint8_t* __res
     }
     if ((b & 3) == 0) {
         const int s = b >> 2;
-        uint8_t* dp = o + 6656 + 4 * (4 * j + s);
+        uint8_t* dp = od + 4 * (4 * j + s);
         dp[0] = row[s * 210 + 208];
         dp[1] = row[s * 210 + 209];
         dp[2] = row[(s + 4) * 210 + 208];
@@ -1508,7 +1526,7 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
         const int lpr = K == 2048 ? 32 : 64;
         const int ngroups = (n + 64 / lpr - 1) / (64 / lpr);
         // 2 workgroups per CU measured best for the head GEMV (24.7 us vs 26.2 at 3)
-        static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
+        const int per_cu = mivi::stream_wg_per_cu(n);
         const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
         if (a.packed && mivi::quad_layout(n, K)) {
             // packed Q6_K row quads on the matrix cores (one segment: the quads span the matrix)
@@ -1703,15 +1721,25 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
 
 namespace mivi {
 
+int stream_wg_per_cu(int n) {
+    // Below 32768 rows a launch is bound by its fixed per-workgroup work (the
+    // activation staging, one to a few ring steps per wave): one workgroup
+    // per CU measured 2 us faster at K = 8192 (7.8 vs 9.8 us) and 0.2-0.5 us
+    // faster on the K = 2048 decode shapes. Large matrices keep two.
+    static const int env = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 0);
+    return env ? env : n >= 32768 ? 2 : 1;
+}
+
 int quad_grid(int n) {
-    static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
+    // 2 workgroups per CU measured best for the 65536-row head (18.7 us vs 20.6 at 3)
+    static const int per_cu = env_int("MIVI_GEMV_QUAD_WG_PER_CU", 2);
     return std::max(1, std::min((n / 4 + 3) / 4, num_cus() * per_cu));
 }
 
 int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || K != 2048 || env_int("MIVI_GEMV_V1", 0)) return 0;
     if (packed && t == MIVI_GGML_Q6_K && quad_layout(n, K)) return 4 * quad_grid(n);
-    static const int per_cu = env_int("MIVI_GEMV_STREAM_WG_PER_CU", 2);
+    const int per_cu = stream_wg_per_cu(n);
     const int ngroups = (n + 1) / 2;
     return 4 * std::max(1, std::min((ngroups + 3) / 4, num_cus() * per_cu));
 }

@@ -327,8 +327,9 @@ def quad_pack_ref(w, rows):
     from its definition: quad Q holds rows 4Q..4Q+3 in 6720 bytes; lane
     l = 4b + j owns units b and b + 16 of row j; slot g = 4i + q (quarter q of
     unit i) is dwords 3g..3g+2 of the lane's codes, byte e of dword 3g+m being
-    c[4m+e] | (bits 2m..2m+1 of c[12+e]) << 6; then the slot scales, then the
-    d pairs (superblock s, s + 4) per (row, s < 4)."""
+    c[4m+e] | (bits 2m..2m+1 of c[12+e]) << 6; then the slot scales; the d
+    pairs (superblock s, s + 4) per (row, s < 4) follow (even quads) or lead
+    (odd quads, whose codes and scales then start 64 bytes in)."""
     nq = rows // 4
     codes = q6k_codes(w, rows, 2048).reshape(nq, 4, 8, 256)
     B = w.reshape(nq, 4, 8, 210)
@@ -350,6 +351,7 @@ def quad_pack_ref(w, rows):
             o = 6656 + 4 * (4 * j + s4)
             out[:, o:o + 2] = B[:, j, s4, 208:210]
             out[:, o + 2:o + 4] = B[:, j, s4 + 4, 208:210]
+    out[1::2] = np.roll(out[1::2], 64, axis=1)  # odd quads: d first
     return out.reshape(-1)
 
 
