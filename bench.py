@@ -35,7 +35,9 @@ def log(msg):
 def gemv_bench(torch, hip, t, rows, cols, steps, warmup, seed, packed=False):
     """Times `steps` launches over rotating weight copies; returns dict.
     packed: the weights are first rewritten once by mivi_hip_pack_weights
-    (a byte permutation of each row; not timed) and the packed GEMV is timed."""
+    (the same bytes rearranged; not timed) and the packed GEMV is timed.
+    Then the same copies are read once each by mivi_hip_read_floor, a plain
+    coalesced read, timed the same way: the floor for these bytes."""
     stream = torch.cuda.current_stream()
     w_host = hip.synth_random_weights(t, seed, rows, cols, 0.02)
     x_host = hip.synth_normal(seed + 1, cols)
@@ -70,9 +72,20 @@ def gemv_bench(torch, hip, t, rows, cols, steps, warmup, seed, packed=False):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = e0.elapsed_time(e1) / steps
+    for i in range(2 * copies):
+        hip.read_floor(ws[i % copies], wbytes, stream=stream)
+    f0 = torch.cuda.Event(enable_timing=True)
+    f1 = torch.cuda.Event(enable_timing=True)
+    f0.record(stream)
+    for i in range(steps):
+        hip.read_floor(ws[i % copies], wbytes, stream=stream)
+    f1.record(stream)
+    torch.cuda.synchronize()
+    floor_ms = f0.elapsed_time(f1) / steps
     algo = wbytes + cols * 4 + rows * 4
     return dict(rows=rows, cols=cols, weight_bytes=wbytes, algo_bytes=algo, copies=copies,
                 ms_per_call=ev_ms, wall_ms_per_call=1e3 * wall / steps, gbs=algo / (ev_ms * 1e-3) / 1e9,
+                read_floor_us=floor_ms * 1e3, frac_of_read_floor=floor_ms / ev_ms,
                 w_host=w_host, x_host=x_host)
 
 
@@ -294,7 +307,8 @@ def main():
     log(f"{hip.version()} on {torch.cuda.get_device_name(0)}")
 
     q6 = gemv_bench(torch, hip, hip.GgmlType.Q6_K, 65536, 2048, a.steps, a.warmup, 100, packed=True)
-    log(f"Q6_K GEMV 65536x2048 (packed rows): {q6['ms_per_call'] * 1e3:.1f} us/call, {q6['gbs']:.0f} GB/s")
+    log(f"Q6_K GEMV 65536x2048 (packed rows): {q6['ms_per_call'] * 1e3:.1f} us/call, {q6['gbs']:.0f} GB/s; "
+        f"plain read of the same bytes {q6['read_floor_us']:.1f} us")
     q6r = gemv_bench(torch, hip, hip.GgmlType.Q6_K, 65536, 2048, a.steps, a.warmup, 100)
     log(f"Q6_K GEMV 65536x2048 (GGUF rows): {q6r['ms_per_call'] * 1e3:.1f} us/call, {q6r['gbs']:.0f} GB/s")
     if a.copy_calib:
@@ -302,14 +316,19 @@ def main():
     if a.only_q6k:
         return
     q4 = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200)
-    log(f"Q4_K GEMV 8192x2048: {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s")
+    log(f"Q4_K GEMV 8192x2048: {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s; "
+        f"plain read of the same bytes {q4['read_floor_us']:.2f} us")
     cpu = None
     if not a.no_cpu:
         cpu = cpu_gemv_baseline(hip.GgmlType.Q6_K, q6["w_host"], q6["x_host"], 65536, 2048, a.cpu_seconds)
         log(f"CPU oracle Q6_K GEMV: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
     extra = {
         "q6k_gemv_config2_gguf_rows": {k: q6r[k] for k in ("ms_per_call", "gbs")},
-        "q4k_gemv_config1": {k: q4[k] for k in ("rows", "cols", "algo_bytes", "ms_per_call", "gbs", "copies")},
+        "q4k_gemv_config1": {k: q4[k] for k in ("rows", "cols", "algo_bytes", "ms_per_call", "gbs", "copies",
+                                                "read_floor_us", "frac_of_read_floor")},
+        "q6k_gemv_config2_read_floor": {"read_floor_us": q6["read_floor_us"],
+                                        "read_floor_gbs": q6["weight_bytes"] / q6["read_floor_us"] / 1e3,
+                                        "packed_frac_of_read_floor": q6["frac_of_read_floor"]},
     }
     extra["q6k_gemv_config2_gguf_rows"]["frac_of_peak"] = q6r["gbs"] / HBM_PEAK_GBS
     extra["q4k_gemv_config1"]["frac_of_peak"] = q4["gbs"] / HBM_PEAK_GBS

@@ -226,6 +226,14 @@ int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t tokens, co
                                     size_t conv_len);
 
 /* ---------------------------------------------------------------------
+ * Measurement (no counterpart in the reference): reads `bytes` bytes at p
+ * (16-byte aligned, bytes % 16 == 0) once with plain coalesced 16-byte loads
+ * on the stream and discards them. Its time is the floor for any kernel that
+ * reads the same bytes, against which the benchmark reports the GEMVs.
+ * ------------------------------------------------------------------- */
+int32_t mivi_hip_read_floor(const uint8_t* p, size_t bytes, void* stream);
+
+/* ---------------------------------------------------------------------
  * Synthetic inputs (no counterpart in the reference, which ships no K-quant
  * quantizer): seeded SplitMix64 + Box-Muller normals and f32 -> Q4_K / Q6_K /
  * Q8_0 encoders, host side, multithreaded. Used to build test and benchmark

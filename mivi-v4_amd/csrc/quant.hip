@@ -1966,9 +1966,56 @@ int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t co
 }
 }  // namespace mivi
 
+// --------------------------------------------------------- read floor probe
+
+// external linkage, so that the store below (and the loads feeding it) stay
+__device__ uint32_t mivi_read_floor_sink;
+
+namespace {
+
+// The floor for any kernel that reads these bytes once: a persistent grid of
+// 2 workgroups per CU reads 16 bytes per lane, four loads in flight per
+// iteration, and folds them into one word per thread that is stored only
+// when it equals `key`, a value known only at run time (so the compiler keeps
+// the loads; a stored word is harmless).
+__global__ void __launch_bounds__(kWG) read_floor_kernel(const u32x4* __restrict__ p, size_t n16, uint32_t key) {
+    const size_t nt = (size_t)gridDim.x * kWG;
+    size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * nt < n16; i += 4 * nt) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = __builtin_nontemporal_load(p + i + u * nt);
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += nt) {
+        const u32x4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == key) mivi_read_floor_sink = acc;
+}
+
+}  // namespace
+
 // -------------------------------------------------------------------- C ABI
 
 using namespace mivi;
+
+extern "C" int32_t mivi_hip_read_floor(const uint8_t* p, size_t bytes, void* stream) {
+    if (bytes % 16) return err_misaligned(bytes, 16);
+    if (bytes && !p) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    if ((uintptr_t)p % 16) return set_error(MIVI_ERR_INVALID_ARGUMENT, "buffer must be 16-byte aligned");
+    clear_error();
+    if (bytes == 0) return MIVI_OK;
+    const size_t n16 = bytes / 16;
+    const size_t need = (n16 + kWG - 1) / kWG;
+    const int grid = (int)std::max<size_t>(1, std::min<size_t>(need, (size_t)num_cus() * 2));
+    hipLaunchKernelGGL(read_floor_kernel, dim3(grid), dim3(kWG), 0, (hipStream_t)stream, (const u32x4*)p, n16,
+                       0x9E3779B9u);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
 
 // Packed rows: Q6_K with d in {2048, 4096, 8192} (the streaming kernel's shapes).
 static bool packable(int32_t t, size_t d) { return t == MIVI_GGML_Q6_K && (d == 2048 || d == 4096 || d == 8192); }

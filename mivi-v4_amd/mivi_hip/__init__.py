@@ -119,6 +119,7 @@ _sig = {
     "mivi_hip_model_set_prefill_tile": ([_P, _S], _I),
     "mivi_hip_model_export_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_model_import_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
+    "mivi_hip_read_floor": ([_P, _S, _P], _I),
     "mivi_synth_normal": ([C.c_uint64, C.c_float, C.c_float, _P, _S], None),
     "mivi_synth_quantize": ([_I, _P, _S, _S, _P, _S], _I),
     "mivi_synth_random_weights": ([_I, C.c_uint64, C.c_float, _S, _S, _P, _S], _I),
@@ -241,6 +242,12 @@ def dot_q8_0_f32(q, k_blocks, out, n: int, stream=None):
     po, lo = _dev(out)
     _check(_lib.mivi_hip_dot_q8_0_f32(pq, lq, C.c_void_p(k_blocks.data_ptr()), _nbytes(k_blocks), po, lo, n,
                                       _stream(stream)))
+
+
+def read_floor(buf, nbytes: int, stream=None):
+    """One plain coalesced read of nbytes of the u8 GPU tensor buf (the floor
+    for any kernel reading those bytes)."""
+    _check(_lib.mivi_hip_read_floor(C.c_void_p(buf.data_ptr()), nbytes, _stream(stream)))
 
 
 # ----------------------------------------------------------- synthetic data
