@@ -52,8 +52,8 @@ struct GemvArgs {
 };
 
 // Most columns one batched streaming launch takes (more are split into
-// launches of at most this many).
-constexpr int kMaxGemvCols = 2;
+// launches of at most this many; fewer at K = 8192 and on packed rows).
+constexpr int kMaxGemvCols = 8;
 
 // What the GEMV does with its row results (streaming kernel, K = 2048).
 enum GemvEpilogue : int {

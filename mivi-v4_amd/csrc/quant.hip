@@ -558,6 +558,8 @@ typedef uint32_t u32x2_a1 __attribute__((ext_vector_type(2), aligned(1)));
 // 2.5e-7 * sqrt(K) * ||w|| * ||x|| (2.3e-5 of ||w|| ||x|| at K = 8192).
 constexpr float kDig1 = 1.0f / 254.0f, kDig2 = 1.0f / 64516.0f;
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
 
 // Digit planes of the K floats staged at xs, written to dig[d * K / 4 + i]
@@ -721,9 +723,10 @@ struct StageIn {
         }
     }
 
-    // Forms the activations, writes the digit planes dig[3][K/4] (and the
-    // Q4_K sub-block sums xsum[K/32] when SUMS) and returns the digit scale s.
-    template <bool SUMS>
+    // Forms the activations, writes the digit planes dig[3][PS] (PS dwords
+    // apart, K/4 when 0; and the Q4_K sub-block sums xsum[K/32] when SUMS)
+    // and returns the digit scale s.
+    template <bool SUMS, int PS = 0>
     __device__ __forceinline__ float finish(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
         __shared__ float red[2][kWG / 64];
         const int K = a.K, e0 = threadIdx.x * E;
@@ -819,11 +822,12 @@ struct StageIn {
                 w2[q] |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
             }
         }
+        const int P = PS ? PS : K / 4;
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
             dig[e0 / 4 + q] = w0[q];
-            dig[K / 4 + e0 / 4 + q] = w1[q];
-            dig[K / 2 + e0 / 4 + q] = w2[q];
+            dig[P + e0 / 4 + q] = w1[q];
+            dig[2 * P + e0 / 4 + q] = w2[q];
         }
         if constexpr (SUMS) {
             // fp32 sums of each 32-value sub-block (32 / E threads share one)
@@ -1155,6 +1159,329 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
+// One column staged by one wave: the digits, sub-block sums and digit scale
+// of StageIn::finish<true, PS> for the same column, bit for bit. Lane l stands
+// in for the workgroup's threads l + 64w (w = 0..3), each owning E
+// consecutive activations, and partial sums are reduced in finish's order
+// (each thread's values in sequence, a butterfly over the 64 threads of a
+// wave, then the four waves in order). Prologues NONE, RMSNORM and CONV.
+template <int PRO, int E, int PS>
+__device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
+    static_assert(PRO != mivi::PRO_SWIGLU, "no SwiGLU prologue here");
+    constexpr int K = E * kWG;
+    const int l = threadIdx.x & 63;
+    float v[4][E], nw[PRO == mivi::PRO_RMSNORM ? 4 : 1][PRO == mivi::PRO_RMSNORM ? E : 1];
+    float ssw[4] = {0.f, 0.f, 0.f, 0.f};
+    float m = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int e0 = (l + 64 * w) * E;
+#pragma unroll
+        for (int i = 0; i < E / 4; i++) {
+            const f32x4 t = *(gf32x4*)(a.x + e0 + 4 * i);
+            v[w][4 * i] = t.x; v[w][4 * i + 1] = t.y; v[w][4 * i + 2] = t.z; v[w][4 * i + 3] = t.w;
+        }
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) {
+                const f32x4 t = *(gf32x4*)(a.norm_w + e0 + 4 * i);
+                nw[w][4 * i] = t.x; nw[w][4 * i + 1] = t.y; nw[w][4 * i + 2] = t.z; nw[w][4 * i + 3] = t.w;
+            }
+#pragma unroll
+            for (int i = 0; i < E; i++) {
+                ssw[w] = fmaf(v[w][i], v[w][i], ssw[w]);
+                m = nanmax(m, fabsf(v[w][i] * nw[w][i]));
+            }
+        } else if constexpr (PRO == mivi::PRO_CONV) {
+            // a.x = [B | C | X] (ssm.rs:80-140), as StageIn
+            const bool swap = a.phase && ((*a.phase) & 1);
+            const float* st_in = swap ? a.st_out : a.st_in;
+            float* st_out = swap ? (float*)a.st_in : a.st_out;
+            float cv[E], xv[E], st[E * kConvKs], cw[E * kConvKs];
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) {
+                const f32x4 c4 = *(gf32x4*)(a.x + a.K + e0 + 4 * i), x4 = *(gf32x4*)(a.x + 2 * a.K + e0 + 4 * i);
+                cv[4 * i] = c4.x; cv[4 * i + 1] = c4.y; cv[4 * i + 2] = c4.z; cv[4 * i + 3] = c4.w;
+                xv[4 * i] = x4.x; xv[4 * i + 1] = x4.y; xv[4 * i + 2] = x4.z; xv[4 * i + 3] = x4.w;
+            }
+#pragma unroll
+            for (int i = 0; i < E * kConvKs / 4; i++) {
+                const f32x4 s4 = *(gf32x4*)(st_in + e0 * kConvKs + 4 * i);
+                st[4 * i] = s4.x; st[4 * i + 1] = s4.y; st[4 * i + 2] = s4.z; st[4 * i + 3] = s4.w;
+                if (a.conv_mode == 0) {
+                    const f32x4 w4 = *(gf32x4*)(a.conv_w + e0 * kConvKs + 4 * i);
+                    cw[4 * i] = w4.x; cw[4 * i + 1] = w4.y; cw[4 * i + 2] = w4.z; cw[4 * i + 3] = w4.w;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < E * kConvKs; i++)
+                if (a.conv_mode != 0) cw[i] = a.conv_mode == 1 ? a.conv_w[i % kConvKs] : 1.0f / (float)kConvKs;
+            float nst[E * kConvKs];
+#pragma unroll
+            for (int d = 0; d < E; d++) {
+                const float bx = v[w][d] * xv[d];
+                float conv = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kConvKs; k++) {
+                    const int o = d * kConvKs + k;
+                    const float sv = k + 1 < kConvKs ? st[o + 1] : bx;
+                    conv += cw[o] * sv;
+                    nst[o] = sv;
+                }
+                v[w][d] = cv[d] * conv;
+            }
+            if (blockIdx.x == 0) {
+#pragma unroll
+                for (int i = 0; i < E * kConvKs / 4; i++)
+                    *(f32x4*)(st_out + e0 * kConvKs + 4 * i) = f32x4{nst[4 * i], nst[4 * i + 1], nst[4 * i + 2], nst[4 * i + 3]};
+            }
+        }
+        if constexpr (PRO != mivi::PRO_RMSNORM) {
+#pragma unroll
+            for (int i = 0; i < E; i++) m = nanmax(m, fabsf(v[w][i]));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) ssw[w] += __shfl_xor(ssw[w], o, 64);
+        }
+        m = nanmax(m, __shfl_xor(m, o, 64));
+    }
+    if constexpr (PRO == mivi::PRO_RMSNORM) {
+        float ss = ssw[0];
+        ss += ssw[1];
+        ss += ssw[2];
+        ss += ssw[3];
+        const float scale = 1.0f / sqrtf(ss / (float)K + a.eps);  // math.rs:7-22
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+#pragma unroll
+            for (int i = 0; i < E; i++) v[w][i] = v[w][i] * scale * nw[w][i];
+        m *= scale;
+    }
+    const bool finite = m > 0.f && m <= 3.40282347e38f;
+    const float inv = finite ? 127.0f / m : 0.0f;
+    const float sc = (m - m) + m / 127.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int e0 = (l + 64 * w) * E;
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float yv = v[w][4 * q + e] * inv;
+                const float d0 = rintf(yv);
+                const float t1 = (yv - d0) * 254.0f;
+                const float d1 = rintf(t1);
+                const float d2 = rintf((t1 - d1) * 254.0f);
+                w0 |= ((uint32_t)(int)d0 & 0xFFu) << (8 * e);
+                w1 |= ((uint32_t)(int)d1 & 0xFFu) << (8 * e);
+                w2 |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
+            }
+            dig[e0 / 4 + q] = w0;
+            dig[PS + e0 / 4 + q] = w1;
+            dig[2 * PS + e0 / 4 + q] = w2;
+        }
+        // fp32 sums of each 32-value sub-block (32 / E threads share one)
+#pragma unroll
+        for (int b = 0; b < (E >= 32 ? E / 32 : 1); b++) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[w][b * 32 + i];
+            if constexpr (E < 32) {
+#pragma unroll
+                for (int o = 1; o < 32 / E; o <<= 1) t += __shfl_xor(t, o, 64);
+            }
+            if (E >= 32 || (l % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t;
+        }
+    }
+    return sc;
+}
+
+// --------------------------------------- batched Q4_K GEMV on the matrix cores
+//
+// Several activation columns (the sequences of a batched decode step, the
+// input rows of a small matmul_rows batch) against Q4_K rows in their GGUF
+// layout: up to 8 columns at K = 2048, up to 4 at K = 8192. A workgroup owns
+// 16 rows at a time (EPI_SWIGLU: gate rows c..c+7 and up rows c..c+7), its
+// wave q the q-th quarter of their units. Per 32-value sub-block and group G
+// of four columns, v_mfma_i32_16x16x32_i8 takes
+//   A  row i = 4c' + p: digit plane p of column 4G + c' (a zero plane for
+//      p = 3) at the sub-block's 32 k (lane l: row l % 16, k = 8 (l / 16) .. +8),
+//   B  the 4-bit codes of the 16 rows (lane l: row l % 16, the low or high
+//      nibbles of the 8 code bytes of k = 8 (l / 16) .. +8),
+// and lane l receives C[4 (l / 16) + p][l % 16] (p = 0..2): column
+// 4G + l / 16, row l % 16, plane p, the exact integer sums of code x digit
+// that the sdot4 kernel forms. The lane applies the sub-block scales and the
+// float steps of q4k_unit_i8 per unit for its row and column. The one-column
+// kernel then sums units over its lanes with a butterfly whose first steps
+// pair unit t with t + 16 (K = 2048) or form lr + (lr + 64) and then pair lr
+// with lr + 32 (K = 8192): here waves 2, 3 hand their per-unit values to
+// waves 0, 1 and wave 1 to wave 0 through LDS, in that order, and wave 0
+// finishes the butterfly in registers, so every column equals a one-column
+// launch bit for bit. Digits sit in LDS (8 KB per column at K = 2048: three
+// planes and the zero plane, padded apart against bank conflicts).
+template <int PRO, int EPI, int KT, int NG>
+__global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a) {
+    static_assert(KT == 2048 || KT == 8192, "decode depths");
+    constexpr int K = KT, nb = K / 256;
+    constexpr int SQ = nb / 4;               // superblocks per wave: 2 or 8
+    constexpr int LW = 4 * SQ;               // units (leaf values) per wave: 8 or 32
+    constexpr int PD = SQ < 4 ? SQ : 4;      // superblock chunks in flight per wave
+    constexpr int NCM = 4 * NG;
+    constexpr int PS = K / 4 + 4;            // digit plane stride (dwords)
+    __shared__ __attribute__((aligned(16))) uint32_t dig[NCM][4 * PS];
+    __shared__ __attribute__((aligned(16))) float xsum[NCM][K / 32];
+    __shared__ float scol[NCM];
+    __shared__ float xch[3][NG * LW][64];    // wave 2 -> 0, wave 3 -> 1, wave 1 -> 0
+    const Segs sg(a, nb * 144);
+    const int n = sg.n, n0 = a.seg[0].n;
+    const int ncol = a.ncol;  // 2..NCM, workgroup-uniform
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, kg = lane >> 4;
+    const int ngroups = EPI == mivi::EPI_SWIGLU ? (n0 + 7) / 8 : (n + 15) / 16;
+    const int cnt = (int)blockIdx.x < ngroups ? (ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+
+    // row of lane row j in group step st (-1: none; loads then use row 0)
+    auto row_of = [&](int st) {
+        const int grp = (int)blockIdx.x + st * (int)gridDim.x;
+        if constexpr (EPI == mivi::EPI_SWIGLU) {
+            const int c = 8 * grp + (j & 7);
+            return c < n0 ? c + (j >> 3) * n0 : -1;
+        } else {
+            const int r = 16 * grp + j;
+            return r < n ? r : -1;
+        }
+    };
+    // ring of superblock chunks: this wave's superblock bb of step st in slot bb % PD
+    u32x4 hdr[PD];
+    u32x2 cq[PD][4];
+    auto load = [&](int slot, int st, int bb) {
+        st = st < cnt ? st : cnt - 1;
+        const int r = row_of(st < 0 ? 0 : st);
+        const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (wave * SQ + bb);
+        hdr[slot] = ldg16(p);
+#pragma unroll
+        for (int g = 0; g < 4; g++) cq[slot][g] = *(const __attribute__((address_space(1))) u32x2*)(p + 16 + 32 * g + 8 * kg);
+    };
+#pragma unroll
+    for (int q = 0; q < PD; q++) load(q, 0, q);
+    // the zero plane of every column; each wave stages columns wave, wave + 4
+    for (int i = threadIdx.x; i < NCM * PS; i += kWG) dig[i / PS][3 * PS + i % PS] = 0u;
+    for (int c = wave; c < ncol; c += 4) {
+        const float sc = stage_col_wave<PRO, K / kWG, PS>(gemv_column(a, c), dig[c], xsum[c]);
+        if (lane == 0) scol[c] = sc;
+    }
+    __syncthreads();
+    if (cnt == 0) return;  // workgroup-uniform
+    float s[NG];
+#pragma unroll
+    for (int G = 0; G < NG; G++) s[G] = scol[min(4 * G + kg, ncol - 1)];
+    const int ci = j >> 2, pi = j & 3;  // A operand of this lane: column 4G + ci, plane pi
+    const uint32_t* dA[NG];
+#pragma unroll
+    for (int G = 0; G < NG; G++) dA[G] = dig[min(4 * G + ci, ncol - 1)] + pi * PS + 2 * kg;
+
+    for (int st = 0; st < cnt; st++) {
+        float leaf[NG][LW];
+#pragma unroll
+        for (int bb = 0; bb < SQ; bb++) {
+            const int slot = bb % PD, b = wave * SQ + bb;
+            const u32x4 h = hdr[slot];
+            u32x2 q[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) q[g] = cq[slot][g];
+            // refill with the chunk PD ahead (into the next group past the end)
+            if (bb + PD < SQ) load(slot, st, bb + PD);
+            else load(slot, st + 1, bb + PD - SQ);
+            const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                uint32_t sc0, m0, sc1, m1;
+                q4k_scales(h.y, h.z, h.w, g, sc0, m0, sc1, m1);
+                const long blo = (long)(((uint64_t)(q[g].y & 0x0F0F0F0Fu) << 32) | (q[g].x & 0x0F0F0F0Fu));
+                const long bhi = (long)(((uint64_t)((q[g].y >> 4) & 0x0F0F0F0Fu) << 32) | ((q[g].x >> 4) & 0x0F0F0F0Fu));
+#pragma unroll
+                for (int G = 0; G < NG; G++) {
+                    const int w0 = (256 * b + 64 * g) / 4;
+                    const u32x2 alo = *(const u32x2*)(dA[G] + w0);
+                    const u32x2 ahi = *(const u32x2*)(dA[G] + w0 + 8);
+                    long al = (long)(((uint64_t)alo.y << 32) | alo.x);
+                    long ah = (long)(((uint64_t)ahi.y << 32) | ahi.x);
+                    // keep units in program order: pure code is otherwise sunk
+                    // to the final reduction and every unit's products stay live
+                    asm volatile("" : "+v"(al), "+v"(ah));
+                    const i32x4 z = {0, 0, 0, 0};
+                    const i32x4 Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, blo, z, 0, 0, 0);
+                    const i32x4 Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bhi, z, 0, 0, 0);
+                    // q4k_unit_i8 for (row j, column 4G + kg)
+                    int A[3];
+#pragma unroll
+                    for (int e = 0; e < 3; e++) A[e] = mul24(Dl[e], (int)sc0) + mul24(Dh[e], (int)sc1);
+                    const float f = fmaf((float)A[2], kDig2, fmaf((float)A[1], kDig1, (float)A[0]));
+                    const int col = min(4 * G + kg, ncol - 1);
+                    const float X0 = xsum[col][b * 8 + 2 * g], X1 = xsum[col][b * 8 + 2 * g + 1];
+                    float v = (d * s[G]) * f - dmin * fmaf((float)m0, X0, (float)m1 * X1);
+                    asm volatile("" : "+v"(v));
+                    leaf[G][4 * bb + g] = 0.f + v;
+                }
+            }
+        }
+        // the butterfly's first steps across the waves (2 -> 0, 3 -> 1, then 1 -> 0)
+        if (wave >= 2) {
+#pragma unroll
+            for (int G = 0; G < NG; G++)
+#pragma unroll
+                for (int t = 0; t < LW; t++) xch[wave - 2][G * LW + t][lane] = leaf[G][t];
+        }
+        __syncthreads();
+        if (wave < 2) {
+#pragma unroll
+            for (int G = 0; G < NG; G++)
+#pragma unroll
+                for (int t = 0; t < LW; t++) leaf[G][t] = leaf[G][t] + xch[wave][G * LW + t][lane];
+            if (wave == 1) {
+#pragma unroll
+                for (int G = 0; G < NG; G++)
+#pragma unroll
+                    for (int t = 0; t < LW; t++) xch[2][G * LW + t][lane] = leaf[G][t];
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int G = 0; G < NG; G++) {
+#pragma unroll
+                for (int t = 0; t < LW; t++) leaf[G][t] = leaf[G][t] + xch[2][G * LW + t][lane];
+#pragma unroll
+                for (int sh = LW / 2; sh >= 1; sh >>= 1)
+#pragma unroll
+                    for (int t = 0; t < sh; t++) leaf[G][t] = leaf[G][t] + leaf[G][t + sh];
+            }
+            const int r = row_of(st);
+#pragma unroll
+            for (int G = 0; G < NG; G++) {
+                const int col = 4 * G + kg;
+                const float v = leaf[G][0];
+                if constexpr (EPI == mivi::EPI_SWIGLU) {
+                    // lanes j < 8: gate c; lanes j + 8: up c (math.rs:87-95)
+                    const float up = __shfl(v, lane + 8, 64);
+                    if (j < 8 && r >= 0 && col < ncol) *(gfloat*)(sg.out(r) + col * a.ys) = silu_f(v) * up;
+                } else {
+                    if (r >= 0 && col < ncol) {
+                        gfloat* y = (gfloat*)(sg.out(r) + col * a.ys);
+                        if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(y, v);
+                        else *y = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------ Q6_K row quads on the matrix cores
 //
 // Packed Q6_K matrices with K = 2048 and a multiple of 4 rows
@@ -1190,7 +1517,6 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
 
 constexpr int kQuadBytes = 6720;
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ i32x4 mfma4x4(uint32_t a, uint32_t b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, c, 0, 0, 0);
@@ -1553,14 +1879,44 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
 #define LSP(KT, LPR, NU, PD, EPI) \
     hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, KT, LPR, NU, PD, PRO, EPI, true>), dim3(grid), dim3(kWG), 0, s, a)
         if (a.ncol > 1) {
-            // batched columns (launch_cols passes at most gemv_max_cols):
+            // batched columns (launch_gemv_ex passes at most gemv_max_cols):
             // the one-column kernel's mapping, so each column's result is
-            // bit-identical to a one-column launch; PD 2 leaves registers for
-            // the columns' digits
+            // bit-identical to a one-column launch. Two columns at K = 2048
+            // keep their digits in registers (PD 2 leaves room for them);
+            // more columns (up to 8 at K = 2048, 4 at K = 8192) read them
+            // from LDS each step (XL), so one launch reads each weight row
+            // once for all of them.
 #define LB(FMT, KT, LPR, NU, PD, EPI, PACK, NC)                                                                 \
     hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, KT, LPR, NU, PD, PRO, EPI, PACK, NC>), dim3(grid), dim3(kWG), 0, \
                        s, a)
+#define LBX(FMT, EPI, G)                                                                                          \
+    hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT, 2048, 32, 1, 2, PRO, EPI, false, mivi::kMaxGemvCols, true>),   \
+                       dim3(G), dim3(kWG), 0, s, a)
             const int ep = a.epilogue;
+            const bool wide = a.ncol > 2 && !a.packed;
+            // Q4_K, 3+ columns at K = 2048 or 2+ at K = 8192, store or SwiGLU
+            // epilogue: the matrix-core kernel (same results, bit for bit)
+            if (PRO != mivi::PRO_SWIGLU && t == MIVI_GGML_Q4_K && !a.packed && ep != mivi::EPI_ARGMAX &&
+                ((K == 2048 && a.ncol > 2) || (K == 8192 && ep == mivi::EPI_STORE && PRO == mivi::PRO_NONE)) &&
+                !env_int("MIVI_GEMV_COLS_SDOT", 0)) {
+                if (ep == mivi::EPI_SWIGLU && (a.nseg != 2 || a.seg[1].n != a.seg[0].n))
+                    return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "SwiGLU epilogue needs gate|up of equal rows");
+                // one workgroup per 16-row group, at most 2 per CU (1 at K = 8192: LDS)
+                const int ngr = ep == mivi::EPI_SWIGLU ? (a.seg[0].n + 7) / 8 : (n + 15) / 16;
+                const int gc = std::max(1, std::min(ngr, mivi::num_cus() * (K == 8192 ? 1 : 2)));
+#define LC(EPI, KT, NG) hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG>), dim3(gc), dim3(kWG), 0, s, a)
+                if constexpr (PRO == mivi::PRO_SWIGLU) {
+                } else if (K == 8192) {
+                    if constexpr (PRO == mivi::PRO_NONE) LC(mivi::EPI_STORE, 8192, 1);
+                } else if (ep == mivi::EPI_SWIGLU) {
+                    if (a.ncol > 4) LC(mivi::EPI_SWIGLU, 2048, 2); else LC(mivi::EPI_SWIGLU, 2048, 1);
+                } else {
+                    if (a.ncol > 4) LC(mivi::EPI_STORE, 2048, 2); else LC(mivi::EPI_STORE, 2048, 1);
+                }
+#undef LC
+                MIVI_HIP_CHECK(hipGetLastError());
+                return MIVI_OK;
+            }
             if (K == 2048) {
                 if (ep == mivi::EPI_STORE) {
                     if (a.packed) {
@@ -1568,6 +1924,8 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                             LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_STORE, true, 2);
                         else
                             return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows take no conv or SwiGLU prologue");
+                    } else if (wide) {
+                        if (t == MIVI_GGML_Q4_K) LBX(FMT_Q4K, mivi::EPI_STORE, grid); else LBX(FMT_Q6K, mivi::EPI_STORE, grid);
                     } else if (t == MIVI_GGML_Q4_K) LB(FMT_Q4K, 2048, 32, 1, 2, mivi::EPI_STORE, false, 2);
                     else LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_STORE, false, 2);
                 } else if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
@@ -1575,7 +1933,9 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                         if (a.nseg != 2 || a.seg[1].n != a.seg[0].n)
                             return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "SwiGLU epilogue needs gate|up of equal rows");
                         const int g1 = std::max(1, std::min((a.seg[0].n + 3) / 4, mivi::num_cus() * per_cu));
-                        if (t == MIVI_GGML_Q4_K)
+                        if (wide) {
+                            if (t == MIVI_GGML_Q4_K) LBX(FMT_Q4K, mivi::EPI_SWIGLU, g1); else LBX(FMT_Q6K, mivi::EPI_SWIGLU, g1);
+                        } else if (t == MIVI_GGML_Q4_K)
                             hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 2048, 32, 1, 2, PRO, mivi::EPI_SWIGLU, false, 2>),
                                                dim3(g1), dim3(kWG), 0, s, a);
                         else
@@ -1583,7 +1943,9 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                                                dim3(g1), dim3(kWG), 0, s, a);
                     } else {
                         if (a.packed) LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, true, 2);
-                        else if (t == MIVI_GGML_Q4_K) LB(FMT_Q4K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, false, 2);
+                        else if (wide) {
+                            if (t == MIVI_GGML_Q4_K) LBX(FMT_Q4K, mivi::EPI_ARGMAX, grid); else LBX(FMT_Q6K, mivi::EPI_ARGMAX, grid);
+                        } else if (t == MIVI_GGML_Q4_K) LB(FMT_Q4K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, false, 2);
                         else LB(FMT_Q6K, 2048, 32, 1, 2, mivi::EPI_ARGMAX, false, 2);
                     }
                 } else {
@@ -1593,10 +1955,10 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                 // two units per lane: the columns' digits stay in LDS
                 if constexpr (PRO == mivi::PRO_NONE) {
                     if (t == MIVI_GGML_Q4_K)
-                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 8192, 64, 2, 2, PRO, mivi::EPI_STORE, false, 2, true>),
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 8192, 64, 2, 2, PRO, mivi::EPI_STORE, false, 4, true>),
                                            dim3(grid), dim3(kWG), 0, s, a);
                     else
-                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, 8192, 64, 2, 2, PRO, mivi::EPI_STORE, false, 2, true>),
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q6K, 8192, 64, 2, 2, PRO, mivi::EPI_STORE, false, 4, true>),
                                            dim3(grid), dim3(kWG), 0, s, a);
                 } else {
                     return mivi::set_error(MIVI_ERR_UNSUPPORTED, "batched d=8192 GEMV takes no prologue");
@@ -1604,6 +1966,7 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
             } else {
                 return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no batched GEMV for d=%d", K);
             }
+#undef LBX
 #undef LB
             MIVI_HIP_CHECK(hipGetLastError());
             return MIVI_OK;
@@ -1745,12 +2108,12 @@ int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
 }
 
 // Most columns one batched streaming launch takes at depth K, 1 where there
-// is no batched kernel. At K = 2048 its lanes hold every column's digits in
-// registers (two columns fit in 164-198 VGPRs); at K = 8192 (two units per
-// lane) they would spill, so that kernel reads them from LDS each step.
-static int gemv_max_cols(int32_t t, int K) {
+// is no batched kernel: 8 at K = 2048 (digits in LDS: 6 KB per column), 4 at
+// K = 8192 (24 KB per column); packed rows take 2.
+static int gemv_max_cols(int32_t t, int K, bool packed) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
-    return K == 2048 || K == 8192 ? kMaxGemvCols : 1;
+    if (packed) return K == 2048 ? 2 : 1;
+    return K == 2048 ? kMaxGemvCols : K == 8192 ? 4 : 1;
 }
 
 // Columns [c0, c0 + nc) of a batched GEMV as one launch's arguments.
@@ -1784,7 +2147,7 @@ int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     if (a.ncol > 1) {
         // column groups of the batched kernel; columns it cannot take run
         // one launch each
-        const int cap = gemv_max_cols(t, a.K);
+        const int cap = gemv_max_cols(t, a.K, a.packed != 0);
         for (int c0 = 0; c0 < a.ncol;) {
             const int nc = std::min(cap, a.ncol - c0);
             int32_t rc = nc > 1 ? launch_by_pro(t, pro, column_args(a, c0, nc), n, s) : MIVI_ERR_UNSUPPORTED;

@@ -97,15 +97,16 @@ def test_batched_sequences_are_independent(hip, small_img):
         assert np.array_equal(out[:, b], one)
 
 
-def test_batched_full_width_matches_single_sequences(hip):
-    # dim 2048 (the decode shapes): the packed Q6_K head, two-column GEMV
-    # launches, the d = 8192 per-column fallback, and an odd batch (3 = 2 + 1
-    # columns); every sequence's greedy tokens and final logits equal its own
+@pytest.mark.parametrize("B", [3, 8])
+def test_batched_full_width_matches_single_sequences(hip, B):
+    # dim 2048 (the decode shapes): the packed Q6_K head (two columns per
+    # launch), the multi-column Q4_K projections on the matrix cores (3 and 8
+    # columns at d = 2048, 3 and 4 + 4 at d = 8192) with the RMSNorm, conv and
+    # SwiGLU stages; every sequence's greedy tokens equal its own
     # single-sequence run bit for bit
     from mivi_hip.synthmodel import build_hybrid
     img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
                        ctx_len=1024, seed=11)
-    B = 3
     mb = hip.Model(img, max_ctx=256, max_batch=B)
     rng = np.random.default_rng(12)
     prompts = [rng.integers(0, 4096, 6 + 3 * b) for b in range(B)]

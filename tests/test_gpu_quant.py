@@ -281,12 +281,14 @@ def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, 
 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
 @pytest.mark.parametrize("batch,rows,cols", [(2, 64, 2048), (3, 1001, 2048), (5, 6144, 2048), (4, 65536, 2048),
-                                             (3, 300, 8192), (2, 130, 4096)])
+                                             (7, 1001, 2048), (8, 8192, 2048), (15, 260, 2048),
+                                             (3, 300, 8192), (6, 2048, 8192), (2, 130, 4096)])
 def test_batched_gemv_columns_bit_exact_with_matvec(hip, oracle, torch_mod, t, batch, rows, cols):
-    # matmul_rows below the MFMA threshold runs the batched streaming GEMV
-    # (inputs as columns, two per launch at d = 2048; one launch per input
-    # otherwise): every input's row of outputs equals its own matvec bit for
-    # bit (lib.rs:404-457), and meets the oracle bound
+    # matmul_rows below the MFMA threshold runs batched GEMVs (inputs as
+    # columns: up to 8 per launch at d = 2048 and 4 at d = 8192, Q4_K on the
+    # int8 matrix cores; one launch per input at other depths): every input's
+    # row of outputs equals its own matvec bit for bit (lib.rs:404-457), and
+    # meets the oracle bound
     torch = torch_mod
     w = hip.synth_random_weights(t, 70 + batch, rows, cols, 0.02)
     X = np.stack([hip.synth_normal(80 + b, cols) for b in range(batch)])
