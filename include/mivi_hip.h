@@ -226,6 +226,28 @@ int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t tokens, co
                                     size_t conv_len);
 
 /* ---------------------------------------------------------------------
+ * Sampling: crates/mivi-model/src/sampler.rs:91-135 (Sampler::sample) with
+ * GenerationConfig's sampling fields (config.rs:163-174). top_k 0 = off.
+ * ------------------------------------------------------------------- */
+typedef struct {
+    float temperature, top_p, min_p, repetition_penalty, presence_penalty, frequency_penalty;
+    uint32_t top_k;
+} mivi_sampler_config;
+
+/* Sampler::sample on the device, one workgroup, asynchronous on the stream:
+ * logits (n floats, device) are modified in place as the reference modifies
+ * its &mut [f32] (penalties, temperature, min-p, top-k, then the softmax
+ * probabilities); recent (n_recent token ids, device) is the penalty window;
+ * rng_state (device u64) is the xorshift64* state, advanced by one draw when
+ * the reference draws (seed it with the reference's rule: 0 ->
+ * 0x853c49e6748fea9b); token (device u32) receives the sampled id. The draw
+ * is bit-exact; cumulative sums are the reference's up to float rounding,
+ * and tied top-p probabilities are ordered by index. */
+int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* recent, size_t n_recent,
+                        const mivi_sampler_config* cfg, uint64_t* rng_state, uint32_t* token,
+                        void* stream);
+
+/* ---------------------------------------------------------------------
  * Measurement (no counterpart in the reference): reads `bytes` bytes at p
  * (16-byte aligned, bytes % 16 == 0) once with plain coalesced 16-byte loads
  * on the stream and discards them. Its time is the floor for any kernel that

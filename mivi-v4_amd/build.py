@@ -33,7 +33,7 @@ DEVICE_FLAGS = [
 ]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall"]
 
-SOURCES = ["errors.cpp", "synth.cpp", "quant.hip", "gemm.hip", "model.hip"]
+SOURCES = ["errors.cpp", "synth.cpp", "quant.hip", "gemm.hip", "model.hip", "sampler.hip"]
 
 
 def _deps(src: str) -> list[str]:

@@ -91,6 +91,17 @@ class MiviModelInfo(C.Structure):
         ("kv_bytes", C.c_size_t)]
 
 
+class SamplerConfig(C.Structure):
+    """GenerationConfig's sampling fields (config.rs:163-194, defaults there)."""
+    _fields_ = [(n, C.c_float) for n in ("temperature", "top_p", "min_p", "repetition_penalty",
+                                         "presence_penalty", "frequency_penalty")] + [("top_k", C.c_uint32)]
+
+    @classmethod
+    def make(cls, temperature=0.2, top_p=0.9, top_k=40, min_p=0.0, repetition_penalty=1.05,
+             presence_penalty=0.0, frequency_penalty=0.0):
+        return cls(temperature, top_p, min_p, repetition_penalty, presence_penalty, frequency_penalty, top_k)
+
+
 _lib = C.CDLL(LIB_PATH)
 _P, _S, _I = C.c_void_p, C.c_size_t, C.c_int32
 _sig = {
@@ -120,6 +131,7 @@ _sig = {
     "mivi_hip_model_export_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_model_import_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_read_floor": ([_P, _S, _P], _I),
+    "mivi_hip_sample": ([_P, _S, _P, _S, C.POINTER(SamplerConfig), _P, _P, _P], _I),
     "mivi_synth_normal": ([C.c_uint64, C.c_float, C.c_float, _P, _S], None),
     "mivi_synth_quantize": ([_I, _P, _S, _S, _P, _S], _I),
     "mivi_synth_random_weights": ([_I, C.c_uint64, C.c_float, _S, _S, _P, _S], _I),
@@ -242,6 +254,17 @@ def dot_q8_0_f32(q, k_blocks, out, n: int, stream=None):
     po, lo = _dev(out)
     _check(_lib.mivi_hip_dot_q8_0_f32(pq, lq, C.c_void_p(k_blocks.data_ptr()), _nbytes(k_blocks), po, lo, n,
                                       _stream(stream)))
+
+
+def sample(logits, recent, cfg: SamplerConfig, rng_state, token, stream=None):
+    """Sampler::sample (sampler.rs:91-135) on the device: logits (f32 GPU
+    tensor) modified in place, recent (u32/i32 GPU tensor of token ids),
+    rng_state (1-element int64 GPU tensor holding the u64 state), token
+    (1-element int32 GPU tensor) receives the id."""
+    _check(_lib.mivi_hip_sample(C.c_void_p(logits.data_ptr()), logits.numel(),
+                                C.c_void_p(recent.data_ptr()) if recent is not None and recent.numel() else None,
+                                recent.numel() if recent is not None else 0, C.byref(cfg),
+                                C.c_void_p(rng_state.data_ptr()), C.c_void_p(token.data_ptr()), _stream(stream)))
 
 
 def read_floor(buf, nbytes: int, stream=None):

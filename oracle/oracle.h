@@ -118,6 +118,21 @@ void or_apply_rope_direct(float* q, size_t q_len, float* k, size_t k_len,
                           size_t head_dim, size_t pos, float rope_base);
 uint32_t or_argmax(const float* logits, size_t n);                  /* sampler.rs:305-316 */
 
+/* sampler.rs: GenerationConfig's sampling fields (config.rs:163-174) */
+typedef struct {
+    float temperature, top_p, min_p, repetition_penalty, presence_penalty, frequency_penalty;
+    uint32_t top_k;
+} or_sampler_config;
+uint64_t or_sampler_seed(uint64_t seed);                             /* sampler.rs:28-57 */
+float or_random_f32(uint64_t* state);                                /* sampler.rs:70-77 */
+void or_apply_penalties(float* l, size_t n, const uint32_t* recent, size_t nr, float rep,
+                        float presence, float frequency);           /* sampler.rs:219-257 */
+void or_apply_min_p(float* l, size_t n, float min_p);                /* sampler.rs:260-276 */
+void or_apply_top_k(float* l, size_t n, size_t k);                   /* sampler.rs:287-301 */
+/* sampler.rs:91-135 Sampler::sample (logits modified in place) */
+uint32_t or_sample(float* l, size_t n, const uint32_t* recent, size_t nr,
+                   const or_sampler_config* c, uint64_t* rng);
+
 /* --- mivi-model + mivi-kv --- */
 enum { OR_KV_F32 = 0, OR_KV_Q8_0 = 1, OR_KV_F16RT = 100 };
 

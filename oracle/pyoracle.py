@@ -50,6 +50,17 @@ class ModelInfo(C.Structure):
     ]
 
 
+class SamplerConfig(C.Structure):
+    """GenerationConfig's sampling fields (config.rs:163-194; defaults there)."""
+    _fields_ = [(n, C.c_float) for n in ("temperature", "top_p", "min_p", "repetition_penalty",
+                                         "presence_penalty", "frequency_penalty")] + [("top_k", C.c_uint32)]
+
+
+def sampler_config(temperature=0.2, top_p=0.9, top_k=40, min_p=0.0, repetition_penalty=1.05,
+                   presence_penalty=0.0, frequency_penalty=0.0) -> SamplerConfig:
+    return SamplerConfig(temperature, top_p, min_p, repetition_penalty, presence_penalty, frequency_penalty, top_k)
+
+
 _lib = None
 
 
@@ -95,6 +106,15 @@ def lib():
         L.or_rope_rotate.argtypes = [P, S, S, P, P]
         L.or_apply_rope_direct.argtypes = [P, S, P, S, S, S, C.c_float]
         L.or_argmax.argtypes = [P, S]
+        L.or_sampler_seed.argtypes = [C.c_uint64]
+        L.or_sampler_seed.restype = C.c_uint64
+        L.or_random_f32.argtypes = [C.POINTER(C.c_uint64)]
+        L.or_random_f32.restype = C.c_float
+        L.or_apply_penalties.argtypes = [P, S, P, S, C.c_float, C.c_float, C.c_float]
+        L.or_apply_min_p.argtypes = [P, S, C.c_float]
+        L.or_apply_top_k.argtypes = [P, S, S]
+        L.or_sample.argtypes = [P, S, P, S, C.POINTER(SamplerConfig), C.POINTER(C.c_uint64)]
+        L.or_sample.restype = C.c_uint32
         L.or_argmax.restype = C.c_uint32
         L.or_attention.argtypes = [P, P, P, C.c_int, S, S, S, S, P]
         L.or_model_create.argtypes = [P, S, S, C.c_int, C.POINTER(P), C.c_char_p, S]
@@ -239,6 +259,43 @@ def apply_rope_direct(q, k, head_dim, pos, base):
 def argmax(v) -> int:
     v = np.ascontiguousarray(v, np.float32)
     return int(lib().or_argmax(_p(v), v.size))
+
+
+class Rng:
+    """The sampler's xorshift64* state (sampler.rs:28-77)."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(lib().or_sampler_seed(seed))
+
+    def random_f32(self) -> float:
+        return lib().or_random_f32(C.byref(self.state))
+
+
+def apply_penalties(l, recent, rep, presence, frequency):
+    l = np.array(l, np.float32)
+    r = np.ascontiguousarray(recent, np.uint32)
+    lib().or_apply_penalties(_p(l), l.size, _p(r), r.size, rep, presence, frequency)
+    return l
+
+
+def apply_min_p(l, min_p):
+    l = np.array(l, np.float32)
+    lib().or_apply_min_p(_p(l), l.size, min_p)
+    return l
+
+
+def apply_top_k(l, k):
+    l = np.array(l, np.float32)
+    lib().or_apply_top_k(_p(l), l.size, k)
+    return l
+
+
+def sample(logits, recent, cfg: SamplerConfig, rng: Rng):
+    """Sampler::sample (sampler.rs:91-135); returns (token, logits as modified)."""
+    l = np.array(logits, np.float32)
+    r = np.ascontiguousarray(recent, np.uint32)
+    t = lib().or_sample(_p(l), l.size, _p(r) if r.size else None, r.size, C.byref(cfg), C.byref(rng.state))
+    return int(t), l
 
 
 def attention(q, K, V, prec, n_heads, n_kv, hd, seq):

@@ -1,0 +1,148 @@
+"""GPU parity of mivi_hip_sample (Sampler::sample, sampler.rs:91-135) against
+the CPU oracle's restatement on identical logits, penalty windows and seeds.
+
+Bars:
+* the generator state equals the oracle's after every step (the draws are
+  bit-exact);
+* greedy path: the token and the penalised logits equal the oracle's bit for
+  bit;
+* sampling paths: the probabilities left in the logits equal the oracle's up
+  to one common factor (the same exponentials, 1e-6; the normaliser within
+  1e-3: the reference sums the exponentials sequentially in f32, whose
+  rounding error over 65536 terms reaches ~1e-4, the device sums them in a
+  tree), and the token equals the oracle's unless the draw falls within that
+  rounding of a cumulative boundary, which is checked in float64 whenever the
+  tokens differ (at most a quarter of the draws; the reference's own result
+  there depends on its f32 summation order).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+MASK = (1 << 64) - 1
+TOL = 2e-4  # cumulative-sum rounding budget (absolute, probabilities sum to 1)
+
+CONFIGS = {
+    "default": dict(),  # GenerationConfig::default (config.rs:176-194)
+    "greedy_penalised": dict(temperature=0.0, presence_penalty=0.5, frequency_penalty=0.25),
+    "categorical": dict(temperature=1.0, top_p=1.0, top_k=0, repetition_penalty=1.0),
+    "nucleus_min_p": dict(temperature=0.8, top_p=0.95, top_k=0, min_p=0.05, presence_penalty=0.5,
+                          frequency_penalty=0.3),
+    "wide_top_k": dict(temperature=1.5, top_p=1.0, top_k=1000),
+    "top_p_zero": dict(temperature=1.0, top_p=0.0, top_k=0),
+}
+
+
+def draw(state: int):
+    """sampler.rs:70-77: (next state, r)."""
+    state ^= state >> 12
+    state ^= (state << 25) & MASK
+    state ^= state >> 27
+    r = ((state * 0x2545F4914F6CDD1D) & MASK) >> 32
+    return state, float(np.float32((r >> 8) / 16777216.0))
+
+
+def near_boundary(tok, probs, r, top_p):
+    """Whether token tok's cumulative interval lies within TOL of the draw, in
+    the order the reference accumulates (index order; descending for top-p)."""
+    p = probs.astype(np.float64)
+    if top_p < 1.0:
+        n = p.size
+        cutoff = (1.0 - top_p) / (n - 1.0) if n > 1 else 0.0
+        cand = np.nonzero((p >= cutoff) & (p > 0) & np.isfinite(p))[0]
+        order = cand[np.lexsort((cand, -p[cand]))]
+        cum = np.cumsum(p[order])
+        m = int(np.searchsorted(cum, top_p - TOL)) + 1
+        r = r * cum[min(m, cum.size) - 1]
+    else:
+        order = np.arange(p.size)
+        cum = np.cumsum(p)
+    k = int(np.nonzero(order == tok)[0][0])
+    lo = cum[k - 1] if k else 0.0
+    return lo - TOL <= r <= cum[k] + TOL
+
+
+def run_pair(hip, oracle, torch, logits, recent, cfgkw, seed, steps):
+    """steps draws on the device and on the oracle with the same state."""
+    cfg_h = hip.SamplerConfig.make(**cfgkw)
+    cfg_o = oracle.sampler_config(**cfgkw)
+    greedy = cfgkw.get("temperature", 0.2) <= 0.0
+    top_p = cfgkw.get("top_p", 0.9)
+    rng_o = oracle.Rng(seed)
+    st = int(rng_o.state.value)
+    rng_d = torch.tensor([st - (1 << 64) if st >= 1 << 63 else st], dtype=torch.int64, device="cuda")
+    tok_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rec = list(recent)
+    mismatches = 0
+    for s in range(steps):
+        l_d = torch.from_numpy(logits.copy()).cuda()
+        r_d = torch.tensor(rec, dtype=torch.int32, device="cuda") if rec else None
+        hip.sample(l_d, r_d, cfg_h, rng_d, tok_d)
+        torch.cuda.synchronize()
+        state0 = int(rng_o.state.value)
+        t_o, l_o = oracle.sample(logits, rec, cfg_o, rng_o)
+        t_d = int(tok_d.item())
+        assert (int(rng_d.item()) & MASK) == rng_o.state.value, (cfgkw, s)
+        got = l_d.cpu().numpy()
+        if greedy:
+            assert t_d == t_o, (cfgkw, seed, s, t_d, t_o)
+            assert np.array_equal(got, l_o)
+        else:
+            nz = l_o > 1e-30
+            assert np.array_equal(got > 1e-30, nz)
+            ratio = got[nz].astype(np.float64) / l_o[nz]
+            assert abs(ratio.mean() - 1.0) < 1e-3 and np.ptp(ratio) < 2e-6 * max(1.0, ratio.mean())
+            if t_d != t_o:
+                mismatches += 1
+                r = draw(state0)[1]
+                assert near_boundary(t_d, l_o, r, top_p) and near_boundary(t_o, l_o, r, top_p), (cfgkw, s, t_d, t_o)
+        rec = (rec + [t_o])[-64:]  # RECENT_TOKENS_WINDOW (config.rs:11)
+    # full-vocabulary categorical draws over 65536 tokens land within rounding
+    # of a boundary most often (about one in seven here)
+    assert mismatches <= steps // 4, (cfgkw, mismatches)
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+@pytest.mark.parametrize("n", [5, 1000, 65536])
+def test_sample_matches_oracle(hip, oracle, torch_mod, name, n):
+    rng = np.random.default_rng(n + len(name))
+    logits = (rng.standard_normal(n) * 3).astype(np.float32)
+    logits[rng.integers(0, n, max(1, n // 50))] = -np.inf
+    recent = rng.integers(0, n, min(n, 40)).tolist()
+    run_pair(hip, oracle, torch_mod, logits, recent, CONFIGS[name], 1234 + n, 64)
+
+
+def test_reference_cases_on_device(hip, oracle, torch_mod):
+    torch = torch_mod
+    # sampler.rs:340-350: zero temperature still applies penalties
+    l = torch.tensor([5.0, 4.0], device="cuda")
+    rng = torch.tensor([1], dtype=torch.int64, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    hip.sample(l, torch.tensor([0], dtype=torch.int32, device="cuda"),
+               hip.SamplerConfig.make(temperature=0.0, presence_penalty=2.0), rng, tok)
+    assert int(tok.item()) == 1
+    # sampler.rs:352-363: top-p reaches past the first 1024 tokens
+    count = 2048
+    p = (count - np.arange(count)).astype(np.float64)
+    p /= p.sum()
+    cfg = hip.SamplerConfig.make(temperature=1.0, top_p=0.9, top_k=0, repetition_penalty=1.0)
+    rng = torch.tensor([1], dtype=torch.int64, device="cuda")
+    seen = []
+    for _ in range(256):
+        l = torch.from_numpy(np.log(p).astype(np.float32)).cuda()
+        hip.sample(l, None, cfg, rng, tok)
+        seen.append(int(tok.item()))
+    assert max(seen) >= 1024
+    # an all -inf row: the softmax's uniform branch (math.rs:43-48), then top-p
+    l = torch.full((8,), float("-inf"), device="cuda")
+    hip.sample(l, None, hip.SamplerConfig.make(temperature=1.0, top_k=0), rng, tok)
+    assert np.all(l.cpu().numpy() == np.float32(0.125))
+
+
+def test_sample_rejects_null_arguments(hip, torch_mod):
+    # validated on the host before any launch
+    assert hip._lib.mivi_hip_sample(None, 4, None, 0, None, None, None, None) != 0
+    assert hip.last_error().code == 101
