@@ -158,7 +158,7 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
     t_chunked = time.perf_counter() - t1
     log(f"decode: prefill {prefill} tokens in {t_chunked * 1e3:.0f} ms chunked (tiles of 512), "
         f"{t_token:.2f} s token by token")
-    state = m.export_state(prefill) if cpu_budget_s > 0 else None
+    state = m.export_state(prefill)
     torch.cuda.synchronize()
     t2 = time.perf_counter()
     toks = m.generate_greedy([int(prompt[-1])], [prefill], steps)
@@ -171,6 +171,21 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
                bytes_per_token=wb + kv_per_tok * mean_t, weight_bytes_per_token=wb, kv_precision="f16",
                working_ctx=ctx, first_tokens=[int(v) for v in toks[:8, 0]])
     out["gbs"] = out["bytes_per_token"] * out["tok_s"] / 1e9
+    # the same steps from the same state with Sampler::sample on the device
+    # (GenerationConfig::default: temperature 0.2, top-p 0.9, top-k 40,
+    # repetition penalty 1.05) in place of the greedy argmax
+    cfg = hip.SamplerConfig.make()
+    m.import_state(prefill, *state)
+    m.generate([int(prompt[-1])], [prefill], 4, cfg, [1])  # graph capture
+    m.import_state(prefill, *state)
+    torch.cuda.synchronize()
+    t4 = time.perf_counter()
+    stoks = m.generate([int(prompt[-1])], [prefill], steps, cfg, [1])
+    ds = time.perf_counter() - t4
+    out["sampled"] = dict(tok_s=steps / ds, ms_per_token=1e3 * ds / steps,
+                          config="GenerationConfig::default (T 0.2, top-p 0.9, top-k 40, repetition 1.05), seed 1",
+                          first_tokens=[int(v) for v in stoks[:8, 0]])
+    log(f"decode: {steps / ds:.1f} tok/s with the device sampler (default GenerationConfig)")
     if cpu_budget_s > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import pyoracle

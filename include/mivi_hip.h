@@ -247,6 +247,35 @@ int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* recent, size_t 
                         const mivi_sampler_config* cfg, uint64_t* rng_state, uint32_t* token,
                         void* stream);
 
+/* Sampler::sample (sampler.rs:91-135) on `rows` rows at once, one sampler
+ * per row (the per-sequence samplers of a batch): row b's logits at
+ * logits + b * row_stride, its penalty window at recent + b * recent_stride
+ * (n_recent ids each), its state rng_states[b], its token tokens[b]; the same
+ * results as mivi_hip_sample on each row. Spread over the whole device (a
+ * chunk kernel over 1024-logit chunks, then one workgroup per row over the
+ * chunks' top-k candidates when top_k <= 128), with `workspace` (device,
+ * 4-byte aligned) of at least mivi_hip_sample_rows_workspace(n, rows)
+ * bytes, which calls running at once must not share. Asynchronous on the
+ * stream. rows <= 65535. */
+size_t mivi_hip_sample_rows_workspace(size_t n, size_t rows);
+int32_t mivi_hip_sample_rows(float* logits, size_t n, size_t rows, size_t row_stride,
+                             const uint32_t* recent, size_t n_recent, size_t recent_stride,
+                             const mivi_sampler_config* cfg, uint64_t* rng_states, uint32_t* tokens,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* The generation loop of model.rs:1130-1180 on the device for `batch`
+ * sequences starting from tokens[b] at pos[b]: n_steps decode steps, each
+ * sampling every sequence's next token with Sampler::sample (its penalty
+ * window = its last 64 generated tokens, RECENT_TOKENS_WINDOW; seeds[b] per
+ * sequence, 0 -> the reference's fallback seed; the eos_ids (at most 4) are
+ * suppressed on the first token as the loop does). Stopping at an
+ * end-of-sequence token is left to the caller: tokens_out[step * batch + b]
+ * holds all n_steps tokens. Errors as mivi_hip_model_generate_greedy. */
+int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const uint32_t* tokens,
+                                const size_t* pos, size_t n_steps, const mivi_sampler_config* cfg,
+                                const uint64_t* seeds, const uint32_t* eos_ids, size_t n_eos,
+                                uint32_t* tokens_out);
+
 /* ---------------------------------------------------------------------
  * Measurement (no counterpart in the reference): reads `bytes` bytes at p
  * (16-byte aligned, bytes % 16 == 0) once with plain coalesced 16-byte loads

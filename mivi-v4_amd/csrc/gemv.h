@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/mivi_hip.h"
+
 namespace mivi {
 
 // How a workgroup forms the activation vector it stages in LDS.
@@ -90,5 +92,22 @@ int32_t launch_rows(int32_t ggml_type, int prologue, const GemvArgs& a, hipStrea
 // rows x cols Q6_K (cols 2048/4096/8192) into the packed layout: row quads
 // when quad_layout(rows, cols), unit planes otherwise
 int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
+
+// End-of-sequence ids suppressed on a generation's first token.
+struct SampleEos {
+    uint32_t id[4];
+    int n;
+};
+
+// Sampler::sample for sequences seq0 .. seq0 + batch - 1 of a decode step
+// (logits of sequence b at logits + b * lstride), penalty window = the last
+// `window` tokens of history[step * hstride + seq]; writes tok[b] and the
+// history at *step. rng: one xorshift64* state per sequence (rng[b]). ws:
+// sample_seq_workspace(n, batch) bytes of device memory (4-byte aligned);
+// the logits are left penalised and divided by the temperature.
+size_t sample_seq_workspace(size_t n, size_t batch);
+int32_t launch_sample_seq(float* logits, int64_t lstride, int n, uint32_t* history, int hstride, int seq0, int batch,
+                          int window, const int* step, const SampleEos& eos, const mivi_sampler_config& cfg,
+                          uint64_t* rng, uint32_t* tok, void* ws, hipStream_t s);
 
 }  // namespace mivi

@@ -1170,6 +1170,14 @@ struct mivi_model {
     int nsplit = 1;
     hipGraphExec_t graph = nullptr;
     size_t graph_batch = 0;
+    // sampled generation: per-sequence xorshift64* states and the step graph
+    // captured for one (batch, config, end-of-sequence ids)
+    uint64_t* rng = nullptr;  // [max_batch]
+    uint8_t* samp_ws = nullptr;  // the sampler's candidates, sample_seq_workspace(vocab, max_batch) bytes
+    hipGraphExec_t graph_s = nullptr;
+    size_t graph_s_batch = 0;
+    mivi_sampler_config graph_s_cfg{};
+    SampleEos graph_s_eos{};
     // chunked prefill (PrefillStrategy::Chunked, model.rs:519-536): rows per
     // tile (0 = token by token) and the tile buffers, allocated on first use
     size_t prefill_tile = 0, pf_cap = 0;
@@ -1180,6 +1188,7 @@ struct mivi_model {
 
     ~mivi_model() {
         if (graph) hipGraphExecDestroy(graph);
+        if (graph_s) hipGraphExecDestroy(graph_s);
         for (void* p : allocs) hipFree(p);
         if (stream) hipStreamDestroy(stream);
     }
@@ -1817,7 +1826,10 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         }
     }
     c.kv_bytes = 2 * max_batch * m->strides.kv;
-    if ((rc = m->alloc(&m->ctrl, 1)) || (rc = m->alloc(&m->history, c.max_seq_len * max_batch))) return fail(rc);
+    if ((rc = m->alloc(&m->ctrl, 1)) || (rc = m->alloc(&m->history, c.max_seq_len * max_batch)) ||
+        (rc = m->alloc(&m->rng, max_batch)) ||
+        (rc = m->alloc(&m->samp_ws, sample_seq_workspace(c.vocab_size, max_batch))))
+        return fail(rc);
     if (hipStreamSynchronize(m->stream) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
         return fail(set_error(MIVI_ERR_HIP, "model setup failed"));
     m->info = c;
@@ -1958,6 +1970,72 @@ extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, c
         m->graph_batch = batch;
     }
     for (size_t i = 0; i < n_steps; i++) MIVI_HIP_CHECK(hipGraphLaunch(m->graph, m->stream));
+    std::vector<uint32_t> hist(n_steps * m->info.max_batch);
+    MIVI_HIP_CHECK(hipMemcpyAsync(hist.data(), m->history, hist.size() * 4, hipMemcpyDeviceToHost, m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    for (size_t i = 0; i < n_steps; i++)
+        for (size_t b = 0; b < batch; b++) tokens_out[i * batch + b] = hist[i * m->info.max_batch + b];
+    return clear_error();
+}
+
+// The generation loop of model.rs:1130-1180 with Sampler::sample on the
+// device: each step runs the decode step of the batch and samples every
+// sequence's next token from its logits (penalty window = its last 64
+// generated tokens, RECENT_TOKENS_WINDOW, config.rs:11; the end-of-sequence
+// ids suppressed on the first token). Stopping at an end-of-sequence token
+// is the caller's: all n_steps tokens are produced.
+extern "C" int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const uint32_t* tokens, const size_t* pos,
+                                           size_t n_steps, const mivi_sampler_config* cfg, const uint64_t* seeds,
+                                           const uint32_t* eos_ids, size_t n_eos, uint32_t* tokens_out) {
+    if (!m || batch == 0 || batch > m->info.max_batch || !tokens || !pos || !cfg || !seeds ||
+        (n_steps && !tokens_out) || (n_eos && !eos_ids) || n_eos > 4)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    for (size_t b = 0; b < batch; b++) {
+        int32_t rc = check_tok_pos(m, tokens[b], pos[b]);
+        if (rc) return rc;
+        if (pos[b] + n_steps > m->info.max_seq_len)
+            return set_error(MIVI_ERR_CONTEXT_OVERFLOW, "Context overflow: current pos %zu >= max_seq_len %zu",
+                             pos[b] + n_steps - 1, m->info.max_seq_len);
+    }
+    if (n_steps == 0) return clear_error();
+    for (size_t b = 0; b < batch; b++) {
+        int32_t rc = set_ctrl(m, b, tokens[b], pos[b]);
+        if (rc) return rc;
+    }
+    // Sampler::with_seed / set_seed (sampler.rs:28-57): seed 0 -> FALLBACK_RNG_SEED
+    std::vector<uint64_t> st(batch);
+    for (size_t b = 0; b < batch; b++) st[b] = seeds[b] ? seeds[b] : 0x853c49e6748fea9bULL;
+    MIVI_HIP_CHECK(hipMemcpyAsync(m->rng, st.data(), batch * 8, hipMemcpyHostToDevice, m->stream));
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step, 0);
+    SampleEos eos{};
+    eos.n = (int)n_eos;
+    for (size_t i = 0; i < n_eos; i++) eos.id[i] = eos_ids[i];
+    if (!m->graph_s || m->graph_s_batch != batch || memcmp(&m->graph_s_cfg, cfg, sizeof(*cfg)) ||
+        memcmp(&m->graph_s_eos, &eos, sizeof(eos))) {
+        if (m->graph_s) {
+            hipGraphExecDestroy(m->graph_s);
+            m->graph_s = nullptr;
+        }
+        const mivi_model_info& c = m->info;
+        hipGraph_t gr;
+        MIVI_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        int32_t rc = enqueue_step(m, 0, batch, true, false, m->stream, true, 0, c.n_layers, true);
+        if (!rc)
+            rc = launch_sample_seq(m->seqs[0].logits, (int64_t)m->strides.logits, (int)c.vocab_size, m->history,
+                                   (int)c.max_batch, 0, (int)batch, 64, &m->ctrl->step, eos, *cfg, m->rng,
+                                   &m->ctrl->tok[0], m->samp_ws, m->stream);
+        if (!rc) hipLaunchKernelGGL(step_counter_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step);
+        hipError_t e = hipStreamEndCapture(m->stream, &gr);
+        if (rc) return rc;
+        if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&m->graph_s, gr, nullptr, nullptr, 0);
+        hipGraphDestroy(gr);
+        if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "graph instantiate failed: %s", hipGetErrorString(e));
+        m->graph_s_batch = batch;
+        m->graph_s_cfg = *cfg;
+        m->graph_s_eos = eos;
+    }
+    for (size_t i = 0; i < n_steps; i++) MIVI_HIP_CHECK(hipGraphLaunch(m->graph_s, m->stream));
     std::vector<uint32_t> hist(n_steps * m->info.max_batch);
     MIVI_HIP_CHECK(hipMemcpyAsync(hist.data(), m->history, hist.size() * 4, hipMemcpyDeviceToHost, m->stream));
     MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));

@@ -132,6 +132,9 @@ _sig = {
     "mivi_hip_model_import_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_read_floor": ([_P, _S, _P], _I),
     "mivi_hip_sample": ([_P, _S, _P, _S, C.POINTER(SamplerConfig), _P, _P, _P], _I),
+    "mivi_hip_sample_rows_workspace": ([_S, _S], _S),
+    "mivi_hip_sample_rows": ([_P, _S, _S, _S, _P, _S, _S, C.POINTER(SamplerConfig), _P, _P, _P, _S, _P], _I),
+    "mivi_hip_model_generate": ([_P, _S, _P, _P, _S, C.POINTER(SamplerConfig), _P, _P, _S, _P], _I),
     "mivi_synth_normal": ([C.c_uint64, C.c_float, C.c_float, _P, _S], None),
     "mivi_synth_quantize": ([_I, _P, _S, _S, _P, _S], _I),
     "mivi_synth_random_weights": ([_I, C.c_uint64, C.c_float, _S, _S, _P, _S], _I),
@@ -265,6 +268,28 @@ def sample(logits, recent, cfg: SamplerConfig, rng_state, token, stream=None):
                                 C.c_void_p(recent.data_ptr()) if recent is not None and recent.numel() else None,
                                 recent.numel() if recent is not None else 0, C.byref(cfg),
                                 C.c_void_p(rng_state.data_ptr()), C.c_void_p(token.data_ptr()), _stream(stream)))
+
+
+def sample_rows(logits, recent, cfg: SamplerConfig, rng_states, tokens, stream=None):
+    """Sampler::sample on every row of logits (2-D f32 GPU tensor, rows
+    contiguous), one sampler per row: recent (2-D u32/i32 GPU tensor, row b =
+    row b's penalty window, or None), rng_states (int64 GPU tensor, one u64
+    state per row), tokens (int32 GPU tensor) receives the ids. The same
+    results as sample() on each row; the workspace comes from torch."""
+    import torch
+
+    rows, n = logits.shape
+    if logits.stride(1) != 1 or (recent is not None and recent.numel() and recent.stride(1) != 1):
+        raise ValueError("rows must be contiguous")
+    ws_bytes = _lib.mivi_hip_sample_rows_workspace(n, rows)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=logits.device)
+    has_recent = recent is not None and recent.numel() > 0
+    _check(_lib.mivi_hip_sample_rows(C.c_void_p(logits.data_ptr()), n, rows, logits.stride(0),
+                                     C.c_void_p(recent.data_ptr()) if has_recent else None,
+                                     recent.shape[1] if has_recent else 0, recent.stride(0) if has_recent else 0,
+                                     C.byref(cfg), C.c_void_p(rng_states.data_ptr()), C.c_void_p(tokens.data_ptr()),
+                                     C.c_void_p(ws.data_ptr()), ws_bytes, _stream(stream)))
+    return ws
 
 
 def read_floor(buf, nbytes: int, stream=None):

@@ -71,6 +71,21 @@ class Model:
                                                    out.ctypes.data_as(C.c_void_p)), ModelError)
         return out
 
+    def generate(self, tokens, pos, n_steps: int, cfg, seeds, eos_ids=()) -> np.ndarray:
+        """The generation loop with Sampler::sample on the device (cfg: a
+        SamplerConfig; seeds: one per sequence). Returns [n_steps, batch] tokens."""
+        t = np.ascontiguousarray(np.atleast_1d(tokens), np.uint32)
+        p = np.ascontiguousarray(np.atleast_1d(pos), np.uint64)
+        sd = np.ascontiguousarray(np.atleast_1d(seeds), np.uint64)
+        eo = np.ascontiguousarray(np.atleast_1d(np.asarray(eos_ids, np.uint32)), np.uint32)
+        out = np.empty((n_steps, t.size), np.uint32)
+        _check(_lib.mivi_hip_model_generate(self._h, t.size, t.ctypes.data_as(C.c_void_p),
+                                            p.ctypes.data_as(C.c_void_p), n_steps, C.byref(cfg),
+                                            sd.ctypes.data_as(C.c_void_p),
+                                            eo.ctypes.data_as(C.c_void_p) if eo.size else None, eo.size,
+                                            out.ctypes.data_as(C.c_void_p)), ModelError)
+        return out
+
     def kv_row_bytes(self) -> int:
         kvd = self.info.kv_dim
         return {0: 4 * kvd, 2: 2 * kvd, 1: kvd // 32 * 34}[self.info.kv_precision]

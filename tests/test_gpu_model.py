@@ -299,3 +299,68 @@ def test_full_width_q8_kv_matrix_core_attention_matches_oracle(hip, oracle):
             tok = oracle.argmax(orc[b].forward(tok, T + 1 + i))
             want.append(tok)
         assert list(got[:, b]) == want, (b, list(got[:, b]), want)
+
+
+def host_sampled_loop(oracle, m, tok, pos, n_steps, cfgkw, seed, eos):
+    """The generation loop of model.rs:1130-1180 on the host: the device
+    decode step's logits (forward), end-of-sequence ids suppressed on the first
+    token, then the oracle's Sampler::sample with the last 64 generated tokens."""
+    cfg = oracle.sampler_config(**cfgkw)
+    rng = oracle.Rng(seed)
+    out, recent = [], []
+    for s in range(n_steps):
+        logits = m.forward(tok, pos + s).copy()
+        if s == 0:
+            logits[list(eos)] = -np.inf
+        tok, _ = oracle.sample(logits, recent, cfg, rng)
+        out.append(tok)
+        recent = (recent + [tok])[-64:]
+    return np.array(out, np.uint32)
+
+
+def test_sampled_generation_matches_host_loop(hip, oracle, small_img):
+    # Sampler::sample inside the captured decode step against the host loop
+    # over the same device logits: the default GenerationConfig, a wider
+    # nucleus with min-p and penalties, and zero temperature (greedy with
+    # penalties)
+    prompt = [3, 17, 250, 9, 41, 77]
+    eos = (2, 5)
+    for cfgkw, seed in ((dict(), 7), (dict(temperature=0.9, top_p=0.95, top_k=0, min_p=0.02,
+                                          presence_penalty=0.3, frequency_penalty=0.2), 99),
+                        (dict(temperature=0.0, repetition_penalty=1.3), 1)):
+        m1 = hip.Model(small_img, max_ctx=128)
+        m1.prefill(prompt[:-1])
+        got = m1.generate([prompt[-1]], [len(prompt) - 1], 40, hip.SamplerConfig.make(**cfgkw), [seed], eos)[:, 0]
+        m2 = hip.Model(small_img, max_ctx=128)
+        m2.prefill(prompt[:-1])
+        ref = host_sampled_loop(oracle, m2, prompt[-1], len(prompt) - 1, 40, cfgkw, seed, eos)
+        assert np.array_equal(got, ref), (cfgkw, got, ref)
+        assert not set(eos) & {int(got[0])}
+
+
+def test_sampled_generation_greedy_config_equals_generate_greedy(hip, small_img):
+    prompt = [11, 12, 13, 14]
+    m1 = hip.Model(small_img, max_ctx=128)
+    m1.prefill(prompt[:-1])
+    g = m1.generate_greedy([prompt[-1]], [len(prompt) - 1], 32)[:, 0]
+    m2 = hip.Model(small_img, max_ctx=128)
+    m2.prefill(prompt[:-1])
+    cfg = hip.SamplerConfig.make(temperature=0.0, repetition_penalty=1.0)
+    s = m2.generate([prompt[-1]], [len(prompt) - 1], 32, cfg, [5])[:, 0]
+    assert np.array_equal(g, s)
+
+
+def test_sampled_generation_batch_matches_single_sequences(hip, small_img):
+    B = 3
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 1024, 5 + 2 * b) for b in range(B)]
+    cfg = hip.SamplerConfig.make(temperature=0.7, top_p=0.9, top_k=50)
+    mb = hip.Model(small_img, max_ctx=128, max_batch=B)
+    for b, pr in enumerate(prompts):
+        mb.prefill(pr[:-1], seq=b)
+    out = mb.generate([int(p[-1]) for p in prompts], [len(p) - 1 for p in prompts], 24, cfg, [10 + b for b in range(B)])
+    for b, pr in enumerate(prompts):
+        m1 = hip.Model(small_img, max_ctx=128)
+        m1.prefill(pr[:-1])
+        one = m1.generate([int(pr[-1])], [len(pr) - 1], 24, cfg, [10 + b])[:, 0]
+        assert np.array_equal(out[:, b], one), b

@@ -1,5 +1,9 @@
-"""GPU parity of mivi_hip_sample (Sampler::sample, sampler.rs:91-135) against
-the CPU oracle's restatement on identical logits, penalty windows and seeds.
+"""GPU parity of mivi_hip_sample and mivi_hip_sample_rows (Sampler::sample,
+sampler.rs:91-135) against the CPU oracle's restatement on identical logits,
+penalty windows and seeds. The rows entry point runs the split path (chunk
+kernel + pick kernel over the chunks' top-k candidates) when top_k <= 128 and
+the whole-row steps otherwise; the cases below reach both, and the fallback
+from the split path when ties overflow a chunk's candidates.
 
 Bars:
 * the generator state equals the oracle's after every step (the draws are
@@ -33,6 +37,7 @@ CONFIGS = {
                           frequency_penalty=0.3),
     "wide_top_k": dict(temperature=1.5, top_p=1.0, top_k=1000),
     "top_p_zero": dict(temperature=1.0, top_p=0.0, top_k=0),
+    "min_p_top_k": dict(temperature=0.7, top_p=0.8, top_k=64, min_p=0.2, presence_penalty=0.3),
 }
 
 
@@ -65,7 +70,14 @@ def near_boundary(tok, probs, r, top_p):
     return lo - TOL <= r <= cum[k] + TOL
 
 
-def run_pair(hip, oracle, torch, logits, recent, cfgkw, seed, steps):
+def device_sample(hip, torch, api, l_d, r_d, cfg_h, rng_d, tok_d):
+    if api == "row":
+        hip.sample(l_d, r_d, cfg_h, rng_d, tok_d)
+    else:
+        hip.sample_rows(l_d.view(1, -1), None if r_d is None else r_d.view(1, -1), cfg_h, rng_d, tok_d)
+
+
+def run_pair(hip, oracle, torch, logits, recent, cfgkw, seed, steps, api="row"):
     """steps draws on the device and on the oracle with the same state."""
     cfg_h = hip.SamplerConfig.make(**cfgkw)
     cfg_o = oracle.sampler_config(**cfgkw)
@@ -80,7 +92,7 @@ def run_pair(hip, oracle, torch, logits, recent, cfgkw, seed, steps):
     for s in range(steps):
         l_d = torch.from_numpy(logits.copy()).cuda()
         r_d = torch.tensor(rec, dtype=torch.int32, device="cuda") if rec else None
-        hip.sample(l_d, r_d, cfg_h, rng_d, tok_d)
+        device_sample(hip, torch, api, l_d, r_d, cfg_h, rng_d, tok_d)
         torch.cuda.synchronize()
         state0 = int(rng_o.state.value)
         t_o, l_o = oracle.sample(logits, rec, cfg_o, rng_o)
@@ -105,14 +117,82 @@ def run_pair(hip, oracle, torch, logits, recent, cfgkw, seed, steps):
     assert mismatches <= steps // 4, (cfgkw, mismatches)
 
 
+@pytest.mark.parametrize("api", ["row", "rows"])
 @pytest.mark.parametrize("name", list(CONFIGS))
 @pytest.mark.parametrize("n", [5, 1000, 65536])
-def test_sample_matches_oracle(hip, oracle, torch_mod, name, n):
+def test_sample_matches_oracle(hip, oracle, torch_mod, name, n, api):
     rng = np.random.default_rng(n + len(name))
     logits = (rng.standard_normal(n) * 3).astype(np.float32)
     logits[rng.integers(0, n, max(1, n // 50))] = -np.inf
     recent = rng.integers(0, n, min(n, 40)).tolist()
-    run_pair(hip, oracle, torch_mod, logits, recent, CONFIGS[name], 1234 + n, 64)
+    run_pair(hip, oracle, torch_mod, logits, recent, CONFIGS[name], 1234 + n, 64, api)
+
+
+@pytest.mark.parametrize("name", ["default", "categorical", "min_p_top_k", "greedy_penalised"])
+def test_rows_ragged_length(hip, oracle, torch_mod, name):
+    # a row length that leaves the last chunk partial and needs 69 chunks
+    n = 70001
+    rng = np.random.default_rng(7 + len(name))
+    logits = (rng.standard_normal(n) * 2).astype(np.float32)
+    recent = rng.integers(0, n, 64).tolist()
+    run_pair(hip, oracle, torch_mod, logits, recent, CONFIGS[name], 99, 24, "rows")
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.3])
+def test_rows_ties(hip, oracle, torch_mod, scale):
+    # few distinct logits: at scale 1 about 70 ties per chunk at or above its
+    # 40th value, handed on; at scale 0.3 about 500, more than a chunk may hand
+    # on, and the row runs the whole-row steps
+    n = 65536
+    rng = np.random.default_rng(5)
+    logits = np.floor(rng.standard_normal(n) * scale + 0.5).astype(np.float32)
+    cfg = dict(temperature=1.0, top_p=0.9, top_k=40)
+    run_pair(hip, oracle, torch_mod, logits, [], cfg, 17, 16, "rows")
+
+
+@pytest.mark.parametrize("name", ["default", "categorical", "greedy_penalised", "min_p_top_k"])
+def test_rows_batch_independent(hip, oracle, torch_mod, name):
+    """Three rows at once, each with its own logits, window and state, against
+    the oracle row by row."""
+    torch = torch_mod
+    n, rows, steps = 65536, 3, 12
+    rng = np.random.default_rng(11 + len(name))
+    logits = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    recent = rng.integers(0, n, (rows, 40)).astype(np.int32)
+    cfgkw = CONFIGS[name]
+    cfg_h = hip.SamplerConfig.make(**cfgkw)
+    cfg_o = oracle.sampler_config(**cfgkw)
+    seeds = [5, 0, 1 << 63]
+    rng_o = [oracle.Rng(s) for s in seeds]
+    st = [int(r.state.value) for r in rng_o]
+    rng_d = torch.tensor([s - (1 << 64) if s >= 1 << 63 else s for s in st], dtype=torch.int64, device="cuda")
+    tok_d = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    greedy = cfgkw.get("temperature", 0.2) <= 0.0
+    top_p = cfgkw.get("top_p", 0.9)
+    mismatches = 0
+    for s in range(steps):
+        l_d = torch.from_numpy(logits.copy()).cuda()
+        hip.sample_rows(l_d, torch.from_numpy(recent).cuda(), cfg_h, rng_d, tok_d)
+        torch.cuda.synchronize()
+        got_l = l_d.cpu().numpy()
+        got_t = tok_d.cpu().numpy()
+        got_s = rng_d.cpu().numpy()
+        for b in range(rows):
+            state0 = int(rng_o[b].state.value)
+            t_o, l_o = oracle.sample(logits[b], recent[b].tolist(), cfg_o, rng_o[b])
+            assert (int(got_s[b]) & MASK) == rng_o[b].state.value, (name, s, b)
+            if greedy:
+                assert int(got_t[b]) == t_o and np.array_equal(got_l[b], l_o), (name, s, b)
+            else:
+                nz = l_o > 1e-30
+                assert np.array_equal(got_l[b] > 1e-30, nz)
+                ratio = got_l[b][nz].astype(np.float64) / l_o[nz]
+                assert abs(ratio.mean() - 1.0) < 1e-3 and np.ptp(ratio) < 2e-6 * max(1.0, ratio.mean())
+                if int(got_t[b]) != t_o:
+                    mismatches += 1
+                    r = draw(state0)[1]
+                    assert near_boundary(int(got_t[b]), l_o, r, top_p) and near_boundary(t_o, l_o, r, top_p)
+    assert mismatches <= rows * steps // 4, (name, mismatches)
 
 
 def test_reference_cases_on_device(hip, oracle, torch_mod):
@@ -145,4 +225,6 @@ def test_reference_cases_on_device(hip, oracle, torch_mod):
 def test_sample_rejects_null_arguments(hip, torch_mod):
     # validated on the host before any launch
     assert hip._lib.mivi_hip_sample(None, 4, None, 0, None, None, None, None) != 0
+    assert hip.last_error().code == 101
+    assert hip._lib.mivi_hip_sample_rows(None, 4, 1, 4, None, 0, 0, None, None, None, None, 0, None) != 0
     assert hip.last_error().code == 101
