@@ -295,6 +295,34 @@ def batched_decode_bench(torch, hip, batch, ctx, steps):
     return res
 
 
+def sampler_bench(torch, hip, calls):
+    """Sampler::sample on one row of 65536 logits (N(0, 9), a 64-token penalty
+    window) with GenerationConfig::default: the split path (mivi_hip_sample_rows,
+    the generation loop's) and the whole-row path (mivi_hip_sample), in µs per
+    call between HIP events on the stream both run on."""
+    n = 65536
+    g = torch.Generator(device="cuda").manual_seed(5)
+    base = torch.randn(n, device="cuda", generator=g) * 3
+    rec = torch.randint(0, n, (1, 64), dtype=torch.int32, device="cuda", generator=g)
+    rng = torch.tensor([1], dtype=torch.int64, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = {"n": n, "config": "GenerationConfig::default", "calls": calls}
+    for name, fn in (("split_us", lambda l: hip.sample_rows(l.view(1, -1), rec, cfg, rng, tok)),
+                     ("whole_row_us", lambda l: hip.sample(l, rec[0], cfg, rng, tok))):
+        cfg = hip.SamplerConfig.make()
+        rows = [base.clone() for _ in range(calls)]
+        fn(base.clone())
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for l in rows:
+            fn(l)
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / calls
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,6 +383,10 @@ def main():
         log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['gbs']:.0f} GB/s)"
             + (f", CPU {dec['cpu_tok_s']:.2f} tok/s" if "cpu_tok_s" in dec else ""))
         extra["decode_config4"] = dec
+        sm = sampler_bench(torch, hip, 50)
+        log(f"sampler (65536 logits, default config): {sm['split_us']:.1f} us split path, "
+            f"{sm['whole_row_us']:.1f} us whole row")
+        extra["sampler"] = sm
     if not a.no_decode and not a.no_config5:
         c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps)
         log(f"config 5: {c5['tok_s']:.0f} tok/s over 8 sequences, {c5['ms_per_step']:.2f} ms per step")
