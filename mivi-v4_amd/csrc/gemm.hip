@@ -7,7 +7,8 @@
 //                      of two 2^-e (so that |x| <= 1), splits it into fp16
 //                      hi + lo (x = hi + lo to about 2^-22 relative) and forms
 //                      the fp32 sums of each 32-value sub-block, also split;
-//   gemm_q4k_kernel    128 x 128 output tiles, v_mfma_f32_32x32x16_f16. The
+//   gemm_q4k_kernel    64 x 256 output tiles (input rows x weight rows),
+//                      v_mfma_f32_32x32x16_f16. The
 //                      B operand is sc*q of the Q4_K sub-block, an integer
 //                      <= 945 and so exact in fp16; one MFMA chain per 256-value
 //                      super-block gives sum(sc q x), folded into the fp32
@@ -35,7 +36,7 @@ using namespace mivi;
 namespace {
 
 constexpr int kMfmaMinBatch = 16;
-constexpr int kTm = 64, kTn = 128;  // output tile (m = input rows, n = weight rows)
+constexpr int kTm = 64;             // input rows of a GEMM tile
 constexpr int kTk = 64;             // k-tile: one Q4_K group (a sub-block pair)
 constexpr int kXs = kTk + 8;        // padded LDS row (halves) of an x or B tile
 
@@ -181,41 +182,55 @@ __device__ __forceinline__ half8 nib8_times(uint32_t w0, uint32_t w1, bool high,
     return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
 }
 
-// grid = (ceil(N / 128), Mp / 64), 256 threads = 2 x 2 waves of 32 input
-// rows x 64 weight rows (two 32 x 32 MFMA tiles each). Per 64-value k-tile
-// the workgroup stages x (fp16 hi and lo, 16 KB) and builds the fp16 B
+// grid = (ceil(N / 256), Mp / 64), 512 threads = 8 waves: wave w computes
+// input rows 32 (w & 1) .. +32 of the tile against weight rows 64 (w >> 1)
+// .. +64 (two 32 x 32 MFMA tiles). Per 64-value k-tile the workgroup stages x
+// (fp16 hi and lo, 16 KB, shared by the eight waves) and builds the fp16 B
 // operand sc*q once into LDS (two threads per weight row, from qs bytes and
-// scales held in registers), so no wave repeats another's conversion. The
-// loop is bound by load latency, not by the matrix cores: each tile's bytes
-// are loaded three tiles ahead into one of three register stages. About
-// 41 KB of LDS: two workgroups (eight waves) per CU.
+// scales held in registers), so no wave repeats another's conversion. LDS
+// holds two k-tiles: while the waves run the products of tile t from one
+// buffer they build tile t + 1 in the other, so a k-tile costs one barrier,
+// and each tile's bytes are loaded two tiles ahead into one of three
+// register stages. 120 KB of LDS: one workgroup (eight waves) per CU.
+constexpr int kGT = 512;  // threads of a GEMM workgroup
+constexpr int kGN = 256;  // weight rows of its tile
+
 struct GemmStage {
-    u32x4 xh[2], xl[2];  // x chunks: rows c/8, chunk c%8 for c = tid, tid + 256
-    u32x4 qs, hdr, ps;    // 16 qs bytes of weight row tid/2; its block header; sub-block sums
+    u32x4 xh, xl;       // x chunk of 8 values: input row tid/8, chunk tid%8
+    u32x4 qs, hdr, ps;  // 16 qs bytes of weight row bn; its block header; sub-block sums (tid < 128)
 };
 
-__global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict__ W, int N, int K,
+struct GemmBuf {
+    _Float16 Xh[kTm][kXs];
+    _Float16 Xl[kTm][kXs];
+    _Float16 Bt[kGN][kXs];  // sc * q of the k-tile, weight-row major
+};
+
+__global__ void __launch_bounds__(kGT) gemm_q4k_kernel(const uint8_t* __restrict__ W, int N, int K,
                                                        const _Float16* __restrict__ xh,
                                                        const _Float16* __restrict__ xl,
                                                        const _Float16* __restrict__ sh,
                                                        const _Float16* __restrict__ sl,
                                                        const float* __restrict__ rowscale, float* __restrict__ Y,
                                                        int M, int64_t ldy, int accumulate) {
-    __shared__ __attribute__((aligned(16))) _Float16 Xh[kTm][kXs];
-    __shared__ __attribute__((aligned(16))) _Float16 Xl[kTm][kXs];
-    __shared__ __attribute__((aligned(16))) _Float16 Bt[kTn][kXs];  // sc * q of the k-tile, weight-row major
-    __shared__ __attribute__((aligned(16))) uint8_t Wh[kTn][16];     // d, dmin, scales of the super-block
-    __shared__ __attribute__((aligned(16))) _Float16 Sh[kTm][8];     // sub-block sums of the super-block
-    __shared__ __attribute__((aligned(16))) _Float16 Sl[kTm][8];
-    const int n0 = blockIdx.x * kTn, m0 = blockIdx.y * kTm;
+    __shared__ __attribute__((aligned(16))) GemmBuf buf[2];
+    // per super-block (by its parity): d, dmin, scales (rows 20 B apart, so
+    // the 32 rows a wave reads fall in distinct banks); sub-block sums of x
+    __shared__ __attribute__((aligned(16))) uint8_t Wh[2][kGN][20];
+    __shared__ __attribute__((aligned(16))) _Float16 Sh[2][kTm][8];
+    __shared__ __attribute__((aligned(16))) _Float16 Sl[2][kTm][8];
+    const int n0 = blockIdx.x * kGN, m0 = blockIdx.y * kTm;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave & 1, wn = wave >> 1;
     const int nb = K / 256;
     const size_t rb = (size_t)nb * 144;
     const int li = lane & 31, lh = lane >> 5;
-    // B building: weight row bn = tid / 2 of the tile, qs bytes [16 bc, 16 bc + 16) of the group
-    const int bn = tid >> 1, bc = tid & 1;
+    // B building: weight row bn of the tile, qs bytes [16 bc, 16 bc + 16) of
+    // the group; each 16 threads cover 8 rows x 2 halves, eight consecutive
+    // lanes on eight rows (their LDS rows 144 B apart hit distinct banks)
+    const int bn = 8 * (tid >> 4) + (tid & 7), bc = (tid >> 3) & 1;
     const uint8_t* brow = W + (size_t)(n0 + bn < N ? n0 + bn : N - 1) * rb;
+    const int xr = tid >> 3, xc = tid & 7;  // x staging: row xr, values 8 xc .. +8 of the k-tile
 
     f32x16 acc[2], c1[2];
 #pragma unroll
@@ -227,14 +242,9 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
     const int ntiles = K / kTk;
     auto load_tile = [&](GemmStage& S, int t) {
         const int k0 = t * kTk;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = tid + 256 * i;  // 0..511: row c/8, chunk c%8
-            const int r = c >> 3, ch = c & 7;
-            const size_t o = (size_t)(m0 + r) * K + k0 + 8 * ch;
-            S.xh[i] = *(const u32x4*)(xh + o);
-            S.xl[i] = *(const u32x4*)(xl + o);
-        }
+        const size_t o = (size_t)(m0 + xr) * K + k0 + 8 * xc;
+        S.xh = *(const u32x4*)(xh + o);
+        S.xl = *(const u32x4*)(xl + o);
         const int b = k0 / 256, g = (k0 % 256) / 64;
         S.qs = *(const u32x4*)(brow + (size_t)b * 144 + 16 + 32 * g + 16 * bc);
         if (g == 0) {
@@ -246,42 +256,42 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
             }
         }
     };
-    u32x4 hdr = {};  // this thread's weight row header of the current super-block
+    u32x4 hdr = {};  // this thread's weight row header of the super-block being built
     auto store_tile = [&](const GemmStage& S, int t) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = tid + 256 * i;
-            const int r = c >> 3, ch = c & 7;
-            *(u32x4*)&Xh[r][8 * ch] = S.xh[i];
-            *(u32x4*)&Xl[r][8 * ch] = S.xl[i];
-        }
-        const int g = t & 3;
+        GemmBuf& B = buf[t & 1];
+        *(u32x4*)&B.Xh[xr][8 * xc] = S.xh;
+        *(u32x4*)&B.Xl[xr][8 * xc] = S.xl;
+        const int g = t & 3, p = (t >> 2) & 1;
         if (g == 0) {
             hdr = S.hdr;
-            if (bc == 0) *(u32x4*)&Wh[bn][0] = S.hdr;
+            if (bc == 0) {
+                uint32_t* w = (uint32_t*)&Wh[p][bn][0];
+                w[0] = S.hdr.x; w[1] = S.hdr.y; w[2] = S.hdr.z; w[3] = S.hdr.w;
+            }
             if (tid < 2 * kTm) {
-                if (tid & 1) *(u32x4*)&Sl[tid >> 1][0] = S.ps;
-                else *(u32x4*)&Sh[tid >> 1][0] = S.ps;
+                if (tid & 1) *(u32x4*)&Sl[p][tid >> 1][0] = S.ps;
+                else *(u32x4*)&Sh[p][tid >> 1][0] = S.ps;
             }
         }
         // values 16bc .. 16bc+15 of sub-blocks 2g (low nibbles) and 2g+1 (high)
         const _Float16 s0 = (_Float16)(float)scale_k4(hdr, 2 * g), s1 = (_Float16)(float)scale_k4(hdr, 2 * g + 1);
-        *(half8*)&Bt[bn][16 * bc] = nib8_times(S.qs.x, S.qs.y, false, s0);
-        *(half8*)&Bt[bn][16 * bc + 8] = nib8_times(S.qs.z, S.qs.w, false, s0);
-        *(half8*)&Bt[bn][32 + 16 * bc] = nib8_times(S.qs.x, S.qs.y, true, s1);
-        *(half8*)&Bt[bn][32 + 16 * bc + 8] = nib8_times(S.qs.z, S.qs.w, true, s1);
+        *(half8*)&B.Bt[bn][16 * bc] = nib8_times(S.qs.x, S.qs.y, false, s0);
+        *(half8*)&B.Bt[bn][16 * bc + 8] = nib8_times(S.qs.z, S.qs.w, false, s0);
+        *(half8*)&B.Bt[bn][32 + 16 * bc] = nib8_times(S.qs.x, S.qs.y, true, s1);
+        *(half8*)&B.Bt[bn][32 + 16 * bc + 8] = nib8_times(S.qs.z, S.qs.w, true, s1);
     };
 
     const int ar = 32 * wm + li;  // this lane's A row (input row of the tile)
     auto compute = [&](int t) {
+        const GemmBuf& B = buf[t & 1];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             // k-step s: values 16s .. 16s+15 of the group; lane half lh holds 8 of them
-            const half8 a_h = *(const half8*)&Xh[ar][16 * s + 8 * lh];
-            const half8 a_l = *(const half8*)&Xl[ar][16 * s + 8 * lh];
+            const half8 a_h = *(const half8*)&B.Xh[ar][16 * s + 8 * lh];
+            const half8 a_l = *(const half8*)&B.Xl[ar][16 * s + 8 * lh];
             half8 bq[2];
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) bq[nt] = *(const half8*)&Bt[64 * wn + 32 * nt + li][16 * s + 8 * lh];
+            for (int nt = 0; nt < 2; nt++) bq[nt] = *(const half8*)&B.Bt[64 * wn + 32 * nt + li][16 * s + 8 * lh];
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) c1[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, bq[nt], c1[nt], 0, 0, 0);
 #pragma unroll
@@ -290,12 +300,13 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
         if ((t & 3) == 3) {
             // end of super-block: acc += d * C, then the min term
             // dmin * sum_sub m_sub * X_sub on the same MFMA shape
+            const int p = (t >> 2) & 1;
             float d[2], dm[2];
             half8 bm[2];
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) {
                 const int r = 64 * wn + 32 * nt + li;
-                const uint32_t w0 = *(const uint32_t*)&Wh[r][0];
+                const uint32_t w0 = *(const uint32_t*)&Wh[p][r][0];
                 d[nt] = half_bits_to_f32(w0);
                 dm[nt] = half_bits_to_f32(w0 >> 16);
                 // B[k][n] = m of sub-block k for k < 8, 0 for k = 8..15 (lane half 1)
@@ -304,7 +315,7 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         uint32_t sc, mm;
-                        scale_min_k4(&Wh[r][4], j, sc, mm);
+                        scale_min_k4(&Wh[p][r][4], j, sc, mm);
                         v[j] = (_Float16)(float)mm;
                     }
                 }
@@ -315,8 +326,8 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
                 acc[nt] += d[nt] * c1[nt];
                 c1[nt] = f32x16{};
             }
-            const half8 s_h = lh == 0 ? *(const half8*)&Sh[ar][0] : half8{};
-            const half8 s_l = lh == 0 ? *(const half8*)&Sl[ar][0] : half8{};
+            const half8 s_h = lh == 0 ? *(const half8*)&Sh[p][ar][0] : half8{};
+            const half8 s_l = lh == 0 ? *(const half8*)&Sl[p][ar][0] : half8{};
 #pragma unroll
             for (int nt = 0; nt < 2; nt++) {
                 f32x16 c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_h, bm[nt], f32x16{}, 0, 0, 0);
@@ -325,22 +336,24 @@ __global__ void __launch_bounds__(256) gemm_q4k_kernel(const uint8_t* __restrict
             }
         }
     };
-    // three register stages with fixed roles (no dynamic indexing)
+    // three register stages with fixed roles (no dynamic indexing): at step t
+    // the stage holding tile t + 1 is built into LDS and tile t + 2 loads
+    // into the stage tile t - 1 used
     GemmStage S0, S1, S2;
-    auto step = [&](GemmStage& S, int t) {
-        __syncthreads();  // the previous tile's LDS reads are done
-        store_tile(S, t);
-        __syncthreads();
-        if (t + 3 < ntiles) load_tile(S, t + 3);
-        compute(t);
-    };
     load_tile(S0, 0);
     if (1 < ntiles) load_tile(S1, 1);
-    if (2 < ntiles) load_tile(S2, 2);
+    store_tile(S0, 0);
+    __syncthreads();
+    auto step = [&](GemmStage& Snext, GemmStage& Sfar, int t) {
+        if (t + 2 < ntiles) load_tile(Sfar, t + 2);
+        compute(t);
+        if (t + 1 < ntiles) store_tile(Snext, t + 1);  // the other buffer: every wave is past tile t - 1
+        __syncthreads();
+    };
     for (int t = 0; t < ntiles; t += 3) {
-        step(S0, t);
-        if (t + 1 < ntiles) step(S1, t + 1);
-        if (t + 2 < ntiles) step(S2, t + 2);
+        step(S1, S2, t);
+        if (t + 1 < ntiles) step(S2, S0, t + 1);
+        if (t + 2 < ntiles) step(S0, S1, t + 2);
     }
     // store: D[i][j] in lane j + 32*((i/4)%2), register 4*(i/8) + i%4
 #pragma unroll
@@ -429,8 +442,8 @@ static int32_t rows_q4k_mfma(int pro, const GemvArgs& a, hipStream_t s) {
     for (int i = 0; i < a.nseg; i++) {
         const int rows = a.seg[i].n;
         if (rows == 0) continue;
-        dim3 grid((unsigned)((rows + kTn - 1) / kTn), (unsigned)(mp / kTm));
-        hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(256), 0, s, a.seg[i].W, rows, (int)K, xh, xl, sh, sl, rs,
+        dim3 grid((unsigned)((rows + kGN - 1) / kGN), (unsigned)(mp / kTm));
+        hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(kGT), 0, s, a.seg[i].W, rows, (int)K, xh, xl, sh, sl, rs,
                            a.seg[i].y, (int)batch, a.ys, a.accumulate);
     }
     MIVI_HIP_CHECK(hipGetLastError());
