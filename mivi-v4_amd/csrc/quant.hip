@@ -1324,9 +1324,20 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
 // finishes the butterfly in registers, so every column equals a one-column
 // launch bit for bit. Digits sit in LDS (8 KB per column at K = 2048: three
 // planes and the zero plane, padded apart against bank conflicts).
+// Columns [c0, c0 + 4) of a batched launch (blockIdx.y = column group of the
+// K = 8192 kernel, whose digits fit LDS for four columns only).
+__device__ __forceinline__ mivi::GemvArgs gemv_col_group(const mivi::GemvArgs& a, int c0) {
+    mivi::GemvArgs v = gemv_column(a, c0);
+    for (int i = 0; i < a.nseg; i++) v.seg[i].y = a.seg[i].y + c0 * a.ys;
+    v.ncol = min(4, a.ncol - c0);
+    return v;
+}
+
 template <int PRO, int EPI, int KT, int NG>
-__global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a) {
+__global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
     static_assert(KT == 2048 || KT == 8192, "decode depths");
+    // K = 8192: column group blockIdx.y, at most four columns
+    const mivi::GemvArgs a = KT == 8192 ? gemv_col_group(a0, 4 * (int)blockIdx.y) : a0;
     constexpr int K = KT, nb = K / 256;
     constexpr int SQ = nb / 4;               // superblocks per wave: 2 or 8
     constexpr int LW = 4 * SQ;               // units (leaf values) per wave: 8 or 32
@@ -1904,7 +1915,9 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                 // one workgroup per 16-row group, at most 2 per CU (1 at K = 8192: LDS)
                 const int ngr = ep == mivi::EPI_SWIGLU ? (a.seg[0].n + 7) / 8 : (n + 15) / 16;
                 const int gc = std::max(1, std::min(ngr, mivi::num_cus() * (K == 8192 ? 1 : 2)));
-#define LC(EPI, KT, NG) hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG>), dim3(gc), dim3(kWG), 0, s, a)
+#define LC(EPI, KT, NG)                                                                                      \
+    hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG>), dim3(gc, KT == 8192 ? (a.ncol + 3) / 4 : 1),   \
+                       dim3(kWG), 0, s, a)
                 if constexpr (PRO == mivi::PRO_SWIGLU) {
                 } else if (K == 8192) {
                     if constexpr (PRO == mivi::PRO_NONE) LC(mivi::EPI_STORE, 8192, 1);
@@ -2110,9 +2123,14 @@ int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
 // Most columns one batched streaming launch takes at depth K, 1 where there
 // is no batched kernel: 8 at K = 2048 (digits in LDS: 6 KB per column), 4 at
 // K = 8192 (24 KB per column); packed rows take 2.
-static int gemv_max_cols(int32_t t, int K, bool packed) {
+static int gemv_max_cols(int32_t t, int K, bool packed, int pro = PRO_NONE, int epilogue = EPI_STORE) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
     if (packed) return K == 2048 ? 2 : 1;
+    // Q4_K at K = 8192 on the matrix cores: column groups of four run side by
+    // side in one launch (one workgroup per CU each)
+    if (K == 8192 && t == MIVI_GGML_Q4_K && pro == PRO_NONE && epilogue == EPI_STORE &&
+        !env_int("MIVI_GEMV_COLS_SDOT", 0))
+        return kMaxGemvCols;
     return K == 2048 ? kMaxGemvCols : K == 8192 ? 4 : 1;
 }
 
@@ -2147,7 +2165,7 @@ int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     if (a.ncol > 1) {
         // column groups of the batched kernel; columns it cannot take run
         // one launch each
-        const int cap = gemv_max_cols(t, a.K, a.packed != 0);
+        const int cap = gemv_max_cols(t, a.K, a.packed != 0, pro, a.epilogue);
         for (int c0 = 0; c0 < a.ncol;) {
             const int nc = std::min(cap, a.ncol - c0);
             int32_t rc = nc > 1 ? launch_by_pro(t, pro, column_args(a, c0, nc), n, s) : MIVI_ERR_UNSUPPORTED;

@@ -282,7 +282,8 @@ def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
 @pytest.mark.parametrize("batch,rows,cols", [(2, 64, 2048), (3, 1001, 2048), (5, 6144, 2048), (4, 65536, 2048),
                                              (7, 1001, 2048), (8, 8192, 2048), (15, 260, 2048),
-                                             (3, 300, 8192), (6, 2048, 8192), (2, 130, 4096)])
+                                             (3, 300, 8192), (6, 2048, 8192), (8, 2048, 8192), (5, 300, 8192),
+                                             (2, 130, 4096)])
 def test_batched_gemv_columns_bit_exact_with_matvec(hip, oracle, torch_mod, t, batch, rows, cols):
     # matmul_rows below the MFMA threshold runs batched GEMVs (inputs as
     # columns: up to 8 per launch at d = 2048 and 4 at d = 8192, Q4_K on the
