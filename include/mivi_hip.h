@@ -277,6 +277,59 @@ int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const uint32_t* tok
                                 uint32_t* tokens_out);
 
 /* ---------------------------------------------------------------------
+ * Prefix cache: PrefixCache of crates/mivi-kv/src/prefix.rs with its
+ * snapshots in device memory. A chunk node holds the KV interval it owns
+ * (every attention layer, as the model's cache stores it) and the ShortConv
+ * state at its boundary, copied device to device from a model sequence at
+ * insert and back at restore; the bookkeeping (chained FNV-1a chunk hashes,
+ * parent links of delta chunks, LRU order with the deepest chunk evicted
+ * first, chunk count and byte budget) is the reference's. Errors of the
+ * reference's KvError::DimMismatch / ContextOverflow are MIVI_ERR_KV_CACHE.
+ * With Q8_0 caches the chunk size must be a multiple of 16 (whole groups).
+ * ------------------------------------------------------------------- */
+typedef struct mivi_prefix_cache mivi_prefix_cache;
+
+/* PrefixCache::with_budget (prefix.rs:148-168); 0 takes the default (1024
+ * chunks, 64 tokens, 512 MB). */
+int32_t mivi_hip_prefix_cache_create(size_t max_chunks, size_t chunk_size,
+                                     size_t max_memory_bytes, mivi_prefix_cache** out);
+void mivi_hip_prefix_cache_destroy(mivi_prefix_cache* pc);
+
+/* compute_chunk_hash (prefix.rs:70-87). */
+uint64_t mivi_hip_prefix_chunk_hash(uint64_t prev_hash, const uint32_t* tokens, size_t n);
+
+/* insert_delta_chunk (prefix.rs:251-303): chunk chunk_index (n_tokens ==
+ * chunk size) of sequence seq of m, which has processed exactly pos =
+ * (chunk_index + 1) * chunk_size tokens; chunk_index > 0 needs its parent
+ * prev_hash cached at the previous boundary. *hash_out = the chunk's hash.
+ * Synchronous. */
+int32_t mivi_hip_prefix_cache_insert_delta(mivi_prefix_cache* pc, mivi_model* m, size_t seq,
+                                           size_t pos, uint64_t prev_hash,
+                                           const uint32_t* tokens, size_t n_tokens,
+                                           size_t chunk_index, uint64_t* hash_out);
+
+/* find_longest_prefix (prefix.rs:200-237): tokens matched by the deepest
+ * cached chunk (0 if none) and its hash; touches it in the LRU order. */
+int32_t mivi_hip_prefix_cache_find(mivi_prefix_cache* pc, const uint32_t* tokens, size_t n,
+                                   size_t* matched, uint64_t* hash_out);
+
+/* restore_longest_prefix (prefix.rs:305-358): the matched chain's KV
+ * intervals into sequence seq's caches and the deepest node's ShortConv
+ * state into the sequence; *matched = 0 when nothing matches. The caller
+ * continues (prefill) from position *matched. Synchronous. */
+int32_t mivi_hip_prefix_cache_restore(mivi_prefix_cache* pc, mivi_model* m, size_t seq,
+                                      const uint32_t* tokens, size_t n, size_t* matched,
+                                      uint64_t* hash_out);
+
+/* len, memory_usage_bytes, prune_to_bytes, clear (prefix.rs:179-196,
+ * 395-423); contains: whether a chunk of that hash is cached. */
+size_t mivi_hip_prefix_cache_len(const mivi_prefix_cache* pc);
+size_t mivi_hip_prefix_cache_memory_bytes(const mivi_prefix_cache* pc);
+size_t mivi_hip_prefix_cache_prune(mivi_prefix_cache* pc, size_t target_bytes);
+void mivi_hip_prefix_cache_clear(mivi_prefix_cache* pc);
+int32_t mivi_hip_prefix_cache_contains(const mivi_prefix_cache* pc, uint64_t hash);
+
+/* ---------------------------------------------------------------------
  * Measurement (no counterpart in the reference): reads `bytes` bytes at p
  * (16-byte aligned, bytes % 16 == 0) once with plain coalesced 16-byte loads
  * on the stream and discards them. Its time is the floor for any kernel that

@@ -2165,3 +2165,321 @@ extern "C" int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t
     MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
     return clear_error();
 }
+
+// ------------------------------------------------------------ prefix cache
+//
+// PrefixCache (crates/mivi-kv/src/prefix.rs) with its snapshots in device
+// memory. A node owns one chunk's KV interval [kv_start, pos) of every
+// attention layer (K then V, as the model's cache stores them: rows, or whole
+// 16-token groups of the Q8_0 group layout) and the ShortConv state at its
+// boundary, copied device to device from a sequence of the model at insert
+// and back at restore. The host keeps the reference's bookkeeping: chained
+// chunk hashes, delta nodes with parent links, LRU order with the deepest
+// chunk evicted first, a chunk count and a byte budget.
+
+namespace {
+
+constexpr size_t kPrefixChunkTokens = 64;          // PREFIX_CHUNK_SIZE (prefix.rs:12)
+constexpr size_t kPrefixMaxChunks = 1024;          // DEFAULT_MAX_CACHED_CHUNKS (prefix.rs:15)
+constexpr size_t kPrefixMaxBytes = 512ull << 20;   // DEFAULT_MAX_PREFIX_CACHE_BYTES (prefix.rs:17)
+
+// compute_chunk_hash (prefix.rs:70-87): 64-bit FNV-1a over the tokens'
+// little-endian bytes, started from the FNV offset basis for a first chunk
+// and from the previous hash xor 0x9E3779B97F4A7C15 otherwise.
+uint64_t prefix_chunk_hash(uint64_t prev, const uint32_t* t, size_t n) {
+    uint64_t h = prev == 0 ? 0xCBF29CE484222325ull : prev ^ 0x9E3779B97F4A7C15ull;
+    for (size_t i = 0; i < n; i++)
+        for (int b = 0; b < 4; b++) {
+            h ^= (t[i] >> (8 * b)) & 0xFFu;
+            h *= 0x00000100000001B3ull;
+        }
+    return h;
+}
+
+struct PrefixNode {
+    size_t chunk_index = 0, pos = 0, kv_start = 0;
+    uint64_t hash = 0, parent = 0;
+    bool has_parent = false;
+    std::vector<uint32_t> tokens;
+    uint8_t* dev = nullptr;  // K interval of every attention layer | V interval | ShortConv state
+    size_t kv_bytes = 0;     // bytes of the K (or V) part
+    size_t conv_bytes = 0;
+    size_t bytes() const { return sizeof(PrefixNode) + tokens.capacity() * 4 + 2 * kv_bytes + conv_bytes; }
+};
+
+// the current ShortConv buffer of a sequence (ping-pong by *phase) into dst
+__global__ void conv_snapshot_kernel(float* dst, const float* a, const float* b, const int* phase, size_t n) {
+    const float* src = (*phase & 1) ? b : a;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+struct mivi_prefix_cache {
+    size_t chunk_size = kPrefixChunkTokens, max_chunks = kPrefixMaxChunks, max_bytes = kPrefixMaxBytes;
+    std::map<uint64_t, PrefixNode> chunks;
+    std::vector<uint64_t> lru;  // least recently used first
+    size_t total = 0;
+    // the model shape the snapshots were taken from
+    size_t n_attn = 0, row_bytes = 0, conv_len = 0;
+    bool shaped = false;
+    ~mivi_prefix_cache() {
+        for (auto& e : chunks)
+            if (e.second.dev) (void)hipFree(e.second.dev);
+    }
+    void lru_remove(uint64_t h) {
+        auto it = std::find(lru.begin(), lru.end(), h);
+        if (it != lru.end()) lru.erase(it);
+    }
+    void touch(uint64_t h) {  // prefix.rs:440-446
+        auto it = std::find(lru.begin(), lru.end(), h);
+        if (it != lru.end()) {
+            lru.erase(it);
+            lru.push_back(h);
+        }
+    }
+    // prefix.rs:425-437: the least recently used of the chunks with the
+    // largest chunk index (leaves go before the ancestors they extend)
+    bool select_eviction(uint64_t* out) const {
+        bool sel = false;
+        size_t idx = 0;
+        for (uint64_t h : lru) {
+            auto it = chunks.find(h);
+            if (it == chunks.end()) continue;
+            if (!sel || it->second.chunk_index > idx) {
+                sel = true;
+                idx = it->second.chunk_index;
+                *out = h;
+            }
+        }
+        if (!sel && !lru.empty()) {
+            *out = lru.front();
+            sel = true;
+        }
+        return sel;
+    }
+    void evict(uint64_t h) {
+        lru_remove(h);
+        auto it = chunks.find(h);
+        if (it == chunks.end()) return;
+        total -= std::min(total, it->second.bytes());
+        if (it->second.dev) (void)hipFree(it->second.dev);
+        chunks.erase(it);
+    }
+    size_t prune(size_t target) {  // prefix.rs:401-423
+        size_t n = 0;
+        uint64_t h;
+        while (total > target && !lru.empty() && select_eviction(&h)) {
+            const bool present = chunks.count(h) != 0;
+            evict(h);
+            n += present;
+        }
+        return n;
+    }
+};
+
+static int32_t prefix_shape(mivi_prefix_cache* pc, mivi_model* m) {
+    const size_t conv_len = m->info.n_layers * m->info.dim * std::max<size_t>(1, m->info.ssm_conv_kernel);
+    if (m->kv_packed && pc->chunk_size % 16)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "chunk size %zu: the Q8_0 group layout needs multiples of 16",
+                         pc->chunk_size);
+    if (!pc->shaped) {
+        pc->n_attn = m->info.n_attn_layers;
+        pc->row_bytes = m->kv_row_bytes;
+        pc->conv_len = conv_len;
+        pc->shaped = true;
+    } else if (pc->n_attn != m->info.n_attn_layers || pc->row_bytes != m->kv_row_bytes || pc->conv_len != conv_len) {
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "prefix cache holds snapshots of a model of another shape");
+    }
+    return MIVI_OK;
+}
+
+static int32_t dim_mismatch(size_t expected, size_t got) {  // KvError::DimMismatch
+    return set_error(MIVI_ERR_KV_CACHE, "KV cache error: dimension mismatch: expected %zu, got %zu", expected, got);
+}
+
+extern "C" int32_t mivi_hip_prefix_cache_create(size_t max_chunks, size_t chunk_size, size_t max_memory_bytes,
+                                                mivi_prefix_cache** out) {
+    if (!out) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
+    mivi_prefix_cache* pc = new mivi_prefix_cache();
+    // PrefixCache::with_budget (prefix.rs:148-168): 0 takes the default
+    if (chunk_size) pc->chunk_size = chunk_size;
+    if (max_chunks) pc->max_chunks = max_chunks;
+    if (max_memory_bytes) pc->max_bytes = max_memory_bytes;
+    *out = pc;
+    return clear_error();
+}
+
+extern "C" void mivi_hip_prefix_cache_destroy(mivi_prefix_cache* pc) { delete pc; }
+
+extern "C" uint64_t mivi_hip_prefix_chunk_hash(uint64_t prev_hash, const uint32_t* tokens, size_t n) {
+    return prefix_chunk_hash(prev_hash, tokens, tokens ? n : 0);
+}
+
+extern "C" size_t mivi_hip_prefix_cache_len(const mivi_prefix_cache* pc) { return pc ? pc->chunks.size() : 0; }
+extern "C" size_t mivi_hip_prefix_cache_memory_bytes(const mivi_prefix_cache* pc) { return pc ? pc->total : 0; }
+extern "C" int32_t mivi_hip_prefix_cache_contains(const mivi_prefix_cache* pc, uint64_t hash) {
+    return pc && pc->chunks.count(hash) ? 1 : 0;
+}
+extern "C" size_t mivi_hip_prefix_cache_prune(mivi_prefix_cache* pc, size_t target_bytes) {
+    return pc ? pc->prune(target_bytes) : 0;
+}
+extern "C" void mivi_hip_prefix_cache_clear(mivi_prefix_cache* pc) {
+    if (!pc) return;
+    while (!pc->chunks.empty()) pc->evict(pc->chunks.begin()->first);
+    pc->lru.clear();
+    pc->total = 0;
+}
+
+// insert_delta_chunk (prefix.rs:251-303) + insert_node (:360-392)
+extern "C" int32_t mivi_hip_prefix_cache_insert_delta(mivi_prefix_cache* pc, mivi_model* m, size_t seq, size_t pos,
+                                                      uint64_t prev_hash, const uint32_t* tokens, size_t n_tokens,
+                                                      size_t chunk_index, uint64_t* hash_out) {
+    if (!pc || !m || !hash_out || (n_tokens && !tokens) || seq >= m->info.max_batch)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    int32_t rc = prefix_shape(pc, m);
+    if (rc) return rc;
+    size_t start, end;
+    if (__builtin_mul_overflow(chunk_index, pc->chunk_size, &start) ||
+        __builtin_add_overflow(start, pc->chunk_size, &end))
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: Context length exceeded: attempted pos %zu >= max_seq_len %zu",
+                         (size_t)-1, pos);
+    if (n_tokens != pc->chunk_size || pos != end) return dim_mismatch(end, pos);
+    if (end > m->info.max_seq_len)
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: Context length exceeded: attempted pos %zu >= max_seq_len %zu",
+                         end, m->info.max_seq_len);
+    bool has_parent = false;
+    if (start == 0) {
+        if (prev_hash != 0) return dim_mismatch(0, start);
+    } else {
+        auto it = pc->chunks.find(prev_hash);
+        if (it == pc->chunks.end()) return dim_mismatch(start, 0);
+        if (it->second.pos != start || it->second.chunk_index != chunk_index - 1)
+            return dim_mismatch(start, it->second.pos);
+        has_parent = true;
+    }
+    const uint64_t hash = prefix_chunk_hash(prev_hash, tokens, n_tokens);
+    *hash_out = hash;
+    clear_error();
+    if (pc->chunks.count(hash)) {  // already cached: the new snapshot is not taken
+        pc->touch(hash);
+        return MIVI_OK;
+    }
+    PrefixNode nd;
+    nd.chunk_index = chunk_index;
+    nd.pos = end;
+    nd.kv_start = start;
+    nd.hash = hash;
+    nd.parent = prev_hash;
+    nd.has_parent = has_parent;
+    nd.tokens.assign(tokens, tokens + n_tokens);
+    const size_t iv = (end - start) * pc->row_bytes;  // one layer's interval (rows, or whole groups)
+    nd.kv_bytes = pc->n_attn * iv;
+    nd.conv_bytes = pc->conv_len * 4;
+    MIVI_HIP_CHECK(hipMalloc(&nd.dev, std::max<size_t>(1, 2 * nd.kv_bytes + nd.conv_bytes)));
+    SeqState& st = m->seqs[seq];
+    const size_t lb = m->kv_layer_bytes, off = start * pc->row_bytes;
+    hipError_t e = hipSuccess;
+    if (pc->n_attn) {
+        e = hipMemcpy2DAsync(nd.dev, iv, st.kc + off, lb, iv, pc->n_attn, hipMemcpyDeviceToDevice, m->stream);
+        if (e == hipSuccess)
+            e = hipMemcpy2DAsync(nd.dev + nd.kv_bytes, iv, st.vc + off, lb, iv, pc->n_attn, hipMemcpyDeviceToDevice,
+                                 m->stream);
+    }
+    if (e == hipSuccess && pc->conv_len) {
+        hipLaunchKernelGGL(conv_snapshot_kernel, dim3(64), dim3(256), 0, m->stream,
+                           (float*)(nd.dev + 2 * nd.kv_bytes), st.conv_a, st.conv_b, &m->ctrl->phase[seq], pc->conv_len);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(nd.dev);
+        return set_error(MIVI_ERR_HIP, "prefix snapshot copy failed: %s", hipGetErrorString(e));
+    }
+    const size_t nb = nd.bytes();
+    pc->chunks.emplace(hash, std::move(nd));
+    pc->lru.push_back(hash);
+    pc->total += nb;
+    uint64_t ev;
+    while (pc->chunks.size() > pc->max_chunks && pc->select_eviction(&ev)) pc->evict(ev);
+    pc->prune(pc->max_bytes);
+    return MIVI_OK;
+}
+
+// find_longest_prefix (prefix.rs:200-237): the deepest cached chunk whose
+// chain of hashes matches the tokens' full chunks (the chain stops at the
+// first miss); touches it in the LRU order
+static const PrefixNode* prefix_find(mivi_prefix_cache* pc, const uint32_t* tokens, size_t n, size_t* matched) {
+    *matched = 0;
+    if (n < pc->chunk_size) return nullptr;
+    uint64_t h = 0, deep = 0;
+    size_t deep_len = 0;
+    for (size_t i = 0; i < n / pc->chunk_size; i++) {
+        h = prefix_chunk_hash(h, tokens + i * pc->chunk_size, pc->chunk_size);
+        if (!pc->chunks.count(h)) break;
+        deep = h;
+        deep_len = (i + 1) * pc->chunk_size;
+    }
+    if (!deep_len) return nullptr;
+    pc->touch(deep);
+    *matched = deep_len;
+    return &pc->chunks.at(deep);
+}
+
+extern "C" int32_t mivi_hip_prefix_cache_find(mivi_prefix_cache* pc, const uint32_t* tokens, size_t n,
+                                              size_t* matched, uint64_t* hash_out) {
+    if (!pc || !matched || !hash_out || (n && !tokens)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
+    const PrefixNode* nd = prefix_find(pc, tokens, n, matched);
+    *hash_out = nd ? nd->hash : 0;
+    return clear_error();
+}
+
+// restore_longest_prefix (prefix.rs:305-358): the matched chain's KV
+// intervals into sequence seq's caches in causal order, then the deepest
+// node's ShortConv state (as mivi_hip_model_import_state leaves it: phase 0's
+// input buffer). *matched = 0 when nothing matches; the caller prefills from
+// position *matched on.
+extern "C" int32_t mivi_hip_prefix_cache_restore(mivi_prefix_cache* pc, mivi_model* m, size_t seq,
+                                                 const uint32_t* tokens, size_t n, size_t* matched,
+                                                 uint64_t* hash_out) {
+    if (!pc || !m || !matched || !hash_out || (n && !tokens) || seq >= m->info.max_batch)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    *matched = 0;
+    *hash_out = 0;
+    size_t len = 0;
+    const PrefixNode* nd = prefix_find(pc, tokens, n, &len);
+    if (!nd) return clear_error();
+    int32_t rc = prefix_shape(pc, m);
+    if (rc) return rc;
+    if (nd->pos != len) return dim_mismatch(len, nd->pos);
+    if (len > m->info.max_seq_len)
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: Context length exceeded: attempted pos %zu >= max_seq_len %zu",
+                         len, m->info.max_seq_len);
+    std::vector<const PrefixNode*> path;
+    for (const PrefixNode* p = nd;;) {
+        path.push_back(p);
+        if (!p->has_parent) break;
+        auto it = pc->chunks.find(p->parent);
+        if (it == pc->chunks.end()) return dim_mismatch(len, 0);
+        p = &it->second;
+    }
+    SeqState& st = m->seqs[seq];
+    const size_t lb = m->kv_layer_bytes;
+    for (auto it = path.rbegin(); it != path.rend(); ++it) {
+        const PrefixNode* p = *it;
+        const size_t iv = (p->pos - p->kv_start) * pc->row_bytes, off = p->kv_start * pc->row_bytes;
+        if (!pc->n_attn) continue;
+        MIVI_HIP_CHECK(hipMemcpy2DAsync(st.kc + off, lb, p->dev, iv, iv, pc->n_attn, hipMemcpyDeviceToDevice, m->stream));
+        MIVI_HIP_CHECK(hipMemcpy2DAsync(st.vc + off, lb, p->dev + p->kv_bytes, iv, iv, pc->n_attn,
+                                        hipMemcpyDeviceToDevice, m->stream));
+    }
+    if (pc->conv_len)
+        MIVI_HIP_CHECK(hipMemcpyAsync(st.conv_a, nd->dev + 2 * nd->kv_bytes, pc->conv_len * 4, hipMemcpyDeviceToDevice,
+                                      m->stream));
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->phase[seq], 0);
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    *matched = len;
+    *hash_out = nd->hash;
+    return clear_error();
+}

@@ -131,6 +131,17 @@ _sig = {
     "mivi_hip_model_export_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_model_import_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_read_floor": ([_P, _S, _P], _I),
+    "mivi_hip_prefix_cache_create": ([_S, _S, _S, C.POINTER(_P)], _I),
+    "mivi_hip_prefix_cache_destroy": ([_P], None),
+    "mivi_hip_prefix_chunk_hash": ([C.c_uint64, _P, _S], C.c_uint64),
+    "mivi_hip_prefix_cache_insert_delta": ([_P, _P, _S, _S, C.c_uint64, _P, _S, _S, C.POINTER(C.c_uint64)], _I),
+    "mivi_hip_prefix_cache_find": ([_P, _P, _S, C.POINTER(_S), C.POINTER(C.c_uint64)], _I),
+    "mivi_hip_prefix_cache_restore": ([_P, _P, _S, _P, _S, C.POINTER(_S), C.POINTER(C.c_uint64)], _I),
+    "mivi_hip_prefix_cache_len": ([_P], _S),
+    "mivi_hip_prefix_cache_memory_bytes": ([_P], _S),
+    "mivi_hip_prefix_cache_prune": ([_P, _S], _S),
+    "mivi_hip_prefix_cache_clear": ([_P], None),
+    "mivi_hip_prefix_cache_contains": ([_P, C.c_uint64], _I),
     "mivi_hip_sample": ([_P, _S, _P, _S, C.POINTER(SamplerConfig), _P, _P, _P], _I),
     "mivi_hip_sample_rows_workspace": ([_S, _S], _S),
     "mivi_hip_sample_rows": ([_P, _S, _S, _S, _P, _S, _S, C.POINTER(SamplerConfig), _P, _P, _P, _S, _P], _I),
@@ -323,4 +334,4 @@ def synth_random_weights(ggml_type, seed: int, rows: int, cols: int, std: float 
     return dst
 
 
-from .model import Model  # noqa: E402,F401
+from .model import Model, PrefixCache, chunk_hash  # noqa: E402,F401

@@ -110,3 +110,72 @@ class Model:
         _check(_lib.mivi_hip_model_import_state(self._h, seq, tokens, k.ctypes.data_as(C.c_void_p),
                                                 v.ctypes.data_as(C.c_void_p), min(k.nbytes, v.nbytes),
                                                 conv.ctypes.data_as(C.c_void_p), conv.size), ModelError)
+
+
+def chunk_hash(prev_hash: int, tokens) -> int:
+    """compute_chunk_hash (prefix.rs:70-87)."""
+    t = np.ascontiguousarray(tokens, np.uint32)
+    return int(_lib.mivi_hip_prefix_chunk_hash(C.c_uint64(prev_hash), t.ctypes.data_as(C.c_void_p), t.size))
+
+
+class PrefixCache:
+    """PrefixCache (crates/mivi-kv/src/prefix.rs) with device-resident
+    snapshots: chunks of a model sequence's KV intervals and ShortConv states,
+    restored device to device."""
+
+    def __init__(self, max_chunks: int = 0, chunk_size: int = 0, max_memory_bytes: int = 0):
+        h = C.c_void_p()
+        _check(_lib.mivi_hip_prefix_cache_create(max_chunks, chunk_size, max_memory_bytes, C.byref(h)), ModelError)
+        self._h = h
+        self.chunk_size = chunk_size or 64
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.mivi_hip_prefix_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __len__(self) -> int:
+        return int(_lib.mivi_hip_prefix_cache_len(self._h))
+
+    def memory_usage_bytes(self) -> int:
+        return int(_lib.mivi_hip_prefix_cache_memory_bytes(self._h))
+
+    def prune_to_bytes(self, target: int) -> int:
+        return int(_lib.mivi_hip_prefix_cache_prune(self._h, target))
+
+    def clear(self):
+        _lib.mivi_hip_prefix_cache_clear(self._h)
+
+    def contains(self, hash_: int) -> bool:
+        return bool(_lib.mivi_hip_prefix_cache_contains(self._h, C.c_uint64(hash_)))
+
+    def insert_delta_chunk(self, model: "Model", prev_hash: int, tokens, chunk_index: int, pos: int,
+                           seq: int = 0) -> int:
+        """insert_delta_chunk (prefix.rs:251-303) from sequence seq of model,
+        which has processed exactly pos tokens."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        h = C.c_uint64()
+        _check(_lib.mivi_hip_prefix_cache_insert_delta(self._h, model._h, seq, pos, C.c_uint64(prev_hash),
+                                                       t.ctypes.data_as(C.c_void_p), t.size, chunk_index,
+                                                       C.byref(h)), ModelError)
+        return int(h.value)
+
+    def find_longest_prefix(self, tokens):
+        """(matched tokens, hash) of the deepest cached chunk, (0, 0) if none."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        n, h = C.c_size_t(), C.c_uint64()
+        _check(_lib.mivi_hip_prefix_cache_find(self._h, t.ctypes.data_as(C.c_void_p), t.size, C.byref(n),
+                                               C.byref(h)), ModelError)
+        return int(n.value), int(h.value)
+
+    def restore_longest_prefix(self, model: "Model", tokens, seq: int = 0):
+        """restore_longest_prefix (prefix.rs:305-358) into sequence seq of
+        model: (matched tokens, hash)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        n, h = C.c_size_t(), C.c_uint64()
+        _check(_lib.mivi_hip_prefix_cache_restore(self._h, model._h, seq, t.ctypes.data_as(C.c_void_p), t.size,
+                                                  C.byref(n), C.byref(h)), ModelError)
+        return int(n.value), int(h.value)
