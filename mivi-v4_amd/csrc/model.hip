@@ -247,12 +247,13 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // Embedding row of token tok (model.rs:355-366): bit-exact dequantization of
 // one row, generic over the stored format.
 // blockIdx.x = b: token tok[b] into x + b * x_stride.
-__global__ void __launch_bounds__(kWG) embed_kernel(int32_t type, const uint8_t* table, size_t row_bytes,
-                                                    const uint32_t* tok, float* x, int dim, int64_t x_stride) {
-    tok += blockIdx.x;
-    x += blockIdx.x * x_stride;
-    const uint8_t* row = table + (size_t)(*tok) * row_bytes;
-    for (int i = threadIdx.x; i < dim; i += kWG) {
+// Row `id` of an embedding table (model.rs:358-375, the token's row
+// dequantized: Q6_K, Q4_K, Q8_0, F16, BF16 or F32) into x, by threads
+// t0, t0 + nt, ... of the caller.
+__device__ __forceinline__ void embed_row(int32_t type, const uint8_t* table, size_t row_bytes, uint32_t id, float* x,
+                                          int dim, int t0, int nt) {
+    const uint8_t* row = table + (size_t)id * row_bytes;
+    for (int i = t0; i < dim; i += nt) {
         float y = 0.f;
         if (type == MIVI_GGML_Q6_K) {
             const uint8_t* blk = row + (size_t)(i / 256) * 210;
@@ -290,6 +291,11 @@ __global__ void __launch_bounds__(kWG) embed_kernel(int32_t type, const uint8_t*
         }
         x[i] = y;
     }
+}
+
+__global__ void __launch_bounds__(kWG) embed_kernel(int32_t type, const uint8_t* table, size_t row_bytes,
+                                                    const uint32_t* tok, float* x, int dim, int64_t x_stride) {
+    embed_row(type, table, row_bytes, tok[blockIdx.x], x + blockIdx.x * x_stride, dim, threadIdx.x, kWG);
 }
 
 // Current token's head vector: optional per-head RMSNorm (transformer.rs:81-96)
@@ -1021,18 +1027,31 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
 // partials of the head GEMV's argmax epilogue.
 // blockIdx.x = b: sequence seq + b of a batched launch (values and indices
 // + b * vstride; tok, pos, phase + b).
+// EmbedNext: with a table, the chosen token's embedding row goes to x (+ b *
+// xs) for the next step, so the step needs no embedding launch of its own.
+struct EmbedNext {
+    const uint8_t* table;
+    size_t row_bytes;
+    float* x;
+    int64_t xs;
+    int32_t type;
+    int dim;
+};
+
 __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, const int* part_idx, int n,
                                                               uint32_t* tok, int* pos, int* phase, uint32_t* history,
                                                               const int* step, int stride, int seq, int do_argmax,
-                                                              int64_t vstride) {
+                                                              int64_t vstride, EmbedNext en) {
     __shared__ float bv[16];
     __shared__ int bi[16];
+    __shared__ uint32_t chosen;
     {
         const int b = blockIdx.x;
         logits += b * vstride;
         if (part_idx) part_idx += b * vstride;
         tok += b; pos += b; phase += b;
         seq += b;
+        en.x += b * en.xs;
     }
     if (do_argmax) {
         float best = -INFINITY;
@@ -1057,7 +1076,12 @@ __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logit
                 if (bv[w] > b || (bv[w] == b && bi[w] < id)) { b = bv[w]; id = bi[w]; }
             if (id == 0x7FFFFFFF) id = 0;
             *tok = (uint32_t)id;
+            chosen = (uint32_t)id;
             if (history) history[(size_t)(*step) * stride + seq] = (uint32_t)id;
+        }
+        if (en.table) {
+            __syncthreads();
+            embed_row(en.type, en.table, en.row_bytes, chosen, en.x, en.dim, threadIdx.x, blockDim.x);
         }
     }
     if (threadIdx.x == 0) {
@@ -1220,8 +1244,24 @@ namespace {
 // advance (do_head). Each projection is one GEMV over the nb sequences'
 // activation columns (weights read once for all of them); attention runs per
 // sequence.
+// The embedding of the next token by the argmax kernel (when `on`), into the
+// activation arena starting at x (sequence b at x + b * strides.x).
+EmbedNext embed_next_args(mivi_model* m, float* x, bool on) {
+    EmbedNext en{};
+    if (!on) return en;
+    size_t bs, ts;
+    format_sizes(m->embd.type, &bs, &ts);
+    en.table = m->embd.w;
+    en.row_bytes = (m->info.dim * ts) / bs;  // model.rs:358-360
+    en.x = x;
+    en.xs = (int64_t)m->strides.x;
+    en.type = m->embd.type;
+    en.dim = (int)m->info.dim;
+    return en;
+}
+
 int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argmax, hipStream_t s, bool do_embed,
-                     size_t l0, size_t l1, bool do_head) {
+                     size_t l0, size_t l1, bool do_head, bool embed_next) {
     const mivi_model_info& c = m->info;
     const SeqStrides& z = m->strides;
     SeqState& s0 = m->seqs[b0];
@@ -1365,19 +1405,22 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
                        parts ? s0.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b0],
                        &m->ctrl->pos[b0], &m->ctrl->phase[b0], argmax ? m->history : nullptr, &m->ctrl->step,
                        (int)c.max_batch, (int)b0, (argmax && logits) ? 1 : 0,
-                       (int64_t)(parts ? z.parts : z.logits));
+                       (int64_t)(parts ? z.parts : z.logits), embed_next_args(m, s0.x, embed_next && argmax && logits));
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
 }
 
 int32_t enqueue_step(mivi_model* m, size_t b, bool logits, bool argmax, hipStream_t s) {
-    return enqueue_step(m, b, 1, logits, argmax, s, true, 0, m->info.n_layers, true);
+    return enqueue_step(m, b, 1, logits, argmax, s, true, 0, m->info.n_layers, true, false);
 }
 
 // One greedy step of sequences 0..batch-1, layer by layer across the
 // sequences: every projection is one GEMV over all the sequences' columns.
+// The step starts from x already holding the tokens' embeddings and ends by
+// embedding the chosen tokens for the next step (the first step's embedding
+// is the caller's).
 int32_t enqueue_batch_step(mivi_model* m, size_t batch, hipStream_t s) {
-    return enqueue_step(m, 0, batch, true, true, s, true, 0, m->info.n_layers, true);
+    return enqueue_step(m, 0, batch, true, true, s, false, 0, m->info.n_layers, true, true);
 }
 
 constexpr int kPrefillSplits = 16;  // attention splits per tile row, at most
@@ -1963,6 +2006,12 @@ extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, c
         if (rc) return rc;
     }
     hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step, 0);
+    {
+        // the first step's embeddings; each step embeds the next tokens itself
+        const EmbedNext en = embed_next_args(m, m->seqs[0].x, true);
+        hipLaunchKernelGGL(embed_kernel, dim3((unsigned)batch), dim3(kWG), 0, m->stream, en.type, en.table,
+                           en.row_bytes, &m->ctrl->tok[0], en.x, en.dim, en.xs);
+    }
     if (!m->graph || m->graph_batch != batch) {
         if (m->graph) {
             hipGraphExecDestroy(m->graph);
@@ -2031,7 +2080,7 @@ extern "C" int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const ui
         const mivi_model_info& c = m->info;
         hipGraph_t gr;
         MIVI_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        int32_t rc = enqueue_step(m, 0, batch, true, false, m->stream, true, 0, c.n_layers, true);
+        int32_t rc = enqueue_step(m, 0, batch, true, false, m->stream, true, 0, c.n_layers, true, false);
         if (!rc)
             rc = launch_sample_seq(m->seqs[0].logits, (int64_t)m->strides.logits, (int)c.vocab_size, m->history,
                                    (int)c.max_batch, 0, (int)batch, 64, &m->ctrl->step, eos, *cfg, m->rng,
