@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include "../../include/mivi_hip.h"
+#include "common.h"
 
 namespace mivi {
 
@@ -93,6 +94,63 @@ int32_t launch_rows(int32_t ggml_type, int prologue, const GemvArgs& a, hipStrea
 // when quad_layout(rows, cols), unit planes otherwise
 int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
 
+// Row `id` of an embedding table (model.rs:358-375, the token's row
+// dequantized: Q6_K, Q4_K, Q8_0, F16, BF16 or F32) into x, by threads
+// t0, t0 + nt, ... of the caller.
+__device__ __forceinline__ void embed_row(int32_t type, const uint8_t* table, size_t row_bytes, uint32_t id, float* x,
+                                          int dim, int t0, int nt) {
+    const uint8_t* row = table + (size_t)id * row_bytes;
+    for (int i = t0; i < dim; i += nt) {
+        float y = 0.f;
+        if (type == MIVI_GGML_Q6_K) {
+            const uint8_t* blk = row + (size_t)(i / 256) * 210;
+            int e = i % 256, half = e / 128, r = e % 128, grp = r / 32, l = r % 32;
+            const uint8_t* ql = blk + half * 64;
+            const uint8_t* qh = blk + 128 + half * 32;
+            const int8_t* sc = (const int8_t*)(blk + 192 + half * 8);
+            float d = half_bits_to_f32(ld_u16(blk + 208));
+            int lo = (grp & 1) ? ql[l + 32] : ql[l];
+            int nib = grp < 2 ? (lo & 0xF) : (lo >> 4);
+            int q = (nib | (((qh[l] >> (2 * grp)) & 3) << 4)) - 32;
+            y = d * (float)sc[l / 16 + 2 * grp] * (float)q;
+        } else if (type == MIVI_GGML_Q4_K) {
+            const uint8_t* blk = row + (size_t)(i / 256) * 144;
+            int e = i % 256, j = e / 64, r = e % 64, hi = r / 32, l = r % 32;
+            float d = half_bits_to_f32(ld_u16(blk)), dmin = half_bits_to_f32(ld_u16(blk + 2));
+            const uint8_t* sc = blk + 4;
+            int jj = 2 * j + hi;
+            uint32_t s, m;
+            if (jj < 4) { s = sc[jj] & 63; m = sc[jj + 4] & 63; }
+            else { s = (sc[jj + 4] & 0xF) | ((sc[jj - 4] >> 6) << 4); m = (sc[jj + 4] >> 4) | ((sc[jj] >> 6) << 4); }
+            uint32_t qb = blk[16 + j * 32 + l];
+            float dd = d * (float)s, mm = dmin * (float)m;
+            y = dd * (float)(hi ? (qb >> 4) : (qb & 0xF)) - mm;
+        } else if (type == MIVI_GGML_Q8_0) {
+            const uint8_t* blk = row + (size_t)(i / 32) * 34;
+            y = (float)(int8_t)blk[2 + i % 32] * half_bits_to_f32(ld_u16(blk));
+        } else if (type == MIVI_GGML_F16) {
+            y = half_bits_to_f32(ld_u16(row + 2 * (size_t)i));
+        } else if (type == MIVI_GGML_BF16) {
+            y = bf16_bits_to_f32(ld_u16(row + 2 * (size_t)i));
+        } else {
+            const uint8_t* p = row + 4 * (size_t)i;
+            y = __uint_as_float(p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24));
+        }
+        x[i] = y;
+    }
+}
+
+// EmbedNext: with a table, the chosen token's embedding row goes to x (+ b *
+// xs) for the next step, so the step needs no embedding launch of its own.
+struct EmbedNext {
+    const uint8_t* table;
+    size_t row_bytes;
+    float* x;
+    int64_t xs;
+    int32_t type;
+    int dim;
+};
+
 // End-of-sequence ids suppressed on a generation's first token.
 struct SampleEos {
     uint32_t id[4];
@@ -105,9 +163,10 @@ struct SampleEos {
 // history at *step. rng: one xorshift64* state per sequence (rng[b]). ws:
 // sample_seq_workspace(n, batch) bytes of device memory (4-byte aligned);
 // the logits are left penalised and divided by the temperature.
+// en: the sampled tokens' embeddings for the next step (EmbedNext).
 size_t sample_seq_workspace(size_t n, size_t batch);
 int32_t launch_sample_seq(float* logits, int64_t lstride, int n, uint32_t* history, int hstride, int seq0, int batch,
                           int window, const int* step, const SampleEos& eos, const mivi_sampler_config& cfg,
-                          uint64_t* rng, uint32_t* tok, void* ws, hipStream_t s);
+                          uint64_t* rng, uint32_t* tok, void* ws, const EmbedNext& en, hipStream_t s);
 
 }  // namespace mivi

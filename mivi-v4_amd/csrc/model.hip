@@ -247,52 +247,6 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // Embedding row of token tok (model.rs:355-366): bit-exact dequantization of
 // one row, generic over the stored format.
 // blockIdx.x = b: token tok[b] into x + b * x_stride.
-// Row `id` of an embedding table (model.rs:358-375, the token's row
-// dequantized: Q6_K, Q4_K, Q8_0, F16, BF16 or F32) into x, by threads
-// t0, t0 + nt, ... of the caller.
-__device__ __forceinline__ void embed_row(int32_t type, const uint8_t* table, size_t row_bytes, uint32_t id, float* x,
-                                          int dim, int t0, int nt) {
-    const uint8_t* row = table + (size_t)id * row_bytes;
-    for (int i = t0; i < dim; i += nt) {
-        float y = 0.f;
-        if (type == MIVI_GGML_Q6_K) {
-            const uint8_t* blk = row + (size_t)(i / 256) * 210;
-            int e = i % 256, half = e / 128, r = e % 128, grp = r / 32, l = r % 32;
-            const uint8_t* ql = blk + half * 64;
-            const uint8_t* qh = blk + 128 + half * 32;
-            const int8_t* sc = (const int8_t*)(blk + 192 + half * 8);
-            float d = half_bits_to_f32(ld_u16(blk + 208));
-            int lo = (grp & 1) ? ql[l + 32] : ql[l];
-            int nib = grp < 2 ? (lo & 0xF) : (lo >> 4);
-            int q = (nib | (((qh[l] >> (2 * grp)) & 3) << 4)) - 32;
-            y = d * (float)sc[l / 16 + 2 * grp] * (float)q;
-        } else if (type == MIVI_GGML_Q4_K) {
-            const uint8_t* blk = row + (size_t)(i / 256) * 144;
-            int e = i % 256, j = e / 64, r = e % 64, hi = r / 32, l = r % 32;
-            float d = half_bits_to_f32(ld_u16(blk)), dmin = half_bits_to_f32(ld_u16(blk + 2));
-            const uint8_t* sc = blk + 4;
-            int jj = 2 * j + hi;
-            uint32_t s, m;
-            if (jj < 4) { s = sc[jj] & 63; m = sc[jj + 4] & 63; }
-            else { s = (sc[jj + 4] & 0xF) | ((sc[jj - 4] >> 6) << 4); m = (sc[jj + 4] >> 4) | ((sc[jj] >> 6) << 4); }
-            uint32_t qb = blk[16 + j * 32 + l];
-            float dd = d * (float)s, mm = dmin * (float)m;
-            y = dd * (float)(hi ? (qb >> 4) : (qb & 0xF)) - mm;
-        } else if (type == MIVI_GGML_Q8_0) {
-            const uint8_t* blk = row + (size_t)(i / 32) * 34;
-            y = (float)(int8_t)blk[2 + i % 32] * half_bits_to_f32(ld_u16(blk));
-        } else if (type == MIVI_GGML_F16) {
-            y = half_bits_to_f32(ld_u16(row + 2 * (size_t)i));
-        } else if (type == MIVI_GGML_BF16) {
-            y = bf16_bits_to_f32(ld_u16(row + 2 * (size_t)i));
-        } else {
-            const uint8_t* p = row + 4 * (size_t)i;
-            y = __uint_as_float(p[0] | (p[1] << 8) | (p[2] << 16) | ((uint32_t)p[3] << 24));
-        }
-        x[i] = y;
-    }
-}
-
 __global__ void __launch_bounds__(kWG) embed_kernel(int32_t type, const uint8_t* table, size_t row_bytes,
                                                     const uint32_t* tok, float* x, int dim, int64_t x_stride) {
     embed_row(type, table, row_bytes, tok[blockIdx.x], x + blockIdx.x * x_stride, dim, threadIdx.x, kWG);
@@ -1027,17 +981,6 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
 // partials of the head GEMV's argmax epilogue.
 // blockIdx.x = b: sequence seq + b of a batched launch (values and indices
 // + b * vstride; tok, pos, phase + b).
-// EmbedNext: with a table, the chosen token's embedding row goes to x (+ b *
-// xs) for the next step, so the step needs no embedding launch of its own.
-struct EmbedNext {
-    const uint8_t* table;
-    size_t row_bytes;
-    float* x;
-    int64_t xs;
-    int32_t type;
-    int dim;
-};
-
 __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, const int* part_idx, int n,
                                                               uint32_t* tok, int* pos, int* phase, uint32_t* history,
                                                               const int* step, int stride, int seq, int do_argmax,
@@ -2068,6 +2011,11 @@ extern "C" int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const ui
     for (size_t b = 0; b < batch; b++) st[b] = seeds[b] ? seeds[b] : 0x853c49e6748fea9bULL;
     MIVI_HIP_CHECK(hipMemcpyAsync(m->rng, st.data(), batch * 8, hipMemcpyHostToDevice, m->stream));
     hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step, 0);
+    {
+        const EmbedNext en = embed_next_args(m, m->seqs[0].x, true);
+        hipLaunchKernelGGL(embed_kernel, dim3((unsigned)batch), dim3(kWG), 0, m->stream, en.type, en.table,
+                           en.row_bytes, &m->ctrl->tok[0], en.x, en.dim, en.xs);
+    }
     SampleEos eos{};
     eos.n = (int)n_eos;
     for (size_t i = 0; i < n_eos; i++) eos.id[i] = eos_ids[i];
@@ -2080,11 +2028,13 @@ extern "C" int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const ui
         const mivi_model_info& c = m->info;
         hipGraph_t gr;
         MIVI_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        int32_t rc = enqueue_step(m, 0, batch, true, false, m->stream, true, 0, c.n_layers, true, false);
+        // x holds the tokens' embeddings when a step starts: the first step's
+        // come from the launch below, each step's sampler embeds the next
+        int32_t rc = enqueue_step(m, 0, batch, true, false, m->stream, false, 0, c.n_layers, true, false);
         if (!rc)
             rc = launch_sample_seq(m->seqs[0].logits, (int64_t)m->strides.logits, (int)c.vocab_size, m->history,
                                    (int)c.max_batch, 0, (int)batch, 64, &m->ctrl->step, eos, *cfg, m->rng,
-                                   &m->ctrl->tok[0], m->samp_ws, m->stream);
+                                   &m->ctrl->tok[0], m->samp_ws, embed_next_args(m, m->seqs[0].x, true), m->stream);
         if (!rc) hipLaunchKernelGGL(step_counter_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step);
         hipError_t e = hipStreamEndCapture(m->stream, &gr);
         if (rc) return rc;

@@ -854,6 +854,7 @@ struct TokOut {
     uint32_t* history;
     int hstride, seq0;
     const int* step;
+    mivi::EmbedNext en;  // with a table: the token's embedding for the next step
 };
 
 struct NoRecent {
@@ -896,6 +897,9 @@ __global__ void __launch_bounds__(kST) sample_pick_kernel(float* logits, int64_t
         out.tok[b] = (uint32_t)tok;
         if (out.history) out.history[(size_t)(*out.step) * out.hstride + out.seq0 + b] = (uint32_t)tok;
     }
+    if (out.en.table)  // every thread holds the token
+        mivi::embed_row(out.en.type, out.en.table, out.en.row_bytes, (uint32_t)tok, out.en.x + b * out.en.xs,
+                        out.en.dim, t, kST);
 }
 
 SampleArgs make_args(const mivi_sampler_config& cfg) {
@@ -948,9 +952,9 @@ size_t sample_seq_workspace(size_t n, size_t batch) { return split_workspace(n, 
 
 int32_t launch_sample_seq(float* logits, int64_t lstride, int n, uint32_t* history, int hstride, int seq0, int batch,
                           int window, const int* step, const SampleEos& eos, const mivi_sampler_config& cfg,
-                          uint64_t* rng, uint32_t* tok, void* ws, hipStream_t s) {
+                          uint64_t* rng, uint32_t* tok, void* ws, const EmbedNext& en, hipStream_t s) {
     return launch_split(logits, lstride, n, batch, HistSrc{history, hstride, seq0, window, step}, eos, step, cfg, rng,
-                        TokOut{tok, history, hstride, seq0, step}, ws, false, s);
+                        TokOut{tok, history, hstride, seq0, step, en}, ws, false, s);
 }
 }  // namespace mivi
 
@@ -991,6 +995,6 @@ extern "C" int32_t mivi_hip_sample_rows(float* logits, size_t n, size_t rows, si
     mivi::clear_error();
     return launch_split(logits, (int64_t)row_stride, (int)n, (int)rows,
                         FlatSrc{n_recent ? recent : nullptr, (int)n_recent, (int64_t)recent_stride}, mivi::SampleEos{},
-                        nullptr, *cfg, rng_states, TokOut{tokens, nullptr, 0, 0, nullptr}, workspace, true,
+                        nullptr, *cfg, rng_states, TokOut{tokens, nullptr, 0, 0, nullptr, mivi::EmbedNext{}}, workspace, true,
                         (hipStream_t)stream);
 }
