@@ -364,3 +364,30 @@ def test_sampled_generation_batch_matches_single_sequences(hip, small_img):
         m1.prefill(pr[:-1])
         one = m1.generate([int(pr[-1])], [len(pr) - 1], 24, cfg, [10 + b])[:, 0]
         assert np.array_equal(out[:, b], one), b
+
+
+def test_full_shape_greedy_256_steps_match_oracle(hip, oracle):
+    """The BASELINE decode bar at the config-4 model shape (1.2B hybrid,
+    random-init Q4_K weights, Q6_K embedding/head, fp16 KV): 256 greedy
+    steps from a short prompt give the oracle's tokens, and the first step's
+    logits are within 1e-3 of the oracle's (relative to max |l|)."""
+    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid
+    img = build_hybrid(**LFM2_1B2, ctx_len=65536, seed=2024)
+    n, steps = 16, 256
+    prompt = np.random.default_rng(21).integers(0, LFM2_1B2["vocab"], n + 1)
+    m = hip.Model(img, max_ctx=n + steps + 8, kv_precision=hip.KvPrecision.F16)
+    o = oracle.Model(img, max_ctx=n + steps + 8, kv_precision=oracle.KV_F16RT)
+    m.prefill(prompt[:-1])
+    for p, t in enumerate(prompt[:-1]):
+        o.forward_step(int(t), p, False)
+    lo = o.forward(int(prompt[-1]), n)
+    lg = m.forward(int(prompt[-1]), n)
+    assert np.max(np.abs(lg - lo)) <= 1e-3 * np.max(np.abs(lo))
+    m.reset_context()
+    m.prefill(prompt[:-1])
+    got = m.generate_greedy([int(prompt[-1])], [n], steps)[:, 0]
+    tok, want = oracle.argmax(lo), [oracle.argmax(lo)]
+    for i in range(1, steps):
+        tok = oracle.argmax(o.forward(tok, n + i))
+        want.append(tok)
+    assert list(got) == want
