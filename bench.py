@@ -342,7 +342,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the GEMV and decode shard by rows / sequences without exchange; see DESIGN.md)", file=sys.stderr)
+              "(the GEMV and decode would shard by rows / sequences without exchange)", file=sys.stderr)
         sys.exit(2)
     import torch
     import mivi_hip as hip
