@@ -297,19 +297,22 @@ def batched_decode_bench(torch, hip, batch, ctx, steps):
 
 def sampler_bench(torch, hip, calls):
     """Sampler::sample on one row of 65536 logits (N(0, 9), a 64-token penalty
-    window) with GenerationConfig::default: the split path (mivi_hip_sample_rows,
-    the generation loop's) and the whole-row path (mivi_hip_sample), in µs per
-    call between HIP events on the stream both run on."""
+    window), µs per call between HIP events on the stream the calls run on:
+    GenerationConfig::default on the split path (chunk kernel + pick kernel
+    over the top-k candidates), and full-vocabulary categorical sampling
+    (temperature 1, no top-k / top-p), which runs the whole-row steps in the
+    pick kernel."""
     n = 65536
     g = torch.Generator(device="cuda").manual_seed(5)
     base = torch.randn(n, device="cuda", generator=g) * 3
     rec = torch.randint(0, n, (1, 64), dtype=torch.int32, device="cuda", generator=g)
     rng = torch.tensor([1], dtype=torch.int64, device="cuda")
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
-    out = {"n": n, "config": "GenerationConfig::default", "calls": calls}
-    for name, fn in (("split_us", lambda l: hip.sample_rows(l.view(1, -1), rec, cfg, rng, tok)),
-                     ("whole_row_us", lambda l: hip.sample(l, rec[0], cfg, rng, tok))):
-        cfg = hip.SamplerConfig.make()
+    out = {"n": n, "calls": calls}
+    for name, cfg in (("default_config_us", hip.SamplerConfig.make()),
+                      ("categorical_whole_row_us",
+                       hip.SamplerConfig.make(temperature=1.0, top_p=1.0, top_k=0, repetition_penalty=1.0))):
+        fn = lambda l: hip.sample(l, rec[0], cfg, rng, tok)  # noqa: E731
         rows = [base.clone() for _ in range(calls)]
         fn(base.clone())
         torch.cuda.synchronize()
@@ -384,8 +387,8 @@ def main():
             + (f", CPU {dec['cpu_tok_s']:.2f} tok/s" if "cpu_tok_s" in dec else ""))
         extra["decode_config4"] = dec
         sm = sampler_bench(torch, hip, 50)
-        log(f"sampler (65536 logits, default config): {sm['split_us']:.1f} us split path, "
-            f"{sm['whole_row_us']:.1f} us whole row")
+        log(f"sampler (65536 logits): {sm['default_config_us']:.1f} us default config (split path), "
+            f"{sm['categorical_whole_row_us']:.1f} us full-vocabulary categorical (whole row)")
         extra["sampler"] = sm
     if not a.no_decode and not a.no_config5:
         c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps)

@@ -234,7 +234,10 @@ typedef struct {
     uint32_t top_k;
 } mivi_sampler_config;
 
-/* Sampler::sample on the device, one workgroup, asynchronous on the stream:
+/* Sampler::sample on the device, asynchronous on the stream (the split path
+ * of mivi_hip_sample_rows on one row, with a workspace the library keeps per
+ * device: the first call on a device allocates it, so do not make that call
+ * under graph capture):
  * logits (n floats, device) are modified in place as the reference modifies
  * its &mut [f32] (penalties, temperature, min-p, top-k, then the softmax
  * probabilities); recent (n_recent token ids, device) is the penalty window;

@@ -27,6 +27,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "common.h"
 #include "gemv.h"
@@ -655,13 +657,6 @@ struct FlatRecent {
     __device__ __forceinline__ uint32_t at(int j) const { return p[j]; }
 };
 
-__global__ void __launch_bounds__(kST) sample_kernel(float* L, int n, const uint32_t* recent, int nr, SampleArgs c,
-                                                     unsigned long long* rng, uint32_t* tok_out) {
-    __shared__ Shared sh;
-    const int t = sample_row<false>(L, n, FlatRecent{recent, nr}, c, rng, sh);
-    if (threadIdx.x == 0) *tok_out = (uint32_t)t;
-}
-
 // ------------------------------------------------------------- split path
 
 // The last `window` tokens a sequence generated, from the step history
@@ -960,6 +955,25 @@ int32_t launch_sample_seq(float* logits, int64_t lstride, int n, uint32_t* histo
 
 // -------------------------------------------------------------------- C ABI
 
+// The workspace of mivi_hip_sample (one row of the split path): one
+// grow-only buffer per device, kept until the process ends; calls on
+// different streams are ordered through an event recorded after each use.
+struct SampleWorkspace {
+    std::mutex mu;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+};
+
+static SampleWorkspace& sample_workspace(int dev) {
+    static std::mutex mu;
+    static std::vector<SampleWorkspace*> all;
+    std::lock_guard<std::mutex> lk(mu);
+    if ((size_t)dev >= all.size()) all.resize(dev + 1, nullptr);
+    if (!all[dev]) all[dev] = new SampleWorkspace();
+    return *all[dev];
+}
+
 extern "C" int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* recent, size_t n_recent,
                                    const mivi_sampler_config* cfg, uint64_t* rng_state, uint32_t* token,
                                    void* stream) {
@@ -967,10 +981,30 @@ extern "C" int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* rece
         return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
     if (n > (size_t)INT32_MAX || n_recent > (size_t)INT32_MAX) return mivi::err_overflow();
     mivi::clear_error();
-    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(kST), 0, (hipStream_t)stream, logits, (int)n, recent,
-                       (int)n_recent, make_args(*cfg), (unsigned long long*)rng_state, token);
-    MIVI_HIP_CHECK(hipGetLastError());
-    return MIVI_OK;
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0;
+    MIVI_HIP_CHECK(hipGetDevice(&dev));
+    SampleWorkspace& ws = sample_workspace(dev);
+    std::lock_guard<std::mutex> lk(ws.mu);
+    if (!ws.done) MIVI_HIP_CHECK(hipEventCreateWithFlags(&ws.done, hipEventDisableTiming));
+    else MIVI_HIP_CHECK(hipStreamWaitEvent(s, ws.done, 0));  // the previous user is done with it
+    const size_t need = split_workspace(n, 1);
+    if (ws.bytes < need) {
+        if (ws.ptr) {
+            MIVI_HIP_CHECK(hipEventSynchronize(ws.done));
+            MIVI_HIP_CHECK(hipFree(ws.ptr));
+            ws.ptr = nullptr;
+            ws.bytes = 0;
+        }
+        MIVI_HIP_CHECK(hipMalloc(&ws.ptr, need));
+        ws.bytes = need;
+    }
+    const int32_t rc = launch_split(logits, (int64_t)n, (int)n, 1,
+                                    FlatSrc{n_recent ? recent : nullptr, (int)n_recent, 0}, mivi::SampleEos{},
+                                    nullptr, *cfg, rng_state, TokOut{token, nullptr, 0, 0, nullptr, mivi::EmbedNext{}},
+                                    ws.ptr, true, s);
+    MIVI_HIP_CHECK(hipEventRecord(ws.done, s));
+    return rc;
 }
 
 extern "C" size_t mivi_hip_sample_rows_workspace(size_t n, size_t rows) { return split_workspace(n, rows); }
