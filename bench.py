@@ -300,8 +300,8 @@ def sampler_bench(torch, hip, calls):
     window), µs per call between HIP events on the stream the calls run on:
     GenerationConfig::default on the split path (chunk kernel + pick kernel
     over the top-k candidates), and full-vocabulary categorical sampling
-    (temperature 1, no top-k / top-p), which runs the whole-row steps in the
-    pick kernel."""
+    (temperature 1, no top-k / top-p: chunk, exp, probability and pick
+    kernels)."""
     n = 65536
     g = torch.Generator(device="cuda").manual_seed(5)
     base = torch.randn(n, device="cuda", generator=g) * 3
@@ -310,7 +310,7 @@ def sampler_bench(torch, hip, calls):
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     out = {"n": n, "calls": calls}
     for name, cfg in (("default_config_us", hip.SamplerConfig.make()),
-                      ("categorical_whole_row_us",
+                      ("categorical_us",
                        hip.SamplerConfig.make(temperature=1.0, top_p=1.0, top_k=0, repetition_penalty=1.0))):
         fn = lambda l: hip.sample(l, rec[0], cfg, rng, tok)  # noqa: E731
         rows = [base.clone() for _ in range(calls)]
@@ -388,7 +388,7 @@ def main():
         extra["decode_config4"] = dec
         sm = sampler_bench(torch, hip, 50)
         log(f"sampler (65536 logits): {sm['default_config_us']:.1f} us default config (split path), "
-            f"{sm['categorical_whole_row_us']:.1f} us full-vocabulary categorical (whole row)")
+            f"{sm['categorical_us']:.1f} us full-vocabulary categorical")
         extra["sampler"] = sm
     if not a.no_decode and not a.no_config5:
         c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps)

@@ -49,7 +49,7 @@ constexpr int kCandVPT = 8;               // candidates per thread of the pick w
 constexpr int kCapB = kST * kCandVPT;     // candidates a row may hold
 constexpr int kMaxChunks = kST;           // chunks the pick workgroup indexes
 
-enum { kModeRow = 0, kModeGreedy = 1, kModeTopK = 2 };
+enum { kModeRow = 0, kModeGreedy = 1, kModeTopK = 2, kModeCat = 3 };
 
 struct SampleArgs {
     float temperature, top_p, min_p, ln_min_p, rep, presence, frequency;
@@ -765,6 +765,22 @@ __global__ void __launch_bounds__(kCT) sample_chunk_kernel(float* logits, int64_
     }
     if (mode == kModeRow) return;
     const size_t base = ((size_t)b * nch + ci) * kCapC;
+    if (mode == kModeCat) {
+        // the chunk's largest finite logit (cval[base]) for the softmax maximum
+        float m = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (i0 + e < cn && isfinite(x[e])) m = fmaxf(m, x[e]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if ((t & 63) == 0) sh.wf[t >> 6] = m;
+        __syncthreads();
+        if (t == 0) {
+            for (int w = 1; w < kCW; w++) m = fmaxf(m, sh.wf[w]);
+            cval[base] = m;
+        }
+        return;
+    }
     if (mode == kModeGreedy) {
         // the chunk's first maximum above -inf (sampler.rs:305-316)
         float best = -INFINITY;
@@ -842,6 +858,76 @@ __global__ void __launch_bounds__(kCT) sample_chunk_kernel(float* logits, int64_
     if (t == 0) ccount[(size_t)b * nch + ci] = (int)total;
 }
 
+// Categorical sampling without top-k / top-p (kModeCat), split over the
+// chunks. sample_cat_exp_kernel: M = the row's largest finite logit (the
+// chunks' maxima), min-p against it (sampler.rs:260-276), e = exp(x - M)
+// written over the chunk and the chunk's sum (cval[base + 1]); a row with no
+// finite logit takes e = 1 (the softmax's uniform branch, math.rs:43-48).
+// sample_cat_prob_kernel: S = the chunk sums in chunk order, p = e * (1/S)
+// written over the chunk (the probabilities the reference leaves) and the
+// chunk's 2^-40 fixed-point mass (cidx[base], [base + 1] as a u64).
+__global__ void __launch_bounds__(kCT) sample_cat_exp_kernel(float* logits, int64_t lstride, int n, SampleArgs c,
+                                                             float* cval) {
+    __shared__ float wf[kCW];
+    const int t = threadIdx.x, ci = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
+    float* L = logits + (int64_t)b * lstride;
+    const int c0 = ci * kCC, cn = min(kCC, n - c0), i0 = 4 * t;
+    float M = -INFINITY;
+    for (int j = 0; j < nch; j++) M = fmaxf(M, cval[((size_t)b * nch + j) * kCapC]);
+    const bool uniform = !isfinite(M);
+    const float thr = (c.min_p > 0.0f && c.min_p < 1.0f) ? M + c.ln_min_p : -INFINITY;
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = c0 + i0 + e;
+        if (i0 + e < cn) {
+            const float x = L[i];
+            const float y = uniform ? 1.0f : (isfinite(x) && !(x < thr)) ? expf(x - M) : 0.0f;
+            L[i] = y;
+            s += y;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((t & 63) == 0) wf[t >> 6] = s;
+    __syncthreads();
+    if (t == 0) {
+        float cs = wf[0];
+        for (int w = 1; w < kCW; w++) cs += wf[w];
+        cval[((size_t)b * nch + ci) * kCapC + 1] = cs;
+    }
+}
+
+__global__ void __launch_bounds__(kCT) sample_cat_prob_kernel(float* logits, int64_t lstride, int n, float* cval,
+                                                              int* cidx) {
+    __shared__ unsigned long long wsum[kCW];
+    const int t = threadIdx.x, ci = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
+    float* L = logits + (int64_t)b * lstride;
+    const int c0 = ci * kCC, cn = min(kCC, n - c0), i0 = 4 * t;
+    float S = 0.0f;
+    for (int j = 0; j < nch; j++) S += cval[((size_t)b * nch + j) * kCapC + 1];
+    const float inv = 1.0f / S;
+    unsigned long long w = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = c0 + i0 + e;
+        if (i0 + e < cn) {
+            const float p = L[i] * inv;
+            L[i] = p;
+            w += fixp(p);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) w += __shfl_xor(w, o, 64);
+    if ((t & 63) == 0) wsum[t >> 6] = w;
+    __syncthreads();
+    if (t == 0) {
+        unsigned long long cs = 0;
+        for (int k = 0; k < kCW; k++) cs += wsum[k];
+        *(unsigned long long*)(cidx + ((size_t)b * nch + ci) * kCapC) = cs;
+    }
+}
+
 // Where a row's token goes: tok[b], and the step history of sequence seq0 + b
 // when history is set.
 struct TokOut {
@@ -867,6 +953,47 @@ __global__ void __launch_bounds__(kST) sample_pick_kernel(float* logits, int64_t
     __shared__ Shared sh;
     const int t = threadIdx.x, b = blockIdx.x;
     float* L = logits + (int64_t)b * lstride;
+    if (mode == kModeCat) {
+        // 7b. categorical (sampler.rs:137-148) over the probabilities the
+        // chunk kernels left: the chunk where the fixed-point mass reaches
+        // r, then the index inside it
+        const float r = draw(rng + b, sh);
+        const unsigned long long tr = (unsigned long long)ceil((double)r * kFix);
+        const unsigned long long cm =
+            t < nch ? *(const unsigned long long*)(cidx + ((size_t)b * nch + t) * kCapC) : 0ull;
+        unsigned long long tot;
+        const unsigned long long ex = bscan_excl<kSW, unsigned long long>(cm, &tot, sh.wsum);
+        if (t == 0) sh.bin = 0;
+        __syncthreads();
+        if (t < nch && cm && ex < tr && tr <= ex + cm) {
+            sh.bin = (uint32_t)t;
+            sh.above = ex;
+        }
+        __syncthreads();
+        int tok;
+        if (tr == 0 || n == 0) {
+            tok = 0;
+        } else if (tot < tr) {
+            tok = n - 1;
+        } else {
+            const int cc = (int)sh.bin, c0 = cc * kCC, cn = min(kCC, n - c0);
+            const unsigned long long tr2 = tr - sh.above;
+            const unsigned long long wv = t < cn ? fixp(L[c0 + t]) : 0ull;
+            unsigned long long tot2;
+            const unsigned long long ex2 = bscan_excl<kSW, unsigned long long>(wv, &tot2, sh.wsum);
+            if (wv && ex2 < tr2 && tr2 <= ex2 + wv) sh.bin = (uint32_t)(c0 + t);
+            __syncthreads();
+            tok = (int)sh.bin;
+        }
+        if (t == 0) {
+            out.tok[b] = (uint32_t)tok;
+            if (out.history) out.history[(size_t)(*out.step) * out.hstride + out.seq0 + b] = (uint32_t)tok;
+        }
+        if (out.en.table)
+            mivi::embed_row(out.en.type, out.en.table, out.en.row_bytes, (uint32_t)tok, out.en.x + b * out.en.xs,
+                            out.en.dim, t, kST);
+        return;
+    }
     bool fast = mode != kModeRow;
     int M = 0;
     if (fast) {
@@ -927,6 +1054,7 @@ int32_t launch_split(float* logits, int64_t lstride, int n, int rows, const Src&
     if (nch <= kMaxChunks) {
         if (a.temperature <= 0.0f) mode = kModeGreedy;
         else if (a.top_k > 0 && a.top_k <= kKMax && a.top_k < n) mode = kModeTopK;
+        else if ((a.top_k <= 0 || a.top_k >= n) && !(a.top_p < 1.0f) && n > 0) mode = kModeCat;
     }
     float* cval = (float*)ws;
     int* cidx = (int*)(cval + (size_t)rows * nch * kCapC);
@@ -934,6 +1062,13 @@ int32_t launch_split(float* logits, int64_t lstride, int n, int rows, const Src&
     hipLaunchKernelGGL(sample_chunk_kernel<Src>, dim3((unsigned)nch, (unsigned)rows), dim3(kCT), 0, s, logits, lstride,
                        n, src, eos, step, a, mode, cval, cidx, ccount);
     MIVI_HIP_CHECK(hipGetLastError());
+    if (mode == kModeCat) {
+        hipLaunchKernelGGL(sample_cat_exp_kernel, dim3((unsigned)nch, (unsigned)rows), dim3(kCT), 0, s, logits, lstride,
+                           n, a, cval);
+        hipLaunchKernelGGL(sample_cat_prob_kernel, dim3((unsigned)nch, (unsigned)rows), dim3(kCT), 0, s, logits,
+                           lstride, n, cval, cidx);
+        MIVI_HIP_CHECK(hipGetLastError());
+    }
     hipLaunchKernelGGL(sample_pick_kernel, dim3((unsigned)rows), dim3(kST), 0, s, logits, lstride, n, nch, a, mode,
                        cval, cidx, ccount, (unsigned long long*)rng, out, write ? 1 : 0);
     MIVI_HIP_CHECK(hipGetLastError());
