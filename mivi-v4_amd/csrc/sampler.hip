@@ -865,15 +865,33 @@ __global__ void __launch_bounds__(kCT) sample_chunk_kernel(float* logits, int64_
 // finite logit takes e = 1 (the softmax's uniform branch, math.rs:43-48).
 // sample_cat_prob_kernel: S = the chunk sums in chunk order, p = e * (1/S)
 // written over the chunk (the probabilities the reference leaves) and the
-// chunk's 2^-40 fixed-point mass (cidx[base], [base + 1] as a u64).
+// chunk's 2^-40 fixed-point mass (cidx[base], [base + 1] as a u64). The
+// row's maximum and sum are block reductions over the chunk values with a
+// fixed tree, so every workgroup of the row gets the same M and S.
+template <class T, class Op>
+__device__ __forceinline__ T chunk_reduce(T v, T* w, Op op) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) w[threadIdx.x >> 6] = v;
+    __syncthreads();
+    T r = w[0];
+#pragma unroll
+    for (int k = 1; k < kCW; k++) r = op(r, w[k]);
+    __syncthreads();
+    return r;
+}
+
 __global__ void __launch_bounds__(kCT) sample_cat_exp_kernel(float* logits, int64_t lstride, int n, SampleArgs c,
                                                              float* cval) {
     __shared__ float wf[kCW];
     const int t = threadIdx.x, ci = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
     float* L = logits + (int64_t)b * lstride;
     const int c0 = ci * kCC, cn = min(kCC, n - c0), i0 = 4 * t;
+    auto fmax_op = [](float u, float v) { return fmaxf(u, v); };
+    auto fadd_op = [](float u, float v) { return u + v; };
     float M = -INFINITY;
-    for (int j = 0; j < nch; j++) M = fmaxf(M, cval[((size_t)b * nch + j) * kCapC]);
+    for (int j = t; j < nch; j += kCT) M = fmaxf(M, cval[((size_t)b * nch + j) * kCapC]);
+    M = chunk_reduce(M, wf, fmax_op);
     const bool uniform = !isfinite(M);
     const float thr = (c.min_p > 0.0f && c.min_p < 1.0f) ? M + c.ln_min_p : -INFINITY;
     float s = 0.0f;
@@ -887,25 +905,20 @@ __global__ void __launch_bounds__(kCT) sample_cat_exp_kernel(float* logits, int6
             s += y;
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-    if ((t & 63) == 0) wf[t >> 6] = s;
-    __syncthreads();
-    if (t == 0) {
-        float cs = wf[0];
-        for (int w = 1; w < kCW; w++) cs += wf[w];
-        cval[((size_t)b * nch + ci) * kCapC + 1] = cs;
-    }
+    s = chunk_reduce(s, wf, fadd_op);
+    if (t == 0) cval[((size_t)b * nch + ci) * kCapC + 1] = s;
 }
 
 __global__ void __launch_bounds__(kCT) sample_cat_prob_kernel(float* logits, int64_t lstride, int n, float* cval,
                                                               int* cidx) {
     __shared__ unsigned long long wsum[kCW];
+    __shared__ float wf[kCW];
     const int t = threadIdx.x, ci = blockIdx.x, b = blockIdx.y, nch = gridDim.x;
     float* L = logits + (int64_t)b * lstride;
     const int c0 = ci * kCC, cn = min(kCC, n - c0), i0 = 4 * t;
     float S = 0.0f;
-    for (int j = 0; j < nch; j++) S += cval[((size_t)b * nch + j) * kCapC + 1];
+    for (int j = t; j < nch; j += kCT) S += cval[((size_t)b * nch + j) * kCapC + 1];
+    S = chunk_reduce(S, wf, [](float u, float v) { return u + v; });
     const float inv = 1.0f / S;
     unsigned long long w = 0;
 #pragma unroll
@@ -917,15 +930,8 @@ __global__ void __launch_bounds__(kCT) sample_cat_prob_kernel(float* logits, int
             w += fixp(p);
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) w += __shfl_xor(w, o, 64);
-    if ((t & 63) == 0) wsum[t >> 6] = w;
-    __syncthreads();
-    if (t == 0) {
-        unsigned long long cs = 0;
-        for (int k = 0; k < kCW; k++) cs += wsum[k];
-        *(unsigned long long*)(cidx + ((size_t)b * nch + ci) * kCapC) = cs;
-    }
+    w = chunk_reduce(w, wsum, [](unsigned long long u, unsigned long long v) { return u + v; });
+    if (t == 0) *(unsigned long long*)(cidx + ((size_t)b * nch + ci) * kCapC) = w;
 }
 
 // Where a row's token goes: tok[b], and the step history of sequence seq0 + b
