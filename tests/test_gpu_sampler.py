@@ -38,6 +38,8 @@ CONFIGS = {
     "wide_top_k": dict(temperature=1.5, top_p=1.0, top_k=1000),
     "top_p_zero": dict(temperature=1.0, top_p=0.0, top_k=0),
     "min_p_top_k": dict(temperature=0.7, top_p=0.8, top_k=64, min_p=0.2, presence_penalty=0.3),
+    "categorical_min_p": dict(temperature=0.9, top_p=1.0, top_k=0, min_p=0.1, presence_penalty=0.4,
+                              frequency_penalty=0.2),
 }
 
 
@@ -136,6 +138,54 @@ def test_rows_ragged_length(hip, oracle, torch_mod, name):
     logits = (rng.standard_normal(n) * 2).astype(np.float32)
     recent = rng.integers(0, n, 64).tolist()
     run_pair(hip, oracle, torch_mod, logits, recent, CONFIGS[name], 99, 24, "rows")
+
+
+@pytest.mark.parametrize("api", ["row", "rows"])
+@pytest.mark.parametrize("finite", [1, 3])
+def test_categorical_masked_rows(hip, oracle, torch_mod, finite, api):
+    # full-vocabulary categorical sampling over a ragged row with only a few
+    # finite logits, in different chunks
+    n = 70001
+    logits = np.full(n, -np.inf, np.float32)
+    logits[[3, 40000, 69999][:finite]] = [0.5, -1.0, 2.0][:finite]
+    run_pair(hip, oracle, torch_mod, logits, [], CONFIGS["categorical"], 21 + finite, 16, api)
+
+
+@pytest.mark.parametrize("api", ["row", "rows"])
+def test_categorical_uniform_row(hip, oracle, torch_mod, api):
+    """A row with no finite logit: the softmax's uniform branch (math.rs:43-48),
+    1/n everywhere. The device takes the first index whose exact cumulative
+    mass reaches r; the reference's float32 running sum (sampler.rs:137-148)
+    drifts by up to ~5e-4 over 70001 equal terms, so its token can sit a few
+    dozen indices away. Each is checked against its own rule."""
+    torch = torch_mod
+    n = 70001
+    logits = np.full(n, -np.inf, np.float32)
+    cfgkw = CONFIGS["categorical"]
+    cfg_h = hip.SamplerConfig.make(**cfgkw)
+    cfg_o = oracle.sampler_config(**cfgkw)
+    rng_o = oracle.Rng(21)
+    st = int(rng_o.state.value)
+    rng_d = torch.tensor([st - (1 << 64) if st >= 1 << 63 else st], dtype=torch.int64, device="cuda")
+    tok_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for s in range(16):
+        l_d = torch.from_numpy(logits.copy()).cuda()
+        device_sample(hip, torch, api, l_d, None, cfg_h, rng_d, tok_d)
+        torch.cuda.synchronize()
+        state0 = int(rng_o.state.value)
+        t_o, l_o = oracle.sample(logits, [], cfg_o, rng_o)
+        assert (int(rng_d.item()) & MASK) == rng_o.state.value
+        got = l_d.cpu().numpy()
+        assert np.all(got == np.float32(1.0 / n)) and np.all(l_o == np.float32(1.0 / n))
+        r = draw(state0)[1]
+        # device: exact masses, index floor-ish of r * n
+        t_d = int(tok_d.item())
+        assert near_boundary(t_d, l_o, r, 1.0), (s, t_d, r)
+        # oracle: the float32 running sum
+        cum32 = np.cumsum(l_o)
+        lo = float(cum32[t_o - 1]) if t_o else 0.0
+        assert lo - 1e-6 <= r <= float(cum32[t_o]) + 1e-6, (s, t_o, r)
+        assert abs(t_d - t_o) <= 0.001 * n, (s, t_d, t_o)
 
 
 @pytest.mark.parametrize("scale", [1.0, 0.3])
