@@ -256,7 +256,9 @@ int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* recent, size_t 
  * (n_recent ids each), its state rng_states[b], its token tokens[b]; the same
  * results as mivi_hip_sample on each row. Spread over the whole device (a
  * chunk kernel over 1024-logit chunks, then one workgroup per row over the
- * chunks' top-k candidates when top_k <= 128), with `workspace` (device,
+ * chunks' top-k candidates when top_k <= 128; with no top-k and top_p >= 1,
+ * softmax kernels per chunk and a pick over the chunks' masses), with
+ * `workspace` (device,
  * 4-byte aligned) of at least mivi_hip_sample_rows_workspace(n, rows)
  * bytes, which calls running at once must not share. Asynchronous on the
  * stream. rows <= 65535. */

@@ -19,7 +19,7 @@ TS = {Q4_K: 144, Q6_K: 210, Q8_0: 34, F16: 2, BF16: 2, F32: 4}
 
 
 def dev(torch, a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return torch.from_numpy(np.array(a, order="C", copy=True)).cuda()
 
 
 def dense_bytes(t, W):
