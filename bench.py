@@ -7,8 +7,13 @@ rotated over enough distinct copies (> 1 GB) that the 256 MB Infinity Cache
 cannot serve repeats; inputs are resident in HBM before timing.
 
 `extra` carries the other configs measured in the same run: the Q4_K GEMV
-(config 1) and, unless --no-decode, the 1.2B-shape hybrid decode (config 4:
-fp16 KV prefilled with 4096 tokens, 256 greedy steps) in tok/s.
+(config 1), the Q4_K prefill GEMM (config 3) and, unless --no-decode, the
+1.2B-shape hybrid decode (config 4: fp16 KV prefilled with 4096 tokens, 256
+greedy steps) and the batched long-context decode (config 5: 8 sequences,
+Q8_0 KV of 32768 tokens, 128 greedy steps) in tok/s. Each carries the CPU
+oracle's figure on this host (the process's CPUs, at most 16, and the
+reference binary's default of 2 threads), and the decodes a parity record:
+the device's greedy tokens against the oracle's from the same state.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-decode] [--no-cpu]
 """
@@ -89,30 +94,79 @@ def gemv_bench(torch, hip, t, rows, cols, steps, warmup, seed, packed=False):
                 w_host=w_host, x_host=x_host)
 
 
-def cpu_gemv_baseline(t, w, x, rows, cols, budget_s):
+REF_THREADS = 2  # the reference binary's default rayon pool: at most 2 threads (src/main.rs:12-24)
+
+
+def cpu_threads():
+    """(threads of the CPU legs, CPUs visible to this process): every CPU the
+    process may run on, at most 16 (the host cores one GPU's box grants)."""
+    try:
+        vis = len(os.sched_getaffinity(0))
+    except AttributeError:
+        vis = os.cpu_count() or 1
+    return max(1, min(vis, 16)), vis
+
+
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
-    threads = min(os.cpu_count() or 1, 16)
-    pyoracle.set_threads(threads)
-    pyoracle.quantized_matvec(int(t), w, x, rows, cols)  # warm-up
+    return pyoracle
+
+
+def cpu_time(fn, budget_s, min_calls=1):
+    """Seconds per call of fn after one untimed call, over about budget_s."""
+    fn()
     n, t0 = 0, time.perf_counter()
     while True:
-        pyoracle.quantized_matvec(int(t), w, x, rows, cols)
+        fn()
         n += 1
-        if time.perf_counter() - t0 > budget_s:
+        if n >= min_calls and time.perf_counter() - t0 > budget_s:
             break
-    sec = (time.perf_counter() - t0) / n
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_gemv_baseline(t, w, x, rows, cols, budget_s):
+    """The oracle's AVX2 restatement of try_matvec on the same bytes at the
+    process's threads (the primary figure) and at the reference binary's 2."""
+    pyoracle = _oracle()
+    threads, vis = cpu_threads()
     algo = w.nbytes + cols * 4 + rows * 4
-    return dict(value=algo / sec / 1e9, unit="GB/s", cores=threads, kind="port",
-                sample=f"{n} calls of the oracle's AVX2 restatement of try_matvec (same {rows}x{cols} bytes), "
-                       f"{sec * 1e3:.2f} ms/call")
+    res = None
+    for th, budget in ((threads, budget_s), (REF_THREADS, budget_s / 2)):
+        pyoracle.set_threads(th)
+        sec, n = cpu_time(lambda: pyoracle.quantized_matvec(int(t), w, x, rows, cols), budget)
+        leg = dict(value=algo / sec / 1e9, unit="GB/s", cores=th, kind="port",
+                   sample=f"{n} calls of the oracle's AVX2 restatement of try_matvec (same {rows}x{cols} bytes), "
+                          f"{sec * 1e3:.2f} ms/call")
+        if res is None:
+            res = dict(leg, host_cpus_visible=vis)
+        else:
+            res["at_reference_default_threads"] = leg
+    return res
 
 
-def gemm_bench(torch, hip, steps, warmup):
+def cpu_gemm_baseline(w, x, batch, rows, cols, budget_s):
+    """Config 3 on the CPU: the oracle's restatement of quantized_matmul_rows
+    (lib.rs:143-357, batch > 8: transposed inputs, per-lane accumulation)."""
+    pyoracle = _oracle()
+    threads, vis = cpu_threads()
+    flop = 2.0 * batch * rows * cols
+    out = {"host_cpus_visible": vis}
+    for th, budget in ((threads, budget_s), (REF_THREADS, budget_s)):
+        pyoracle.set_threads(th)
+        sec, n = cpu_time(lambda: pyoracle.quantized_matmul_rows(12, w, x, batch, rows, cols), budget)
+        out[f"threads_{th}"] = dict(value=flop / sec / 1e12, unit="TFLOP/s", cores=th, kind="port",
+                                    sample=f"{n} calls at batch {batch}, {sec * 1e3:.0f} ms/call")
+    return out
+
+
+def gemm_bench(torch, hip, steps, warmup, cpu_budget_s=0.0):
     """Config 3: X [512 x 2048] ~ N(0,1) times W [8192 x 2048]^T Q4_K on MFMA."""
     rows, cols, batch = 8192, 2048, 512
-    w = torch.from_numpy(hip.synth_random_weights(hip.GgmlType.Q4_K, 300, rows, cols, 0.02)).cuda()
-    x = torch.from_numpy(hip.synth_normal(301, batch * cols)).cuda()
+    w_host = hip.synth_random_weights(hip.GgmlType.Q4_K, 300, rows, cols, 0.02)
+    x_host = hip.synth_normal(301, batch * cols)
+    w = torch.from_numpy(w_host).cuda()
+    x = torch.from_numpy(x_host).cuda()
     y = torch.empty(batch * rows, dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
@@ -127,9 +181,12 @@ def gemm_bench(torch, hip, steps, warmup):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     flop = 2.0 * batch * rows * cols
-    return dict(batch=batch, rows=rows, cols=cols, algo_flop=flop, ms_per_call=ms,
-                tflops=flop / (ms * 1e-3) / 1e12, frac_of_fp16_mfma_peak=flop / (ms * 1e-3) / 2.5e15,
-                note="includes the activation split kernel (fp16 hi/lo + sub-block sums) run per call")
+    res = dict(batch=batch, rows=rows, cols=cols, algo_flop=flop, ms_per_call=ms,
+               tflops=flop / (ms * 1e-3) / 1e12, frac_of_fp16_mfma_peak=flop / (ms * 1e-3) / 2.5e15,
+               note="includes the activation split kernel (fp16 hi/lo + sub-block sums) run per call")
+    if cpu_budget_s > 0:
+        res["cpu_baseline"] = cpu_gemm_baseline(w_host, x_host, batch, rows, cols, cpu_budget_s)
+    return res
 
 
 def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
@@ -187,34 +244,69 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
                           first_tokens=[int(v) for v in stoks[:8, 0]])
     log(f"decode: {steps / ds:.1f} tok/s with the device sampler (default GenerationConfig)")
     if cpu_budget_s > 0:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import pyoracle
-        threads = min(os.cpu_count() or 1, 16)
-        pyoracle.set_threads(threads)
-        o = pyoracle.Model(img, max_ctx=ctx, kv_precision=pyoracle.KV_F16RT)
-        k, v, conv = state
-        ok, ov = o.kv_views()
-        row = m.kv_row_bytes()
-        per = ok.size // 6
-        import numpy as np
-        for l in range(6):
-            kh = k[l * prefill * row:(l + 1) * prefill * row].view(np.float16).astype(np.float32).view(np.uint8)
-            vh = v[l * prefill * row:(l + 1) * prefill * row].view(np.float16).astype(np.float32).view(np.uint8)
-            ok[l * per:l * per + kh.size] = kh
-            ov[l * per:l * per + vh.size] = vh
-        o.conv_view()[:] = conv
-        tok, n, t3 = int(prompt[-1]), 0, time.perf_counter()
-        while n < steps:
-            lg = o.forward(tok, prefill + n)
-            tok = pyoracle.argmax(lg)
-            n += 1
-            if time.perf_counter() - t3 > cpu_budget_s:
-                break
-        sec = (time.perf_counter() - t3) / n
-        out["cpu_tok_s"] = 1.0 / sec
-        out["cpu_sample"] = f"{n} greedy steps of the oracle forward_step after importing the GPU-built state"
-        out["cpu_threads"] = threads
+        out.update(decode_cpu_leg(img, state, prompt, prefill, steps, ctx, toks[:, 0], cpu_budget_s))
         out["speedup_vs_cpu"] = out["tok_s"] / out["cpu_tok_s"]
+    return out
+
+
+def oracle_import(o, k, v, conv, tokens, row, n_layers, f16):
+    """State rows [n_layers, tokens, row] (the export layout) into the
+    oracle's [n_layers, max_seq, row] caches (fp16 rows widened to f32)."""
+    import numpy as np
+    ok, ov = o.kv_views()
+    per = ok.size // n_layers
+    for l in range(n_layers):
+        kk = k[l * tokens * row:(l + 1) * tokens * row]
+        vv = v[l * tokens * row:(l + 1) * tokens * row]
+        if f16:
+            kk = kk.view(np.float16).astype(np.float32).view(np.uint8)
+            vv = vv.view(np.float16).astype(np.float32).view(np.uint8)
+        ok[l * per:l * per + kk.size] = kk
+        ov[l * per:l * per + vv.size] = vv
+    o.conv_view()[:] = conv
+
+
+def oracle_greedy(pyoracle, o, tok, pos, n, budget_s):
+    """Up to n greedy steps of the oracle (stops after budget_s); returns
+    (tokens, seconds per step)."""
+    toks, t0 = [], time.perf_counter()
+    while len(toks) < n:
+        tok = pyoracle.argmax(o.forward(tok, pos + len(toks)))
+        toks.append(tok)
+        if time.perf_counter() - t0 > budget_s:
+            break
+    return toks, (time.perf_counter() - t0) / max(1, len(toks))
+
+
+def parity_record(got, want):
+    """Token-by-token comparison of the device's greedy tokens with the
+    oracle's over the steps the oracle ran."""
+    n = len(want)
+    div = next((i for i in range(n) if int(got[i]) != int(want[i])), None)
+    return dict(steps_compared=n, tokens_equal=div is None, first_divergence=div)
+
+
+def decode_cpu_leg(img, state, prompt, prefill, steps, ctx, gpu_toks, budget_s):
+    """Config 4 on the CPU: the oracle's forward_step continuing greedily from
+    the GPU-built state (the 4096-token prefill on the CPU would take minutes),
+    timed at the process's threads and at the reference default's 2; its
+    tokens are compared with the device's (parity)."""
+    pyoracle = _oracle()
+    threads, vis = cpu_threads()
+    k, v, conv = state
+    out = {}
+    for th, budget, n in ((threads, budget_s, steps), (REF_THREADS, budget_s / 2, steps)):
+        pyoracle.set_threads(th)
+        o = pyoracle.Model(img, max_ctx=ctx, kv_precision=pyoracle.KV_F16RT)
+        oracle_import(o, k, v, conv, prefill, 2 * 512, 6, True)
+        toks, sec = oracle_greedy(pyoracle, o, int(prompt[-1]), prefill, n, budget)
+        o.close()
+        if th == threads:
+            out.update(cpu_tok_s=1.0 / sec, cpu_threads=th, host_cpus_visible=vis,
+                       cpu_sample=f"{len(toks)} greedy steps of the oracle forward_step after importing the "
+                                  f"GPU-built state", parity=parity_record(gpu_toks, toks))
+        else:
+            out["cpu_at_reference_default_threads"] = dict(tok_s=1.0 / sec, threads=th, steps=len(toks))
     return out
 
 
@@ -250,7 +342,21 @@ def copy_calibration(torch, mib, reps):
     log(f"counter calibration: fill, {reps} copies and {reps} reductions of {n * 4} bytes")
 
 
-def batched_decode_bench(torch, hip, batch, ctx, steps):
+def config5_weight_bytes(cfg, batch):
+    """Weight bytes one batched step streams with the current column grouping:
+    the d = 2048 Q4_K projections take all the batch's columns (up to 8) in one
+    launch and read their weights once; the K = 8192 FFN down runs groups of
+    four columns side by side, each reading the matrix; the packed Q6_K head
+    takes two columns per launch."""
+    from mivi_hip.synthmodel import weight_bytes_per_token
+    wb = weight_bytes_per_token(**cfg)
+    down = cfg["n_layers"] * cfg["dim"] * cfg["hidden"] // 256 * 144
+    head = cfg["vocab"] * cfg["dim"] // 256 * 210
+    rest = wb - down - head
+    return rest * -(-batch // 8) + down * -(-batch // 4) + head * -(-batch // 2)
+
+
+def batched_decode_bench(torch, hip, batch, ctx, steps, cpu_budget_s=0.0):
     """Config 5: 8 sequences, Q8_0 KV with `ctx` cached tokens each, greedy.
 
     The caches hold seeded synthetic Q8_0 rows (N(0, 1) values quantized with
@@ -258,21 +364,28 @@ def batched_decode_bench(torch, hip, batch, ctx, steps):
     the state-import entry point: prefilling 8 x 32768 tokens one at a time
     would take minutes, and attention reads the same bytes whatever they hold.
     """
-    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid, weight_bytes_per_token
+    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid
     img = build_hybrid(**LFM2_1B2, ctx_len=65536, seed=2024)
     m = hip.Model(img, max_ctx=ctx + steps, kv_precision=hip.KvPrecision.Q8_0, max_batch=batch)
     info = m.info
-    t0 = time.perf_counter()
-    for b in range(batch):
+
+    def state(b):
         k = hip.synth_random_weights(hip.GgmlType.Q8_0, 500 + 2 * b, info.n_attn_layers * ctx, info.kv_dim, 1.0)
         v = hip.synth_random_weights(hip.GgmlType.Q8_0, 501 + 2 * b, info.n_attn_layers * ctx, info.kv_dim, 1.0)
-        conv = hip.synth_normal(600 + b, m.conv_len(), std=0.1)
-        m.import_state(ctx, k, v, conv, seq=b)
-        del k, v
+        return k, v, hip.synth_normal(600 + b, m.conv_len(), std=0.1)
+
+    t0 = time.perf_counter()
+    for b in range(batch):
+        m.import_state(ctx, *state(b), seq=b)
     log(f"config 5: {batch} synthetic Q8_0 caches of {ctx} tokens imported in {time.perf_counter() - t0:.1f}s")
     rng = __import__("numpy").random.default_rng(12)
     toks = [int(t) for t in rng.integers(0, LFM2_1B2["vocab"], batch)]
     m.generate_greedy(toks, [ctx] * batch, 4)  # graph capture; rewrites positions ctx.. below
+    # the warm-up advanced each sequence's ShortConv state: back to the
+    # imported one (an interval import of no rows with the state)
+    empty = __import__("numpy").empty(0, __import__("numpy").uint8)
+    for b in range(batch):
+        m.import_state_at(0, 0, empty, empty, hip.synth_normal(600 + b, m.conv_len(), std=0.1), seq=b)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     out = m.generate_greedy(toks, [ctx] * batch, steps)
@@ -280,18 +393,56 @@ def batched_decode_bench(torch, hip, batch, ctx, steps):
     kv_row = info.kv_dim // 32 * 34
     mean_t = ctx + (steps + 1) / 2
     kv_bytes = batch * info.n_attn_layers * 2 * kv_row * mean_t
-    wb = weight_bytes_per_token(**LFM2_1B2)
-    down = LFM2_1B2["n_layers"] * LFM2_1B2["dim"] * LFM2_1B2["hidden"] // 256 * 144
-    cols = 2  # columns per batched GEMV launch (d = 2048)
+    wbs = config5_weight_bytes(LFM2_1B2, batch)
     res = dict(batch=batch, cached_tokens=ctx, steps=steps, kv_precision="q8_0", tok_s=batch * steps / dt,
                ms_per_step=1e3 * dt / steps, kv_bytes_per_step=kv_bytes,
-               kv_gbs_over_whole_step=kv_bytes * steps / dt / 1e9,
-               weight_bytes_per_step=(wb - down) * -(-batch // cols) + down * batch,
-               note=("d = 2048 projections and the head read their weights once per 2 sequences (batched GEMV), "
-                     "the d = 8192 FFN down once per sequence; kv_gbs_over_whole_step divides the KV bytes by the "
-                     "whole step time, not the attention kernels' time; caches synthetic, see docstring"),
+               kv_gbs_over_whole_step=kv_bytes * steps / dt / 1e9, weight_bytes_per_step=wbs,
+               gbs_whole_step=(kv_bytes + wbs) * steps / dt / 1e9,
+               note=("weight_bytes_per_step: the d = 2048 projections read their weights once for the 8 columns, "
+                     "the K = 8192 FFN down once per group of four columns, the packed head once per two; "
+                     "kv_gbs_over_whole_step divides the KV bytes by the whole step time, not the attention "
+                     "kernels' time; caches synthetic, see docstring"),
                first_tokens=[int(v) for v in out[:4, 0]])
     m.close()
+    if cpu_budget_s > 0:
+        res.update(config5_cpu_leg(img, state, toks, ctx, steps, out, cpu_budget_s))
+        res["speedup_vs_cpu"] = res["tok_s"] / res["cpu_tok_s"]
+    return res
+
+
+def config5_cpu_leg(img, state, toks, ctx, steps, gpu_out, budget_s):
+    """Config 5 on the CPU: 8 sequential single-sequence decodes (the
+    reference runs one Model per sequence) from the same imported states, a
+    few greedy steps each within the budget; their tokens against the
+    device's batched ones (parity). Then sequence 0 at the reference
+    default's 2 threads."""
+    pyoracle = _oracle()
+    threads, vis = cpu_threads()
+    batch = len(toks)
+    per_seq = max(1, min(steps, 3))
+    pyoracle.set_threads(threads)
+    o = pyoracle.Model(img, max_ctx=ctx + steps, kv_precision=pyoracle.KV_Q8_0)
+    row = o.info.kv_dim // 32 * 34
+    secs, n_steps, par = 0.0, 0, []
+    for b in range(batch):
+        o.reset()
+        oracle_import(o, *state(b), ctx, row, 6, False)
+        got, sec = oracle_greedy(pyoracle, o, toks[b], ctx, per_seq, budget_s / batch)
+        secs += sec * len(got)
+        n_steps += len(got)
+        par.append(parity_record(gpu_out[:, b], got))
+    res = dict(cpu_tok_s=n_steps / secs, cpu_threads=threads, host_cpus_visible=vis,
+               cpu_sample=f"{n_steps} oracle forward_step calls over the {batch} sequences "
+                          f"({per_seq} greedy steps each at {ctx}+ cached tokens), state imported, not timed",
+               parity=dict(steps_compared=sum(p["steps_compared"] for p in par),
+                           tokens_equal=all(p["tokens_equal"] for p in par),
+                           per_sequence_first_divergence=[p["first_divergence"] for p in par]))
+    pyoracle.set_threads(REF_THREADS)
+    o.reset()
+    oracle_import(o, *state(0), ctx, row, 6, False)
+    got, sec = oracle_greedy(pyoracle, o, toks[0], ctx, 2, budget_s / 2)
+    res["cpu_at_reference_default_threads"] = dict(tok_s=1.0 / sec, threads=REF_THREADS, steps=len(got))
+    o.close()
     return res
 
 
@@ -378,7 +529,10 @@ def main():
     }
     extra["q6k_gemv_config2_gguf_rows"]["frac_of_peak"] = q6r["gbs"] / HBM_PEAK_GBS
     extra["q4k_gemv_config1"]["frac_of_peak"] = q4["gbs"] / HBM_PEAK_GBS
-    g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3)
+    if not a.no_cpu:
+        extra["q4k_gemv_config1"]["cpu_baseline"] = cpu_gemv_baseline(hip.GgmlType.Q4_K, q4["w_host"], q4["x_host"],
+                                                                       8192, 2048, a.cpu_seconds / 2)
+    g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3, 0 if a.no_cpu else a.cpu_seconds / 2)
     log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s")
     extra["q4k_gemm_config3"] = g3
     if not a.no_decode:
@@ -391,7 +545,7 @@ def main():
             f"{sm['categorical_us']:.1f} us full-vocabulary categorical")
         extra["sampler"] = sm
     if not a.no_decode and not a.no_config5:
-        c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps)
+        c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps, 0 if a.no_cpu else a.cpu_seconds)
         log(f"config 5: {c5['tok_s']:.0f} tok/s over 8 sequences, {c5['ms_per_step']:.2f} ms per step")
         extra["decode_config5"] = c5
     line = {
@@ -405,7 +559,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        # x enters the GEMV as three int8 digit planes against one scale per
+        # launch; codes x digits accumulate exactly in int32 (matrix cores),
+        # sub-block scales and the output are f32
+        "dtype": "i8x3 digit planes x 6-bit codes -> i32, f32 scales and output",
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q6_K by this build's encoder; x ~ N(0,1))",
         "config": {"workload": "config2_q6k_head_gemv", "rows": 65536, "cols": 2048, "weight_type": "Q6_K",
                    "weight_layout": "packed row quads (mivi_hip_pack_weights, done once, not timed)",

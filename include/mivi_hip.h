@@ -190,6 +190,16 @@ int32_t mivi_hip_model_forward_step(mivi_model* m, size_t seq, uint32_t token, s
 int32_t mivi_hip_model_forward(mivi_model* m, size_t seq, uint32_t token, size_t pos,
                                float* logits_host);
 
+/* model.rs:488-491 Model::forward of sequences 0..batch-1 (tokens[b] at
+ * pos[b], host arrays) in one batched step: the batched decode's kernels
+ * (each projection one GEMV over the batch's columns, one attention launch
+ * with the batch's split count). logits_host (batch * vocab_size floats,
+ * host, row b = sequence b) may be NULL. The reference runs one Model per
+ * sequence; each row equals that sequence's forward up to float rounding.
+ * Synchronous. */
+int32_t mivi_hip_model_forward_batch(mivi_model* m, size_t batch, const uint32_t* tokens,
+                                     const size_t* pos, float* logits_host);
+
 /* Greedy decode loop (the argmax feedback of oracle_comparison_test.rs:37-50
  * and sampler.rs:305-316, without penalties): feeds `token` at `pos`, then
  * n_steps - 1 times the argmax of the previous logits; writes the n_steps
@@ -225,6 +235,27 @@ int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t tokens, co
                                     const void* v_in, size_t kv_len, const float* conv_in,
                                     size_t conv_len);
 
+/* cache.rs:688-746 KvCache::export_state_range for sequence seq: the K and V
+ * rows of positions [start, start + tokens) of every attention layer, laid
+ * out as mivi_hip_model_export_state's ([n_attn_layers, tokens, row]; kv_len
+ * bytes each, at least that size); with conv_out non-NULL also the
+ * ShortConv state (arena.rs:110-114). An interval past max_seq_len returns
+ * MIVI_ERR_KV_CACHE (KvError::ContextOverflow). Host buffers; synchronous. */
+int32_t mivi_hip_model_export_state_range(mivi_model* m, size_t seq, size_t start, size_t tokens,
+                                          void* k_out, void* v_out, size_t kv_len, float* conv_out,
+                                          size_t conv_len);
+
+/* cache.rs:827-914 KvCache::import_state_at: an interval export into
+ * positions [start, start + tokens) of sequence seq's caches, every other
+ * position left as it is; kv_len must be exactly n_attn_layers * tokens *
+ * row (else MIVI_ERR_KV_CACHE, KvError::DimMismatch). With conv_in non-NULL
+ * (conv_len exact) the ShortConv state is imported too (arena.rs:116-123),
+ * else left as it is. The device model keeps no cache position, so this is
+ * also import_state_range (cache.rs:814-822). Host buffers; synchronous. */
+int32_t mivi_hip_model_import_state_at(mivi_model* m, size_t seq, size_t start, size_t tokens,
+                                       const void* k_in, const void* v_in, size_t kv_len,
+                                       const float* conv_in, size_t conv_len);
+
 /* ---------------------------------------------------------------------
  * Sampling: crates/mivi-model/src/sampler.rs:91-135 (Sampler::sample) with
  * GenerationConfig's sampling fields (config.rs:163-174). top_k 0 = off.
@@ -259,7 +290,7 @@ int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* recent, size_t 
  * chunks' top-k candidates when top_k <= 128; with no top-k and top_p >= 1,
  * softmax kernels per chunk and a pick over the chunks' masses), with
  * `workspace` (device,
- * 4-byte aligned) of at least mivi_hip_sample_rows_workspace(n, rows)
+ * 8-byte aligned) of at least mivi_hip_sample_rows_workspace(n, rows)
  * bytes, which calls running at once must not share. Asynchronous on the
  * stream. rows <= 65535. */
 size_t mivi_hip_sample_rows_workspace(size_t n, size_t rows);
@@ -312,6 +343,27 @@ int32_t mivi_hip_prefix_cache_insert_delta(mivi_prefix_cache* pc, mivi_model* m,
                                            size_t pos, uint64_t prev_hash,
                                            const uint32_t* tokens, size_t n_tokens,
                                            size_t chunk_index, uint64_t* hash_out);
+
+/* insert_chunk (prefix.rs:239-249): a full snapshot, the whole prefix
+ * [0, pos) of sequence seq's KV caches and its ShortConv state in one node
+ * with no parent (restoring it needs no other chunk); its hash chains the
+ * chunk's tokens on prev_hash. Synchronous. */
+int32_t mivi_hip_prefix_cache_insert(mivi_prefix_cache* pc, mivi_model* m, size_t seq, size_t pos,
+                                     uint64_t prev_hash, const uint32_t* tokens, size_t n_tokens,
+                                     size_t chunk_index, uint64_t* hash_out);
+
+/* find_longest_suffix_match (prefix.rs:453-517): the longest suffix of
+ * tokens, k whole chunks starting at an absolute position (start_pos + its
+ * offset) that is a multiple of the chunk size, whose tokens equal a cached
+ * chunk's (by the chunk's standalone hash). *suffix_len = the matched tokens
+ * (0 if none), *match_pos = the position the chunk's state was taken at,
+ * *hash_out = its hash; touches it in the LRU order. Only the tokens are
+ * matched: the caller must check that its state fits the preceding context.
+ * Several matching chunks: the lowest hash (the reference's order is that
+ * of its hash map). */
+int32_t mivi_hip_prefix_cache_find_suffix(mivi_prefix_cache* pc, size_t start_pos, const uint32_t* tokens,
+                                          size_t n, size_t* suffix_len, size_t* match_pos,
+                                          uint64_t* hash_out);
 
 /* find_longest_prefix (prefix.rs:200-237): tokens matched by the deepest
  * cached chunk (0 if none) and its hash; touches it in the LRU order. */

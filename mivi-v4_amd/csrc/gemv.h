@@ -161,8 +161,10 @@ struct SampleEos {
 // (logits of sequence b at logits + b * lstride), penalty window = the last
 // `window` tokens of history[step * hstride + seq]; writes tok[b] and the
 // history at *step. rng: one xorshift64* state per sequence (rng[b]). ws:
-// sample_seq_workspace(n, batch) bytes of device memory (4-byte aligned);
-// the logits are left penalised and divided by the temperature.
+// sample_seq_workspace(n, batch) bytes of device memory (8-byte aligned);
+// the logits are left as the reference's sample() leaves its slice (the
+// probabilities, or the penalised logits divided by the temperature on the
+// greedy path).
 // en: the sampled tokens' embeddings for the next step (EmbedNext).
 size_t sample_seq_workspace(size_t n, size_t batch);
 int32_t launch_sample_seq(float* logits, int64_t lstride, int n, uint32_t* history, int hstride, int seq0, int batch,

@@ -1894,6 +1894,32 @@ extern "C" int32_t mivi_hip_model_forward(mivi_model* m, size_t seq, uint32_t to
     return mivi_hip_model_forward_step(m, seq, token, pos, 1, logits);
 }
 
+// Model::forward (model.rs:488-491) of sequences 0..batch-1 in one batched
+// step: the kernels of the batched decode (every projection one GEMV over the
+// batch's columns, one attention launch with the batch's split count), the
+// head storing logits.
+extern "C" int32_t mivi_hip_model_forward_batch(mivi_model* m, size_t batch, const uint32_t* tokens,
+                                                const size_t* pos, float* logits_host) {
+    if (!m || batch == 0 || batch > m->info.max_batch || !tokens || !pos)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    for (size_t b = 0; b < batch; b++) {
+        int32_t rc = check_tok_pos(m, tokens[b], pos[b]);
+        if (rc) return rc;
+    }
+    for (size_t b = 0; b < batch; b++) {
+        int32_t rc = set_ctrl(m, b, tokens[b], pos[b]);
+        if (rc) return rc;
+    }
+    int32_t rc = enqueue_step(m, 0, batch, true, false, m->stream, true, 0, m->info.n_layers, true, false);
+    if (rc) return rc;
+    if (logits_host)
+        MIVI_HIP_CHECK(hipMemcpy2DAsync(logits_host, m->info.vocab_size * 4, m->seqs[0].logits,
+                                        m->strides.logits * 4, m->info.vocab_size * 4, batch,
+                                        hipMemcpyDeviceToHost, m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return clear_error();
+}
+
 extern "C" int32_t mivi_hip_model_set_prefill_tile(mivi_model* m, size_t tile_tokens) {
     if (!m) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null model");
     if (tile_tokens > 4096) return set_error(MIVI_ERR_INVALID_ARGUMENT, "prefill tile of %zu tokens (at most 4096)", tile_tokens);
@@ -2057,14 +2083,17 @@ extern "C" int32_t mivi_hip_model_generate(mivi_model* m, size_t batch, const ui
 
 // One layer's Q8_0 cache between the reference's rows (tokens x n_kv x 68
 // bytes: per kv head two blocks of f16 scale + 32 quants) and the q8g_* group
-// layout (whole groups; bytes of tokens past `tokens` left as they are).
-static void q8_rows_to_groups(const uint8_t* rows, size_t tokens, int n_kv, bool is_v, uint8_t* groups) {
+// layout. `groups` holds whole groups starting with the one that contains
+// the first row's position; p0 = that position mod 16. Bytes of positions
+// outside the rows are left as they are.
+static void q8_rows_to_groups(const uint8_t* rows, size_t p0, size_t tokens, int n_kv, bool is_v, uint8_t* groups) {
     const size_t rb = (size_t)n_kv * 68;
     for (size_t p = 0; p < tokens; p++) {
-        const int t = (int)(p % 16);
+        const size_t r = p0 + p;
+        const int t = (int)(r % 16);
         for (int h = 0; h < n_kv; h++) {
             const uint8_t* src = rows + p * rb + (size_t)h * 68;
-            uint8_t* g = groups + q8g_base(p, h, n_kv);
+            uint8_t* g = groups + q8g_base(r, h, n_kv);
             for (int b = 0; b < 2; b++) {
                 memcpy(g + q8g_d_off(t, b), src + 34 * b, 2);
                 for (int i = 0; i < 32; i++) g[is_v ? q8g_v_off(t, 32 * b + i) : q8g_k_off(t, 32 * b + i)] = src[34 * b + 2 + i];
@@ -2072,19 +2101,127 @@ static void q8_rows_to_groups(const uint8_t* rows, size_t tokens, int n_kv, bool
         }
     }
 }
-static void q8_groups_to_rows(const uint8_t* groups, size_t tokens, int n_kv, bool is_v, uint8_t* rows) {
+static void q8_groups_to_rows(const uint8_t* groups, size_t p0, size_t tokens, int n_kv, bool is_v, uint8_t* rows) {
     const size_t rb = (size_t)n_kv * 68;
     for (size_t p = 0; p < tokens; p++) {
-        const int t = (int)(p % 16);
+        const size_t r = p0 + p;
+        const int t = (int)(r % 16);
         for (int h = 0; h < n_kv; h++) {
             uint8_t* dst = rows + p * rb + (size_t)h * 68;
-            const uint8_t* g = groups + q8g_base(p, h, n_kv);
+            const uint8_t* g = groups + q8g_base(r, h, n_kv);
             for (int b = 0; b < 2; b++) {
                 memcpy(dst + 34 * b, g + q8g_d_off(t, b), 2);
                 for (int i = 0; i < 32; i++) dst[34 * b + 2 + i] = g[is_v ? q8g_v_off(t, 32 * b + i) : q8g_k_off(t, 32 * b + i)];
             }
         }
     }
+}
+
+static size_t conv_state_len(const mivi_model* m) {
+    return m->info.n_layers * m->info.dim * std::max<size_t>(1, m->info.ssm_conv_kernel);
+}
+
+// KvError::ContextOverflow of an interval [start, start + tokens)
+// (cache.rs:692-697, :834-839)
+static int32_t kv_interval_check(mivi_model* m, size_t seq, size_t start, size_t tokens) {
+    if (!m || seq >= m->info.max_batch) return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad model or sequence");
+    const size_t mx = m->info.max_seq_len;
+    if (start > mx || tokens > mx - start)
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: Context length exceeded: attempted pos %zu >= max_seq_len %zu",
+                         start > mx ? start : start + tokens, mx);
+    return MIVI_OK;
+}
+
+// K and V rows of positions [start, start + tokens) of every attention layer
+// of sequence seq, to host buffers laid out [n_attn_layers, tokens, row]
+// (cache.rs:688-746). The Q8_0 group layout goes through the host as the
+// whole groups covering the interval.
+static int32_t kv_rows_out(mivi_model* m, size_t seq, size_t start, size_t tokens, void* k_out, void* v_out) {
+    const mivi_model_info& c = m->info;
+    SeqState& st = m->seqs[seq];
+    const size_t lb = m->kv_layer_bytes, rb = m->kv_row_bytes, tb = tokens * rb;
+    if (tokens == 0) return MIVI_OK;
+    if (m->kv_packed) {
+        const int nkv = (int)c.n_kv_heads;
+        const size_t g0 = start / 16, g1 = (start + tokens + 15) / 16, gb = (g1 - g0) * 16 * rb;
+        std::vector<uint8_t> kg(gb), vg(gb);
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            MIVI_HIP_CHECK(hipMemcpyAsync(kg.data(), st.kc + l * lb + g0 * 16 * rb, gb, hipMemcpyDeviceToHost, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync(vg.data(), st.vc + l * lb + g0 * 16 * rb, gb, hipMemcpyDeviceToHost, m->stream));
+            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+            q8_groups_to_rows(kg.data(), start % 16, tokens, nkv, false, (uint8_t*)k_out + l * tb);
+            q8_groups_to_rows(vg.data(), start % 16, tokens, nkv, true, (uint8_t*)v_out + l * tb);
+        }
+        return MIVI_OK;
+    }
+    for (size_t l = 0; l < c.n_attn_layers; l++) {
+        MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)k_out + l * tb, st.kc + l * lb + start * rb, tb, hipMemcpyDeviceToHost,
+                                      m->stream));
+        MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)v_out + l * tb, st.vc + l * lb + start * rb, tb, hipMemcpyDeviceToHost,
+                                      m->stream));
+    }
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return MIVI_OK;
+}
+
+// The host rows of an interval export into positions [start, start +
+// tokens) of sequence seq's caches, other positions untouched
+// (cache.rs:827-914). In the Q8_0 group layout, groups only partly inside
+// the interval are read back first and rewritten whole.
+static int32_t kv_rows_in(mivi_model* m, size_t seq, size_t start, size_t tokens, const void* k_in, const void* v_in) {
+    const mivi_model_info& c = m->info;
+    SeqState& st = m->seqs[seq];
+    const size_t lb = m->kv_layer_bytes, rb = m->kv_row_bytes, tb = tokens * rb;
+    if (tokens == 0) return MIVI_OK;
+    if (m->kv_packed) {
+        const int nkv = (int)c.n_kv_heads;
+        const size_t g0 = start / 16, g1 = (start + tokens + 15) / 16, gb = (g1 - g0) * 16 * rb;
+        const bool partial = (start % 16) != 0 || ((start + tokens) % 16) != 0;
+        std::vector<uint8_t> kg(gb, 0), vg(gb, 0);
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            uint8_t* kd = st.kc + l * lb + g0 * 16 * rb;
+            uint8_t* vd = st.vc + l * lb + g0 * 16 * rb;
+            if (partial) {
+                MIVI_HIP_CHECK(hipMemcpyAsync(kg.data(), kd, gb, hipMemcpyDeviceToHost, m->stream));
+                MIVI_HIP_CHECK(hipMemcpyAsync(vg.data(), vd, gb, hipMemcpyDeviceToHost, m->stream));
+            }
+            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));  // and the previous layer's uploads have read kg/vg
+            q8_rows_to_groups((const uint8_t*)k_in + l * tb, start % 16, tokens, nkv, false, kg.data());
+            q8_rows_to_groups((const uint8_t*)v_in + l * tb, start % 16, tokens, nkv, true, vg.data());
+            MIVI_HIP_CHECK(hipMemcpyAsync(kd, kg.data(), gb, hipMemcpyHostToDevice, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync(vd, vg.data(), gb, hipMemcpyHostToDevice, m->stream));
+        }
+    } else {
+        for (size_t l = 0; l < c.n_attn_layers; l++) {
+            MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb + start * rb, (const uint8_t*)k_in + l * tb, tb,
+                                          hipMemcpyHostToDevice, m->stream));
+            MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb + start * rb, (const uint8_t*)v_in + l * tb, tb,
+                                          hipMemcpyHostToDevice, m->stream));
+        }
+    }
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return MIVI_OK;
+}
+
+// arena.rs:110-114: the sequence's current ShortConv state (the ping-pong
+// buffer its phase selects) to the host
+static int32_t conv_out_host(mivi_model* m, size_t seq, float* conv_out) {
+    Ctrl ctl;
+    MIVI_HIP_CHECK(hipMemcpyAsync(&ctl, m->ctrl, sizeof(Ctrl), hipMemcpyDeviceToHost, m->stream));
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    const SeqState& st = m->seqs[seq];
+    const float* cur = (ctl.phase[seq] & 1) ? st.conv_b : st.conv_a;
+    MIVI_HIP_CHECK(hipMemcpy(conv_out, cur, conv_state_len(m) * 4, hipMemcpyDeviceToHost));
+    return MIVI_OK;
+}
+
+// arena.rs:116-123: the state becomes phase 0's input buffer
+static int32_t conv_in_host(mivi_model* m, size_t seq, const float* conv_in) {
+    MIVI_HIP_CHECK(hipMemcpyAsync(m->seqs[seq].conv_a, conv_in, conv_state_len(m) * 4, hipMemcpyHostToDevice, m->stream));
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->phase[seq], 0);
+    MIVI_HIP_CHECK(hipGetLastError());
+    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    return MIVI_OK;
 }
 
 static int32_t state_sizes(mivi_model* m, size_t seq, size_t tokens, size_t kv_len, size_t conv_len) {
@@ -2094,7 +2231,7 @@ static int32_t state_sizes(mivi_model* m, size_t seq, size_t tokens, size_t kv_l
                          tokens, m->info.max_seq_len);
     size_t need = m->info.n_attn_layers * tokens * m->kv_row_bytes;
     if (kv_len < need) return err_buffer_too_small(need, kv_len);
-    size_t cl = m->info.n_layers * m->info.dim * std::max<size_t>(1, m->info.ssm_conv_kernel);
+    size_t cl = conv_state_len(m);
     if (conv_len < cl) return err_buffer_too_small(cl, conv_len);
     return MIVI_OK;
 }
@@ -2103,32 +2240,8 @@ extern "C" int32_t mivi_hip_model_export_state(mivi_model* m, size_t seq, size_t
                                                size_t kv_len, float* conv_out, size_t conv_len) {
     int32_t rc = state_sizes(m, seq, tokens, kv_len, conv_len);
     if (rc) return rc;
-    const mivi_model_info& c = m->info;
-    SeqState& st = m->seqs[seq];
-    size_t lb = m->kv_layer_bytes, tb = tokens * m->kv_row_bytes;
-    if (m->kv_packed) {  // whole groups to the host, then the reference's rows
-        const int nkv = (int)c.n_kv_heads;
-        const size_t gb = (tokens + 15) / 16 * 16 * m->kv_row_bytes;
-        std::vector<uint8_t> kg(gb), vg(gb);
-        for (size_t l = 0; l < c.n_attn_layers; l++) {
-            MIVI_HIP_CHECK(hipMemcpyAsync(kg.data(), st.kc + l * lb, gb, hipMemcpyDeviceToHost, m->stream));
-            MIVI_HIP_CHECK(hipMemcpyAsync(vg.data(), st.vc + l * lb, gb, hipMemcpyDeviceToHost, m->stream));
-            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
-            q8_groups_to_rows(kg.data(), tokens, nkv, false, (uint8_t*)k_out + l * tb);
-            q8_groups_to_rows(vg.data(), tokens, nkv, true, (uint8_t*)v_out + l * tb);
-        }
-    } else {
-        for (size_t l = 0; l < c.n_attn_layers; l++) {
-            MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)k_out + l * tb, st.kc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
-            MIVI_HIP_CHECK(hipMemcpyAsync((uint8_t*)v_out + l * tb, st.vc + l * lb, tb, hipMemcpyDeviceToHost, m->stream));
-        }
-    }
-    Ctrl ctl;
-    MIVI_HIP_CHECK(hipMemcpyAsync(&ctl, m->ctrl, sizeof(Ctrl), hipMemcpyDeviceToHost, m->stream));
-    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
-    size_t cl = c.n_layers * c.dim * std::max<size_t>(1, c.ssm_conv_kernel);
-    const float* cur = (ctl.phase[seq] & 1) ? st.conv_b : st.conv_a;
-    MIVI_HIP_CHECK(hipMemcpy(conv_out, cur, cl * 4, hipMemcpyDeviceToHost));
+    if ((rc = kv_rows_out(m, seq, 0, tokens, k_out, v_out))) return rc;
+    if ((rc = conv_out_host(m, seq, conv_out))) return rc;
     return clear_error();
 }
 
@@ -2137,31 +2250,37 @@ extern "C" int32_t mivi_hip_model_import_state(mivi_model* m, size_t seq, size_t
                                                size_t conv_len) {
     int32_t rc = state_sizes(m, seq, tokens, kv_len, conv_len);
     if (rc) return rc;
-    const mivi_model_info& c = m->info;
-    SeqState& st = m->seqs[seq];
-    size_t lb = m->kv_layer_bytes, tb = tokens * m->kv_row_bytes;
-    if (m->kv_packed) {  // the reference's rows into whole groups on the host, then to the device
-        const int nkv = (int)c.n_kv_heads;
-        const size_t gb = (tokens + 15) / 16 * 16 * m->kv_row_bytes;
-        std::vector<uint8_t> kg(gb, 0), vg(gb, 0);
-        for (size_t l = 0; l < c.n_attn_layers; l++) {
-            MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));  // the previous layer's copies have read kg/vg
-            q8_rows_to_groups((const uint8_t*)k_in + l * tb, tokens, nkv, false, kg.data());
-            q8_rows_to_groups((const uint8_t*)v_in + l * tb, tokens, nkv, true, vg.data());
-            MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb, kg.data(), gb, hipMemcpyHostToDevice, m->stream));
-            MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb, vg.data(), gb, hipMemcpyHostToDevice, m->stream));
-        }
-    } else {
-        for (size_t l = 0; l < c.n_attn_layers; l++) {
-            MIVI_HIP_CHECK(hipMemcpyAsync(st.kc + l * lb, (const uint8_t*)k_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
-            MIVI_HIP_CHECK(hipMemcpyAsync(st.vc + l * lb, (const uint8_t*)v_in + l * tb, tb, hipMemcpyHostToDevice, m->stream));
-        }
-    }
-    size_t cl = c.n_layers * c.dim * std::max<size_t>(1, c.ssm_conv_kernel);
-    // the imported state becomes phase 0's input buffer
-    MIVI_HIP_CHECK(hipMemcpyAsync(st.conv_a, conv_in, cl * 4, hipMemcpyHostToDevice, m->stream));
-    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->phase[seq], 0);
-    MIVI_HIP_CHECK(hipStreamSynchronize(m->stream));
+    if ((rc = kv_rows_in(m, seq, 0, tokens, k_in, v_in))) return rc;
+    if ((rc = conv_in_host(m, seq, conv_in))) return rc;
+    return clear_error();
+}
+
+extern "C" int32_t mivi_hip_model_export_state_range(mivi_model* m, size_t seq, size_t start, size_t tokens,
+                                                     void* k_out, void* v_out, size_t kv_len, float* conv_out,
+                                                     size_t conv_len) {
+    int32_t rc = kv_interval_check(m, seq, start, tokens);
+    if (rc) return rc;
+    const size_t need = m->info.n_attn_layers * tokens * m->kv_row_bytes;
+    if ((tokens && (!k_out || !v_out)) || kv_len < need) return err_buffer_too_small(need, kv_len);
+    if (conv_out && conv_len < conv_state_len(m)) return err_buffer_too_small(conv_state_len(m), conv_len);
+    if ((rc = kv_rows_out(m, seq, start, tokens, k_out, v_out))) return rc;
+    if (conv_out && (rc = conv_out_host(m, seq, conv_out))) return rc;
+    return clear_error();
+}
+
+extern "C" int32_t mivi_hip_model_import_state_at(mivi_model* m, size_t seq, size_t start, size_t tokens,
+                                                  const void* k_in, const void* v_in, size_t kv_len,
+                                                  const float* conv_in, size_t conv_len) {
+    int32_t rc = kv_interval_check(m, seq, start, tokens);
+    if (rc) return rc;
+    const size_t need = m->info.n_attn_layers * tokens * m->kv_row_bytes;
+    if (kv_len != need || (tokens && (!k_in || !v_in)))  // KvError::DimMismatch (cache.rs:851-856)
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: dimension mismatch: expected %zu, got %zu", need, kv_len);
+    if (conv_in && conv_len != conv_state_len(m))
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: dimension mismatch: expected %zu, got %zu",
+                         conv_state_len(m), conv_len);
+    if ((rc = kv_rows_in(m, seq, start, tokens, k_in, v_in))) return rc;
+    if (conv_in && (rc = conv_in_host(m, seq, conv_in))) return rc;
     return clear_error();
 }
 
@@ -2198,6 +2317,7 @@ uint64_t prefix_chunk_hash(uint64_t prev, const uint32_t* t, size_t n) {
 struct PrefixNode {
     size_t chunk_index = 0, pos = 0, kv_start = 0;
     uint64_t hash = 0, parent = 0;
+    uint64_t standalone = 0;  // compute_chunk_hash(0, tokens): the suffix search's key (prefix.rs:24-26)
     bool has_parent = false;
     std::vector<uint32_t> tokens;
     uint8_t* dev = nullptr;  // K interval of every attention layer | V interval | ShortConv state
@@ -2331,7 +2451,66 @@ extern "C" void mivi_hip_prefix_cache_clear(mivi_prefix_cache* pc) {
     pc->total = 0;
 }
 
-// insert_delta_chunk (prefix.rs:251-303) + insert_node (:360-392)
+// insert_node (prefix.rs:360-392): a node for the chunk `tokens` (hash
+// chained on prev_hash) owning positions [kv_start, pos) of sequence seq's
+// KV caches and the sequence's ShortConv state, copied device to device. In
+// the Q8_0 group layout the interval is stored as the whole groups covering
+// it (rows past pos in the last group come along and are rewritten by the
+// decode before they are read).
+static int32_t prefix_insert_node(mivi_prefix_cache* pc, mivi_model* m, size_t seq, uint64_t prev_hash,
+                                  const uint32_t* tokens, size_t n_tokens, size_t chunk_index, size_t kv_start,
+                                  size_t pos, bool has_parent, uint64_t* hash_out) {
+    const uint64_t hash = prefix_chunk_hash(prev_hash, tokens, n_tokens);
+    *hash_out = hash;
+    clear_error();
+    if (pc->chunks.count(hash)) {  // already cached: the new snapshot is not taken
+        pc->touch(hash);
+        return MIVI_OK;
+    }
+    PrefixNode nd;
+    nd.chunk_index = chunk_index;
+    nd.pos = pos;
+    nd.kv_start = kv_start;
+    nd.hash = hash;
+    nd.parent = prev_hash;
+    nd.has_parent = has_parent;
+    nd.standalone = prefix_chunk_hash(0, tokens, n_tokens);
+    nd.tokens.assign(tokens, tokens + n_tokens);
+    const size_t end = m->kv_packed ? std::min<size_t>((pos + 15) / 16 * 16, m->info.max_seq_len) : pos;
+    const size_t iv = (end - kv_start) * pc->row_bytes;  // one layer's interval (rows, or whole groups)
+    nd.kv_bytes = pc->n_attn * iv;
+    nd.conv_bytes = pc->conv_len * 4;
+    MIVI_HIP_CHECK(hipMalloc(&nd.dev, std::max<size_t>(1, 2 * nd.kv_bytes + nd.conv_bytes)));
+    SeqState& st = m->seqs[seq];
+    const size_t lb = m->kv_layer_bytes, off = kv_start * pc->row_bytes;
+    hipError_t e = hipSuccess;
+    if (pc->n_attn && iv) {
+        e = hipMemcpy2DAsync(nd.dev, iv, st.kc + off, lb, iv, pc->n_attn, hipMemcpyDeviceToDevice, m->stream);
+        if (e == hipSuccess)
+            e = hipMemcpy2DAsync(nd.dev + nd.kv_bytes, iv, st.vc + off, lb, iv, pc->n_attn, hipMemcpyDeviceToDevice,
+                                 m->stream);
+    }
+    if (e == hipSuccess && pc->conv_len) {
+        hipLaunchKernelGGL(conv_snapshot_kernel, dim3(64), dim3(256), 0, m->stream,
+                           (float*)(nd.dev + 2 * nd.kv_bytes), st.conv_a, st.conv_b, &m->ctrl->phase[seq], pc->conv_len);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(nd.dev);
+        return set_error(MIVI_ERR_HIP, "prefix snapshot copy failed: %s", hipGetErrorString(e));
+    }
+    const size_t nb = nd.bytes();
+    pc->chunks.emplace(hash, std::move(nd));
+    pc->lru.push_back(hash);
+    pc->total += nb;
+    uint64_t ev;
+    while (pc->chunks.size() > pc->max_chunks && pc->select_eviction(&ev)) pc->evict(ev);
+    pc->prune(pc->max_bytes);
+    return MIVI_OK;
+}
+
+// insert_delta_chunk (prefix.rs:251-303)
 extern "C" int32_t mivi_hip_prefix_cache_insert_delta(mivi_prefix_cache* pc, mivi_model* m, size_t seq, size_t pos,
                                                       uint64_t prev_hash, const uint32_t* tokens, size_t n_tokens,
                                                       size_t chunk_index, uint64_t* hash_out) {
@@ -2358,51 +2537,58 @@ extern "C" int32_t mivi_hip_prefix_cache_insert_delta(mivi_prefix_cache* pc, miv
             return dim_mismatch(start, it->second.pos);
         has_parent = true;
     }
-    const uint64_t hash = prefix_chunk_hash(prev_hash, tokens, n_tokens);
-    *hash_out = hash;
+    return prefix_insert_node(pc, m, seq, prev_hash, tokens, n_tokens, chunk_index, start, end, has_parent, hash_out);
+}
+
+// insert_chunk (prefix.rs:239-249): a full snapshot, the whole prefix
+// [0, pos) of sequence seq and its ShortConv state in one node with no
+// parent; restoring it needs no other node.
+extern "C" int32_t mivi_hip_prefix_cache_insert(mivi_prefix_cache* pc, mivi_model* m, size_t seq, size_t pos,
+                                                uint64_t prev_hash, const uint32_t* tokens, size_t n_tokens,
+                                                size_t chunk_index, uint64_t* hash_out) {
+    if (!pc || !m || !hash_out || (n_tokens && !tokens) || seq >= m->info.max_batch)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "bad argument");
+    int32_t rc = prefix_shape(pc, m);
+    if (rc) return rc;
+    if (pos > m->info.max_seq_len)
+        return set_error(MIVI_ERR_KV_CACHE, "KV cache error: Context length exceeded: attempted pos %zu >= max_seq_len %zu",
+                         pos, m->info.max_seq_len);
+    return prefix_insert_node(pc, m, seq, prev_hash, tokens, n_tokens, chunk_index, 0, pos, false, hash_out);
+}
+
+// find_longest_suffix_match (prefix.rs:453-517): for k full chunks from the
+// longest down, the suffix of the last k * chunk_size tokens (its absolute
+// position start_pos + offset a multiple of chunk_size) against the cached
+// chunks of that many tokens by their standalone hash; the first found is
+// touched in the LRU order. The reference scans its hash map in no defined
+// order; here the chunks are scanned in ascending hash order.
+extern "C" int32_t mivi_hip_prefix_cache_find_suffix(mivi_prefix_cache* pc, size_t start_pos, const uint32_t* tokens,
+                                                     size_t n, size_t* suffix_len, size_t* match_pos,
+                                                     uint64_t* hash_out) {
+    if (!pc || !suffix_len || !match_pos || !hash_out || (n && !tokens))
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
+    *suffix_len = 0;
+    *match_pos = 0;
+    *hash_out = 0;
     clear_error();
-    if (pc->chunks.count(hash)) {  // already cached: the new snapshot is not taken
-        pc->touch(hash);
-        return MIVI_OK;
+    const size_t cs = pc->chunk_size;
+    if (n < cs || pc->chunks.empty()) return MIVI_OK;
+    const size_t max_k = (n > start_pos ? n - start_pos : 0) / cs;
+    for (size_t k = max_k; k >= 1; k--) {
+        const size_t len = k * cs, s0 = n - len;
+        if (s0 < start_pos || (start_pos + s0) % cs) continue;
+        const uint64_t sh = prefix_chunk_hash(0, tokens + s0, len);
+        for (const auto& e : pc->chunks) {
+            const PrefixNode& nd = e.second;
+            if (nd.tokens.size() == len && nd.standalone == sh) {
+                pc->touch(e.first);
+                *suffix_len = len;
+                *match_pos = nd.pos;
+                *hash_out = e.first;
+                return MIVI_OK;
+            }
+        }
     }
-    PrefixNode nd;
-    nd.chunk_index = chunk_index;
-    nd.pos = end;
-    nd.kv_start = start;
-    nd.hash = hash;
-    nd.parent = prev_hash;
-    nd.has_parent = has_parent;
-    nd.tokens.assign(tokens, tokens + n_tokens);
-    const size_t iv = (end - start) * pc->row_bytes;  // one layer's interval (rows, or whole groups)
-    nd.kv_bytes = pc->n_attn * iv;
-    nd.conv_bytes = pc->conv_len * 4;
-    MIVI_HIP_CHECK(hipMalloc(&nd.dev, std::max<size_t>(1, 2 * nd.kv_bytes + nd.conv_bytes)));
-    SeqState& st = m->seqs[seq];
-    const size_t lb = m->kv_layer_bytes, off = start * pc->row_bytes;
-    hipError_t e = hipSuccess;
-    if (pc->n_attn) {
-        e = hipMemcpy2DAsync(nd.dev, iv, st.kc + off, lb, iv, pc->n_attn, hipMemcpyDeviceToDevice, m->stream);
-        if (e == hipSuccess)
-            e = hipMemcpy2DAsync(nd.dev + nd.kv_bytes, iv, st.vc + off, lb, iv, pc->n_attn, hipMemcpyDeviceToDevice,
-                                 m->stream);
-    }
-    if (e == hipSuccess && pc->conv_len) {
-        hipLaunchKernelGGL(conv_snapshot_kernel, dim3(64), dim3(256), 0, m->stream,
-                           (float*)(nd.dev + 2 * nd.kv_bytes), st.conv_a, st.conv_b, &m->ctrl->phase[seq], pc->conv_len);
-        e = hipGetLastError();
-    }
-    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
-    if (e != hipSuccess) {
-        (void)hipFree(nd.dev);
-        return set_error(MIVI_ERR_HIP, "prefix snapshot copy failed: %s", hipGetErrorString(e));
-    }
-    const size_t nb = nd.bytes();
-    pc->chunks.emplace(hash, std::move(nd));
-    pc->lru.push_back(hash);
-    pc->total += nb;
-    uint64_t ev;
-    while (pc->chunks.size() > pc->max_chunks && pc->select_eviction(&ev)) pc->evict(ev);
-    pc->prune(pc->max_bytes);
     return MIVI_OK;
 }
 
@@ -2467,8 +2653,8 @@ extern "C" int32_t mivi_hip_prefix_cache_restore(mivi_prefix_cache* pc, mivi_mod
     const size_t lb = m->kv_layer_bytes;
     for (auto it = path.rbegin(); it != path.rend(); ++it) {
         const PrefixNode* p = *it;
-        const size_t iv = (p->pos - p->kv_start) * pc->row_bytes, off = p->kv_start * pc->row_bytes;
-        if (!pc->n_attn) continue;
+        if (!pc->n_attn || !p->kv_bytes) continue;
+        const size_t iv = p->kv_bytes / pc->n_attn, off = p->kv_start * pc->row_bytes;
         MIVI_HIP_CHECK(hipMemcpy2DAsync(st.kc + off, lb, p->dev, iv, iv, pc->n_attn, hipMemcpyDeviceToDevice, m->stream));
         MIVI_HIP_CHECK(hipMemcpy2DAsync(st.vc + off, lb, p->dev + p->kv_bytes, iv, iv, pc->n_attn,
                                         hipMemcpyDeviceToDevice, m->stream));

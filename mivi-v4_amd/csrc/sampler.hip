@@ -1166,7 +1166,8 @@ extern "C" int32_t mivi_hip_sample_rows(float* logits, size_t n, size_t rows, si
     if (workspace_bytes < split_workspace(n, rows))
         return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "workspace of %zu bytes, %zu needed", workspace_bytes,
                                split_workspace(n, rows));
-    if ((uintptr_t)workspace & 3) return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "workspace not 4-byte aligned");
+    // the categorical path keeps 64-bit chunk masses in the workspace
+    if ((uintptr_t)workspace & 7) return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "workspace not 8-byte aligned");
     mivi::clear_error();
     return launch_split(logits, (int64_t)row_stride, (int)n, (int)rows,
                         FlatSrc{n_recent ? recent : nullptr, (int)n_recent, (int64_t)recent_stride}, mivi::SampleEos{},

@@ -125,16 +125,21 @@ _sig = {
     "mivi_hip_model_reset": ([_P], _I),
     "mivi_hip_model_forward_step": ([_P, _S, C.c_uint32, _S, _I, _P], _I),
     "mivi_hip_model_forward": ([_P, _S, C.c_uint32, _S, _P], _I),
+    "mivi_hip_model_forward_batch": ([_P, _S, _P, _P, _P], _I),
     "mivi_hip_model_generate_greedy": ([_P, _S, _P, _P, _S, _P], _I),
     "mivi_hip_model_prefill": ([_P, _S, _P, _S, _S], _I),
     "mivi_hip_model_set_prefill_tile": ([_P, _S], _I),
     "mivi_hip_model_export_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_model_import_state": ([_P, _S, _S, _P, _P, _S, _P, _S], _I),
+    "mivi_hip_model_export_state_range": ([_P, _S, _S, _S, _P, _P, _S, _P, _S], _I),
+    "mivi_hip_model_import_state_at": ([_P, _S, _S, _S, _P, _P, _S, _P, _S], _I),
     "mivi_hip_read_floor": ([_P, _S, _P], _I),
     "mivi_hip_prefix_cache_create": ([_S, _S, _S, C.POINTER(_P)], _I),
     "mivi_hip_prefix_cache_destroy": ([_P], None),
     "mivi_hip_prefix_chunk_hash": ([C.c_uint64, _P, _S], C.c_uint64),
     "mivi_hip_prefix_cache_insert_delta": ([_P, _P, _S, _S, C.c_uint64, _P, _S, _S, C.POINTER(C.c_uint64)], _I),
+    "mivi_hip_prefix_cache_insert": ([_P, _P, _S, _S, C.c_uint64, _P, _S, _S, C.POINTER(C.c_uint64)], _I),
+    "mivi_hip_prefix_cache_find_suffix": ([_P, _S, _P, _S, C.POINTER(_S), C.POINTER(_S), C.POINTER(C.c_uint64)], _I),
     "mivi_hip_prefix_cache_find": ([_P, _P, _S, C.POINTER(_S), C.POINTER(C.c_uint64)], _I),
     "mivi_hip_prefix_cache_restore": ([_P, _P, _S, _P, _S, C.POINTER(_S), C.POINTER(C.c_uint64)], _I),
     "mivi_hip_prefix_cache_len": ([_P], _S),

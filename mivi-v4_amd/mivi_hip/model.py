@@ -52,6 +52,17 @@ class Model:
     def forward(self, token: int, pos: int, seq: int = 0) -> np.ndarray:
         return self.forward_step(token, pos, True, seq)
 
+    def forward_batch(self, tokens, pos) -> np.ndarray:
+        """Model::forward of sequences 0..batch-1 in one batched step (the
+        batched decode's kernels). Returns [batch, vocab] logits."""
+        t = np.ascontiguousarray(np.atleast_1d(tokens), np.uint32)
+        p = np.ascontiguousarray(np.atleast_1d(pos), np.uint64)
+        out = np.empty((t.size, self.info.vocab_size), np.float32)
+        _check(_lib.mivi_hip_model_forward_batch(self._h, t.size, t.ctypes.data_as(C.c_void_p),
+                                                 p.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p)),
+               ModelError)
+        return out
+
     def prefill(self, tokens, pos0: int = 0, seq: int = 0):
         t = np.ascontiguousarray(tokens, np.uint32)
         _check(_lib.mivi_hip_model_prefill(self._h, seq, t.ctypes.data_as(C.c_void_p), t.size, pos0), ModelError)
@@ -112,6 +123,33 @@ class Model:
                                                 conv.ctypes.data_as(C.c_void_p), conv.size), ModelError)
 
 
+    def export_state_range(self, start: int, tokens: int, seq: int = 0, conv: bool = False):
+        """KvCache::export_state_range (cache.rs:688-746): K and V rows of
+        positions [start, start + tokens) of every attention layer (and the
+        ShortConv state when conv). Returns (k, v) or (k, v, conv)."""
+        n = self.info.n_attn_layers * tokens * self.kv_row_bytes()
+        k = np.empty(n, np.uint8)
+        v = np.empty(n, np.uint8)
+        cs = np.empty(self.conv_len(), np.float32) if conv else None
+        _check(_lib.mivi_hip_model_export_state_range(self._h, seq, start, tokens, k.ctypes.data_as(C.c_void_p),
+                                                      v.ctypes.data_as(C.c_void_p), n,
+                                                      cs.ctypes.data_as(C.c_void_p) if conv else None,
+                                                      cs.size if conv else 0), ModelError)
+        return (k, v, cs) if conv else (k, v)
+
+    def import_state_at(self, start: int, tokens: int, k: np.ndarray, v: np.ndarray, conv=None, seq: int = 0):
+        """KvCache::import_state_at (cache.rs:827-914): rows of an interval
+        export into positions [start, start + tokens); the ShortConv state too
+        when conv is given."""
+        k = np.ascontiguousarray(k, np.uint8)
+        v = np.ascontiguousarray(v, np.uint8)
+        cs = None if conv is None else np.ascontiguousarray(conv, np.float32)
+        _check(_lib.mivi_hip_model_import_state_at(self._h, seq, start, tokens, k.ctypes.data_as(C.c_void_p),
+                                                   v.ctypes.data_as(C.c_void_p), min(k.nbytes, v.nbytes),
+                                                   None if cs is None else cs.ctypes.data_as(C.c_void_p),
+                                                   0 if cs is None else cs.size), ModelError)
+
+
 def chunk_hash(prev_hash: int, tokens) -> int:
     """compute_chunk_hash (prefix.rs:70-87)."""
     t = np.ascontiguousarray(tokens, np.uint32)
@@ -162,6 +200,25 @@ class PrefixCache:
                                                        t.ctypes.data_as(C.c_void_p), t.size, chunk_index,
                                                        C.byref(h)), ModelError)
         return int(h.value)
+
+    def insert_chunk(self, model: "Model", prev_hash: int, tokens, chunk_index: int, pos: int, seq: int = 0) -> int:
+        """insert_chunk (prefix.rs:239-249): a full snapshot of positions
+        [0, pos) of sequence seq of model and its ShortConv state."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        h = C.c_uint64()
+        _check(_lib.mivi_hip_prefix_cache_insert(self._h, model._h, seq, pos, C.c_uint64(prev_hash),
+                                                 t.ctypes.data_as(C.c_void_p), t.size, chunk_index, C.byref(h)),
+               ModelError)
+        return int(h.value)
+
+    def find_longest_suffix_match(self, start_pos: int, tokens):
+        """find_longest_suffix_match (prefix.rs:453-517): (suffix_len,
+        match_pos, hash) of the matched chunk, or None."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        n, p, h = C.c_size_t(), C.c_size_t(), C.c_uint64()
+        _check(_lib.mivi_hip_prefix_cache_find_suffix(self._h, start_pos, t.ctypes.data_as(C.c_void_p), t.size,
+                                                      C.byref(n), C.byref(p), C.byref(h)), ModelError)
+        return (int(n.value), int(p.value), int(h.value)) if n.value else None
 
     def find_longest_prefix(self, tokens):
         """(matched tokens, hash) of the deepest cached chunk, (0, 0) if none."""

@@ -67,8 +67,10 @@ def build_hybrid(dim: int, hidden: int, n_layers: int, attn_layers, n_heads: int
             mat(p + "attn_v.weight", kv_dim, dim)
             mat(p + "attn_output.weight", dim, dim)
             if qk_norm:
-                g.add_f32_vector(p + "attn_q_norm.weight", 1.0 + synth_normal(nxt(), head_dim, 0.0, 0.1))
-                g.add_f32_vector(p + "attn_k_norm.weight", 1.0 + synth_normal(nxt(), head_dim, 0.0, 0.1))
+                # seeds of their own: every other tensor equals the qk_norm=False model's
+                qs = seed * 1000 + 900_000 + 2 * i
+                g.add_f32_vector(p + "attn_q_norm.weight", 1.0 + synth_normal(qs, head_dim, 0.0, 0.1))
+                g.add_f32_vector(p + "attn_k_norm.weight", 1.0 + synth_normal(qs + 1, head_dim, 0.0, 0.1))
         else:
             g.add_f32_vector(p + "ssm_norm.weight", ones)
             mat(p + "shortconv.in_proj.weight", 3 * dim, dim)

@@ -586,8 +586,12 @@ static void gqa_attention_rows(const float* q, const uint8_t* kc, const uint8_t*
     size_t hpk = nh / (nkv ? nkv : 1);
     if (hpk < 1) hpk = 1;
     float scale = 1.0f / sqrtf((float)hd);
-    float vbuf[256];
+    /* query heads are independent (each keeps its own running max, sum and
+     * output, in token order), so long caches spread them over the threads */
+    int nt = seq * nh >= 65536 ? or_get_threads() : 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
     for (size_t h = 0; h < nh; h++) {
+        float vbuf[256];
         size_t kvh = h / hpk;
         const float* qh = q + h * hd;
         float* oh = attn_out + h * hd;

@@ -12,7 +12,7 @@ import os
 import numpy as np
 import pytest
 
-from conftest import GOLDEN
+from conftest import GOLDEN, import_into_oracle, q8_rows_close
 
 pytestmark = pytest.mark.gpu
 
@@ -325,9 +325,15 @@ def test_sampled_generation_matches_host_loop(hip, oracle, small_img):
     # penalties)
     prompt = [3, 17, 250, 9, 41, 77]
     eos = (2, 5)
+    # the fourth is full-vocabulary categorical sampling (top_k 0, top_p 1:
+    # the split path's exp / probability kernels and the pick's categorical
+    # branch, with end-of-sequence suppression, penalties from the history
+    # and the next-step embedding inside the graph)
     for cfgkw, seed in ((dict(), 7), (dict(temperature=0.9, top_p=0.95, top_k=0, min_p=0.02,
                                           presence_penalty=0.3, frequency_penalty=0.2), 99),
-                        (dict(temperature=0.0, repetition_penalty=1.3), 1)):
+                        (dict(temperature=0.0, repetition_penalty=1.3), 1),
+                        (dict(temperature=0.9, top_p=1.0, top_k=0, min_p=0.05, repetition_penalty=1.1,
+                              presence_penalty=0.3, frequency_penalty=0.2), 123)):
         m1 = hip.Model(small_img, max_ctx=128)
         m1.prefill(prompt[:-1])
         got = m1.generate([prompt[-1]], [len(prompt) - 1], 40, hip.SamplerConfig.make(**cfgkw), [seed], eos)[:, 0]
@@ -350,11 +356,16 @@ def test_sampled_generation_greedy_config_equals_generate_greedy(hip, small_img)
     assert np.array_equal(g, s)
 
 
-def test_sampled_generation_batch_matches_single_sequences(hip, small_img):
+@pytest.mark.parametrize("cfgkw", [dict(temperature=0.7, top_p=0.9, top_k=50),
+                                   dict(temperature=0.9, top_p=1.0, top_k=0, min_p=0.05, repetition_penalty=1.1,
+                                        presence_penalty=0.3, frequency_penalty=0.2)])
+def test_sampled_generation_batch_matches_single_sequences(hip, small_img, cfgkw):
+    # the second configuration is full-vocabulary categorical: the batch's
+    # history windows and next-step embeddings per sequence
     B = 3
     rng = np.random.default_rng(5)
     prompts = [rng.integers(0, 1024, 5 + 2 * b) for b in range(B)]
-    cfg = hip.SamplerConfig.make(temperature=0.7, top_p=0.9, top_k=50)
+    cfg = hip.SamplerConfig.make(**cfgkw)
     mb = hip.Model(small_img, max_ctx=128, max_batch=B)
     for b, pr in enumerate(prompts):
         mb.prefill(pr[:-1], seq=b)
@@ -391,3 +402,107 @@ def test_full_shape_greedy_256_steps_match_oracle(hip, oracle):
         tok = oracle.argmax(o.forward(tok, n + i))
         want.append(tok)
     assert list(got) == want
+
+
+def oracle_from_device(oracle, img, m, n, oprec, max_ctx):
+    """An oracle model holding the state the device model m built over n
+    tokens (its exported caches and ShortConv state, bytes as stored)."""
+    k, v, conv = m.export_state(n)
+    o = oracle.Model(img, max_ctx=max_ctx, kv_precision=oprec)
+    import_into_oracle(o, k, v, conv, n, m.kv_row_bytes(), m.info.n_attn_layers, f16=(oprec == 100))
+    return o
+
+
+@pytest.mark.parametrize("prec,oprec", [(0, 0), (2, 100), (1, 1)])
+def test_qk_norm_token_and_chunked_paths_match_oracle(hip, oracle, prec, oprec):
+    """transformer.rs:81-96 (token path) and :459-466 (tile path): per-head
+    RMSNorm of q with attn_q_norm and of k with attn_k_norm before RoPE, as
+    real LFM2 checkpoints carry them.
+
+    F32 and fp16 caches: the logits at every prompt position on the token
+    path, and the chunked path's next-token logits, against the oracle's own
+    run. Q8_0 cache: a K value within rounding of a Q8_0 step quantizes to
+    the neighbouring code under any other float order, and with QK-norm's
+    sharp scores that moves logits by more than 1e-3 over a long prompt (the
+    oracle's AVX2 and scalar kernels, both the reference's, differ by 2.6e-3
+    here after 119 tokens). So the Q8_0 cache is checked code by code against
+    the oracle's (each within one step, few different), and the logits
+    against the oracle continuing from the device's own cache bytes. Then
+    greedy tokens from the captured graph."""
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(**SMALL, ctx_len=4096, seed=19, qk_norm=True)
+    prompt = np.random.default_rng(23).integers(0, SMALL["vocab"], 120)
+    n = len(prompt) - 1
+    o = oracle.Model(img, max_ctx=512, kv_precision=oprec)
+    mt = hip.Model(img, max_ctx=512, kv_precision=prec)
+    worst = 0.0
+    for p, t in enumerate(prompt[:-1]):
+        worst = max(worst, rel_err(mt.forward(int(t), p), o.forward(int(t), p)))
+    # Q8_0: only a sanity bound here (the codes and the per-step arithmetic
+    # are checked below)
+    assert worst <= (1e-3 if prec != 1 else 1e-2), worst
+    mc = hip.Model(img, max_ctx=512, kv_precision=prec)
+    mc.set_prefill_strategy(32)
+    mc.prefill(prompt[:-1])
+    tok = int(prompt[-1])
+    row, L = mt.kv_row_bytes(), mt.info.n_attn_layers
+    if prec == 1:
+        ko, vo = o.kv_views()
+        per = ko.size // L
+        for mm in (mt, mc):
+            k, v, _ = mm.export_state(n)
+            for l in range(L):
+                assert q8_rows_close(k[l * n * row:(l + 1) * n * row], ko[l * per:l * per + n * row], n, 1, row)
+                assert q8_rows_close(v[l * n * row:(l + 1) * n * row], vo[l * per:l * per + n * row], n, 1, row)
+        ot, oc = oracle_from_device(oracle, img, mt, n, oprec, 512), oracle_from_device(oracle, img, mc, n, oprec, 512)
+    else:
+        ot = oc = o
+    lo = ot.forward(tok, n)
+    assert rel_err(mt.forward(tok, n), lo) <= 1e-3
+    assert rel_err(mc.forward(tok, n), lo if oc is ot else oc.forward(tok, n)) <= 1e-3
+    # the norm weights matter: the same model without them gives other logits
+    mp = hip.Model(build_hybrid(**SMALL, ctx_len=4096, seed=19), max_ctx=512, kv_precision=prec)
+    mp.prefill(prompt[:-1])
+    assert rel_err(mp.forward(tok, n), lo) > 1e-2
+    # 12 greedy steps from the next token (both models stand at position n + 1)
+    first, want = oracle.argmax(lo), []
+    t = first
+    for i in range(12):
+        t = oracle.argmax(ot.forward(t, n + 1 + i))
+        want.append(t)
+    assert list(mt.generate_greedy([first], [n + 1], 12)[:, 0]) == want
+    if oc is ot:
+        assert list(mc.generate_greedy([first], [n + 1], 12)[:, 0]) == want
+
+
+@pytest.mark.parametrize("prec,oprec", [(2, 100), (1, 1)])
+def test_qk_norm_full_width_matches_oracle(hip, oracle, prec, oprec):
+    # the decode shapes (dim 2048, 32 query heads over 8 kv heads, head_dim 64)
+    # with QK-norm: token path and tiles of 64 rows (the MFMA GEMM, a ragged
+    # last tile) against the oracle; the Q8_0 cache runs the matrix-core
+    # attention and, as above, is checked code by code and then from the
+    # device's own cache bytes
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=2048, hidden=8192, n_layers=2, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
+                       ctx_len=1024, seed=41, qk_norm=True)
+    prompt = np.random.default_rng(24).integers(0, 4096, 151)
+    n = len(prompt) - 1
+    o = oracle.Model(img, max_ctx=512, kv_precision=oprec)
+    for p, t in enumerate(prompt[:-1]):
+        o.forward_step(int(t), p, False)
+    tok = int(prompt[-1])
+    ko, vo = o.kv_views()
+    ko, vo = ko.copy(), vo.copy()
+    lo_own = o.forward(tok, n)
+    for tile in (0, 64):
+        m = hip.Model(img, max_ctx=512, kv_precision=prec)
+        m.set_prefill_strategy(tile)
+        m.prefill(prompt[:-1])
+        if prec == 1:
+            row = m.kv_row_bytes()
+            k, v, _ = m.export_state(n)
+            assert q8_rows_close(k, ko[:n * row], n, 1, row) and q8_rows_close(v, vo[:n * row], n, 1, row), tile
+            lo = oracle_from_device(oracle, img, m, n, oprec, 512).forward(tok, n)
+        else:
+            lo = lo_own
+        assert rel_err(m.forward(tok, n), lo) <= 1e-3, tile

@@ -151,3 +151,112 @@ def test_branches_share_root_under_byte_budget(hip, img):
     assert np.array_equal(m2.forward(int(prompt[-1]), 2 * CS), want)
     pc.clear()
     assert len(pc) == 0 and pc.memory_usage_bytes() == 0
+
+
+@pytest.mark.parametrize("kv", ["F32", "F16", "Q8_0"])
+def test_state_interval_export_import(hip, img, kv):
+    """export_state_range / import_state_at (cache.rs:688-746, :827-914):
+    an interval export equals the same rows of a whole export; a prompt
+    rebuilt from three interval imports at unaligned offsets (partial 16-token
+    groups in the Q8_0 layout) continues bit for bit like the original; an
+    interval import leaves the other positions as they were."""
+    kvp = getattr(hip.KvPrecision, kv)
+    rng = np.random.default_rng(31)
+    prompt = rng.integers(0, SMALL["vocab"], 151).astype(np.uint32)
+    n = len(prompt) - 1
+    m = model(hip, img, kvp)
+    m.prefill(prompt[:-1], 0)
+    k, v, conv = m.export_state(n)
+    row, L = m.kv_row_bytes(), m.info.n_attn_layers
+
+    def rows(a, s0, t):  # rows [s0, s0 + t) of every layer of a whole export of n tokens
+        return np.concatenate([a[(l * n + s0) * row:(l * n + s0 + t) * row] for l in range(L)])
+
+    for s0, t in ((0, 37), (37, 50), (87, 63), (5, 3), (16, 32)):
+        ki, vi = m.export_state_range(s0, t)
+        assert np.array_equal(ki, rows(k, s0, t)) and np.array_equal(vi, rows(v, s0, t)), (s0, t)
+    want = m.forward(int(prompt[-1]), n)
+    m2 = model(hip, img, kvp)
+    for s0, t in ((87, 63), (0, 37), (37, 50)):
+        m2.import_state_at(s0, t, rows(k, s0, t), rows(v, s0, t), conv if s0 == 0 else None)
+    assert np.array_equal(m2.forward(int(prompt[-1]), n), want)
+    # an interval import touches nothing outside it
+    m3 = model(hip, img, kvp)
+    other = rng.integers(0, SMALL["vocab"], 150).astype(np.uint32)
+    m3.prefill(other, 0)
+    k3, v3, c3 = m3.export_state(n)
+    m3.import_state_at(37, 50, rows(k, 37, 50), rows(v, 37, 50))
+    k4, v4, c4 = m3.export_state(n)
+    for a, b, src in ((k3, k4, k), (v3, v4, v)):
+        assert np.array_equal(rows(b, 0, 37), rows(a, 0, 37)) and np.array_equal(rows(b, 87, 63), rows(a, 87, 63))
+        assert np.array_equal(rows(b, 37, 50), rows(src, 37, 50))
+    assert np.array_equal(c3, c4)
+
+
+def test_state_interval_errors(hip, img):
+    m = hip.Model(img, max_ctx=256, kv_precision=hip.KvPrecision.Q8_0)
+    row, L = m.kv_row_bytes(), m.info.n_attn_layers
+    with pytest.raises(hip.ModelError) as e:  # KvError::ContextOverflow (cache.rs:692-697)
+        m.export_state_range(200, 57)
+    assert e.value.code == 115
+    with pytest.raises(hip.ModelError) as e:  # KvError::DimMismatch (cache.rs:851-856)
+        m.import_state_at(0, 10, np.zeros(L * 10 * row - 1, np.uint8), np.zeros(L * 10 * row - 1, np.uint8))
+    assert e.value.code == 115
+    with pytest.raises(hip.ModelError) as e:
+        m.import_state_at(250, 10, np.zeros(L * 10 * row, np.uint8), np.zeros(L * 10 * row, np.uint8))
+    assert e.value.code == 115
+
+
+@pytest.mark.parametrize("kv", ["F16", "Q8_0"])
+def test_full_snapshots_restore_bit_exact(hip, img, kv):
+    """insert_chunk (prefix.rs:239-249): chained full snapshots (each holds
+    the whole prefix, no parent link); the lookup of prefix.rs:672-722
+    (two chunks plus extra tokens match 128, a different second chunk 64),
+    and restoring the deeper one into a fresh model continues bit for bit."""
+    kvp = getattr(hip.KvPrecision, kv)
+    rng = np.random.default_rng(41)
+    prompt = rng.integers(0, SMALL["vocab"], 2 * CS + 3).astype(np.uint32)
+    ref = model(hip, img, kvp)
+    ref.prefill(prompt[:-1], 0)
+    want = ref.forward(int(prompt[-1]), len(prompt) - 1)
+    pc = hip.PrefixCache()
+    m = model(hip, img, kvp)
+    m.prefill(prompt[:CS], 0)
+    h0 = pc.insert_chunk(m, 0, prompt[:CS], 0, CS)
+    m.prefill(prompt[CS:2 * CS], CS)
+    h1 = pc.insert_chunk(m, h0, prompt[CS:2 * CS], 1, 2 * CS)
+    assert len(pc) == 2 and h1 == hip.chunk_hash(h0, prompt[CS:2 * CS])
+    assert pc.find_longest_prefix(prompt) == (2 * CS, h1)
+    assert pc.find_longest_prefix(np.concatenate([prompt[:CS], np.full(CS, 500, np.uint32)])) == (CS, h0)
+    # restoring copies the deepest node alone: it holds the whole prefix
+    fresh = model(hip, img, kvp)
+    matched, h = pc.restore_longest_prefix(fresh, prompt)
+    assert (matched, h) == (2 * CS, h1)
+    fresh.prefill(prompt[2 * CS:-1], 2 * CS)
+    assert np.array_equal(fresh.forward(int(prompt[-1]), len(prompt) - 1), want)
+
+
+def test_suffix_match(hip, img):
+    """find_longest_suffix_match, the reference's tests prefix.rs:771-862 on
+    device snapshots: a cached chunk found as the suffix of a later prompt
+    (skip 64, its position), no match on different content, the right one of
+    two chunks, and a chunk cached under a chained hash found by its
+    standalone hash."""
+    m = model(hip, img, hip.KvPrecision.F16)
+    pc = hip.PrefixCache(max_chunks=5)
+    chunk = np.arange(64, dtype=np.uint32)
+    m.prefill(chunk, 0)
+    h = pc.insert_chunk(m, 0, chunk, 0, 64)
+    history = np.arange(100, 164, dtype=np.uint32)
+    assert pc.find_longest_suffix_match(64, np.concatenate([history, chunk])) == (64, 64, h)
+    assert pc.find_longest_suffix_match(64, np.concatenate([history, np.arange(200, 264, dtype=np.uint32)])) is None
+    assert pc.find_longest_suffix_match(64, chunk) is None  # nothing past start_pos
+    # chunk1 cached at position 128 under the chain (h, chunk1)
+    chunk1 = np.arange(900, 964, dtype=np.uint32)  # the small model has 1024 tokens
+    m.prefill(chunk1, 64)
+    h1 = pc.insert_chunk(m, h, chunk1, 1, 128)
+    assert h1 != hip.chunk_hash(0, chunk1)
+    got = pc.find_longest_suffix_match(64, np.concatenate([np.arange(500, 564, dtype=np.uint32), chunk1]))
+    assert got == (64, 128, h1)
+    # suffix positions must be chunk-aligned: a 64-token suffix at absolute 70 is skipped
+    assert pc.find_longest_suffix_match(6, np.concatenate([history, chunk1])) is None

@@ -52,9 +52,10 @@ def draw(state: int):
     return state, float(np.float32((r >> 8) / 16777216.0))
 
 
-def near_boundary(tok, probs, r, top_p):
-    """Whether token tok's cumulative interval lies within TOL of the draw, in
+def near_boundary(tok, probs, r, top_p, tol=TOL):
+    """Whether token tok's cumulative interval lies within tol of the draw, in
     the order the reference accumulates (index order; descending for top-p)."""
+    TOL = tol
     p = probs.astype(np.float64)
     if top_p < 1.0:
         n = p.size
@@ -109,6 +110,13 @@ def run_pair(hip, oracle, torch, logits, recent, cfgkw, seed, steps, api="row"):
             assert np.array_equal(got > 1e-30, nz)
             ratio = got[nz].astype(np.float64) / l_o[nz]
             assert abs(ratio.mean() - 1.0) < 1e-3 and np.ptp(ratio) < 2e-6 * max(1.0, ratio.mean())
+            # the device's own rule: exact fixed-point sums over the
+            # probabilities it returned, so without a nucleus (whose size is
+            # a knife edge where tied probabilities sum to top_p exactly) the
+            # draw lies in its token's interval of their float64 cumulative
+            # sum to within 1e-6
+            if top_p >= 1.0:
+                assert near_boundary(t_d, got, draw(state0)[1], top_p, tol=1e-6), (cfgkw, s, t_d)
             if t_d != t_o:
                 mismatches += 1
                 r = draw(state0)[1]
@@ -238,6 +246,8 @@ def test_rows_batch_independent(hip, oracle, torch_mod, name):
                 assert np.array_equal(got_l[b] > 1e-30, nz)
                 ratio = got_l[b][nz].astype(np.float64) / l_o[nz]
                 assert abs(ratio.mean() - 1.0) < 1e-3 and np.ptp(ratio) < 2e-6 * max(1.0, ratio.mean())
+                if top_p >= 1.0:
+                    assert near_boundary(int(got_t[b]), got_l[b], draw(state0)[1], top_p, tol=1e-6), (name, s, b)
                 if int(got_t[b]) != t_o:
                     mismatches += 1
                     r = draw(state0)[1]

@@ -84,6 +84,84 @@ def test_yarn_ramp_limits(oracle):
     assert np.allclose(invy[wl > 4096], inv0[wl > 4096] / scale, rtol=1e-5)
 
 
+def _yarn_ramp_violations(wl, ratio, scale, lo=4096 / 32, hi=4096 / 1):
+    """Properties the YaRN ramp of rope.rs:71-105 fixes, checked on the
+    per-frequency ratio r = inv_freq_yarn / inv_freq_base at wavelengths wl:
+    r = 1 below orig/beta_fast, r = 1/scale above orig/beta_slow, and in
+    between ramp = (1 - r) / (1 - 1/scale) is a straight line in the
+    wavelength that meets 0 at the lower and 1 at the upper end. Returns the
+    list of failed properties (empty when all hold)."""
+    bad = []
+    below, above = wl < lo, wl > hi
+    inner = ~below & ~above
+    if not np.allclose(ratio[below], 1.0, rtol=1e-6, atol=0):
+        bad.append("below")
+    if not np.allclose(ratio[above], 1.0 / scale, rtol=2e-5, atol=0):
+        bad.append("above")
+    ramp = (1.0 - ratio[inner]) / (1.0 - 1.0 / scale)
+    if inner.sum() < 8:
+        return bad + ["too few interior frequencies"]
+    if np.any(ramp < -1e-4) or np.any(ramp > 1 + 1e-4):
+        bad.append("ramp outside [0, 1]")
+    # least-squares line through the interior points, in float64
+    a, b = np.polyfit(wl[inner], ramp, 1)
+    if np.max(np.abs(a * wl[inner] + b - ramp)) > 5e-4:
+        bad.append("not linear in wavelength")
+    if abs(a * lo + b) > 2e-3 or abs(a * hi + b - 1.0) > 2e-3:
+        bad.append("does not meet the ends")
+    return bad
+
+
+@pytest.mark.parametrize("scale", [4352 / 4096, 32896 / 4096, 16.0])
+def test_yarn_ramp_interior_linear_in_wavelength(oracle, scale):
+    # rope.rs:71-105 with the model's parameters (model.rs:194-206: orig 4096,
+    # beta_fast 32, beta_slow 1; scale = working ctx / 4096, configs 4 and 5).
+    # head_dim 1024 gives 512 frequencies, about 130 of them inside the ramp
+    # (wavelengths 128..4096). inv_freq is recovered from the pos-1 angles of
+    # the table (angle = 1 * inv_freq, below pi).
+    hd, base = 1024, 1_000_000.0
+    c0, s0 = oracle.rope_table(hd, 2, base)
+    cy, sy = oracle.rope_table(hd, 2, base, scaling=2, scale=scale)
+    inv0 = np.arctan2(s0[1].astype(np.float64), c0[1].astype(np.float64))
+    invy = np.arctan2(sy[1].astype(np.float64), cy[1].astype(np.float64))
+    wl = 2 * math.pi / inv0
+    assert _yarn_ramp_violations(wl, invy / inv0, scale) == []
+    # the check tells plausible mistakes apart: a ramp in 1/wavelength (the
+    # frequency-space form), a reversed ramp, swapped betas (a step at 4096)
+    lo, hi = 128.0, 4096.0
+    good = np.clip((wl - lo) / (hi - lo), 0, 1)
+    mutants = {
+        "ramp in 1/wavelength": np.clip((1 / wl - 1 / lo) / (1 / hi - 1 / lo), 0, 1),
+        "reversed ramp": np.where((wl >= lo) & (wl <= hi), 1 - good, good),
+        "swapped betas": (wl >= hi).astype(np.float64),
+    }
+    for name, ramp in mutants.items():
+        ratio = (1 - ramp) + ramp / scale
+        assert _yarn_ramp_violations(wl, ratio, scale), name
+    # the model's head_dim (64): its 32 frequencies lie on the same curve
+    c0, s0 = oracle.rope_table(64, 2, base)
+    cy, sy = oracle.rope_table(64, 2, base, scaling=2, scale=scale)
+    inv0_64 = np.arctan2(s0[1].astype(np.float64), c0[1].astype(np.float64))
+    r64 = np.arctan2(sy[1].astype(np.float64), cy[1].astype(np.float64)) / inv0_64
+    wl64 = 2 * math.pi / inv0_64
+    curve = np.interp(wl64, wl, invy / inv0)
+    inside = (wl64 > lo) & (wl64 < hi)
+    assert inside.sum() == 9
+    assert np.allclose(r64, curve, rtol=2e-4)
+
+
+def test_model_yarn_decision(oracle):
+    # model.rs:194-206: YaRN when the working context exceeds 4096, with
+    # scale = working ctx / 4096 (configs 4 and 5 run it)
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=256, hidden=512, n_layers=2, attn_layers=(1,), n_heads=4, n_kv=2, vocab=256,
+                       ctx_len=65536, seed=3)
+    for ctx, yarn in ((4096, 0), (4352, 1), (32896, 1)):
+        m = oracle.Model(img, max_ctx=ctx)
+        assert m.info.yarn == yarn
+        assert m.info.yarn_scale == (np.float32(ctx) / np.float32(4096) if yarn else 1.0)
+
+
 def test_argmax_first_strict_max(oracle):
     # sampler.rs:305-316
     assert oracle.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
