@@ -281,6 +281,19 @@ int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* recent, size_t 
                         const mivi_sampler_config* cfg, uint64_t* rng_state, uint32_t* token,
                         void* stream);
 
+/* No counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). The same
+ * computation as mivi_hip_sample, bit for bit, with the workspace in a
+ * fixed-size device array of the library (513 KB per GPU, held until the
+ * process ends) instead of a buffer allocated on the first call: it calls no
+ * hipMalloc or hipFree. n at most 262144 logits (larger n returns
+ * MIVI_ERR_INVALID_ARGUMENT before anything runs). Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (other streams
+ * or threads) race; order them. Asynchronous on the stream. */
+int32_t mivi_hip_sample_noalloc(float* logits, size_t n, const uint32_t* recent, size_t n_recent,
+                                const mivi_sampler_config* cfg, uint64_t* rng_state, uint32_t* token,
+                                void* stream);
+
 /* Sampler::sample (sampler.rs:91-135) on `rows` rows at once, one sampler
  * per row (the per-sequence samplers of a batch): row b's logits at
  * logits + b * row_stride, its penalty window at recent + b * recent_stride

@@ -1148,6 +1148,62 @@ extern "C" int32_t mivi_hip_sample(float* logits, size_t n, const uint32_t* rece
     return rc;
 }
 
+// mivi_hip_sample_noalloc: the split path's workspace for one row of at most
+// kNoAllocMaxN logits lives in this file-scope device array, one copy per
+// GPU, held until the process ends (513 KB). In host code `scratch` names a
+// host-side stand-in, not device memory: the device address of each GPU's
+// copy comes from hipGetSymbolAddress, resolved once per device (with that
+// device current) and kept in g_scratch_dev. Every call on a GPU shares its
+// copy, so calls that overlap on one GPU (different streams, threads) race.
+// The kernels write every workspace word they later read within one call,
+// so nothing needs clearing between calls.
+constexpr size_t kNoAllocMaxN = 262144;
+constexpr size_t kNoAllocScratchBytes =
+    ((kNoAllocMaxN + kCC - 1) / kCC * kCapC * 8 + (kNoAllocMaxN + kCC - 1) / kCC * 4 + 255) & ~(size_t)255;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kNoAllocMaxDevices];  // device address of `scratch` per GPU, null until resolved
+
+static int32_t noalloc_scratch(int dev, void** out) {
+    if (dev < 0 || dev >= kNoAllocMaxDevices)
+        return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "device %d beyond the %d the scratch table holds", dev,
+                               kNoAllocMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        MIVI_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return mivi::set_error(MIVI_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch");
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return MIVI_OK;
+}
+
+extern "C" int32_t mivi_hip_sample_noalloc(float* logits, size_t n, const uint32_t* recent, size_t n_recent,
+                                           const mivi_sampler_config* cfg, uint64_t* rng_state, uint32_t* token,
+                                           void* stream) {
+    if (!cfg || !rng_state || !token || (n && !logits) || (n_recent && !recent))
+        return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "null argument");
+    if (n > kNoAllocMaxN)
+        return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT,
+                               "%zu logits: mivi_hip_sample_noalloc takes at most %zu (its scratch is fixed)", n,
+                               kNoAllocMaxN);
+    if (n_recent > (size_t)INT32_MAX) return mivi::err_overflow();
+    if (split_workspace(n, 1) > kNoAllocScratchBytes)
+        return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "scratch too small for %zu logits", n);
+    mivi::clear_error();
+    int dev = 0;
+    MIVI_HIP_CHECK(hipGetDevice(&dev));
+    void* ws = nullptr;
+    int32_t rc = noalloc_scratch(dev, &ws);
+    if (rc) return rc;
+    return launch_split(logits, (int64_t)n, (int)n, 1, FlatSrc{n_recent ? recent : nullptr, (int)n_recent, 0},
+                        mivi::SampleEos{}, nullptr, *cfg, rng_state,
+                        TokOut{token, nullptr, 0, 0, nullptr, mivi::EmbedNext{}}, ws, true, (hipStream_t)stream);
+}
+
 extern "C" size_t mivi_hip_sample_rows_workspace(size_t n, size_t rows) { return split_workspace(n, rows); }
 
 extern "C" int32_t mivi_hip_sample_rows(float* logits, size_t n, size_t rows, size_t row_stride,

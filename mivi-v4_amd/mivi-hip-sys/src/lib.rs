@@ -166,6 +166,11 @@ pub mod ffi {
         // sampler.rs:91-135 Sampler::sample on the device
         pub fn mivi_hip_sample(logits: *mut f32, n: usize, recent: *const u32, n_recent: usize,
             cfg: *const MiviSamplerConfig, rng_state: *mut u64, token: *mut u32, stream: *mut c_void) -> i32;
+        // no counterpart in the reference: mivi_hip_sample with the library's
+        // fixed device scratch (n <= 262144), for callers that cannot
+        // allocate (graph capture); calls overlapping on one GPU race
+        pub fn mivi_hip_sample_noalloc(logits: *mut f32, n: usize, recent: *const u32, n_recent: usize,
+            cfg: *const MiviSamplerConfig, rng_state: *mut u64, token: *mut u32, stream: *mut c_void) -> i32;
         pub fn mivi_hip_sample_rows_workspace(n: usize, rows: usize) -> usize;
         pub fn mivi_hip_sample_rows(logits: *mut f32, n: usize, rows: usize, row_stride: usize,
             recent: *const u32, n_recent: usize, recent_stride: usize, cfg: *const MiviSamplerConfig,

@@ -148,6 +148,7 @@ _sig = {
     "mivi_hip_prefix_cache_clear": ([_P], None),
     "mivi_hip_prefix_cache_contains": ([_P, C.c_uint64], _I),
     "mivi_hip_sample": ([_P, _S, _P, _S, C.POINTER(SamplerConfig), _P, _P, _P], _I),
+    "mivi_hip_sample_noalloc": ([_P, _S, _P, _S, C.POINTER(SamplerConfig), _P, _P, _P], _I),
     "mivi_hip_sample_rows_workspace": ([_S, _S], _S),
     "mivi_hip_sample_rows": ([_P, _S, _S, _S, _P, _S, _S, C.POINTER(SamplerConfig), _P, _P, _P, _S, _P], _I),
     "mivi_hip_model_generate": ([_P, _S, _P, _P, _S, C.POINTER(SamplerConfig), _P, _P, _S, _P], _I),
@@ -284,6 +285,17 @@ def sample(logits, recent, cfg: SamplerConfig, rng_state, token, stream=None):
                                 C.c_void_p(recent.data_ptr()) if recent is not None and recent.numel() else None,
                                 recent.numel() if recent is not None else 0, C.byref(cfg),
                                 C.c_void_p(rng_state.data_ptr()), C.c_void_p(token.data_ptr()), _stream(stream)))
+
+
+def sample_noalloc(logits, recent, cfg: SamplerConfig, rng_state, token, stream=None):
+    """sample() with the library's fixed device scratch in place of an
+    allocated workspace (at most 262144 logits; calls overlapping on one GPU
+    race): it allocates nothing, for callers that cannot."""
+    _check(_lib.mivi_hip_sample_noalloc(C.c_void_p(logits.data_ptr()), logits.numel(),
+                                        C.c_void_p(recent.data_ptr()) if recent is not None and recent.numel() else None,
+                                        recent.numel() if recent is not None else 0, C.byref(cfg),
+                                        C.c_void_p(rng_state.data_ptr()), C.c_void_p(token.data_ptr()),
+                                        _stream(stream)))
 
 
 def sample_rows(logits, recent, cfg: SamplerConfig, rng_states, tokens, stream=None):
