@@ -63,6 +63,9 @@ enum GemvEpilogue : int {
     EPI_STORE = 0,    // y (=|+=) result
     EPI_SWIGLU = 1,   // two segments gate|up of n rows each: y_gate[i] = silu(gate_i) * up_i (ffn.rs:84-95)
     EPI_ARGMAX = 2,   // store, and each wave's (max, first row) into part_val/part_idx
+    EPI_CONV = 3,     // one segment [B|C|X] of 3D rows (the ShortConv in_proj): the gated conv of
+                      // ssm.rs:80-140 per channel into y[0..D) (C * conv(window, B * X)), the next
+                      // window into st_out (conv fields and ncol strides as for PRO_CONV)
 };
 
 // Number of per-wave argmax partials an EPI_ARGMAX launch of this shape

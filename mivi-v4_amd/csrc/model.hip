@@ -1223,25 +1223,40 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
         GemvArgs g = {};
         if (!L.attn) {
             if (c.ssm_conv_kernel == 0) continue;  // ssm.rs:60-62
-            // in_proj on rms_norm(x, ssm_norm)
+            // in_proj on rms_norm(x, ssm_norm) with the gated conv (ssm.rs:80-140)
+            // in its epilogue, which writes C * conv to sc_in[0, D) and the next
+            // window; shapes the epilogue does not take store [B|C|X] and run
+            // the conv as out_proj's prologue instead
+            const size_t ks = c.ssm_conv_kernel;
             g.seg[0] = {L.in_proj.w, s0.sc_in, 3 * D};
             g.nseg = 1; g.K = D; g.x = s0.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = ncol; g.xs = z.x; g.ys = z.sc_in;
-            if ((rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
-            // out_proj on the gated conv, residual add into x
-            const size_t ks = c.ssm_conv_kernel;
-            g = {};
-            g.seg[0] = {L.out_proj.w, s0.x, D};
-            g.nseg = 1; g.K = D; g.x = s0.sc_in;
             g.conv_w = L.conv;
             g.conv_mode = (L.conv && L.conv_len >= (size_t)D * ks) ? 0 : (L.conv && L.conv_len >= ks) ? 1 : 2;
             g.ksize = (int)ks;
             g.st_in = s0.conv_a + l * (size_t)D * ks;
             g.st_out = s0.conv_b + l * (size_t)D * ks;
             g.phase = &m->ctrl->phase[b0];
-            g.accumulate = 1;
-            g.ncol = ncol; g.xs = z.sc_in; g.sts = z.conv; g.ys = z.x;
-            if ((rc = launch_gemv_ex(L.out_proj.type, PRO_CONV, g, s))) return rc;
+            g.sts = z.conv;
+            g.epilogue = EPI_CONV;
+            rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s);
+            const bool conv_fused = rc == MIVI_OK;
+            if (rc && rc != MIVI_ERR_UNSUPPORTED) return rc;
+            if (!conv_fused) {
+                g.epilogue = EPI_STORE;
+                if ((rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
+            }
+            // out_proj on the gated conv, residual add into x
+            GemvArgs go = {};
+            go.seg[0] = {L.out_proj.w, s0.x, D};
+            go.nseg = 1; go.K = D; go.x = s0.sc_in;
+            go.accumulate = 1;
+            go.ncol = ncol; go.xs = z.sc_in; go.ys = z.x;
+            if (!conv_fused) {
+                go.conv_w = g.conv_w; go.conv_mode = g.conv_mode; go.ksize = g.ksize;
+                go.st_in = g.st_in; go.st_out = g.st_out; go.phase = g.phase; go.sts = g.sts;
+            }
+            if ((rc = launch_gemv_ex(L.out_proj.type, conv_fused ? PRO_NONE : PRO_CONV, go, s))) return rc;
         } else {
             g.seg[0] = {L.wq.w, s0.q, D};
             g.seg[1] = {L.wk.w, s0.k, KV};

@@ -915,6 +915,30 @@ __device__ __forceinline__ mivi::GemvArgs gemv_column(const mivi::GemvArgs& a, i
     return v;
 }
 
+// EPI_CONV: the ShortConv step of channel c of column col from its in_proj
+// rows B, C, X (ssm.rs:80-140), in the operation order of the PRO_CONV
+// prologue (StageIn::finish), so out_proj's input is the same bit for bit:
+// bx = B * X, the window shifts in bx, conv = sum_k w_k * window_k from
+// zero, y = C * conv; the window goes to the column's other ping-pong buffer.
+__device__ __forceinline__ void conv_epilogue(const mivi::GemvArgs& a, int col, int c, float B, float C, float X) {
+    const bool swap = a.phase && (a.phase[col] & 1);
+    const float* st_in = (swap ? a.st_out : a.st_in) + col * a.sts + (size_t)c * kConvKs;
+    float* st_out = (swap ? (float*)a.st_in : a.st_out) + col * a.sts + (size_t)c * kConvKs;
+    const float bx = B * X;
+    float conv = 0.0f;
+    float sv[kConvKs];
+#pragma unroll
+    for (int k = 0; k < kConvKs; k++) {
+        sv[k] = k + 1 < kConvKs ? st_in[k + 1] : bx;
+        const float w = a.conv_mode == 0 ? a.conv_w[(size_t)c * kConvKs + k]
+                      : a.conv_mode == 1 ? a.conv_w[k] : 1.0f / (float)kConvKs;
+        conv += w * sv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < kConvKs; k++) st_out[k] = sv[k];
+    a.seg[0].y[col * a.ys + c] = C * conv;
+}
+
 // K-quant GEMV for the decode shapes (K = 2048/4096/8192). A persistent grid
 // of waves walks groups of RPW = 64/LPR rows; in each group a row is covered
 // by LPR lanes, each owning NU fixed 64-value units, so a lane's activation
@@ -934,6 +958,7 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     static_assert(!PACK || FMT == FMT_Q6K, "only Q6_K has a packed layout");
     constexpr int RPW = 64 / LPR;
     static_assert(EPI != mivi::EPI_SWIGLU || LPR == 32, "the pair epilogue takes two rows per wave");
+    static_assert(EPI != mivi::EPI_CONV || (FMT == FMT_Q4K && KT == 2048), "the conv epilogue is the Q4_K in_proj");
     constexpr int K = KT, nb = K / 256, units = nb * 4;
     constexpr int row_bytes = nb * KQ<FMT>::bytes;
     __shared__ __attribute__((aligned(16))) uint32_t dig[NC][3 * K / 4];
@@ -942,11 +967,15 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     const int n = sg.n;
     const int ncol = NC == 1 ? 1 : a.ncol;  // workgroup-uniform, <= NC
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane % LPR, sub = lane / LPR;
-    // EPI_SWIGLU: group c is the row pair (gate c, up c) = rows c and n0 + c
+    // EPI_SWIGLU: group c is the row pair (gate c, up c) = rows c and n0 + c.
+    // EPI_CONV: group g is channels RPW g .. RPW g + RPW - 1, taken in three
+    // steps, their B rows, C rows, X rows (rows c, D + c, 2D + c); the conv
+    // runs after the X step from the B and C sums kept in registers
     const int n0 = a.seg[0].n;
-    const int ngroups = EPI == mivi::EPI_SWIGLU ? n0 : (n + RPW - 1) / RPW;
+    const int D3 = n0 / 3;
+    const int ngroups = EPI == mivi::EPI_SWIGLU ? n0 : EPI == mivi::EPI_CONV ? (D3 + RPW - 1) / RPW : (n + RPW - 1) / RPW;
     const int nw = gridDim.x * (kWG / 64), wid = blockIdx.x * (kWG / 64) + wave;
-    const int cnt = wid < ngroups ? (ngroups - wid + nw - 1) / nw : 0;  // wave-uniform
+    const int cnt = (wid < ngroups ? (ngroups - wid + nw - 1) / nw : 0) * (EPI == mivi::EPI_CONV ? 3 : 1);  // wave-uniform
 
     // row of this lane in step s of this wave (steps past the end re-read
     // the wave's last row, and waves without rows read row 0; such rows are
@@ -959,6 +988,10 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
             int c = wid + st * nw;
             c = c < 0 ? 0 : c < n0 ? c : n0 - 1;
             return c + sub * n0;
+        } else if constexpr (EPI == mivi::EPI_CONV) {
+            int c = (wid + (st / 3) * nw) * RPW + sub;
+            c = c < 0 ? 0 : c < D3 ? c : D3 - 1;
+            return c + (st % 3) * D3;
         } else {
             const int r = (wid + st * nw) * RPW + sub;
             return r < 0 ? 0 : r < n ? r : n - 1;
@@ -1074,6 +1107,10 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
                 }
         }
     }
+    // EPI_CONV: the channels' B and C sums between their steps
+    float keepB[NC], keepC[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) keepB[c] = keepC[c] = 0.f;
     // EPI_ARGMAX: per column, this lane's maximum and its first row
     float best[NC];
     int bidx[NC];
@@ -1128,6 +1165,16 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
                 const float up = __shfl(sum, 32, 64);
                 const int c = wid + st * nw;
                 if (lane == 0 && c < n0) *(gfloat*)(sg.out(c) + cc * a.ys) = silu_f(sum) * up;
+            } else if constexpr (EPI == mivi::EPI_CONV) {
+                // every lane of a row holds its sum: B and C wait in
+                // registers for the X step of the same channels
+                const int kind = st % 3;
+                if (kind == 0) keepB[cc] = sum;
+                else if (kind == 1) keepC[cc] = sum;
+                else {
+                    const int c = (wid + (st / 3) * nw) * RPW + sub;
+                    if (lr == 0 && c < D3) conv_epilogue(a, cc, c, keepB[cc], keepC[cc], sum);
+                }
             } else {
                 const int r = (wid + st * nw) * RPW + sub;
                 if (lr == 0 && r < n) {
@@ -1354,7 +1401,11 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
     const int ncol = a.ncol;  // 2..NCM, workgroup-uniform
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kg = lane >> 4;
-    const int ngroups = EPI == mivi::EPI_SWIGLU ? (n0 + 7) / 8 : (n + 15) / 16;
+    // EPI_CONV: a group holds channels 5g .. 5g+4, lane row j = 3i + k their
+    // B, C, X rows (k = 0, 1, 2); lane row 15 repeats row 14 and is not stored
+    static_assert(EPI != mivi::EPI_CONV || KT == 2048, "the conv epilogue is the K = 2048 in_proj");
+    const int D3 = n0 / 3;
+    const int ngroups = EPI == mivi::EPI_SWIGLU ? (n0 + 7) / 8 : EPI == mivi::EPI_CONV ? (D3 + 4) / 5 : (n + 15) / 16;
     const int cnt = (int)blockIdx.x < ngroups ? (ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
 
     // row of lane row j in group step st (-1: none; loads then use row 0)
@@ -1363,6 +1414,10 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
         if constexpr (EPI == mivi::EPI_SWIGLU) {
             const int c = 8 * grp + (j & 7);
             return c < n0 ? c + (j >> 3) * n0 : -1;
+        } else if constexpr (EPI == mivi::EPI_CONV) {
+            const int jj = j < 15 ? j : 14;
+            const int c = 5 * grp + jj / 3;
+            return c < D3 ? c + (jj % 3) * D3 : -1;
         } else {
             const int r = 16 * grp + j;
             return r < n ? r : -1;
@@ -1482,6 +1537,10 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
                     // lanes j < 8: gate c; lanes j + 8: up c (math.rs:87-95)
                     const float up = __shfl(v, lane + 8, 64);
                     if (j < 8 && r >= 0 && col < ncol) *(gfloat*)(sg.out(r) + col * a.ys) = silu_f(v) * up;
+                } else if constexpr (EPI == mivi::EPI_CONV) {
+                    // lanes j = 3i hold B of channel 5g + i, j + 1 its C, j + 2 its X
+                    const float cv = __shfl(v, lane + 1, 64), xv = __shfl(v, lane + 2, 64);
+                    if (j < 15 && j % 3 == 0 && r >= 0 && col < ncol) conv_epilogue(a, col, r, v, cv, xv);
                 } else {
                     if (r >= 0 && col < ncol) {
                         gfloat* y = (gfloat*)(sg.out(r) + col * a.ys);
@@ -1866,6 +1925,40 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
         // 2 workgroups per CU measured best for the head GEMV (24.7 us vs 26.2 at 3)
         const int per_cu = mivi::stream_wg_per_cu(n);
         const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
+        if (a.epilogue == mivi::EPI_CONV) {
+            // the ShortConv in_proj with the gated conv in its epilogue: Q4_K
+            // rows at K = 2048, one segment of 3D rows [B|C|X]
+            if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
+                if (t != MIVI_GGML_Q4_K || K != 2048 || a.packed || a.nseg != 1 || a.seg[0].n % 3 != 0 ||
+                    a.ksize != kConvKs || !a.st_in || !a.st_out || (a.conv_mode != 2 && !a.conv_w) ||
+                    a.ncol > mivi::kMaxGemvCols)
+                    return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no conv epilogue for this shape");
+                const int D3 = a.seg[0].n / 3;
+                if (a.ncol > 2) {
+                    const int gc = std::max(1, std::min((D3 + 4) / 5, mivi::num_cus() * 2));
+                    if (a.ncol > 4)
+                        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, mivi::EPI_CONV, 2048, 2>), dim3(gc), dim3(kWG),
+                                           0, s, a);
+                    else
+                        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, mivi::EPI_CONV, 2048, 1>), dim3(gc), dim3(kWG),
+                                           0, s, a);
+                } else {
+                    // in_proj's own mapping (two rows per wave), the channels'
+                    // three row steps a ring round of three
+                    const int gcv = std::max(1, std::min(((D3 + 1) / 2 + 3) / 4, mivi::num_cus() * per_cu));
+                    if (a.ncol == 2)
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 2048, 32, 1, 3, PRO, mivi::EPI_CONV, false, 2>),
+                                           dim3(gcv), dim3(kWG), 0, s, a);
+                    else
+                        hipLaunchKernelGGL((gemv_kq_stream_kernel<FMT_Q4K, 2048, 32, 1, 3, PRO, mivi::EPI_CONV>),
+                                           dim3(gcv), dim3(kWG), 0, s, a);
+                }
+                MIVI_HIP_CHECK(hipGetLastError());
+                return MIVI_OK;
+            } else {
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "the conv epilogue takes no conv or SwiGLU prologue");
+            }
+        }
         if (a.packed && mivi::quad_layout(n, K)) {
             // packed Q6_K row quads on the matrix cores (one segment: the quads span the matrix)
             if (t != MIVI_GGML_Q6_K || a.nseg != 1 || a.epilogue == mivi::EPI_SWIGLU)
