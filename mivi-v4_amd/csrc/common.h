@@ -104,6 +104,43 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
+// Cross-lane moves without LDS: DPP within rows of 16 lanes and the gfx950
+// half/row swaps.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// (value of this lane, value of lane ^ 32) as (lower half's, upper half's)
+__device__ __forceinline__ void swap32(float v, float& lo, float& hi) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(p[0]);
+    hi = __uint_as_float(p[1]);
+}
+// (value of this lane, value of lane ^ 16) as (even row's, odd row's)
+__device__ __forceinline__ void swap16(float v, float& ev, float& od) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    ev = __uint_as_float(p[0]);
+    od = __uint_as_float(p[1]);
+}
+
+// The butterfly of group_sum<W> (v += value of lane ^ o for o = W/2 .. 1, in
+// that order) without LDS traffic. The xor-4 step reads lane (i + 4) mod 16,
+// so the result is group_sum<W>'s bit for bit in the lanes with bit 2 clear
+// (lanes 0-3, 8-11, ... of each group), the lanes that use it here; the
+// other steps pair exactly (IEEE addition is commutative).
+template <int W>
+__device__ __forceinline__ float xsum_desc(float v) {
+    static_assert(W >= 8 && W <= 64, "groups of 8 to 64 lanes");
+    float a, b;
+    if constexpr (W >= 64) { swap32(v, a, b); v = a + b; }
+    if constexpr (W >= 32) { swap16(v, a, b); v = a + b; }
+    if constexpr (W >= 16) v += dpp_mov<0x128>(v);  // row_ror:8   (lane ^ 8)
+    v += dpp_mov<0x12C>(v);                          // row_ror:12  (lane ^ 4 where bit 2 is clear)
+    v += dpp_mov<0x4E>(v);                           // quad_perm [2,3,0,1] (lane ^ 2)
+    v += dpp_mov<0xB1>(v);                           // quad_perm [1,0,3,2] (lane ^ 1)
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, 64));

@@ -97,6 +97,12 @@ int32_t launch_rows(int32_t ggml_type, int prologue, const GemvArgs& a, hipStrea
 // when quad_layout(rows, cols), unit planes otherwise
 int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
 
+// rows x cols Q4_K (cols 2048 or 8192, rows a multiple of 4) into row quads,
+// the layout of the matrix-core GEMV for one column (packed = 1): bit-identical
+// results to the streaming kernel on the GGUF rows
+inline bool q4k_quad_layout(size_t rows, size_t cols) { return (cols == 2048 || cols == 8192) && rows % 4 == 0; }
+int32_t launch_pack_q4k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
+
 // Row `id` of an embedding table (model.rs:358-375, the token's row
 // dequantized: Q6_K, Q4_K, Q8_0, F16, BF16 or F32) into x, by threads
 // t0, t0 + nt, ... of the caller.

@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <map>
 #include <string>
+#include <initializer_list>
 #include <vector>
 
 #include "common.h"
@@ -1048,6 +1049,7 @@ struct Mat {
     int32_t type = 0;
     const uint8_t* w = nullptr;  // device
     size_t rows = 0, cols = 0;
+    const uint8_t* quad = nullptr;  // Q4_K: the same rows packed as row quads (one-column GEMVs), else null
 };
 
 struct Layer {
@@ -1203,6 +1205,23 @@ EmbedNext embed_next_args(mivi_model* m, float* x, bool on) {
     return en;
 }
 
+// A decode projection over the matrices ms[0 .. g.nseg): with one column and
+// every matrix held as Q4_K row quads, the matrix-core GEMV on the quads
+// (the same results bit for bit); otherwise the GGUF rows.
+int32_t launch_proj(int32_t t, int pro, const GemvArgs& g, std::initializer_list<const Mat*> ms, hipStream_t s) {
+    bool quads = g.ncol <= 1 && (int)ms.size() == g.nseg;
+    for (const Mat* x : ms) quads = quads && x->quad;
+    if (quads) {
+        GemvArgs q = g;
+        int i = 0;
+        for (const Mat* x : ms) q.seg[i++].W = x->quad;
+        q.packed = 1;
+        const int32_t rc = launch_gemv_ex(t, pro, q, s);
+        if (rc != MIVI_ERR_UNSUPPORTED) return rc;
+    }
+    return launch_gemv_ex(t, pro, g, s);
+}
+
 int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argmax, hipStream_t s, bool do_embed,
                      size_t l0, size_t l1, bool do_head, bool embed_next) {
     const mivi_model_info& c = m->info;
@@ -1239,7 +1258,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.phase = &m->ctrl->phase[b0];
             g.sts = z.conv;
             g.epilogue = EPI_CONV;
-            rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s);
+            rc = launch_proj(L.in_proj.type, PRO_RMSNORM, g, {&L.in_proj}, s);
             const bool conv_fused = rc == MIVI_OK;
             if (rc && rc != MIVI_ERR_UNSUPPORTED) return rc;
             if (!conv_fused) {
@@ -1256,7 +1275,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
                 go.conv_w = g.conv_w; go.conv_mode = g.conv_mode; go.ksize = g.ksize;
                 go.st_in = g.st_in; go.st_out = g.st_out; go.phase = g.phase; go.sts = g.sts;
             }
-            if ((rc = launch_gemv_ex(L.out_proj.type, conv_fused ? PRO_NONE : PRO_CONV, go, s))) return rc;
+            if ((rc = launch_proj(L.out_proj.type, conv_fused ? PRO_NONE : PRO_CONV, go, {&L.out_proj}, s))) return rc;
         } else {
             g.seg[0] = {L.wq.w, s0.q, D};
             g.seg[1] = {L.wk.w, s0.k, KV};
@@ -1264,14 +1283,14 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.nseg = 3; g.K = D; g.x = s0.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = ncol; g.xs = z.x; g.ys = z.qkv;
             if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
-                if ((rc = launch_gemv_ex(L.wq.type, PRO_RMSNORM, g, s))) return rc;
+                if ((rc = launch_proj(L.wq.type, PRO_RMSNORM, g, {&L.wq, &L.wk, &L.wv}, s))) return rc;
             } else {
                 const Mat* ms[3] = {&L.wq, &L.wk, &L.wv};
                 for (int i = 0; i < 3; i++) {
                     GemvArgs g1 = g;
                     g1.seg[0] = g.seg[i];
                     g1.nseg = 1;
-                    if ((rc = launch_gemv_ex(ms[i]->type, PRO_RMSNORM, g1, s))) return rc;
+                    if ((rc = launch_proj(ms[i]->type, PRO_RMSNORM, g1, {ms[i]}, s))) return rc;
                 }
             }
             {
@@ -1299,7 +1318,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.seg[0] = {L.wo.w, s0.x, D};
             g.nseg = 1; g.K = D; g.x = s0.attn_out; g.accumulate = 1;
             g.ncol = ncol; g.xs = z.x; g.ys = z.x;
-            if ((rc = launch_gemv_ex(L.wo.type, PRO_NONE, g, s))) return rc;
+            if ((rc = launch_proj(L.wo.type, PRO_NONE, g, {&L.wo}, s))) return rc;
         }
         // ffn.rs:56-108
         g = {};
@@ -1312,26 +1331,26 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             // gate|up with the SwiGLU epilogue writes silu(gate) * up into hb
             // directly where the streaming kernel takes the shape
             g.epilogue = EPI_SWIGLU;
-            rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g, s);
+            rc = launch_proj(L.gate.type, PRO_RMSNORM, g, {&L.gate, &L.up}, s);
             fused = rc == MIVI_OK;
             if (rc && rc != MIVI_ERR_UNSUPPORTED) return rc;
             g.epilogue = EPI_STORE;
         }
         if (fused) {
         } else if (L.gate.type == L.up.type) {
-            if ((rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g, s))) return rc;
+            if ((rc = launch_proj(L.gate.type, PRO_RMSNORM, g, {&L.gate, &L.up}, s))) return rc;
         } else {
             GemvArgs g1 = g;
             g1.nseg = 1;
-            if ((rc = launch_gemv_ex(L.gate.type, PRO_RMSNORM, g1, s))) return rc;
+            if ((rc = launch_proj(L.gate.type, PRO_RMSNORM, g1, {&L.gate}, s))) return rc;
             g1.seg[0] = g.seg[1];
-            if ((rc = launch_gemv_ex(L.up.type, PRO_RMSNORM, g1, s))) return rc;
+            if ((rc = launch_proj(L.up.type, PRO_RMSNORM, g1, {&L.up}, s))) return rc;
         }
         g = {};
         g.seg[0] = {L.down.w, s0.x, D};
         g.nseg = 1; g.K = H; g.x = s0.hb; g.x2 = s0.hb2; g.accumulate = 1;
         g.ncol = ncol; g.xs = z.hb; g.ys = z.x;
-        if ((rc = launch_gemv_ex(L.down.type, fused ? PRO_NONE : PRO_SWIGLU, g, s))) return rc;
+        if ((rc = launch_proj(L.down.type, fused ? PRO_NONE : PRO_SWIGLU, g, {&L.down}, s))) return rc;
     }
     if (!do_head) {
         MIVI_HIP_CHECK(hipGetLastError());
@@ -1746,6 +1765,30 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         if ((rc = m->alloc(&m->head_packed, bytes))) return fail(rc);
         if ((rc = launch_pack_q6k(m->head.w, m->head_packed, c.vocab_size, c.dim, nullptr))) return fail(rc);
         if (hipDeviceSynchronize() != hipSuccess) return fail(set_error(MIVI_ERR_HIP, "packing the head failed"));
+    }
+    // one-column decode GEMVs stream Q4_K projections as row quads (matrix
+    // cores, bit-identical to the GGUF rows): a packed copy of each, the GGUF
+    // rows staying for the batched and prefill products
+    if (!getenv("MIVI_NO_PACK")) {
+        std::vector<Mat*> qm;
+        for (size_t i = 0; i < c.n_layers; i++) {
+            Layer& L = m->layers[i];
+            Mat* all[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.in_proj, &L.out_proj, &L.gate, &L.up, &L.down};
+            for (Mat* x : all)
+                if (x->w && x->type == MIVI_GGML_Q4_K && q4k_quad_layout(x->rows, x->cols) && (uintptr_t)x->w % 16 == 0)
+                    qm.push_back(x);
+        }
+        size_t total = 0;
+        for (Mat* x : qm) total += x->rows * (x->cols / 256) * 144;
+        uint8_t* q = nullptr;
+        if (total && (rc = m->alloc(&q, total))) return fail(rc);
+        for (Mat* x : qm) {
+            if ((rc = launch_pack_q4k(x->w, q, x->rows, x->cols, nullptr))) return fail(rc);
+            x->quad = q;
+            q += x->rows * (x->cols / 256) * 144;
+        }
+        if (total && hipDeviceSynchronize() != hipSuccess)
+            return fail(set_error(MIVI_ERR_HIP, "packing the Q4_K projections failed"));
     }
     {
         size_t bs, ts;

@@ -695,16 +695,25 @@ struct StageIn {
     f32x4 st[kConv ? E * kConvKs / 4 : 1];    // CONV: previous window of the E channels
     f32x4 cw[kConv ? E * kConvKs / 4 : 1];    // CONV: per-channel weights (mode 0)
 
+    // NONE / RMSNORM / SWIGLU: chunk i of this thread is the 16 bytes at
+    // 16 (threadIdx.x + kWG i), so each wave load reads 1 KB contiguous;
+    // finish() hands the values to their owners (E consecutive per thread)
+    // through LDS. CONV: the thread's own E values directly.
     __device__ __forceinline__ void load(const mivi::GemvArgs& a) {
         const int e0 = threadIdx.x * E;
+        if constexpr (!kConv) {
 #pragma unroll
-        for (int i = 0; i < E / 4; i++) x[i] = *(gf32x4*)(a.x + e0 + 4 * i);
+            for (int i = 0; i < E / 4; i++) x[i] = *(gf32x4*)(a.x + 4 * (threadIdx.x + kWG * i));
+        } else {
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) x[i] = *(gf32x4*)(a.x + e0 + 4 * i);
+        }
         if constexpr (PRO == mivi::PRO_RMSNORM) {
 #pragma unroll
-            for (int i = 0; i < E / 4; i++) y[i] = *(gf32x4*)(a.norm_w + e0 + 4 * i);
+            for (int i = 0; i < E / 4; i++) y[i] = *(gf32x4*)(a.norm_w + 4 * (threadIdx.x + kWG * i));
         } else if constexpr (PRO == mivi::PRO_SWIGLU) {
 #pragma unroll
-            for (int i = 0; i < E / 4; i++) y[i] = *(gf32x4*)(a.x2 + e0 + 4 * i);
+            for (int i = 0; i < E / 4; i++) y[i] = *(gf32x4*)(a.x2 + 4 * (threadIdx.x + kWG * i));
         } else if constexpr (kConv) {
             // a.x = [B | C | X], ssm.rs:80-140
 #pragma unroll
@@ -730,6 +739,22 @@ struct StageIn {
     __device__ __forceinline__ float finish(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
         __shared__ float red[2][kWG / 64];
         const int K = a.K, e0 = threadIdx.x * E;
+        if constexpr (!kConv) {
+            // the loaded chunks to their owners
+            constexpr bool two = PRO == mivi::PRO_RMSNORM || PRO == mivi::PRO_SWIGLU;
+            __shared__ __attribute__((aligned(16))) float tx[two ? 2 : 1][E * kWG];
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) {
+                *(f32x4*)&tx[0][4 * (threadIdx.x + kWG * i)] = x[i];
+                if constexpr (two) *(f32x4*)&tx[two ? 1 : 0][4 * (threadIdx.x + kWG * i)] = y[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < E / 4; i++) {
+                x[i] = *(const f32x4*)&tx[0][e0 + 4 * i];
+                if constexpr (two) y[i] = *(const f32x4*)&tx[two ? 1 : 0][e0 + 4 * i];
+            }
+        }
         float v[E];
 #pragma unroll
         for (int i = 0; i < E; i++) v[i] = x[i / 4][i % 4];
@@ -778,11 +803,19 @@ struct StageIn {
 #pragma unroll
             for (int i = 0; i < E; i++) m = nanmax(m, fabsf(v[i]));
         }
-        // one workgroup reduction of (ss, m)
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            if constexpr (PRO == mivi::PRO_RMSNORM) ss += __shfl_xor(ss, o, 64);
-            m = nanmax(m, __shfl_xor(m, o, 64));
+        // one workgroup reduction of (ss, m): the xor butterfly of the wave
+        // (lane 0's sums), then the waves in order
+        if constexpr (PRO == mivi::PRO_RMSNORM) ss = xsum_desc<64>(ss);
+        {
+            float lo, hi;
+            swap32(m, lo, hi);
+            m = nanmax(lo, hi);
+            swap16(m, lo, hi);
+            m = nanmax(lo, hi);
+            m = nanmax(m, dpp_mov<0x128>(m));
+            m = nanmax(m, dpp_mov<0x12C>(m));
+            m = nanmax(m, dpp_mov<0x4E>(m));
+            m = nanmax(m, dpp_mov<0xB1>(m));
         }
         if ((threadIdx.x & 63) == 0) {
             red[0][threadIdx.x >> 6] = ss;
@@ -836,10 +869,12 @@ struct StageIn {
                 float t = 0.f;
 #pragma unroll
                 for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[b * 32 + i];
-                if constexpr (E < 32) {
-#pragma unroll
-                    for (int o = 1; o < 32 / E; o <<= 1) t += __shfl_xor(t, o, 64);
-                }
+                // xor 1, 2, 4 in that order (the writers, lanes with bit 2 clear,
+                // see their exact partners; row_ror:12 reads lane (i + 4) mod 16)
+                if constexpr (E < 32) t += dpp_mov<0xB1>(t);
+                if constexpr (E < 16) t += dpp_mov<0x4E>(t);
+                if constexpr (E < 8) t += dpp_mov<0x12C>(t);
+                static_assert(E >= 4, "at least four activations per thread");
                 if (E >= 32 || (threadIdx.x % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t;
             }
         }
@@ -1158,7 +1193,7 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
                     acc += q6k_unit_i8(B[i].ql0, B[i].ql1, B[i].qh, PACK ? packed_q6k_scales(B[i].sc.x) : B[i].sc,
                                        B[i].d, xd[cr][i], off[cr][i]);
             }
-            float sum = group_sum<LPR>(acc);
+            float sum = xsum_desc<LPR>(acc);  // exact in the lr == 0 lanes that use it
             if (FMT == FMT_Q6K) sum *= s[cc];
             if constexpr (EPI == mivi::EPI_SWIGLU) {
                 // lane 0 holds gate c, lane 32 up c (math.rs:87-95)
@@ -1588,12 +1623,29 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
 
 constexpr int kQuadBytes = 6720;
 
+// v summed over b for lanes 4b + j: b xor 8, 4, 2, 1 in that order (lane xor
+// 32, 16, 8, 4), exact in lanes 0-3, which hold the four rows' sums
+__device__ __forceinline__ float quad_lane_sum(float v) {
+    float a, b;
+    swap32(v, a, b);
+    v = a + b;
+    swap16(v, a, b);
+    v = a + b;
+    v += dpp_mov<0x128>(v);  // row_ror:8   (lane ^ 8)
+    v += dpp_mov<0x12C>(v);  // row_ror:12  (lane ^ 4 for lanes 0-3)
+    return v;
+}
+
 
 __device__ __forceinline__ i32x4 mfma4x4(uint32_t a, uint32_t b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_4x4x4i8((int)a, (int)b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ u32x4 ldg16_nt(const uint8_t* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+// (through a global-address-space pointer: a flat load would also count
+// against the LDS counter, so every LDS wait would wait for it)
+__device__ __forceinline__ u32x4 ldg16_nt(const uint8_t* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)p);
+}
 
 // the 6-bit code of value 128h + 32q + l of the Q6_K superblock at blk (q6_k.rs:8-43, before the -32)
 __device__ __forceinline__ uint32_t q6_code(const uint8_t* blk, int h, int q, int l) {
@@ -1755,10 +1807,7 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs
                 v += half_bits_to_f32(i ? dw[p] >> 16 : dw[p]) * f;
             }
             // sum over the row's 16 lanes (b), in group_sum<16>'s order
-            v += __shfl_xor(v, 32, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 4, 64);
+            v = quad_lane_sum(v);
             v *= s[c];
             if (lane < 4) {
                 gfloat* y = (gfloat*)(a.seg[0].y + r + c * a.ys);
@@ -1794,6 +1843,330 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs
     for (int p = 0; p < PD; p++)
         if (st + p < cnt) compute(p, st + p);
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+}
+
+// ------------------------------------------ Q4_K row quads on the matrix cores
+//
+// Packed Q4_K matrices with K = 2048 S (S = 1 or 4) columns and a multiple of
+// 4 rows (mivi_hip_pack_weights) are stored as row quads: quad Q (rows 4Q ..
+// 4Q+3) is S sub-quads of 4608 contiguous bytes, sub-quad s holding values
+// [2048 s, 2048 s + 2048) of the four rows, laid out for the 64 lanes
+// l = 4b + j of one wave (j = row of the quad, b = 0..15). Lane (b, j) owns
+// units t = 32 s + b and t + 16 of row j, where unit t is sub-blocks 2g and
+// 2g + 1 of superblock t / 4 (g = t & 3, q4_k_m.rs:24-63): the units lanes
+// b and b + 16 (K = 2048), or b + 16 i (K = 8192), of the streaming kernel own.
+//   [0, 4096)     the units' 32 code bytes each, 16 B per lane at
+//                 1024 k + 16 l: k = 0, 1 unit t (its bytes 0-15, 16-31),
+//                 k = 2, 3 unit t + 16; byte e holds value 64 g + e (low
+//                 nibble) and 64 g + 32 + e (high nibble) of the unit
+//   [4096, 4480)  6 B per lane at 6 l: the 6-bit scales of sub-blocks
+//                 (2g, 2g + 1) of unit t, then of unit t + 16, in bits 0-23,
+//                 their 6-bit mins in bits 24-47
+//   [4480, 4608)  f16 d | f16 dmin of the superblocks of units t and t + 16
+//                 of row j, 8 B per (j, b / 4) at 4480 + 8 (4 j + b / 4)
+// A sub-quad is 36 lines of 128 B and every 1 KB wave load of codes is
+// contiguous; a packed matrix keeps the GGUF matrix's size.
+//
+// The products run on v_mfma_i32_4x4x4_16b_i8 as in the Q6_K quad kernel:
+// in block b, lane 4b + v supplies digit plane v of x (zeros for v = 3) at
+// four values and lane 4b + j four codes of row j at the same values, and
+// lane 4b + j receives the plane sums of its row. Eight instructions cover a
+// 32-value sub-block; the integer sums are the sdot4 kernel's, the per-unit
+// float steps are q4k_unit_i8's, and the unit values are summed in the
+// streaming kernel's butterfly order (units t, t + 16 first at K = 2048;
+// t + 64, then t + 32, then t + 16 at K = 8192; then the lanes), so every
+// row equals the streaming kernel's result on the GGUF rows bit for bit.
+
+constexpr int kQ4SubQuadBytes = 4608;
+
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+// One sub-quad's bytes as lane l loads them.
+struct Q4Item {
+    u32x4 c[4];          // code bytes of unit t (c[0], c[1]) and t + 16 (c[2], c[3])
+    uint32_t slo, shi;   // 8 B at (6 l) & ~3: the lane's six scale bytes at bit 16 (l & 1)
+    u32x2 dp;            // d | dmin << 16 of the superblocks of units t and t + 16
+};
+
+__device__ __forceinline__ void load_q4_item(Q4Item& it, const uint8_t* sub, int lane) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) it.c[k] = ldg16_nt(sub + 1024 * k + 16 * lane);
+    const u32x2_a4 sw = *(const __attribute__((address_space(1))) u32x2_a4*)(sub + 4096 + ((6 * lane) & ~3));
+    it.slo = sw.x;
+    it.shi = sw.y;
+    it.dp = *(const __attribute__((address_space(1))) u32x2*)(sub + 4480 + 8 * (4 * (lane & 3) + (lane >> 4)));
+}
+
+// The lane's two unit values of one sub-quad (q4k_unit_i8's steps), from its
+// digit operands A[i][h][m] (unit i, sub-block 2g + h, values 4m .. 4m + 3)
+// and fp32 sub-block sums X[i][h].
+__device__ __forceinline__ void q4_item_units(const Q4Item& it, const uint32_t (&A)[2][2][8], const float (&X)[2][2],
+                                              float s, int lane, float (&u)[2]) {
+    const uint32_t sh = 16u * (uint32_t)(lane & 1);
+    const uint32_t lo = __builtin_amdgcn_alignbit(it.shi, it.slo, sh), hi = it.shi >> sh;
+    const uint32_t scf[2][2] = {{lo & 63u, (lo >> 6) & 63u}, {(lo >> 12) & 63u, (lo >> 18) & 63u}};
+    const uint32_t mf[2][2] = {{(lo >> 24) & 63u, __builtin_amdgcn_alignbit(hi, lo, 30) & 63u},
+                               {(hi >> 4) & 63u, (hi >> 10) & 63u}};
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t w[8] = {it.c[2 * i].x, it.c[2 * i].y, it.c[2 * i].z, it.c[2 * i].w,
+                               it.c[2 * i + 1].x, it.c[2 * i + 1].y, it.c[2 * i + 1].z, it.c[2 * i + 1].w};
+        i32x4 Dl = {0, 0, 0, 0}, Dh = {0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            Dl = mfma4x4(A[i][0][m], w[m] & 0x0F0F0F0Fu, Dl);
+            Dh = mfma4x4(A[i][1][m], (w[m] >> 4) & 0x0F0F0F0Fu, Dh);
+        }
+        int Ae[3];
+#pragma unroll
+        for (int e = 0; e < 3; e++) Ae[e] = mul24(Dl[e], (int)scf[i][0]) + mul24(Dh[e], (int)scf[i][1]);
+        const float f = fmaf((float)Ae[2], kDig2, fmaf((float)Ae[1], kDig1, (float)Ae[0]));
+        const uint32_t dpv = i ? it.dp.y : it.dp.x;
+        const float d = half_bits_to_f32(dpv), dmin = half_bits_to_f32(dpv >> 16);
+        u[i] = (d * s) * f - dmin * fmaf((float)mf[i][0], X[i][0], (float)mf[i][1] * X[i][1]);
+    }
+}
+
+// One column; a step is one quad (store), the gate and up quads of the same
+// rows (EPI_SWIGLU: seg[0] gate, seg[1] up), or the B, C and X quads of four
+// channels (EPI_CONV: one segment [B | C | X]); PD steps in flight per wave.
+template <int PRO, int EPI, int S, int PD>
+__global__ void __launch_bounds__(kWG) gemv_q4k_quad_kernel(const mivi::GemvArgs a) {
+    constexpr int K = 2048 * S;
+    constexpr int G = EPI == mivi::EPI_SWIGLU ? 2 : EPI == mivi::EPI_CONV ? 3 : 1;
+    static_assert(EPI != mivi::EPI_ARGMAX, "the argmax epilogue is the Q6_K head's");
+    __shared__ __attribute__((aligned(16))) uint32_t dig[3 * K / 4];
+    __shared__ __attribute__((aligned(16))) float xsum[K / 32];
+    const Segs sg(a, (size_t)S * 1152);
+    const int n0 = a.seg[0].n, D3 = n0 / 3;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = lane >> 2, jv = lane & 3;
+    const int nw = gridDim.x * (kWG / 64), wid = blockIdx.x * (kWG / 64) + wave;
+    const int nsteps = EPI == mivi::EPI_SWIGLU ? n0 / 4 : EPI == mivi::EPI_CONV ? D3 / 4 : sg.n / 4;
+    const int cnt = wid < nsteps ? (nsteps - wid + nw - 1) / nw : 0;  // wave-uniform
+
+    // first row of quad g of step st (steps past the end re-read the wave's
+    // last step and waves without steps read step 0; nothing is stored for them)
+    auto quad_row = [&](int st, int g) {
+        st = st < cnt ? st : cnt - 1;
+        int q = wid + st * nw;
+        q = q < 0 ? 0 : q < nsteps ? q : nsteps - 1;
+        return 4 * q + g * (EPI == mivi::EPI_SWIGLU ? n0 : EPI == mivi::EPI_CONV ? D3 : 0);
+    };
+    Q4Item buf[PD][G][S];
+    auto load = [&](int p, int st) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint8_t* base = sg.row(quad_row(st, g));
+#pragma unroll
+            for (int q = 0; q < S; q++) load_q4_item(buf[p][g][q], base + q * kQ4SubQuadBytes, lane);
+        }
+    };
+    // activation loads, then the first PD steps, then the activation math
+    StageIn<PRO, K / kWG> in;
+    in.load(a);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PD; p++) load(p, p);
+    __builtin_amdgcn_sched_barrier(0);
+    const float s = in.template finish<true>(a, dig, xsum);
+
+    // digit operands and sub-block sums of sub-quad q for this lane
+    auto fetch = [&](int q, uint32_t (&Ao)[2][2][8], float (&Xo)[2][2]) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int t = 32 * q + b + 16 * i;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t* src = dig + (jv < 3 ? jv : 0) * (K / 4) + 16 * t + 8 * h;
+                u32x4 v0 = *(const u32x4*)src, v1 = *(const u32x4*)(src + 4);
+                if (jv == 3) v0 = v1 = u32x4{0, 0, 0, 0};
+                Ao[i][h][0] = v0.x; Ao[i][h][1] = v0.y; Ao[i][h][2] = v0.z; Ao[i][h][3] = v0.w;
+                Ao[i][h][4] = v1.x; Ao[i][h][5] = v1.y; Ao[i][h][6] = v1.z; Ao[i][h][7] = v1.w;
+            }
+            Xo[i][0] = xsum[2 * t];
+            Xo[i][1] = xsum[2 * t + 1];
+        }
+    };
+    uint32_t A1[2][2][8];
+    float X1[2][2];
+    if constexpr (S == 1) fetch(0, A1, X1);
+    if (cnt == 0) return;  // wave-uniform; no barrier follows
+
+    auto compute = [&](int p, int st) {
+        float rv[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float u[S][2];
+#pragma unroll
+            for (int q = 0; q < S; q++) {
+                if constexpr (S == 1) {
+                    q4_item_units(buf[p][g][q], A1, X1, s, lane, u[q]);
+                } else {
+                    uint32_t Ao[2][2][8];
+                    float Xo[2][2];
+                    fetch(q, Ao, Xo);
+                    q4_item_units(buf[p][g][q], Ao, Xo, s, lane, u[q]);
+                }
+            }
+            float v;
+            if constexpr (S == 1) {
+                v = (0.f + u[0][0]) + (0.f + u[0][1]);
+            } else {
+                const float a00 = (0.f + u[0][0]) + u[2][0], a01 = (0.f + u[0][1]) + u[2][1];
+                const float a10 = (0.f + u[1][0]) + u[3][0], a11 = (0.f + u[1][1]) + u[3][1];
+                v = (a00 + a10) + (a01 + a11);
+            }
+            // the remaining butterfly levels over b (lanes 4b + j)
+            rv[g] = quad_lane_sum(v);
+        }
+        const int r = 4 * (wid + st * nw) + jv;
+        if (lane < 4) {
+            if constexpr (EPI == mivi::EPI_SWIGLU) {
+                *(gfloat*)sg.out(r) = silu_f(rv[0]) * rv[1];  // math.rs:87-95
+            } else if constexpr (EPI == mivi::EPI_CONV) {
+                conv_epilogue(a, 0, r, rv[0], rv[1], rv[2]);
+            } else {
+                store_out(sg, a.accumulate, r, rv[0]);
+            }
+        }
+    };
+    // the ring as in the Q6_K quad kernel: the last full round refills only
+    // steps that exist (the code loads are non-temporal)
+    int st = 0;
+    for (; st + 2 * PD <= cnt; st += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, st + p);
+            load(p, st + p + PD);
+        }
+    }
+    if (st + PD <= cnt) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, st + p);
+            if (st + p + PD < cnt) load(p, st + p + PD);
+        }
+        st += PD;
+    }
+#pragma unroll
+    for (int p = 0; p < PD; p++)
+        if (st + p < cnt) compute(p, st + p);
+}
+
+// K = 8192 (S = 4): the workgroup's waves take the four sub-quads of the
+// same quads (wave w sub-quad w, its digit operands fixed for the launch)
+// and hand their unit values to wave 0 through LDS, which sums them in the
+// streaming kernel's order (t + 64, t + 32, t + 16, then the lanes).
+template <int PRO, int PD>
+__global__ void __launch_bounds__(kWG) gemv_q4k_quad8k_kernel(const mivi::GemvArgs a) {
+    constexpr int K = 8192;
+    __shared__ __attribute__((aligned(16))) uint32_t dig[3 * K / 4];
+    __shared__ __attribute__((aligned(16))) float xsum[K / 32];
+    __shared__ float xch[2][4][2][64];  // [step parity][sub-quad][unit][lane]
+    const Segs sg(a, (size_t)4 * 1152);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = lane >> 2, jv = lane & 3;
+    const int nsteps = sg.n / 4;
+    const int cnt = (int)blockIdx.x < nsteps ? (nsteps - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+    auto load = [&](Q4Item& it, int st) {
+        st = st < cnt ? st : cnt - 1;
+        int q = (int)blockIdx.x + st * (int)gridDim.x;
+        q = q < 0 ? 0 : q < nsteps ? q : nsteps - 1;
+        load_q4_item(it, sg.row(4 * q) + wave * kQ4SubQuadBytes, lane);
+    };
+    Q4Item buf[PD];
+    StageIn<PRO, K / kWG> in;
+    in.load(a);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PD; p++) load(buf[p], p);
+    __builtin_amdgcn_sched_barrier(0);
+    const float s = in.template finish<true>(a, dig, xsum);
+    uint32_t A[2][2][8];
+    float X[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = 32 * wave + b + 16 * i;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t* src = dig + (jv < 3 ? jv : 0) * (K / 4) + 16 * t + 8 * h;
+            u32x4 v0 = *(const u32x4*)src, v1 = *(const u32x4*)(src + 4);
+            if (jv == 3) v0 = v1 = u32x4{0, 0, 0, 0};
+            A[i][h][0] = v0.x; A[i][h][1] = v0.y; A[i][h][2] = v0.z; A[i][h][3] = v0.w;
+            A[i][h][4] = v1.x; A[i][h][5] = v1.y; A[i][h][6] = v1.z; A[i][h][7] = v1.w;
+        }
+        X[i][0] = xsum[2 * t];
+        X[i][1] = xsum[2 * t + 1];
+    }
+    if (cnt == 0) return;  // workgroup-uniform
+
+    auto compute = [&](const Q4Item& it, int st) {
+        float u[2];
+        q4_item_units(it, A, X, s, lane, u);
+        xch[st & 1][wave][0][lane] = u[0];
+        xch[st & 1][wave][1][lane] = u[1];
+        __syncthreads();
+        if (wave == 0) {
+            float w[4][2];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                w[q][0] = xch[st & 1][q][0][lane];
+                w[q][1] = xch[st & 1][q][1][lane];
+            }
+            const float a00 = (0.f + w[0][0]) + w[2][0], a01 = (0.f + w[0][1]) + w[2][1];
+            const float a10 = (0.f + w[1][0]) + w[3][0], a11 = (0.f + w[1][1]) + w[3][1];
+            const float v = quad_lane_sum((a00 + a10) + (a01 + a11));
+            if (lane < 4) store_out(sg, a.accumulate, 4 * ((int)blockIdx.x + st * (int)gridDim.x) + jv, v);
+        }
+    };
+    int st = 0;
+    for (; st + 2 * PD <= cnt; st += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(buf[p], st + p);
+            load(buf[p], st + p + PD);
+        }
+    }
+    if (st + PD <= cnt) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(buf[p], st + p);
+            if (st + p + PD < cnt) load(buf[p], st + p + PD);
+        }
+        st += PD;
+    }
+#pragma unroll
+    for (int p = 0; p < PD; p++)
+        if (st + p < cnt) compute(buf[p], st + p);
+}
+
+// One thread per (quad, sub-quad, lane): the lane's code bytes and scale
+// bytes, and (lanes with b % 4 == 0) the d pairs of its row.
+__global__ void __launch_bounds__(kWG) pack_q4k_quad_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                            size_t nquads, int S) {
+    const size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= nquads * (size_t)S * 64) return;
+    const size_t Q = i / (64 * (size_t)S);
+    const int sq = (int)((i >> 6) % (size_t)S), l = (int)(i & 63), b = l >> 2, j = l & 3;
+    const uint8_t* row = src + (4 * Q + j) * ((size_t)S * 1152);
+    uint8_t* o = dst + (Q * S + sq) * kQ4SubQuadBytes;
+    uint64_t w = 0;
+    for (int ii = 0; ii < 2; ii++) {
+        const int t = 32 * sq + b + 16 * ii, g = t & 3;
+        const uint8_t* blk = row + (t >> 2) * 144;
+        for (int k = 0; k < 32; k++) o[1024 * (2 * ii + (k >> 4)) + 16 * l + (k & 15)] = blk[16 + 32 * g + k];
+        uint32_t sd[3];
+        for (int k = 0; k < 3; k++)
+            sd[k] = blk[4 + 4 * k] | (blk[5 + 4 * k] << 8) | (blk[6 + 4 * k] << 16) | ((uint32_t)blk[7 + 4 * k] << 24);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(sd[0], sd[1], sd[2], g, sc0, m0, sc1, m1);
+        w |= (uint64_t)(sc0 | (sc1 << 6)) << (12 * ii);
+        w |= (uint64_t)(m0 | (m1 << 6)) << (24 + 12 * ii);
+        if ((b & 3) == 0)
+            for (int k = 0; k < 4; k++) o[4480 + 8 * (4 * j + (b >> 2)) + 4 * ii + k] = blk[k];
+    }
+    for (int k = 0; k < 6; k++) o[4096 + 6 * l + k] = (uint8_t)(w >> (8 * k));
 }
 
 // One thread per (quad, lane): writes the lane's codes, scales and (lanes
@@ -1925,6 +2298,45 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
         // 2 workgroups per CU measured best for the head GEMV (24.7 us vs 26.2 at 3)
         const int per_cu = mivi::stream_wg_per_cu(n);
         const int grid = std::max(1, std::min((ngroups + 3) / 4, mivi::num_cus() * per_cu));
+        if (a.packed && t == MIVI_GGML_Q4_K) {
+            // packed Q4_K row quads on the matrix cores (one column)
+            if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
+                const int ep = a.epilogue;
+                bool ok = (K == 2048 || K == 8192) && a.ncol <= 1 && ep != mivi::EPI_ARGMAX;
+                for (int i = 0; i < a.nseg; i++) ok = ok && a.seg[i].n % 4 == 0;
+                if (ep == mivi::EPI_SWIGLU) ok = ok && K == 2048 && a.nseg == 2 && a.seg[1].n == a.seg[0].n;
+                if (ep == mivi::EPI_CONV)
+                    ok = ok && K == 2048 && a.nseg == 1 && a.seg[0].n % 12 == 0 && a.ksize == kConvKs && a.st_in &&
+                         a.st_out && (a.conv_mode == 2 || a.conv_w);
+                if (!ok) return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no Q4_K row-quad GEMV for this shape");
+                const int nsteps = ep == mivi::EPI_SWIGLU ? a.seg[0].n / 4 : ep == mivi::EPI_CONV ? a.seg[0].n / 12 : n / 4;
+                // one workgroup per CU at most, each wave a whole number of steps;
+                // PD: steps in flight, no more than a wave has
+                const int qg = std::max(1, std::min((nsteps + 3) / 4, mivi::num_cus()));
+                const int cmax = (nsteps + qg * 4 - 1) / (qg * 4);
+                const int pd = (cmax >= 4 && K == 2048) ? 4 : cmax >= 2 ? 2 : 1;  // K = 8192: 2 (registers)
+#define LQ4(EPI, S, PD) hipLaunchKernelGGL((gemv_q4k_quad_kernel<PRO, EPI, S, PD>), dim3(qg), dim3(kWG), 0, s, a)
+#define LQ4P(EPI, S) \
+    if (pd == 4) LQ4(EPI, S, 4); else if (pd == 2) LQ4(EPI, S, 2); else LQ4(EPI, S, 1)
+                if (ep == mivi::EPI_SWIGLU) { LQ4P(mivi::EPI_SWIGLU, 1); }
+                else if (ep == mivi::EPI_CONV) { LQ4P(mivi::EPI_CONV, 1); }
+                else if (K == 2048) { LQ4P(mivi::EPI_STORE, 1); }
+                else {
+                    // K = 8192: the four waves of a workgroup split each quad
+                    const int g8 = std::max(1, std::min(n / 4, mivi::num_cus()));
+                    const int c8 = (n / 4 + g8 - 1) / g8;
+#define LQ8(PD) hipLaunchKernelGGL((gemv_q4k_quad8k_kernel<PRO, PD>), dim3(g8), dim3(kWG), 0, s, a)
+                    if (c8 >= 4) LQ8(4); else if (c8 >= 2) LQ8(2); else LQ8(1);
+#undef LQ8
+                }
+#undef LQ4P
+#undef LQ4
+                MIVI_HIP_CHECK(hipGetLastError());
+                return MIVI_OK;
+            } else {
+                return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed rows take no conv or SwiGLU prologue");
+            }
+        }
         if (a.epilogue == mivi::EPI_CONV) {
             // the ShortConv in_proj with the gated conv in its epilogue: Q4_K
             // rows at K = 2048, one segment of 3D rows [B|C|X]
@@ -2230,7 +2642,7 @@ int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
 // K = 8192 (24 KB per column); packed rows take 2.
 static int gemv_max_cols(int32_t t, int K, bool packed, int pro = PRO_NONE, int epilogue = EPI_STORE) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
-    if (packed) return K == 2048 ? 2 : 1;
+    if (packed) return (t == MIVI_GGML_Q6_K && K == 2048) ? 2 : 1;
     // Q4_K at K = 8192 on the matrix cores: column groups of four run side by
     // side in one launch (one workgroup per CU each)
     if (K == 8192 && t == MIVI_GGML_Q4_K && pro == PRO_NONE && epilogue == EPI_STORE &&
@@ -2450,6 +2862,16 @@ int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t co
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
 }
+
+int32_t launch_pack_q4k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s) {
+    const int S = (int)(cols / 2048);
+    const size_t threads = rows / 4 * (size_t)S * 64;
+    if (threads == 0) return MIVI_OK;
+    hipLaunchKernelGGL(pack_q4k_quad_kernel, dim3((unsigned)((threads + kWG - 1) / kWG)), dim3(kWG), 0, s, src, dst,
+                       rows / 4, S);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
 }  // namespace mivi
 
 // --------------------------------------------------------- read floor probe
@@ -2503,8 +2925,12 @@ extern "C" int32_t mivi_hip_read_floor(const uint8_t* p, size_t bytes, void* str
     return MIVI_OK;
 }
 
-// Packed rows: Q6_K with d in {2048, 4096, 8192} (the streaming kernel's shapes).
-static bool packable(int32_t t, size_t d) { return t == MIVI_GGML_Q6_K && (d == 2048 || d == 4096 || d == 8192); }
+// Packed rows: Q6_K with d in {2048, 4096, 8192} (the streaming kernel's
+// shapes), Q4_K with d in {2048, 8192} and a multiple of 4 rows (row quads).
+static bool packable(int32_t t, size_t d, size_t rows) {
+    if (t == MIVI_GGML_Q6_K) return d == 2048 || d == 4096 || d == 8192;
+    return t == MIVI_GGML_Q4_K && (d == 2048 || d == 8192) && rows % 4 == 0;
+}
 
 extern "C" int32_t mivi_hip_pack_weights(int32_t t, const uint8_t* src, size_t src_len, uint8_t* dst,
                                          size_t dst_len, size_t rows, size_t cols, void* stream) {
@@ -2515,11 +2941,13 @@ extern "C" int32_t mivi_hip_pack_weights(int32_t t, const uint8_t* src, size_t s
     if (__builtin_mul_overflow(rows, (cols / bs) * ts, &need)) return err_overflow();
     if (src_len < need) return err_buffer_too_small(need, src_len);
     if (dst_len < need) return err_buffer_too_small(need, dst_len);
-    if (!packable(t, cols))
-        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu columns", t, cols);
+    if (!packable(t, cols, rows))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu rows of %zu columns", t, rows,
+                         cols);
     if (rows && (!src || !dst)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
     if (src == dst && rows) return set_error(MIVI_ERR_INVALID_ARGUMENT, "packing needs distinct buffers");
     clear_error();
+    if (t == MIVI_GGML_Q4_K) return launch_pack_q4k(src, dst, rows, cols, (hipStream_t)stream);
     return launch_pack_q6k(src, dst, rows, cols, (hipStream_t)stream);
 }
 
@@ -2528,8 +2956,8 @@ extern "C" int32_t mivi_hip_quantized_matvec_packed(float* out, size_t out_len, 
                                                     size_t d, void* stream) {
     int32_t rc = validate_matvec(t, out_len, packed_len, x_len, n, d, nullptr);
     if (rc) return rc;
-    if (!packable(t, d))
-        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu columns", t, d);
+    if (!packable(t, d, n))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu rows of %zu columns", t, n, d);
     if (n && (!out || !packed || !x)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
     if ((uintptr_t)packed % 16) return set_error(MIVI_ERR_INVALID_ARGUMENT, "packed rows must be 16-byte aligned");
     if (n > (size_t)INT32_MAX) return err_overflow();

@@ -389,12 +389,71 @@ def test_packed_q6k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols
         check_bound(oracle, Q6_K, w, x, a, rows, cols)
 
 
+def q4k_quad_pack_ref(oracle, w, nq, cols):
+    """The row-quad packed layout of the first nq quads of a Q4_K matrix with
+    cols = 2048 S columns, restated from its definition: sub-quad s of quad Q
+    (4608 bytes) holds values [2048 s, 2048 s + 2048) of rows 4Q..4Q+3; lane
+    l = 4b + j owns units t = 32 s + b and t + 16 of row j (unit t: sub-blocks
+    2g, 2g + 1 of superblock t / 4, g = t & 3); the units' 32 code bytes at
+    1024 k + 16 l (k = 0, 1 unit t, k = 2, 3 unit t + 16), the four sub-blocks'
+    6-bit scales (bits 0-23) and mins (bits 24-47) in 6 bytes at 4096 + 6 l,
+    the superblocks' d | dmin at 4480 + 8 (4 j + b / 4)."""
+    S = cols // 2048
+    B = w.reshape(-1, 4, cols // 256, 144)[:nq]
+    out = np.zeros((nq, S, 4608), np.uint8)
+    for q in range(nq):
+        for l in range(64):
+            b, j = l >> 2, l & 3
+            for sq in range(S):
+                bits = 0
+                for ii in range(2):
+                    t = 32 * sq + b + 16 * ii
+                    g, blk = t & 3, B[q, j, t >> 2]
+                    out[q, sq, 1024 * 2 * ii + 16 * l:1024 * 2 * ii + 16 * l + 16] = blk[16 + 32 * g:32 + 32 * g]
+                    out[q, sq, 1024 * (2 * ii + 1) + 16 * l:1024 * (2 * ii + 1) + 16 * l + 16] = blk[32 + 32 * g:48 + 32 * g]
+                    (s0, m0), (s1, m1) = (oracle.get_scale_min_k4(2 * g + h, blk[4:16]) for h in range(2))
+                    bits |= (s0 | s1 << 6) << (12 * ii) | (m0 | m1 << 6) << (24 + 12 * ii)
+                    o = 4480 + 8 * (4 * j + (b >> 2)) + 4 * ii
+                    out[q, sq, o:o + 4] = blk[0:4]
+                out[q, sq, 4096 + 6 * l:4096 + 6 * l + 6] = np.frombuffer(bits.to_bytes(6, "little"), np.uint8)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(4, 2048), (3072, 2048), (8192, 2048), (20000, 2048), (12, 8192), (2048, 8192)])
+def test_packed_q4k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols):
+    # Q4_K row quads (matrix cores): the packed GEMV gives the GGUF-row
+    # streaming GEMV's result bit for bit, and meets the oracle bound
+    torch = torch_mod
+    w = hip.synth_random_weights(Q4_K, 70 + cols + rows, rows, cols, 0.02)
+    x = hip.synth_normal(71 + rows, cols)
+    dw, dx = dev(torch, w), dev(torch, x)
+    packed = torch.empty_like(dw)
+    hip.pack_weights(Q4_K, dw, packed, rows, cols)
+    y_raw = torch.empty(rows, dtype=torch.float32, device="cuda")
+    y_pk = torch.full((rows + 1,), 7.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matvec(y_raw, Q4_K, dw, dx, rows, cols)
+    hip.quantized_matvec_packed(y_pk[:rows], Q4_K, packed, dx, rows, cols)
+    torch.cuda.synchronize()
+    a, b = y_raw.cpu().numpy(), y_pk.cpu().numpy()
+    assert b[-1] == 7.0
+    assert np.array_equal(a.view(np.uint32), b[:-1].view(np.uint32))
+    nq = min(rows // 4, 3)
+    assert np.array_equal(packed.cpu().numpy()[:nq * 4 * cols // 256 * 144], q4k_quad_pack_ref(oracle, w, nq, cols))
+    if rows <= 3072:
+        check_bound(oracle, Q4_K, w, x, a, rows, cols)
+
+
 def test_packed_rejects_other_types_and_shapes(hip, torch_mod):
     torch = torch_mod
-    w = torch.zeros(144 * 8 * 4, dtype=torch.uint8, device="cuda")
+    w = torch.zeros(144 * 8 * 6, dtype=torch.uint8, device="cuda")
     dst = torch.zeros_like(w)
     with pytest.raises(hip.QuantError):
-        hip.pack_weights(Q4_K, w, dst, 4, 2048)
+        hip.pack_weights(Q4_K, w, dst, 6, 2048)    # Q4_K row quads need rows % 4 == 0
+    with pytest.raises(hip.QuantError):
+        hip.pack_weights(Q4_K, w, dst, 3, 4096)    # and 2048 or 8192 columns
+    w8 = torch.zeros(34 * 64 * 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(hip.QuantError):
+        hip.pack_weights(Q8_0, w8, torch.zeros_like(w8), 4, 2048)
     w6 = torch.zeros(210 * 4 * 4, dtype=torch.uint8, device="cuda")
     with pytest.raises(hip.QuantError):
         hip.pack_weights(Q6_K, w6, torch.zeros_like(w6), 4, 1024)   # no packed layout for d = 1024
