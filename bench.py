@@ -513,8 +513,10 @@ def main():
     if a.only_q6k:
         return
     q4 = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200)
-    log(f"Q4_K GEMV 8192x2048: {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s; "
+    log(f"Q4_K GEMV 8192x2048 (GGUF rows): {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s; "
         f"plain read of the same bytes {q4['read_floor_us']:.2f} us")
+    q4p = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200, packed=True)
+    log(f"Q4_K GEMV 8192x2048 (packed row quads): {q4p['ms_per_call'] * 1e3:.2f} us/call, {q4p['gbs']:.0f} GB/s")
     cpu = None
     if not a.no_cpu:
         cpu = cpu_gemv_baseline(hip.GgmlType.Q6_K, q6["w_host"], q6["x_host"], 65536, 2048, a.cpu_seconds)
@@ -529,6 +531,11 @@ def main():
     }
     extra["q6k_gemv_config2_gguf_rows"]["frac_of_peak"] = q6r["gbs"] / HBM_PEAK_GBS
     extra["q4k_gemv_config1"]["frac_of_peak"] = q4["gbs"] / HBM_PEAK_GBS
+    # the same matrix packed once into row quads (mivi_hip_pack_weights, not
+    # timed; the model's one-column decode GEMVs read this layout)
+    extra["q4k_gemv_config1_packed"] = {k: q4p[k] for k in ("ms_per_call", "gbs", "read_floor_us", "frac_of_read_floor")}
+    extra["q4k_gemv_config1_packed"]["frac_of_peak"] = q4p["gbs"] / HBM_PEAK_GBS
+    extra["q4k_gemv_config1_packed"]["weight_layout"] = "packed row quads (matrix cores; bit-identical to GGUF rows)"
     if not a.no_cpu:
         extra["q4k_gemv_config1"]["cpu_baseline"] = cpu_gemv_baseline(hip.GgmlType.Q4_K, q4["w_host"], q4["x_host"],
                                                                        8192, 2048, a.cpu_seconds / 2)

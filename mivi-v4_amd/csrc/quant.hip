@@ -562,6 +562,36 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
 
+// The three digit planes of four scaled activations y (|y| <= 127.5):
+// d0 = rint(y), d1 = rint((y - d0) 254), d2 = rint((t1 - d1) 254) as signed
+// bytes, value e in byte e of w0, w1, w2. Adding 1.5 * 2^23 rounds to the
+// nearest integer with ties to even (as rintf) and leaves the integer's
+// two's complement in the low mantissa bits, so its low byte is the digit;
+// subtracting it again gives the rounded value exactly. (Non-finite inputs
+// give a NaN digit scale, so their digits never matter.)
+__device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);  // a.byte0, b.byte0 in bytes 0, 1
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000c0cu);  // c.byte0, d.byte0 in bytes 2, 3
+    return ab | cd;
+}
+__device__ __forceinline__ void digits4(const float (&y)[4], uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+    constexpr float kRound = 12582912.0f;  // 1.5 * 2^23
+    uint32_t b0[4], b1[4], b2[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float r0 = y[e] + kRound;
+        const float t1 = (y[e] - (r0 - kRound)) * 254.0f;
+        const float r1 = t1 + kRound;
+        const float r2 = (t1 - (r1 - kRound)) * 254.0f + kRound;
+        b0[e] = __float_as_uint(r0);
+        b1[e] = __float_as_uint(r1);
+        b2[e] = __float_as_uint(r2);
+    }
+    w0 = low_bytes4(b0[0], b0[1], b0[2], b0[3]);
+    w1 = low_bytes4(b1[0], b1[1], b1[2], b1[3]);
+    w2 = low_bytes4(b2[0], b2[1], b2[2], b2[3]);
+}
+
 // Digit planes of the K floats staged at xs, written to dig[d * K / 4 + i]
 // (four values per dword, value 4i + e in byte e). Returns s (NaN when x
 // holds a NaN or an infinity, so the products come out NaN as in fp32).
@@ -581,18 +611,9 @@ __device__ __forceinline__ float stage_digits(const float* xs, uint32_t* dig, in
     const float sc = (m - m) + m / 127.0f;
     for (int i = threadIdx.x; i < K / 4; i += kWG) {
         const f32x4 v = *(const f32x4*)(xs + 4 * i);
-        uint32_t w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float y = v[e] * inv;
-            const float d0 = rintf(y);
-            const float t1 = (y - d0) * 254.0f;
-            const float d1 = rintf(t1);
-            const float d2 = rintf((t1 - d1) * 254.0f);
-            w0 |= ((uint32_t)(int)d0 & 0xFFu) << (8 * e);
-            w1 |= ((uint32_t)(int)d1 & 0xFFu) << (8 * e);
-            w2 |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
-        }
+        uint32_t w0, w1, w2;
+        const float y[4] = {v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv};
+        digits4(y, w0, w1, w2);
         dig[i] = w0;
         dig[K / 4 + i] = w1;
         dig[K / 2 + i] = w2;
@@ -842,18 +863,8 @@ struct StageIn {
         uint32_t w0[E / 4], w1[E / 4], w2[E / 4];
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
-            w0[q] = w1[q] = w2[q] = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float yv = v[4 * q + e] * inv;
-                const float d0 = rintf(yv);
-                const float t1 = (yv - d0) * 254.0f;
-                const float d1 = rintf(t1);
-                const float d2 = rintf((t1 - d1) * 254.0f);
-                w0[q] |= ((uint32_t)(int)d0 & 0xFFu) << (8 * e);
-                w1[q] |= ((uint32_t)(int)d1 & 0xFFu) << (8 * e);
-                w2[q] |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
-            }
+            const float y[4] = {v[4 * q] * inv, v[4 * q + 1] * inv, v[4 * q + 2] * inv, v[4 * q + 3] * inv};
+            digits4(y, w0[q], w1[q], w2[q]);
         }
         const int P = PS ? PS : K / 4;
 #pragma unroll
@@ -1351,18 +1362,9 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
         const int e0 = (l + 64 * w) * E;
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
-            uint32_t w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float yv = v[w][4 * q + e] * inv;
-                const float d0 = rintf(yv);
-                const float t1 = (yv - d0) * 254.0f;
-                const float d1 = rintf(t1);
-                const float d2 = rintf((t1 - d1) * 254.0f);
-                w0 |= ((uint32_t)(int)d0 & 0xFFu) << (8 * e);
-                w1 |= ((uint32_t)(int)d1 & 0xFFu) << (8 * e);
-                w2 |= ((uint32_t)(int)d2 & 0xFFu) << (8 * e);
-            }
+            uint32_t w0, w1, w2;
+            const float y[4] = {v[w][4 * q] * inv, v[w][4 * q + 1] * inv, v[w][4 * q + 2] * inv, v[w][4 * q + 3] * inv};
+            digits4(y, w0, w1, w2);
             dig[e0 / 4 + q] = w0;
             dig[PS + e0 / 4 + q] = w1;
             dig[2 * PS + e0 / 4 + q] = w2;
