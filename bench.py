@@ -488,6 +488,8 @@ def main():
     ap.add_argument("--decode-prefill", type=int, default=4096)
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--only-q6k", action="store_true", help="config 2 only (counter runs)")
+    ap.add_argument("--only-gemm", action="store_true", help="config 3 only (counter runs)")
+    ap.add_argument("--only-config5", action="store_true", help="config 5 only (counter runs)")
     ap.add_argument("--no-config5", action="store_true")
     ap.add_argument("--config5-ctx", type=int, default=32768)
     ap.add_argument("--config5-steps", type=int, default=128)
@@ -503,6 +505,14 @@ def main():
     torch.cuda.set_device(0)
     log(f"{hip.version()} on {torch.cuda.get_device_name(0)}")
 
+    if a.only_gemm:
+        g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3)
+        log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s")
+        return
+    if a.only_config5:
+        c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps)
+        log(f"config 5: {c5['tok_s']:.0f} tok/s over 8 sequences, {c5['ms_per_step']:.2f} ms per step")
+        return
     q6 = gemv_bench(torch, hip, hip.GgmlType.Q6_K, 65536, 2048, a.steps, a.warmup, 100, packed=True)
     log(f"Q6_K GEMV 65536x2048 (packed rows): {q6['ms_per_call'] * 1e3:.1f} us/call, {q6['gbs']:.0f} GB/s; "
         f"plain read of the same bytes {q6['read_floor_us']:.1f} us")
