@@ -111,13 +111,16 @@ int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t ggml_
                                        size_t rows, size_t cols, void* stream);
 
 /* No counterpart in the reference (its Rust kernels read the GGUF layout):
- * rewrites rows x cols Q6_K weights (cols 2048, 4096 or 8192) into the layout
- * of the packed GEMV, of the same size: with cols 2048 and rows a multiple of
- * 4, row quads (four rows' codes, scales and d interleaved for the matrix-core
- * GEMV, codes re-encoded six bits to a byte); otherwise unit planes, a byte
- * permutation of each row. dst must not overlap src. Other types/shapes
- * return MIVI_ERR_UNSUPPORTED. For callers that keep weights resident (the
- * model loader does this once for the Q6_K head). */
+ * rewrites rows x cols weights into the layout of the packed GEMV, of the
+ * same size. Q6_K (cols 2048, 4096 or 8192): with cols 2048 and rows a
+ * multiple of 4, row quads (four rows' codes, scales and d interleaved for the
+ * matrix-core GEMV, codes re-encoded six bits to a byte); otherwise unit
+ * planes, a byte permutation of each row. Q4_K (cols 2048 or 8192, rows a
+ * multiple of 4): row quads of 4608-byte sub-quads (four rows' code bytes,
+ * 6-bit scales and mins, d and dmin laid out for the matrix-core GEMV). dst
+ * must not overlap src. Other types/shapes return MIVI_ERR_UNSUPPORTED. For
+ * callers that keep weights resident (the model loader packs the Q6_K head
+ * and every Q4_K projection once). */
 int32_t mivi_hip_pack_weights(int32_t ggml_type, const uint8_t* src, size_t src_len, uint8_t* dst,
                               size_t dst_len, size_t rows, size_t cols, void* stream);
 
