@@ -35,6 +35,11 @@ HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall"]
 
 SOURCES = ["errors.cpp", "synth.cpp", "quant.hip", "gemm.hip", "model.hip", "sampler.hip"]
 
+# Per-source device flags. quant.hip: MFMA results straight into VGPRs (the
+# GEMV kernels consume each result at once; in AGPRs every one of them costs a
+# v_accvgpr_read). The GEMM keeps the default: its accumulator tiles live in AGPRs.
+EXTRA_FLAGS = {"quant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def _deps(src: str) -> list[str]:
     return [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")] + [
@@ -49,7 +54,7 @@ def _compile(src: str, force: bool) -> str:
         if all(os.path.getmtime(d) <= t for d in _deps(path)):
             return obj
     if src.endswith(".hip"):
-        cmd = [HIPCC, *DEVICE_FLAGS, "-c", path, "-o", obj]
+        cmd = [HIPCC, *DEVICE_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", path, "-o", obj]
     else:
         cmd = [HIPCC, *HOST_FLAGS, "-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -128,6 +128,26 @@ __device__ __forceinline__ void swap16(float v, float& ev, float& od) {
 // so the result is group_sum<W>'s bit for bit in the lanes with bit 2 clear
 // (lanes 0-3, 8-11, ... of each group), the lanes that use it here; the
 // other steps pair exactly (IEEE addition is commutative).
+// The same butterfly (v + value of lane ^ o, o = 32 .. 1) exact in every
+// lane: the xor-4 partner is lane (i + 4) mod 16 where bit 2 is clear and
+// (i - 4) mod 16 where it is set.
+__device__ __forceinline__ float xor4_mov(float v) {
+    const float up = dpp_mov<0x12C>(v), dn = dpp_mov<0x124>(v);  // row_ror:12, row_ror:4
+    return (threadIdx.x & 4) ? dn : up;
+}
+__device__ __forceinline__ float xsum_all64(float v) {
+    float a, b;
+    swap32(v, a, b);
+    v = a + b;
+    swap16(v, a, b);
+    v = a + b;
+    v += dpp_mov<0x128>(v);
+    v += xor4_mov(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0xB1>(v);
+    return v;
+}
+
 template <int W>
 __device__ __forceinline__ float xsum_desc(float v) {
     static_assert(W >= 8 && W <= 64, "groups of 8 to 64 lanes");

@@ -628,6 +628,8 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 // a * b for |a| < 2^23 and 8-bit b: the explicit 24-bit sign extension lets
 // the compiler use the full-rate v_mad_i32_i24 instead of v_mul_lo_u32.
 __device__ __forceinline__ int mul24(int a, int b) { return (int)__builtin_amdgcn_sbfe(a, 0, 24) * b; }
+// a * b + c with the same bounds (v_mad_i32_i24)
+__device__ __forceinline__ int mad24(int a, int b, int c) { return (int)__builtin_amdgcn_sbfe(a, 0, 24) * b + c; }
 
 // One Q6_K unit (16 values of each of the sub-blocks l, l+32, l+64, l+96 of
 // half h, q6_k.rs:68-111): sum over the unit of sc * (q - 32) * digits, per
@@ -782,10 +784,11 @@ struct StageIn {
         float m = 0.f, ss = 0.f;
         if constexpr (PRO == mivi::PRO_RMSNORM) {
             // ss and max|x w| in one reduction; max|x * scale * w| = scale * max|x w|
+            // (a NaN or infinite x makes ss, so the scale and m, NaN)
 #pragma unroll
             for (int i = 0; i < E; i++) {
                 ss = fmaf(v[i], v[i], ss);
-                m = nanmax(m, fabsf(v[i] * y[i / 4][i % 4]));
+                m = fmaxf(m, fabsf(v[i] * y[i / 4][i % 4]));
             }
         } else if constexpr (PRO == mivi::PRO_SWIGLU) {
 #pragma unroll
@@ -821,8 +824,14 @@ struct StageIn {
             }
         }
         if constexpr (PRO != mivi::PRO_RMSNORM) {
+            // fmaxf passes NaNs over: nn, a sum of v * 0, turns m NaN for them
+            float nn = 0.f;
 #pragma unroll
-            for (int i = 0; i < E; i++) m = nanmax(m, fabsf(v[i]));
+            for (int i = 0; i < E; i++) {
+                m = fmaxf(m, fabsf(v[i]));
+                nn = fmaf(v[i], 0.f, nn);
+            }
+            m += nn;
         }
         // one workgroup reduction of (ss, m): the xor butterfly of the wave
         // (lane 0's sums), then the waves in order
@@ -1283,7 +1292,7 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
 #pragma unroll
             for (int i = 0; i < E; i++) {
                 ssw[w] = fmaf(v[w][i], v[w][i], ssw[w]);
-                m = nanmax(m, fabsf(v[w][i] * nw[w][i]));
+                m = fmaxf(m, fabsf(v[w][i] * nw[w][i]));  // (non-finite x: ss, so m, NaN)
             }
         } else if constexpr (PRO == mivi::PRO_CONV) {
             // a.x = [B | C | X] (ssm.rs:80-140), as StageIn
@@ -1330,17 +1339,30 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
             }
         }
         if constexpr (PRO != mivi::PRO_RMSNORM) {
+            float nn = 0.f;  // NaN for a NaN v (fmaxf passes it over)
 #pragma unroll
-            for (int i = 0; i < E; i++) m = nanmax(m, fabsf(v[w][i]));
+            for (int i = 0; i < E; i++) {
+                m = fmaxf(m, fabsf(v[w][i]));
+                nn = fmaf(v[w][i], 0.f, nn);
+            }
+            m += nn;
         }
     }
+    // the butterflies of finish's wave reductions, exact in every lane
+    if constexpr (PRO == mivi::PRO_RMSNORM) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        if constexpr (PRO == mivi::PRO_RMSNORM) {
-#pragma unroll
-            for (int w = 0; w < 4; w++) ssw[w] += __shfl_xor(ssw[w], o, 64);
-        }
-        m = nanmax(m, __shfl_xor(m, o, 64));
+        for (int w = 0; w < 4; w++) ssw[w] = xsum_all64(ssw[w]);
+    }
+    {
+        float lo, hi;
+        swap32(m, lo, hi);
+        m = nanmax(lo, hi);
+        swap16(m, lo, hi);
+        m = nanmax(lo, hi);
+        m = nanmax(m, dpp_mov<0x128>(m));
+        m = nanmax(m, xor4_mov(m));
+        m = nanmax(m, dpp_mov<0x4E>(m));
+        m = nanmax(m, dpp_mov<0xB1>(m));
     }
     if constexpr (PRO == mivi::PRO_RMSNORM) {
         float ss = ssw[0];
@@ -1375,10 +1397,10 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
             float t = 0.f;
 #pragma unroll
             for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[w][b * 32 + i];
-            if constexpr (E < 32) {
-#pragma unroll
-                for (int o = 1; o < 32 / E; o <<= 1) t += __shfl_xor(t, o, 64);
-            }
+            // xor 1, 2, 4 in that order (the writers' partners are exact)
+            if constexpr (E < 32) t += dpp_mov<0xB1>(t);
+            if constexpr (E < 16) t += dpp_mov<0x4E>(t);
+            if constexpr (E < 8) t += dpp_mov<0x12C>(t);
             if (E >= 32 || (l % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t;
         }
     }
@@ -1391,23 +1413,23 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
 // input rows of a small matmul_rows batch) against Q4_K rows in their GGUF
 // layout: up to 8 columns at K = 2048, up to 4 at K = 8192. A workgroup owns
 // 16 rows at a time (EPI_SWIGLU: gate rows c..c+7 and up rows c..c+7), its
-// wave q the q-th quarter of their units. Per 32-value sub-block and group G
-// of four columns, v_mfma_i32_16x16x32_i8 takes
+// wave q the q-th quarter of their superblocks. Per 32-value sub-block and
+// group G of four columns, v_mfma_i32_16x16x32_i8 takes
 //   A  row i = 4c' + p: digit plane p of column 4G + c' (a zero plane for
 //      p = 3) at the sub-block's 32 k (lane l: row l % 16, k = 8 (l / 16) .. +8),
 //   B  the 4-bit codes of the 16 rows (lane l: row l % 16, the low or high
 //      nibbles of the 8 code bytes of k = 8 (l / 16) .. +8),
 // and lane l receives C[4 (l / 16) + p][l % 16] (p = 0..2): column
-// 4G + l / 16, row l % 16, plane p, the exact integer sums of code x digit
-// that the sdot4 kernel forms. The lane applies the sub-block scales and the
-// float steps of q4k_unit_i8 per unit for its row and column. The one-column
-// kernel then sums units over its lanes with a butterfly whose first steps
-// pair unit t with t + 16 (K = 2048) or form lr + (lr + 64) and then pair lr
-// with lr + 32 (K = 8192): here waves 2, 3 hand their per-unit values to
-// waves 0, 1 and wave 1 to wave 0 through LDS, in that order, and wave 0
-// finishes the butterfly in registers, so every column equals a one-column
-// launch bit for bit. Digits sit in LDS (8 KB per column at K = 2048: three
-// planes and the zero plane, padded apart against bank conflicts).
+// 4G + l / 16, row l % 16, plane p, the exact integer sums of code x digit.
+// The lane sums sc x C over the superblock's eight sub-blocks in int32 and
+// the min terms m x X in f32, then takes one float step per superblock:
+// d s (A0 + A1/254 + A2/254^2) - dmin sum m X (q4_k_m.rs:144-214). The
+// per-unit float steps of the one-column kernels are 2.2 times the VALU work
+// and this kernel is VALU-bound, so a batched column agrees with its
+// one-column GEMV to float rounding, not bit for bit (both within the digit
+// representation's bound). Waves 1-3 hand their partial row sums to wave 0
+// through LDS. Digits sit in LDS (8 KB per column at K = 2048: three planes
+// and the zero plane, padded apart against bank conflicts).
 // Columns [c0, c0 + 4) of a batched launch (blockIdx.y = column group of the
 // K = 8192 kernel, whose digits fit LDS for four columns only).
 __device__ __forceinline__ mivi::GemvArgs gemv_col_group(const mivi::GemvArgs& a, int c0) {
@@ -1425,14 +1447,13 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
     const mivi::GemvArgs a = (KT == 8192 || (NG == 1 && gridDim.y > 1)) ? gemv_col_group(a0, 4 * (int)blockIdx.y) : a0;
     constexpr int K = KT, nb = K / 256;
     constexpr int SQ = nb / 4;               // superblocks per wave: 2 or 8
-    constexpr int LW = 4 * SQ;               // units (leaf values) per wave: 8 or 32
     constexpr int PD = SQ < 4 ? SQ : 4;      // superblock chunks in flight per wave
     constexpr int NCM = 4 * NG;
     constexpr int PS = K / 4 + 4;            // digit plane stride (dwords)
     __shared__ __attribute__((aligned(16))) uint32_t dig[NCM][4 * PS];
     __shared__ __attribute__((aligned(16))) float xsum[NCM][K / 32];
     __shared__ float scol[NCM];
-    __shared__ float xch[3][NG * LW][64];    // wave 2 -> 0, wave 3 -> 1, wave 1 -> 0
+    __shared__ float xq[2][3][NG][64];       // waves 1-3 -> wave 0, by group-step parity
     const Segs sg(a, nb * 144);
     const int n = sg.n, n0 = a.seg[0].n;
     const int ncol = a.ncol;  // 2..NCM, workgroup-uniform
@@ -1490,7 +1511,11 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
     for (int G = 0; G < NG; G++) dA[G] = dig[min(4 * G + ci, ncol - 1)] + pi * PS + 2 * kg;
 
     for (int st = 0; st < cnt; st++) {
-        float leaf[NG][LW];
+        // this wave's superblocks of the group, each summed in int32 over its
+        // four units before the float steps
+        float part[NG];
+#pragma unroll
+        for (int G = 0; G < NG; G++) part[G] = 0.f;
 #pragma unroll
         for (int bb = 0; bb < SQ; bb++) {
             const int slot = bb % PD, b = wave * SQ + bb;
@@ -1502,10 +1527,18 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
             if (bb + PD < SQ) load(slot, st, bb + PD);
             else load(slot, st + 1, bb + PD - SQ);
             const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
+            int Acc[NG][3];
+            float Mac[NG];
+#pragma unroll
+            for (int G = 0; G < NG; G++) {
+                Acc[G][0] = Acc[G][1] = Acc[G][2] = 0;
+                Mac[G] = 0.f;
+            }
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 uint32_t sc0, m0, sc1, m1;
                 q4k_scales(h.y, h.z, h.w, g, sc0, m0, sc1, m1);
+                const float m0f = (float)m0, m1f = (float)m1;
                 const long blo = (long)(((uint64_t)(q[g].y & 0x0F0F0F0Fu) << 32) | (q[g].x & 0x0F0F0F0Fu));
                 const long bhi = (long)(((uint64_t)((q[g].y >> 4) & 0x0F0F0F0Fu) << 32) | ((q[g].x >> 4) & 0x0F0F0F0Fu));
 #pragma unroll
@@ -1515,72 +1548,49 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
                     const u32x2 ahi = *(const u32x2*)(dA[G] + w0 + 8);
                     long al = (long)(((uint64_t)alo.y << 32) | alo.x);
                     long ah = (long)(((uint64_t)ahi.y << 32) | ahi.x);
-                    // keep units in program order: pure code is otherwise sunk
-                    // to the final reduction and every unit's products stay live
-                    asm volatile("" : "+v"(al), "+v"(ah));
                     const i32x4 z = {0, 0, 0, 0};
                     const i32x4 Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, blo, z, 0, 0, 0);
                     const i32x4 Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bhi, z, 0, 0, 0);
-                    // q4k_unit_i8 for (row j, column 4G + kg)
-                    int A[3];
+                    // |D| <= 32 * 15 * 127 < 2^16, sc < 64: the superblock sum
+                    // stays below 8 * 2 * 2^22 < 2^31 (exact)
 #pragma unroll
-                    for (int e = 0; e < 3; e++) A[e] = mul24(Dl[e], (int)sc0) + mul24(Dh[e], (int)sc1);
-                    const float f = fmaf((float)A[2], kDig2, fmaf((float)A[1], kDig1, (float)A[0]));
-                    const int col = min(4 * G + kg, ncol - 1);
-                    const float X0 = xsum[col][b * 8 + 2 * g], X1 = xsum[col][b * 8 + 2 * g + 1];
-                    float v = (d * s[G]) * f - dmin * fmaf((float)m0, X0, (float)m1 * X1);
-                    asm volatile("" : "+v"(v));
-                    leaf[G][4 * bb + g] = 0.f + v;
+                    for (int e = 0; e < 3; e++) Acc[G][e] = mad24(Dh[e], (int)sc1, mad24(Dl[e], (int)sc0, Acc[G][e]));
+                    const int cl = min(4 * G + kg, ncol - 1);
+                    const float2 X = *(const float2*)&xsum[cl][b * 8 + 2 * g];
+                    Mac[G] = fmaf(m1f, X.y, fmaf(m0f, X.x, Mac[G]));
                 }
             }
-        }
-        // the butterfly's first steps across the waves (2 -> 0, 3 -> 1, then 1 -> 0)
-        if (wave >= 2) {
 #pragma unroll
-            for (int G = 0; G < NG; G++)
-#pragma unroll
-                for (int t = 0; t < LW; t++) xch[wave - 2][G * LW + t][lane] = leaf[G][t];
-        }
-        __syncthreads();
-        if (wave < 2) {
-#pragma unroll
-            for (int G = 0; G < NG; G++)
-#pragma unroll
-                for (int t = 0; t < LW; t++) leaf[G][t] = leaf[G][t] + xch[wave][G * LW + t][lane];
-            if (wave == 1) {
-#pragma unroll
-                for (int G = 0; G < NG; G++)
-#pragma unroll
-                    for (int t = 0; t < LW; t++) xch[2][G * LW + t][lane] = leaf[G][t];
+            for (int G = 0; G < NG; G++) {
+                // q4_k_m.rs:144-214 per superblock: d * s * sum sc * (q . x~/s) - dmin * sum m * X
+                const float f = fmaf((float)Acc[G][2], kDig2, fmaf((float)Acc[G][1], kDig1, (float)Acc[G][0]));
+                part[G] += (d * s[G]) * f - dmin * Mac[G];
             }
+        }
+        // the four waves' quarters of the depth, summed by wave 0 (one LDS
+        // exchange; the buffer alternates with the group step's parity)
+        if (wave > 0) {
+#pragma unroll
+            for (int G = 0; G < NG; G++) xq[st & 1][wave - 1][G][lane] = part[G];
         }
         __syncthreads();
         if (wave == 0) {
-#pragma unroll
-            for (int G = 0; G < NG; G++) {
-#pragma unroll
-                for (int t = 0; t < LW; t++) leaf[G][t] = leaf[G][t] + xch[2][G * LW + t][lane];
-#pragma unroll
-                for (int sh = LW / 2; sh >= 1; sh >>= 1)
-#pragma unroll
-                    for (int t = 0; t < sh; t++) leaf[G][t] = leaf[G][t] + leaf[G][t + sh];
-            }
             const int r = row_of(st);
 #pragma unroll
             for (int G = 0; G < NG; G++) {
-                const int col = 4 * G + kg;
-                const float v = leaf[G][0];
+                const float v = ((part[G] + xq[st & 1][0][G][lane]) + xq[st & 1][1][G][lane]) + xq[st & 1][2][G][lane];
+                const int cc = 4 * G + kg;
                 if constexpr (EPI == mivi::EPI_SWIGLU) {
                     // lanes j < 8: gate c; lanes j + 8: up c (math.rs:87-95)
                     const float up = __shfl(v, lane + 8, 64);
-                    if (j < 8 && r >= 0 && col < ncol) *(gfloat*)(sg.out(r) + col * a.ys) = silu_f(v) * up;
+                    if (j < 8 && r >= 0 && cc < ncol) *(gfloat*)(sg.out(r) + cc * a.ys) = silu_f(v) * up;
                 } else if constexpr (EPI == mivi::EPI_CONV) {
                     // lanes j = 3i hold B of channel 5g + i, j + 1 its C, j + 2 its X
                     const float cv = __shfl(v, lane + 1, 64), xv = __shfl(v, lane + 2, 64);
-                    if (j < 15 && j % 3 == 0 && r >= 0 && col < ncol) conv_epilogue(a, col, r, v, cv, xv);
+                    if (j < 15 && j % 3 == 0 && r >= 0 && cc < ncol) conv_epilogue(a, cc, r, v, cv, xv);
                 } else {
-                    if (r >= 0 && col < ncol) {
-                        gfloat* y = (gfloat*)(sg.out(r) + col * a.ys);
+                    if (r >= 0 && cc < ncol) {
+                        gfloat* y = (gfloat*)(sg.out(r) + cc * a.ys);
                         if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(y, v);
                         else *y = v;
                     }

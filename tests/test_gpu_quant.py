@@ -284,12 +284,15 @@ def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, 
                                              (7, 1001, 2048), (8, 8192, 2048), (15, 260, 2048),
                                              (3, 300, 8192), (6, 2048, 8192), (8, 2048, 8192), (5, 300, 8192),
                                              (2, 130, 4096)])
-def test_batched_gemv_columns_bit_exact_with_matvec(hip, oracle, torch_mod, t, batch, rows, cols):
+def test_batched_gemv_columns_match_matvec(hip, oracle, torch_mod, t, batch, rows, cols):
     # matmul_rows below the MFMA threshold runs batched GEMVs (inputs as
     # columns: up to 8 per launch at d = 2048 and 4 at d = 8192, Q4_K on the
     # int8 matrix cores; one launch per input at other depths): every input's
-    # row of outputs equals its own matvec bit for bit (lib.rs:404-457), and
-    # meets the oracle bound
+    # row of outputs equals its own matvec (lib.rs:404-457) bit for bit, except
+    # on the Q4_K matrix-core kernel (3+ columns at d = 2048, any batch at
+    # d = 8192), which sums each superblock in int32 before its float steps
+    # and agrees to float rounding (1e-5 ||w_row|| ||x||, a tenth of the bar);
+    # all meet the oracle bound
     torch = torch_mod
     w = hip.synth_random_weights(t, 70 + batch, rows, cols, 0.02)
     X = np.stack([hip.synth_normal(80 + b, cols) for b in range(batch)])
@@ -304,8 +307,17 @@ def test_batched_gemv_columns_bit_exact_with_matvec(hip, oracle, torch_mod, t, b
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert got[-1] == 5.0
+    mfma_cols = t == Q4_K and ((cols == 2048 and batch > 2) or cols == 8192)
+    if mfma_cols:
+        rc, deq, _ = oracle.dequantize_slice(t, w, rows * cols)
+        wn = np.linalg.norm(deq.reshape(rows, cols).astype(np.float64), axis=1)
     for b in range(batch):
-        assert np.array_equal(got[b * rows:(b + 1) * rows].view(np.uint32), ones[b].cpu().numpy().view(np.uint32))
+        g, one = got[b * rows:(b + 1) * rows], ones[b].cpu().numpy()
+        if mfma_cols:
+            tol = 1e-5 * wn * np.linalg.norm(X[b].astype(np.float64))
+            assert np.all(np.abs(g.astype(np.float64) - one) <= tol), b
+        else:
+            assert np.array_equal(g.view(np.uint32), one.view(np.uint32))
     if rows <= 1001:
         for b in range(batch):
             check_bound(oracle, t, w, X[b], got[b * rows:(b + 1) * rows], rows, cols)
