@@ -1261,20 +1261,43 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
-// One column staged by one wave: the digits, sub-block sums and digit scale
-// of StageIn::finish<true, PS> for the same column, bit for bit. Lane l stands
-// in for the workgroup's threads l + 64w (w = 0..3), each owning E
-// consecutive activations, and partial sums are reduced in finish's order
-// (each thread's values in sequence, a butterfly over the 64 threads of a
-// wave, then the four waves in order). Prologues NONE, RMSNORM and CONV.
+// Base-256 digit planes of four values: Y = rint(u * mul) for |Y| < 2^22
+// (adding 1.5 * 2^23 in the fma rounds once, ties to even, and leaves Y in
+// the low mantissa bits), written as balanced base-256 digits
+// Y = 65536 d0 + 256 d1 + d2 with d1, d2 in [-128, 127]: the bytes of
+// Y + 0x808080 are d + 128, so a byte permute gathers each plane and an xor
+// with 0x80 per byte makes the digits signed. Value e in byte e of w0 (d0),
+// w1 (d1) and w2 (d2).
+__device__ __forceinline__ void digits4_b256(const float (&u)[4], float mul, uint32_t& w0, uint32_t& w1,
+                                             uint32_t& w2) {
+    uint32_t z[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) z[e] = __float_as_uint(fmaf(u[e], mul, 12582912.0f)) - 0x4ABF7F80u;  // - bits(1.5*2^23) + 0x808080
+    const uint32_t lo01 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.b0 z1.b0 z0.b1 z1.b1
+    const uint32_t lo23 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);  // z2.b0 z3.b0 z2.b1 z3.b1
+    w2 = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+    w1 = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+    w0 = (__builtin_amdgcn_perm(z[1], z[0], 0x0c0c0602u) | __builtin_amdgcn_perm(z[3], z[2], 0x06020c0cu)) ^ 0x80808080u;
+}
+constexpr float kB256_1 = 1.0f / 256.0f, kB256_2 = 1.0f / 65536.0f;
+
+// One column staged by one wave for the batched kernel: base-256 digit
+// planes (digits4_b256 of Y = rint(x * 127 * 2^15 / max|x|), |Y| < 2^22, so
+// d0 lies in [-64, 64]), the fp32 sums of each 32-value sub-block, and the
+// returned digit scale s = 2 max|x| / 127 with x ~ s (d0 + d1/256 + d2/65536)
+// (NaN when x holds a NaN or an infinity, so the products come out NaN as in
+// fp32). Lane l owns the E consecutive activations at (l + 64 w) E,
+// w = 0..3. Under RMSNORM the digits are taken of u = x * norm_w: the norm's
+// 1 / rms cancels in u * 127 / max|u| and only scales s and the sub-block
+// sums. Each value costs one fma and one subtract, plus the permutes shared
+// by four values. Prologues NONE, RMSNORM and CONV.
 template <int PRO, int E, int PS>
 __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
     static_assert(PRO != mivi::PRO_SWIGLU, "no SwiGLU prologue here");
     constexpr int K = E * kWG;
     const int l = threadIdx.x & 63;
-    float v[4][E], nw[PRO == mivi::PRO_RMSNORM ? 4 : 1][PRO == mivi::PRO_RMSNORM ? E : 1];
-    float ssw[4] = {0.f, 0.f, 0.f, 0.f};
-    float m = 0.f;
+    float v[4][E];
+    float ss = 0.f, m = 0.f, nn = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         const int e0 = (l + 64 * w) * E;
@@ -1287,12 +1310,14 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
 #pragma unroll
             for (int i = 0; i < E / 4; i++) {
                 const f32x4 t = *(gf32x4*)(a.norm_w + e0 + 4 * i);
-                nw[w][4 * i] = t.x; nw[w][4 * i + 1] = t.y; nw[w][4 * i + 2] = t.z; nw[w][4 * i + 3] = t.w;
-            }
+                const float nw[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-            for (int i = 0; i < E; i++) {
-                ssw[w] = fmaf(v[w][i], v[w][i], ssw[w]);
-                m = fmaxf(m, fabsf(v[w][i] * nw[w][i]));  // (non-finite x: ss, so m, NaN)
+                for (int e = 0; e < 4; e++) {
+                    float& x = v[w][4 * i + e];
+                    ss = fmaf(x, x, ss);  // (non-finite x: ss, so s, NaN)
+                    x *= nw[e];
+                    m = fmaxf(m, fabsf(x));
+                }
             }
         } else if constexpr (PRO == mivi::PRO_CONV) {
             // a.x = [B | C | X] (ssm.rs:80-140), as StageIn
@@ -1339,20 +1364,15 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
             }
         }
         if constexpr (PRO != mivi::PRO_RMSNORM) {
-            float nn = 0.f;  // NaN for a NaN v (fmaxf passes it over)
 #pragma unroll
             for (int i = 0; i < E; i++) {
                 m = fmaxf(m, fabsf(v[w][i]));
-                nn = fmaf(v[w][i], 0.f, nn);
+                nn = fmaf(v[w][i], 0.f, nn);  // NaN for a non-finite v (fmaxf passes a NaN over)
             }
-            m += nn;
         }
     }
-    // the butterflies of finish's wave reductions, exact in every lane
-    if constexpr (PRO == mivi::PRO_RMSNORM) {
-#pragma unroll
-        for (int w = 0; w < 4; w++) ssw[w] = xsum_all64(ssw[w]);
-    }
+    m += nn;
+    if constexpr (PRO == mivi::PRO_RMSNORM) ss = xsum_all64(ss);
     {
         float lo, hi;
         swap32(m, lo, hi);
@@ -1364,44 +1384,35 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
         m = nanmax(m, dpp_mov<0x4E>(m));
         m = nanmax(m, dpp_mov<0xB1>(m));
     }
-    if constexpr (PRO == mivi::PRO_RMSNORM) {
-        float ss = ssw[0];
-        ss += ssw[1];
-        ss += ssw[2];
-        ss += ssw[3];
-        const float scale = 1.0f / sqrtf(ss / (float)K + a.eps);  // math.rs:7-22
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-#pragma unroll
-            for (int i = 0; i < E; i++) v[w][i] = v[w][i] * scale * nw[w][i];
-        m *= scale;
-    }
+    // RMSNORM: x = u / rms (math.rs:7-22); else scale 1
+    const float scale = PRO == mivi::PRO_RMSNORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
     const bool finite = m > 0.f && m <= 3.40282347e38f;
-    const float inv = finite ? 127.0f / m : 0.0f;
-    const float sc = (m - m) + m / 127.0f;
+    const float mul = finite ? 4161536.0f / m : 0.0f;  // 127 * 2^15 / max|u|
+    const float sc = PRO == mivi::PRO_RMSNORM ? ((m - m) + m * scale) * (2.0f / 127.0f) : ((m - m) + m) * (2.0f / 127.0f);
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         const int e0 = (l + 64 * w) * E;
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
             uint32_t w0, w1, w2;
-            const float y[4] = {v[w][4 * q] * inv, v[w][4 * q + 1] * inv, v[w][4 * q + 2] * inv, v[w][4 * q + 3] * inv};
-            digits4(y, w0, w1, w2);
+            const float u[4] = {v[w][4 * q], v[w][4 * q + 1], v[w][4 * q + 2], v[w][4 * q + 3]};
+            digits4_b256(u, mul, w0, w1, w2);
             dig[e0 / 4 + q] = w0;
             dig[PS + e0 / 4 + q] = w1;
             dig[2 * PS + e0 / 4 + q] = w2;
         }
-        // fp32 sums of each 32-value sub-block (32 / E threads share one)
+        // fp32 sums of each 32-value sub-block (32 / E lanes share one)
 #pragma unroll
         for (int b = 0; b < (E >= 32 ? E / 32 : 1); b++) {
             float t = 0.f;
 #pragma unroll
             for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[w][b * 32 + i];
-            // xor 1, 2, 4 in that order (the writers' partners are exact)
+            // xor 1, 2, 4 (the writers, lanes with bit 2 clear, see their
+            // exact partners; row_ror:12 reads lane (i + 4) mod 16)
             if constexpr (E < 32) t += dpp_mov<0xB1>(t);
             if constexpr (E < 16) t += dpp_mov<0x4E>(t);
             if constexpr (E < 8) t += dpp_mov<0x12C>(t);
-            if (E >= 32 || (l % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t;
+            if (E >= 32 || (l % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t * scale;
         }
     }
     return sc;
@@ -1527,11 +1538,11 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
             if (bb + PD < SQ) load(slot, st, bb + PD);
             else load(slot, st + 1, bb + PD - SQ);
             const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
-            int Acc[NG][3];
+            int AL[NG][3], AH[NG][3];  // low- and high-nibble sub-blocks, one product per step
             float Mac[NG];
 #pragma unroll
             for (int G = 0; G < NG; G++) {
-                Acc[G][0] = Acc[G][1] = Acc[G][2] = 0;
+                AL[G][0] = AL[G][1] = AL[G][2] = AH[G][0] = AH[G][1] = AH[G][2] = 0;
                 Mac[G] = 0.f;
             }
 #pragma unroll
@@ -1551,10 +1562,16 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
                     const i32x4 z = {0, 0, 0, 0};
                     const i32x4 Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, blo, z, 0, 0, 0);
                     const i32x4 Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bhi, z, 0, 0, 0);
-                    // |D| <= 32 * 15 * 127 < 2^16, sc < 64: the superblock sum
-                    // stays below 8 * 2 * 2^22 < 2^31 (exact)
+                    // |D| <= 32 * 15 * 128 < 2^16, sc < 64: the superblock sum
+                    // stays below 8 * 2^22 < 2^31 (exact)
 #pragma unroll
-                    for (int e = 0; e < 3; e++) Acc[G][e] = mad24(Dh[e], (int)sc1, mad24(Dl[e], (int)sc0, Acc[G][e]));
+                    for (int e = 0; e < 3; e++) {
+                        AL[G][e] = mad24(Dl[e], (int)sc0, AL[G][e]);
+                        AH[G][e] = mad24(Dh[e], (int)sc1, AH[G][e]);
+                        // keep each step one v_mad_i32_i24 (not re-associated
+                        // into multiplies and three-input adds)
+                        asm("" : "+v"(AL[G][e]), "+v"(AH[G][e]));
+                    }
                     const int cl = min(4 * G + kg, ncol - 1);
                     const float2 X = *(const float2*)&xsum[cl][b * 8 + 2 * g];
                     Mac[G] = fmaf(m1f, X.y, fmaf(m0f, X.x, Mac[G]));
@@ -1563,7 +1580,8 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
 #pragma unroll
             for (int G = 0; G < NG; G++) {
                 // q4_k_m.rs:144-214 per superblock: d * s * sum sc * (q . x~/s) - dmin * sum m * X
-                const float f = fmaf((float)Acc[G][2], kDig2, fmaf((float)Acc[G][1], kDig1, (float)Acc[G][0]));
+                const float f = fmaf((float)(AL[G][2] + AH[G][2]), kB256_2,
+                                     fmaf((float)(AL[G][1] + AH[G][1]), kB256_1, (float)(AL[G][0] + AH[G][0])));
                 part[G] += (d * s[G]) * f - dmin * Mac[G];
             }
         }
