@@ -105,10 +105,13 @@ __device__ __forceinline__ float group_sum(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 // Cross-lane moves without LDS: DPP within rows of 16 lanes and the gfx950
-// half/row swaps.
+// half/row swaps. CTRL is a full permutation (quad_perm, row_ror), so every
+// lane reads a valid source; bound_ctrl set lets the compiler fold the move
+// into the instruction that consumes it (v_add_f32_dpp and the like).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    static_assert((CTRL & ~0xFF) == 0 || (CTRL >= 0x121 && CTRL <= 0x12F), "quad_perm or row_ror only");
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 // (value of this lane, value of lane ^ 32) as (lower half's, upper half's)
 __device__ __forceinline__ void swap32(float v, float& lo, float& hi) {

@@ -1281,99 +1281,146 @@ __device__ __forceinline__ void digits4_b256(const float (&u)[4], float mul, uin
 }
 constexpr float kB256_1 = 1.0f / 256.0f, kB256_2 = 1.0f / 65536.0f;
 
-// One column staged by one wave for the batched kernel: base-256 digit
-// planes (digits4_b256 of Y = rint(x * 127 * 2^15 / max|x|), |Y| < 2^22, so
-// d0 lies in [-64, 64]), the fp32 sums of each 32-value sub-block, and the
-// returned digit scale s = 2 max|x| / 127 with x ~ s (d0 + d1/256 + d2/65536)
-// (NaN when x holds a NaN or an infinity, so the products come out NaN as in
-// fp32). Lane l owns the E consecutive activations at (l + 64 w) E,
-// w = 0..3. Under RMSNORM the digits are taken of u = x * norm_w: the norm's
-// 1 / rms cancels in u * 127 / max|u| and only scales s and the sub-block
-// sums. Each value costs one fma and one subtract, plus the permutes shared
-// by four values. Prologues NONE, RMSNORM and CONV.
-template <int PRO, int E, int PS>
-__device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
+// --------------------------------------- batched Q4_K GEMV on the matrix cores
+//
+// Several activation columns (the sequences of a batched decode step, the
+// input rows of a small matmul_rows batch) against Q4_K rows in their GGUF
+// layout: up to 8 columns at K = 2048, up to 4 at K = 8192 (blockIdx.y picks
+// a group of four columns where a launch holds more). A workgroup is eight
+// waves in R = 8 / DQ teams of DQ waves; a team owns 16 rows at a time
+// (EPI_SWIGLU: gate rows c..c+7 and up rows c..c+7) and its wave q the q-th
+// of DQ slices of their superblocks. Per 32-value sub-block and group G of
+// four columns, v_mfma_i32_16x16x32_i8 takes
+//   A  row i = 4c' + p: digit plane p of column 4G + c' (a zero plane for
+//      p = 3) at the sub-block's 32 k (lane l: row l % 16, k = 8 (l / 16) .. +8),
+//   B  the 4-bit codes of the 16 rows (lane l: row l % 16, the low or high
+//      nibbles of the 8 code bytes of k = 8 (l / 16) .. +8),
+// and lane l receives C[4 (l / 16) + p][l % 16] (p = 0..2): column
+// 4G + l / 16, row l % 16, plane p, the exact integer sums of code x digit.
+// The lane sums sc x C over the superblock's eight sub-blocks in int32 (one
+// 24-bit multiply-add a step) and the min terms m x X in f32, then takes one
+// float step per superblock: d s (A0 + A1/256 + A2/65536) - dmin sum m X
+// (q4_k_m.rs:144-214). The activations are base-256 digits of a 23-bit
+// rounding (ColStage) where the one-column kernels use base-254 digits of a
+// 24-bit one, so a batched column agrees with its one-column GEMV to within
+// both representations' bounds, not bit for bit. Waves 1.. of a team hand
+// their partial row sums to wave 0 through LDS. Digits sit in LDS (8 KB per
+// column at K = 2048: three planes and the zero plane, padded apart against
+// bank conflicts).
+
+constexpr int kColWaves = 8;              // waves of a batched-column workgroup
+constexpr int kColWG = 64 * kColWaves;
+
+// One wave's share of the activation staging: part h of P of column c, V =
+// K / P consecutive values, lane l holding values 4 (l + 64 i) .. +3 of the
+// part (i < V / 256), so every load is one coalesced 1 KB wave access.
+// issue() starts the loads; the kernel calls it before its weight prefetch
+// so that the in-order completion of loads does not queue the activations
+// behind the weights. part() applies the prologue and forms the part's
+// max |u|, the NaN flag and (RMSNORM) sum x^2; finish() takes the column's
+// totals and writes the digit planes (digits4_b256 of
+// Y = rint(u * 127 * 2^15 / max|u|), |Y| < 2^22, so d0 lies in [-64, 64])
+// and the fp32 sums of every 32-value sub-block, and returns the digit scale
+// s = 2 max|x| / 127 with x ~ s (d0 + d1/256 + d2/65536) (NaN when x holds a
+// NaN or an infinity, so the products come out NaN as in fp32). Under
+// RMSNORM the digits are taken of u = x * norm_w: the norm's 1 / rms cancels
+// in u * 127 / max|u| and only scales s and the sub-block sums. Prologues
+// NONE, RMSNORM and CONV (a.x = [B | C | X], ssm.rs:80-140; issue() loads B,
+// part() the rest; u = C * conv, the window written back by the column's
+// first workgroup).
+template <int PRO, int K, int P>
+struct ColStage {
     static_assert(PRO != mivi::PRO_SWIGLU, "no SwiGLU prologue here");
-    constexpr int K = E * kWG;
-    const int l = threadIdx.x & 63;
-    float v[4][E];
-    float ss = 0.f, m = 0.f, nn = 0.f;
+    static constexpr int V = K / P, NL = V / 256;
+    f32x4 u[NL];
+    f32x4 aux[PRO == mivi::PRO_RMSNORM ? NL : 1];
+    float t4[NL];  // sums of the lane's four values
+    float m = 0.f, ss = 0.f;
+
+    // u[i] holds chunk ch(i) = (i + blockIdx.x) mod NL of the part: the
+    // workgroups of an XCD start at different chunks, so their simultaneous
+    // first loads spread over the L2 channels instead of all asking one line
+    __device__ __forceinline__ int ch(int i) const { return (i + (int)blockIdx.x) & (NL - 1); }
+    __device__ __forceinline__ void issue(const mivi::GemvArgs& a, int h) {
+        static_assert((NL & (NL - 1)) == 0, "a power of two of chunks");
+        const int l = threadIdx.x & 63, o = h * V;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const int e0 = (l + 64 * w) * E;
-#pragma unroll
-        for (int i = 0; i < E / 4; i++) {
-            const f32x4 t = *(gf32x4*)(a.x + e0 + 4 * i);
-            v[w][4 * i] = t.x; v[w][4 * i + 1] = t.y; v[w][4 * i + 2] = t.z; v[w][4 * i + 3] = t.w;
-        }
+        for (int i = 0; i < NL; i++) u[i] = *(const gf32x4*)(a.x + o + 4 * (l + 64 * ch(i)));
         if constexpr (PRO == mivi::PRO_RMSNORM) {
 #pragma unroll
-            for (int i = 0; i < E / 4; i++) {
-                const f32x4 t = *(gf32x4*)(a.norm_w + e0 + 4 * i);
-                const float nw[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float& x = v[w][4 * i + e];
-                    ss = fmaf(x, x, ss);  // (non-finite x: ss, so s, NaN)
-                    x *= nw[e];
-                    m = fmaxf(m, fabsf(x));
-                }
-            }
-        } else if constexpr (PRO == mivi::PRO_CONV) {
-            // a.x = [B | C | X] (ssm.rs:80-140), as StageIn
+            for (int i = 0; i < NL; i++) aux[i] = *(const gf32x4*)(a.norm_w + o + 4 * (l + 64 * ch(i)));
+        }
+    }
+    __device__ __forceinline__ void part(const mivi::GemvArgs& a, int h) {
+        const int l = threadIdx.x & 63, o = h * V;
+        float nn = 0.f;  // NaN for a NaN value (fmaxf passes it over)
+        if constexpr (PRO == mivi::PRO_CONV) {
             const bool swap = a.phase && ((*a.phase) & 1);
             const float* st_in = swap ? a.st_out : a.st_in;
             float* st_out = swap ? (float*)a.st_in : a.st_out;
-            float cv[E], xv[E], st[E * kConvKs], cw[E * kConvKs];
 #pragma unroll
-            for (int i = 0; i < E / 4; i++) {
-                const f32x4 c4 = *(gf32x4*)(a.x + a.K + e0 + 4 * i), x4 = *(gf32x4*)(a.x + 2 * a.K + e0 + 4 * i);
-                cv[4 * i] = c4.x; cv[4 * i + 1] = c4.y; cv[4 * i + 2] = c4.z; cv[4 * i + 3] = c4.w;
-                xv[4 * i] = x4.x; xv[4 * i + 1] = x4.y; xv[4 * i + 2] = x4.z; xv[4 * i + 3] = x4.w;
+            for (int i = 0; i < NL; i++) {
+                const int d0 = o + 4 * (l + 64 * ch(i));  // channels d0 .. d0 + 3
+                float st[4 * kConvKs], cw[4 * kConvKs];
+#pragma unroll
+                for (int q = 0; q < kConvKs; q++) {
+                    const f32x4 s4 = *(const gf32x4*)(st_in + (size_t)d0 * kConvKs + 4 * q);
+                    st[4 * q] = s4.x; st[4 * q + 1] = s4.y; st[4 * q + 2] = s4.z; st[4 * q + 3] = s4.w;
+                    if (a.conv_mode == 0) {
+                        const f32x4 w4 = *(const gf32x4*)(a.conv_w + (size_t)d0 * kConvKs + 4 * q);
+                        cw[4 * q] = w4.x; cw[4 * q + 1] = w4.y; cw[4 * q + 2] = w4.z; cw[4 * q + 3] = w4.w;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            cw[4 * q + e] = a.conv_mode == 1 ? a.conv_w[(4 * q + e) % kConvKs] : 1.0f / (float)kConvKs;
+                    }
+                }
+                const f32x4 c4 = *(const gf32x4*)(a.x + a.K + d0), x4 = *(const gf32x4*)(a.x + 2 * a.K + d0);
+                const float b[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+                const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+                float y[4], nst[4 * kConvKs];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float bx = b[e] * xv[e];
+                    float conv = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < kConvKs; k++) {
+                        const int q = e * kConvKs + k;
+                        const float sv = k + 1 < kConvKs ? st[q + 1] : bx;
+                        conv += cw[q] * sv;
+                        nst[q] = sv;
+                    }
+                    y[e] = cv[e] * conv;
+                }
+                if (blockIdx.x == 0) {
+#pragma unroll
+                    for (int q = 0; q < kConvKs; q++)
+                        *(f32x4*)(st_out + (size_t)d0 * kConvKs + 4 * q) =
+                            f32x4{nst[4 * q], nst[4 * q + 1], nst[4 * q + 2], nst[4 * q + 3]};
+                }
+                u[i] = f32x4{y[0], y[1], y[2], y[3]};
             }
+        }
 #pragma unroll
-            for (int i = 0; i < E * kConvKs / 4; i++) {
-                const f32x4 s4 = *(gf32x4*)(st_in + e0 * kConvKs + 4 * i);
-                st[4 * i] = s4.x; st[4 * i + 1] = s4.y; st[4 * i + 2] = s4.z; st[4 * i + 3] = s4.w;
-                if (a.conv_mode == 0) {
-                    const f32x4 w4 = *(gf32x4*)(a.conv_w + e0 * kConvKs + 4 * i);
-                    cw[4 * i] = w4.x; cw[4 * i + 1] = w4.y; cw[4 * i + 2] = w4.z; cw[4 * i + 3] = w4.w;
+        for (int i = 0; i < NL; i++) {
+            float x[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+            if constexpr (PRO == mivi::PRO_RMSNORM) {
+                const float nw[4] = {aux[i].x, aux[i].y, aux[i].z, aux[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    ss = fmaf(x[e], x[e], ss);  // (non-finite x: ss, so s, NaN)
+                    x[e] *= nw[e];
                 }
             }
 #pragma unroll
-            for (int i = 0; i < E * kConvKs; i++)
-                if (a.conv_mode != 0) cw[i] = a.conv_mode == 1 ? a.conv_w[i % kConvKs] : 1.0f / (float)kConvKs;
-            float nst[E * kConvKs];
-#pragma unroll
-            for (int d = 0; d < E; d++) {
-                const float bx = v[w][d] * xv[d];
-                float conv = 0.0f;
-#pragma unroll
-                for (int k = 0; k < kConvKs; k++) {
-                    const int o = d * kConvKs + k;
-                    const float sv = k + 1 < kConvKs ? st[o + 1] : bx;
-                    conv += cw[o] * sv;
-                    nst[o] = sv;
-                }
-                v[w][d] = cv[d] * conv;
-            }
-            if (blockIdx.x == 0) {
-#pragma unroll
-                for (int i = 0; i < E * kConvKs / 4; i++)
-                    *(f32x4*)(st_out + e0 * kConvKs + 4 * i) = f32x4{nst[4 * i], nst[4 * i + 1], nst[4 * i + 2], nst[4 * i + 3]};
-            }
+            for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(x[e]));
+            t4[i] = ((x[0] + x[1]) + x[2]) + x[3];
+            if constexpr (PRO != mivi::PRO_RMSNORM) nn = fmaf(t4[i], 0.f, nn);  // a NaN (an infinity is in m)
+            u[i] = f32x4{x[0], x[1], x[2], x[3]};
         }
-        if constexpr (PRO != mivi::PRO_RMSNORM) {
-#pragma unroll
-            for (int i = 0; i < E; i++) {
-                m = fmaxf(m, fabsf(v[w][i]));
-                nn = fmaf(v[w][i], 0.f, nn);  // NaN for a non-finite v (fmaxf passes a NaN over)
-            }
-        }
-    }
-    m += nn;
-    if constexpr (PRO == mivi::PRO_RMSNORM) ss = xsum_all64(ss);
-    {
+        m += nn;
+        if constexpr (PRO == mivi::PRO_RMSNORM) ss = xsum_all64(ss);
         float lo, hi;
         swap32(m, lo, hi);
         m = nanmax(lo, hi);
@@ -1384,102 +1431,86 @@ __device__ __forceinline__ float stage_col_wave(const mivi::GemvArgs& a, uint32_
         m = nanmax(m, dpp_mov<0x4E>(m));
         m = nanmax(m, dpp_mov<0xB1>(m));
     }
-    // RMSNORM: x = u / rms (math.rs:7-22); else scale 1
-    const float scale = PRO == mivi::PRO_RMSNORM ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
-    const bool finite = m > 0.f && m <= 3.40282347e38f;
-    const float mul = finite ? 4161536.0f / m : 0.0f;  // 127 * 2^15 / max|u|
-    const float sc = PRO == mivi::PRO_RMSNORM ? ((m - m) + m * scale) * (2.0f / 127.0f) : ((m - m) + m) * (2.0f / 127.0f);
+    // mt, sst: the column's max |u| and sum x^2 over its P parts
+    template <int PS>
+    __device__ __forceinline__ float finish(const mivi::GemvArgs& a, int h, float mt, float sst, uint32_t* dig,
+                                            float* xsum) {
+        const int l = threadIdx.x & 63, o = h * V;
+        // RMSNORM: x = u / rms (math.rs:7-22); else scale 1
+        const float scale = PRO == mivi::PRO_RMSNORM ? 1.0f / sqrtf(sst / (float)K + a.eps) : 1.0f;
+        const bool finite = mt > 0.f && mt <= 3.40282347e38f;
+        const float mul = finite ? 4161536.0f / mt : 0.0f;  // 127 * 2^15 / max|u|
+        const float sc = ((mt - mt) + mt * scale) * (2.0f / 127.0f);
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const int e0 = (l + 64 * w) * E;
-#pragma unroll
-        for (int q = 0; q < E / 4; q++) {
+        for (int i = 0; i < NL; i++) {
+            const int w = (o >> 2) + l + 64 * ch(i);  // the dword of values 4w .. 4w + 3
+            const float x[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
             uint32_t w0, w1, w2;
-            const float u[4] = {v[w][4 * q], v[w][4 * q + 1], v[w][4 * q + 2], v[w][4 * q + 3]};
-            digits4_b256(u, mul, w0, w1, w2);
-            dig[e0 / 4 + q] = w0;
-            dig[PS + e0 / 4 + q] = w1;
-            dig[2 * PS + e0 / 4 + q] = w2;
+            digits4_b256(x, mul, w0, w1, w2);
+            dig[w] = w0;
+            dig[PS + w] = w1;
+            dig[2 * PS + w] = w2;
+            // sub-block sums: eight lanes, xor 1, 2, 4 (the writers, lanes
+            // with bit 2 clear, see their exact partners; row_ror:12 reads
+            // lane (i + 4) mod 16)
+            float t = t4[i];
+            t += dpp_mov<0xB1>(t);
+            t += dpp_mov<0x4E>(t);
+            t += dpp_mov<0x12C>(t);
+            if ((l & 7) == 0) xsum[w >> 3] = t * scale;
         }
-        // fp32 sums of each 32-value sub-block (32 / E lanes share one)
-#pragma unroll
-        for (int b = 0; b < (E >= 32 ? E / 32 : 1); b++) {
-            float t = 0.f;
-#pragma unroll
-            for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[w][b * 32 + i];
-            // xor 1, 2, 4 (the writers, lanes with bit 2 clear, see their
-            // exact partners; row_ror:12 reads lane (i + 4) mod 16)
-            if constexpr (E < 32) t += dpp_mov<0xB1>(t);
-            if constexpr (E < 16) t += dpp_mov<0x4E>(t);
-            if constexpr (E < 8) t += dpp_mov<0x12C>(t);
-            if (E >= 32 || (l % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t * scale;
-        }
+        return sc;
     }
-    return sc;
-}
+};
 
-// --------------------------------------- batched Q4_K GEMV on the matrix cores
-//
-// Several activation columns (the sequences of a batched decode step, the
-// input rows of a small matmul_rows batch) against Q4_K rows in their GGUF
-// layout: up to 8 columns at K = 2048, up to 4 at K = 8192. A workgroup owns
-// 16 rows at a time (EPI_SWIGLU: gate rows c..c+7 and up rows c..c+7), its
-// wave q the q-th quarter of their superblocks. Per 32-value sub-block and
-// group G of four columns, v_mfma_i32_16x16x32_i8 takes
-//   A  row i = 4c' + p: digit plane p of column 4G + c' (a zero plane for
-//      p = 3) at the sub-block's 32 k (lane l: row l % 16, k = 8 (l / 16) .. +8),
-//   B  the 4-bit codes of the 16 rows (lane l: row l % 16, the low or high
-//      nibbles of the 8 code bytes of k = 8 (l / 16) .. +8),
-// and lane l receives C[4 (l / 16) + p][l % 16] (p = 0..2): column
-// 4G + l / 16, row l % 16, plane p, the exact integer sums of code x digit.
-// The lane sums sc x C over the superblock's eight sub-blocks in int32 and
-// the min terms m x X in f32, then takes one float step per superblock:
-// d s (A0 + A1/254 + A2/254^2) - dmin sum m X (q4_k_m.rs:144-214). The
-// per-unit float steps of the one-column kernels are 2.2 times the VALU work
-// and this kernel is VALU-bound, so a batched column agrees with its
-// one-column GEMV to float rounding, not bit for bit (both within the digit
-// representation's bound). Waves 1-3 hand their partial row sums to wave 0
-// through LDS. Digits sit in LDS (8 KB per column at K = 2048: three planes
-// and the zero plane, padded apart against bank conflicts).
-// Columns [c0, c0 + 4) of a batched launch (blockIdx.y = column group of the
-// K = 8192 kernel, whose digits fit LDS for four columns only).
+// Columns [c0, c0 + 4) of a batched launch (blockIdx.y = column group).
 __device__ __forceinline__ mivi::GemvArgs gemv_col_group(const mivi::GemvArgs& a, int c0) {
     mivi::GemvArgs v = gemv_column(a, c0);
-    for (int i = 0; i < a.nseg; i++) v.seg[i].y = a.seg[i].y + c0 * a.ys;
+#pragma unroll
+    for (int i = 0; i < 3; i++)  // static indices: the arguments stay in registers
+        if (i < a.nseg) v.seg[i].y = a.seg[i].y + c0 * a.ys;
     v.ncol = min(4, a.ncol - c0);
     return v;
 }
 
-template <int PRO, int EPI, int KT, int NG>
-__global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
+template <int PRO, int EPI, int KT, int NG, int DQ>
+__global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
     static_assert(KT == 2048 || KT == 8192, "decode depths");
-    // K = 8192, or NG = 1 launched with several column groups: column group
-    // blockIdx.y, at most four columns
-    const mivi::GemvArgs a = (KT == 8192 || (NG == 1 && gridDim.y > 1)) ? gemv_col_group(a0, 4 * (int)blockIdx.y) : a0;
+    static_assert(DQ == 4 || DQ == 8, "depth slices per team");
+    // NG = 1 launched with several column groups: column group blockIdx.y,
+    // at most four columns
+    const mivi::GemvArgs a = (NG == 1 && gridDim.y > 1) ? gemv_col_group(a0, 4 * (int)blockIdx.y) : a0;
     constexpr int K = KT, nb = K / 256;
-    constexpr int SQ = nb / 4;               // superblocks per wave: 2 or 8
-    constexpr int PD = SQ < 4 ? SQ : 4;      // superblock chunks in flight per wave
+    constexpr int R = kColWaves / DQ;       // teams
+    constexpr int SQ = nb / DQ;             // superblocks per wave and group: 1, 2, 4 or 8
+    constexpr int PD = SQ < 4 ? SQ : 4;     // superblock chunks in flight per wave
     constexpr int NCM = 4 * NG;
-    constexpr int PS = K / 4 + 4;            // digit plane stride (dwords)
+    constexpr int P = kColWaves / NCM;      // staging parts per column (one per wave)
+    constexpr int PS = K / 4 + 4;           // digit plane stride (dwords)
     __shared__ __attribute__((aligned(16))) uint32_t dig[NCM][4 * PS];
     __shared__ __attribute__((aligned(16))) float xsum[NCM][K / 32];
     __shared__ float scol[NCM];
-    __shared__ float xq[2][3][NG][64];       // waves 1-3 -> wave 0, by group-step parity
+    __shared__ float red[2][NCM][P];        // parts' max |u| and sum x^2
+    __shared__ float xq[R][2][DQ - 1][NG][64];  // waves 1.. -> wave 0 of a team, by group-step parity
     const Segs sg(a, nb * 144);
     const int n = sg.n, n0 = a.seg[0].n;
-    const int ncol = a.ncol;  // 2..NCM, workgroup-uniform
+    const int ncol = a.ncol;  // 1..NCM, workgroup-uniform
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int team = wave / DQ, wq = wave % DQ;
     const int j = lane & 15, kg = lane >> 4;
     // EPI_CONV: a group holds channels 5g .. 5g+4, lane row j = 3i + k their
     // B, C, X rows (k = 0, 1, 2); lane row 15 repeats row 14 and is not stored
     static_assert(EPI != mivi::EPI_CONV || KT == 2048, "the conv epilogue is the K = 2048 in_proj");
     const int D3 = n0 / 3;
     const int ngroups = EPI == mivi::EPI_SWIGLU ? (n0 + 7) / 8 : EPI == mivi::EPI_CONV ? (D3 + 4) / 5 : (n + 15) / 16;
-    const int cnt = (int)blockIdx.x < ngroups ? (ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+    // group steps (workgroup-uniform): team t takes group
+    // blockIdx.x + (st R + t) gridDim.x in step st
+    const int stride = R * (int)gridDim.x;
+    const int cnt = (int)blockIdx.x < ngroups ? (ngroups - (int)blockIdx.x + stride - 1) / stride : 0;
 
     // row of lane row j in group step st (-1: none; loads then use row 0)
     auto row_of = [&](int st) {
-        const int grp = (int)blockIdx.x + st * (int)gridDim.x;
+        const int grp = (int)blockIdx.x + (st * R + team) * (int)gridDim.x;
         if constexpr (EPI == mivi::EPI_SWIGLU) {
             const int c = 8 * grp + (j & 7);
             return c < n0 ? c + (j >> 3) * n0 : -1;
@@ -1492,24 +1523,49 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
             return r < n ? r : -1;
         }
     };
+    // the activations first (see ColStage), then the weight ring
+    const int task_c = wave / P, task_h = wave % P;  // this wave's column and part
+    const bool stager = task_c < ncol;               // wave-uniform
+    ColStage<PRO, K, P> stg;
+    if (stager) stg.issue(gemv_column(a, task_c), task_h);
     // ring of superblock chunks: this wave's superblock bb of step st in slot bb % PD
     u32x4 hdr[PD];
     u32x2 cq[PD][4];
     auto load = [&](int slot, int st, int bb) {
         st = st < cnt ? st : cnt - 1;
         const int r = row_of(st < 0 ? 0 : st);
-        const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (wave * SQ + bb);
+        const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (wq * SQ + bb);
         hdr[slot] = ldg16(p);
 #pragma unroll
         for (int g = 0; g < 4; g++) cq[slot][g] = *(const __attribute__((address_space(1))) u32x2*)(p + 16 + 32 * g + 8 * kg);
     };
 #pragma unroll
     for (int q = 0; q < PD; q++) load(q, 0, q);
-    // the zero plane of every column; each wave stages columns wave, wave + 4
-    for (int i = threadIdx.x; i < NCM * PS; i += kWG) dig[i / PS][3 * PS + i % PS] = 0u;
-    for (int c = wave; c < ncol; c += 4) {
-        const float sc = stage_col_wave<PRO, K / kWG, PS>(gemv_column(a, c), dig[c], xsum[c]);
-        if (lane == 0) scol[c] = sc;
+    // the zero plane of every column
+#pragma unroll
+    for (int c = 0; c < NCM; c++)
+        for (int i = threadIdx.x; i < PS / 4; i += kColWG) *(u32x4*)&dig[c][3 * PS + 4 * i] = u32x4{0u, 0u, 0u, 0u};
+    if (stager) stg.part(gemv_column(a, task_c), task_h);
+    if constexpr (P > 1) {
+        if (stager && lane == 0) {
+            red[0][task_c][task_h] = stg.m;
+            red[1][task_c][task_h] = stg.ss;
+        }
+        __syncthreads();
+    }
+    if (stager) {
+        float mt = stg.m, sst = stg.ss;
+        if constexpr (P > 1) {
+            mt = red[0][task_c][0];
+            sst = red[1][task_c][0];
+#pragma unroll
+            for (int h = 1; h < P; h++) {
+                mt = nanmax(mt, red[0][task_c][h]);
+                sst += red[1][task_c][h];
+            }
+        }
+        const float sc = stg.template finish<PS>(gemv_column(a, task_c), task_h, mt, sst, dig[task_c], xsum[task_c]);
+        if (lane == 0 && task_h == 0) scol[task_c] = sc;
     }
     __syncthreads();
     if (cnt == 0) return;  // workgroup-uniform
@@ -1529,14 +1585,14 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
         for (int G = 0; G < NG; G++) part[G] = 0.f;
 #pragma unroll
         for (int bb = 0; bb < SQ; bb++) {
-            const int slot = bb % PD, b = wave * SQ + bb;
+            const int slot = bb % PD, b = wq * SQ + bb;
             const u32x4 h = hdr[slot];
             u32x2 q[4];
 #pragma unroll
             for (int g = 0; g < 4; g++) q[g] = cq[slot][g];
-            // refill with the chunk PD ahead (into the next group past the end)
+            // refill with the chunk PD ahead (of the next group, if any)
             if (bb + PD < SQ) load(slot, st, bb + PD);
-            else load(slot, st + 1, bb + PD - SQ);
+            else if (st + 1 < cnt) load(slot, st + 1, bb + PD - SQ);
             const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
             int AL[NG][3], AH[NG][3];  // low- and high-nibble sub-blocks, one product per step
             float Mac[NG];
@@ -1585,18 +1641,20 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
                 part[G] += (d * s[G]) * f - dmin * Mac[G];
             }
         }
-        // the four waves' quarters of the depth, summed by wave 0 (one LDS
-        // exchange; the buffer alternates with the group step's parity)
-        if (wave > 0) {
+        // the team's DQ slices of the depth, summed by its wave 0 in slice
+        // order (one LDS exchange; the buffer alternates with the step's parity)
+        if (wq > 0) {
 #pragma unroll
-            for (int G = 0; G < NG; G++) xq[st & 1][wave - 1][G][lane] = part[G];
+            for (int G = 0; G < NG; G++) xq[team][st & 1][wq - 1][G][lane] = part[G];
         }
         __syncthreads();
-        if (wave == 0) {
+        if (wq == 0) {
             const int r = row_of(st);
 #pragma unroll
             for (int G = 0; G < NG; G++) {
-                const float v = ((part[G] + xq[st & 1][0][G][lane]) + xq[st & 1][1][G][lane]) + xq[st & 1][2][G][lane];
+                float v = part[G];
+#pragma unroll
+                for (int i = 0; i < DQ - 1; i++) v += xq[team][st & 1][i][G][lane];
                 const int cc = 4 * G + kg;
                 if constexpr (EPI == mivi::EPI_SWIGLU) {
                     // lanes j < 8: gate c; lanes j + 8: up c (math.rs:87-95)
@@ -1616,6 +1674,24 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_cols_kernel(const mivi::GemvArgs
             }
         }
     }
+}
+
+// Launch of the batched kernel over ngr row groups and gy column groups:
+// two teams of four waves a workgroup (DQ = 4) where the groups fill 1.5
+// workgroups per CU at K = 2048, else one team of eight (DQ = 8); at most one
+// workgroup per CU, whose staging its waves then share.
+template <int PRO, int EPI, int KT, int NG>
+void launch_cols(const mivi::GemvArgs& a, int ngr, int gy, hipStream_t s) {
+    const int cus = mivi::num_cus();
+    if constexpr (KT == 2048) {
+        if (2 * ngr >= 3 * cus) {
+            const int gc = std::max(1, std::min((ngr + 1) / 2, cus));
+            hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 4>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+            return;
+        }
+    }
+    const int gc = std::max(1, std::min(ngr, cus));
+    hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8>), dim3(gc, gy), dim3(kColWG), 0, s, a);
 }
 
 // ------------------------------------------ Q6_K row quads on the matrix cores
@@ -2377,13 +2453,8 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                     return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no conv epilogue for this shape");
                 const int D3 = a.seg[0].n / 3;
                 if (a.ncol > 2) {
-                    const int gc = std::max(1, std::min((D3 + 4) / 5, mivi::num_cus() * 2));
-                    if (a.ncol > 4)
-                        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, mivi::EPI_CONV, 2048, 2>), dim3(gc), dim3(kWG),
-                                           0, s, a);
-                    else
-                        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, mivi::EPI_CONV, 2048, 1>), dim3(gc), dim3(kWG),
-                                           0, s, a);
+                    if (a.ncol > 4) launch_cols<PRO, mivi::EPI_CONV, 2048, 2>(a, (D3 + 4) / 5, 1, s);
+                    else launch_cols<PRO, mivi::EPI_CONV, 2048, 1>(a, (D3 + 4) / 5, 1, s);
                 } else {
                     // in_proj's own mapping (two rows per wave), the channels'
                     // three row steps a ring round of three
@@ -2448,32 +2519,28 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                 !env_int("MIVI_GEMV_COLS_SDOT", 0)) {
                 if (ep == mivi::EPI_SWIGLU && (a.nseg != 2 || a.seg[1].n != a.seg[0].n))
                     return mivi::set_error(MIVI_ERR_INVALID_ARGUMENT, "SwiGLU epilogue needs gate|up of equal rows");
-                // one workgroup per 16-row group, at most 2 per CU (1 at K = 8192: LDS)
+                // 16-row groups (8 gate|up channel pairs)
                 const int ngr = ep == mivi::EPI_SWIGLU ? (a.seg[0].n + 7) / 8 : (n + 15) / 16;
-                const int gc = std::max(1, std::min(ngr, mivi::num_cus() * (K == 8192 ? 1 : 2)));
-#define LC(EPI, KT, NG)                                                                                      \
-    hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG>), dim3(gc, KT == 8192 ? (a.ncol + 3) / 4 : 1),   \
-                       dim3(kWG), 0, s, a)
+                const int gy = (a.ncol + 3) / 4;
                 if constexpr (PRO == mivi::PRO_SWIGLU) {
                 } else if (K == 8192) {
-                    if constexpr (PRO == mivi::PRO_NONE) LC(mivi::EPI_STORE, 8192, 1);
+                    if constexpr (PRO == mivi::PRO_NONE) launch_cols<PRO, mivi::EPI_STORE, 8192, 1>(a, ngr, gy, s);
                 } else if (ep == mivi::EPI_SWIGLU) {
-                    if (a.ncol > 4) LC(mivi::EPI_SWIGLU, 2048, 2); else LC(mivi::EPI_SWIGLU, 2048, 1);
-                } else {
-                    if (a.ncol > 4 && PRO == mivi::PRO_CONV && ngr < mivi::num_cus()) {
-                        // the ShortConv out_proj (2048 rows: 128 row groups): the
-                        // two groups of four columns side by side on all CUs
-                        // (25.7 -> 23.9 µs at 8 columns; not for the other
-                        // projections, whose staging then doubles for nothing)
-                        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, mivi::EPI_STORE, 2048, 1>),
-                                           dim3(gc, (a.ncol + 3) / 4), dim3(kWG), 0, s, a);
-                    } else if (a.ncol > 4) {
-                        LC(mivi::EPI_STORE, 2048, 2);
+                    if (a.ncol > 4 && PRO != mivi::PRO_CONV) {
+                        if constexpr (PRO != mivi::PRO_CONV) launch_cols<PRO, mivi::EPI_SWIGLU, 2048, 2>(a, ngr, 1, s);
                     } else {
-                        LC(mivi::EPI_STORE, 2048, 1);
+                        launch_cols<PRO, mivi::EPI_SWIGLU, 2048, 1>(a, ngr, gy, s);
                     }
+                } else if (a.ncol > 4 && (ngr < mivi::num_cus() || PRO == mivi::PRO_CONV)) {
+                    // fewer row groups than CUs (the 2048-row projections), or
+                    // the conv prologue (whose eight columns at once would not
+                    // fit the registers): the two groups of four columns side by side
+                    launch_cols<PRO, mivi::EPI_STORE, 2048, 1>(a, ngr, gy, s);
+                } else if (a.ncol > 4) {
+                    if constexpr (PRO != mivi::PRO_CONV) launch_cols<PRO, mivi::EPI_STORE, 2048, 2>(a, ngr, 1, s);
+                } else {
+                    launch_cols<PRO, mivi::EPI_STORE, 2048, 1>(a, ngr, 1, s);
                 }
-#undef LC
                 MIVI_HIP_CHECK(hipGetLastError());
                 return MIVI_OK;
             }
