@@ -617,8 +617,9 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
 // ------------------------------------------- Q8_0 attention on the matrix cores
 //
 // Q8_0 caches (q8g_* group layout) with head_dim 64 and at most 4 query heads
-// per kv head. One wave per (kv head, split), a workgroup = 4 kv heads of one
-// split (placed as attn_tile_of places its workgroups). Each wave walks its
+// per kv head. One wave per (kv head, split), a workgroup = W kv heads of one
+// split (all of them for 8 kv heads, so it reads whole cache rows; placed as
+// attn_tile_of places its workgroups). Each wave walks its
 // split's 16-token groups (1088 contiguous bytes of K and of V each, one
 // 16-byte load per lane) with an online softmax of its own; no workgroup
 // barriers.
@@ -686,15 +687,15 @@ __device__ __forceinline__ void rows_all(float x, float& r0, float& r1, float& r
     r1 = __uint_as_float(o[0]); r3 = __uint_as_float(o[1]);
 }
 
-template <int PD>  // groups in flight per wave
-__global__ void __launch_bounds__(kWG, 4) attn_q8_mfma_kernel(AttnArgs a) {
+template <int PD, int W>  // groups in flight per wave; waves (kv heads) per workgroup
+__global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
     constexpr int HD = 64, G = kQ8GroupTokens;
-    __shared__ __attribute__((aligned(16))) float qs[4][4][HD];   // [wave][head][dim]
-    __shared__ __attribute__((aligned(16))) float cur[4][2][HD];  // owner: current K/V as stored
+    __shared__ __attribute__((aligned(16))) float qs[W][4][HD];   // [wave][head][dim]
+    __shared__ __attribute__((aligned(16))) float cur[W][2][HD];  // owner: current K/V as stored
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     int kvg, split;
-    if (!attn_tile_of((a.n_kv_heads + 3) >> 2, a.nsplit, &kvg, &split)) return;  // workgroup-uniform
-    const int kvh = kvg * 4 + wave;
+    if (!attn_tile_of((a.n_kv_heads + W - 1) / W, a.nsplit, &kvg, &split)) return;  // workgroup-uniform
+    const int kvh = kvg * W + wave;
     if (kvh >= a.n_kv_heads) return;  // wave-uniform (no workgroup barrier below)
     {
         const int b = blockIdx.y;
@@ -731,10 +732,11 @@ __global__ void __launch_bounds__(kWG, 4) attn_q8_mfma_kernel(AttnArgs a) {
         g = min(g, g1 - 1);
         const uint8_t* kg = kc + (size_t)g * gstride;
         const uint8_t* vg = vc + (size_t)g * gstride;
-        q.k = *(gau32x4*)(kg + o_kv);
-        q.dk = *(gau32*)(kg + o_dk);
-        q.v = *(gau32x4*)(vg + o_kv);
-        q.dv = *(gau16*)(vg + o_dv);
+        // streamed once per step: non-temporal loads
+        q.k = __builtin_nontemporal_load((gau32x4*)(kg + o_kv));
+        q.dk = __builtin_nontemporal_load((gau32*)(kg + o_dk));
+        q.v = __builtin_nontemporal_load((gau32x4*)(vg + o_kv));
+        q.dv = __builtin_nontemporal_load((gau16*)(vg + o_dv));
     };
     Q8Group ring[PD];
 #pragma unroll
@@ -1090,13 +1092,19 @@ struct Ctrl {  // device control block
 
 }  // namespace
 
+// Waves (kv heads) per workgroup of the Q8_0 group kernel: every kv head of
+// a split in one workgroup (8 for the 1.2B model), so a workgroup reads whole
+// cache rows (all kv heads of 16 tokens, contiguous).
+inline int attn_q8_waves(int n_kv) { return n_kv > 4 ? 8 : 4; }
+
 // Splits per sequence of the Q8_0 group kernel for a batch of nb sequences:
-// about two workgroups (of four kv heads) per CU in all, at most `cap`.
-// Fewer, longer splits keep each wave streaming: at 8 sequences 32 splits
-// beat 64 (4067 against 3820 tok/s), while 16 and 8 leave CUs idle.
+// about eight waves per CU in all, at most `cap`. Fewer, longer splits keep
+// each wave streaming: for config 5 (8 sequences) 8 waves per CU give 7131
+// tok/s against 6607 at 16 and 6353 at 4.
 int attn_q8_splits(int cap, int nb, int n_kv) {
-    const int groups = std::max(1, nb * ((n_kv + 3) / 4));
-    return std::max(1, std::min(cap, 2 * num_cus() / groups));
+    const int w = attn_q8_waves(n_kv);
+    const int waves = std::max(1, nb * w * ((n_kv + w - 1) / w));
+    return std::max(1, std::min(cap, 8 * num_cus() / waves));
 }
 
 // Attention of nseq sequences (tile rows) over their caches, then the merge of
@@ -1105,8 +1113,12 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
                        hipStream_t s) {
     int tt;
     if (a.packed) {  // Q8_0 group layout (attn_q8_mfma_ok shapes)
-        dim3 grid(attn_tile_grid(((int)c.n_kv_heads + 3) / 4, a.nsplit), nseq);
-        hipLaunchKernelGGL(attn_q8_mfma_kernel<3>, grid, dim3(kWG), 0, s, a);
+        // three groups in flight per wave: other depths measured slower
+        // (config 5: 6583 tok/s at 2, 7095 at 3, 6645 at 4, 6356 at 6)
+        const int w = attn_q8_waves((int)c.n_kv_heads);
+        dim3 grid(attn_tile_grid(((int)c.n_kv_heads + w - 1) / w, a.nsplit), nseq);
+        if (w == 8) hipLaunchKernelGGL((attn_q8_mfma_kernel<3, 8>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((attn_q8_mfma_kernel<3, 4>), grid, dim3(kWG), 0, s, a);
         tt = kQ8GroupTokens;
     } else {
         dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
