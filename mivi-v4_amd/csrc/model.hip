@@ -920,6 +920,11 @@ __global__ void iota_kernel(int* dst, int base, int n) {
 // reciprocal multiply of transformer.rs:293-298.
 // blockIdx.y: sequence of a batched launch (partials + b * part_s (m, l) and
 // + b * part_s * hd (acc), out + b * out_s, position posp[b]).
+// The position and every partial the launch needs (up to kCombineRegs
+// splits per thread) are loaded at once, before nv is known (entries of
+// splits past nv are masked, never multiplied), so the kernel waits for
+// memory once; splits beyond that take a loop.
+constexpr int kCombineRegs = 16;
 __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, const float* part_l,
                                                            const float* part_acc, float* out, const int* posp,
                                                            int nsplit, int tt, int hd, int64_t part_s,
@@ -930,20 +935,37 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
     const int h = blockIdx.x, b = blockIdx.y;
     part_m += b * part_s; part_l += b * part_s; part_acc += b * part_s * hd;
     out += b * out_s;
-    posp += b;
-    const int ntiles = (*posp + 1 + tt - 1) / tt;
-    const int tps = (ntiles + nsplit - 1) / nsplit;
-    const int nv = (ntiles + tps - 1) / tps;  // splits that hold tiles
     const float* pm = part_m + (size_t)h * nsplit;
     const float* pl = part_l + (size_t)h * nsplit;
-    float M = -INFINITY;
-    for (int s = threadIdx.x; s < nv; s += kWG) M = fmaxf(M, pm[s]);
+    // thread (g, d): dims d < hd, splits s = g, g + G, ...
+    const int hdp = hd <= 64 ? 64 : 128, G = kWG / hdp;
+    const int d = threadIdx.x % hdp, g = threadIdx.x / hdp;
+    const float* acc = part_acc + (size_t)h * nsplit * hd + d;
+    const int pos = posp[b];
+    const bool own = (int)threadIdx.x < nsplit;
+    const float m0 = own ? pm[threadIdx.x] : -INFINITY, l0 = own ? pl[threadIdx.x] : 0.f;
+    float av[kCombineRegs];
+#pragma unroll
+    for (int k = 0; k < kCombineRegs; k++) {
+        const int sk = g + k * G;
+        av[k] = (d < hd && sk < nsplit) ? acc[(size_t)sk * hd] : 0.f;
+    }
+    const int ntiles = (pos + 1 + tt - 1) / tt;
+    const int tps = (ntiles + nsplit - 1) / nsplit;
+    const int nv = (ntiles + tps - 1) / tps;  // splits that hold tiles
+    float M = (int)threadIdx.x < nv ? m0 : -INFINITY;
+    for (int s = threadIdx.x + kWG; s < nv; s += kWG) M = fmaxf(M, pm[s]);
     M = wave_max(M);
     if ((threadIdx.x & 63) == 0) red[0][threadIdx.x >> 6] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     float L = 0.f;
-    for (int s = threadIdx.x; s < nv; s += kWG) {
+    if ((int)threadIdx.x < nv) {
+        const float ws = expf(m0 - M);
+        w[threadIdx.x] = ws;
+        L = l0 * ws;
+    }
+    for (int s = threadIdx.x + kWG; s < nv; s += kWG) {
         const float ws = expf(pm[s] - M);
         w[s] = ws;
         L = fmaf(pl[s], ws, L);
@@ -952,22 +974,12 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
     if ((threadIdx.x & 63) == 0) red[1][threadIdx.x >> 6] = L;
     __syncthreads();
     L = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-    // thread (g, d): dims d < hd, splits s = g, g + G, ...
-    const int hdp = hd <= 64 ? 64 : 128, G = kWG / hdp;
-    const int d = threadIdx.x % hdp, g = threadIdx.x / hdp;
     float o = 0.f;
     if (d < hd) {
-        const float* acc = part_acc + (size_t)h * nsplit * hd + d;
-        int s = g;
-        for (; s + 3 * G < nv; s += 4 * G) {
-            const float a0 = acc[(size_t)s * hd], a1 = acc[(size_t)(s + G) * hd];
-            const float a2 = acc[(size_t)(s + 2 * G) * hd], a3 = acc[(size_t)(s + 3 * G) * hd];
-            o = fmaf(a0, w[s], o);
-            o = fmaf(a1, w[s + G], o);
-            o = fmaf(a2, w[s + 2 * G], o);
-            o = fmaf(a3, w[s + 3 * G], o);
-        }
-        for (; s < nv; s += G) o = fmaf(acc[(size_t)s * hd], w[s], o);
+#pragma unroll
+        for (int k = 0; k < kCombineRegs; k++)
+            if (g + k * G < nv) o = fmaf(av[k], w[g + k * G], o);
+        for (int s = g + kCombineRegs * G; s < nv; s += G) o = fmaf(acc[(size_t)s * hd], w[s], o);
     }
     part[threadIdx.x] = o;
     __syncthreads();
