@@ -548,48 +548,41 @@ typedef uint32_t u32x2_a1 __attribute__((ext_vector_type(2), aligned(1)));
 // ------------------------------------------------ activations as int8 digits
 //
 // The tiled kernels multiply the weight codes by x in integer arithmetic.
-// x is represented against one scale per launch, s = max|x| / 127, as
-//     x ~= s * (d0 + d1 / 254 + d2 / 254^2),   d0, d1, d2 in [-127, 127],
-// with |x - x~| < 2.5e-7 * max|x|. A row's dot product is then
-//     s * sum_d 254^-d * sum_i w_i d_i,
+// x is represented against one scale per launch, s = 2 max|x| / 127, as
+//     x ~= s * (d0 + d1 / 256 + d2 / 256^2),   d0 in [-64, 64], d1, d2 in [-128, 127],
+// the balanced base-256 digits of Y = rint(x * 127 * 2^15 / max|x|)
+// (|Y| <= 127 * 2^15 < 2^22), so |x - x~| <= 1.2e-7 * max|x|. A row's dot
+// product is then
+//     s * sum_d 256^-d * sum_i w_i d_i,
 // where every sum of code * digit is exact in int32 (v_dot4_i32_i8) and the
 // per-sub-block scales are applied with exact 24-bit integer multiplies.
 // The error of the whole dot is below 2.5e-7 * ||w||_1 * max|x|, i.e.
 // 2.5e-7 * sqrt(K) * ||w|| * ||x|| (2.3e-5 of ||w|| ||x|| at K = 8192).
-constexpr float kDig1 = 1.0f / 254.0f, kDig2 = 1.0f / 64516.0f;
+constexpr float kDig1 = 1.0f / 256.0f, kDig2 = 1.0f / 65536.0f;
+constexpr float kDigMul = 4161536.0f;  // 127 * 2^15: Y = rint(x * kDigMul / max|x|)
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
 
-// The three digit planes of four scaled activations y (|y| <= 127.5):
-// d0 = rint(y), d1 = rint((y - d0) 254), d2 = rint((t1 - d1) 254) as signed
-// bytes, value e in byte e of w0, w1, w2. Adding 1.5 * 2^23 rounds to the
-// nearest integer with ties to even (as rintf) and leaves the integer's
-// two's complement in the low mantissa bits, so its low byte is the digit;
-// subtracting it again gives the rounded value exactly. (Non-finite inputs
-// give a NaN digit scale, so their digits never matter.)
-__device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);  // a.byte0, b.byte0 in bytes 0, 1
-    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000c0cu);  // c.byte0, d.byte0 in bytes 2, 3
-    return ab | cd;
-}
-__device__ __forceinline__ void digits4(const float (&y)[4], uint32_t& w0, uint32_t& w1, uint32_t& w2) {
-    constexpr float kRound = 12582912.0f;  // 1.5 * 2^23
-    uint32_t b0[4], b1[4], b2[4];
+// The digit planes of four values: Y = rint(u * mul) for |Y| < 2^22 (adding
+// 1.5 * 2^23 in the fma rounds once, ties to even, and leaves Y in the low
+// mantissa bits), written as balanced base-256 digits
+// Y = 65536 d0 + 256 d1 + d2 with d1, d2 in [-128, 127]: the bytes of
+// Y + 0x808080 are d + 128, so a byte permute gathers each plane and an xor
+// with 0x80 per byte makes the digits signed. Value e in byte e of w0 (d0),
+// w1 (d1) and w2 (d2). (Non-finite inputs give a NaN digit scale, so their
+// digits never matter.)
+__device__ __forceinline__ void digits4_b256(const float (&u)[4], float mul, uint32_t& w0, uint32_t& w1,
+                                             uint32_t& w2) {
+    uint32_t z[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float r0 = y[e] + kRound;
-        const float t1 = (y[e] - (r0 - kRound)) * 254.0f;
-        const float r1 = t1 + kRound;
-        const float r2 = (t1 - (r1 - kRound)) * 254.0f + kRound;
-        b0[e] = __float_as_uint(r0);
-        b1[e] = __float_as_uint(r1);
-        b2[e] = __float_as_uint(r2);
-    }
-    w0 = low_bytes4(b0[0], b0[1], b0[2], b0[3]);
-    w1 = low_bytes4(b1[0], b1[1], b1[2], b1[3]);
-    w2 = low_bytes4(b2[0], b2[1], b2[2], b2[3]);
+    for (int e = 0; e < 4; e++) z[e] = __float_as_uint(fmaf(u[e], mul, 12582912.0f)) - 0x4ABF7F80u;  // - bits(1.5*2^23) + 0x808080
+    const uint32_t lo01 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.b0 z1.b0 z0.b1 z1.b1
+    const uint32_t lo23 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);  // z2.b0 z3.b0 z2.b1 z3.b1
+    w2 = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+    w1 = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+    w0 = (__builtin_amdgcn_perm(z[1], z[0], 0x0c0c0602u) | __builtin_amdgcn_perm(z[3], z[2], 0x06020c0cu)) ^ 0x80808080u;
 }
 
 // Digit planes of the K floats staged at xs, written to dig[d * K / 4 + i]
@@ -607,13 +600,13 @@ __device__ __forceinline__ float stage_digits(const float* xs, uint32_t* dig, in
 #pragma unroll
     for (int i = 1; i < kWG / 64; i++) m = nanmax(m, red[i]);
     const bool finite = m > 0.f && m <= 3.40282347e38f;
-    const float inv = finite ? 127.0f / m : 0.0f;
-    const float sc = (m - m) + m / 127.0f;
+    const float mul = finite ? kDigMul / m : 0.0f;
+    const float sc = ((m - m) + m) * (2.0f / 127.0f);
     for (int i = threadIdx.x; i < K / 4; i += kWG) {
         const f32x4 v = *(const f32x4*)(xs + 4 * i);
         uint32_t w0, w1, w2;
-        const float y[4] = {v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv};
-        digits4(y, w0, w1, w2);
+        const float u[4] = {v[0], v[1], v[2], v[3]};
+        digits4_b256(u, mul, w0, w1, w2);
         dig[i] = w0;
         dig[K / 4 + i] = w1;
         dig[K / 2 + i] = w2;
@@ -634,7 +627,7 @@ __device__ __forceinline__ int mad24(int a, int b, int c) { return (int)__builti
 // One Q6_K unit (16 values of each of the sub-blocks l, l+32, l+64, l+96 of
 // half h, q6_k.rs:68-111): sum over the unit of sc * (q - 32) * digits, per
 // digit plane, in int32; off[k][d] = -32 * sum of the 16 digits of quad k.
-// Returns d * (A0 + A1/254 + A2/254^2) in units of s.
+// Returns d * (A0 + A1/256 + A2/256^2) in units of s.
 __device__ __forceinline__ float q6k_unit_i8(u32x4 ql0, u32x4 ql1, u32x4 qh, u32x2 scw, uint32_t dbits,
                                              const uint32_t (&xd)[3][16], const int (&off)[4][3]) {
     const uint32_t L0[4] = {ql0.x, ql0.y, ql0.z, ql0.w};
@@ -673,7 +666,7 @@ __device__ __forceinline__ float q6k_unit_i8(u32x4 ql0, u32x4 ql1, u32x4 qh, u32
 }
 
 // One Q4_K unit (sub-blocks 2g and 2g+1, q4_k_m.rs:144-214):
-// d * s * sum_d 254^-d (sc0 * sum(q xd) + sc1 * ...) - dmin * (m0 X0 + m1 X1),
+// d * s * sum_d 256^-d (sc0 * sum(q xd) + sc1 * ...) - dmin * (m0 X0 + m1 X1),
 // X0, X1 the fp32 sums of x over the two sub-blocks.
 __device__ __forceinline__ float q4k_unit_i8(u32x4 hdr, u32x4 qa, u32x4 qb, int g, const uint32_t (&xd)[3][16],
                                              float s, float X0, float X1) {
@@ -859,21 +852,24 @@ struct StageIn {
             m = nanmax(m, red[1][i]);
             ss += red[0][i];
         }
+        // RMSNORM: x = (v w) / rms (math.rs:7-22); the digits are those of
+        // u = v w, since 1 / rms cancels in u * kDigMul / max|u|, and the
+        // scale goes into s and the sub-block sums
+        float scale = 1.0f;
         if constexpr (PRO == mivi::PRO_RMSNORM) {
-            const float scale = 1.0f / sqrtf(ss / (float)K + a.eps);  // math.rs:7-22
+            scale = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
-            for (int i = 0; i < E; i++) v[i] = v[i] * scale * y[i / 4][i % 4];
-            m *= scale;
+            for (int i = 0; i < E; i++) v[i] = v[i] * y[i / 4][i % 4];
         }
         // digits (see the representation above)
         const bool finite = m > 0.f && m <= 3.40282347e38f;
-        const float inv = finite ? 127.0f / m : 0.0f;
-        const float sc = (m - m) + m / 127.0f;
+        const float mul = finite ? kDigMul / m : 0.0f;
+        const float sc = ((m - m) + m * scale) * (2.0f / 127.0f);
         uint32_t w0[E / 4], w1[E / 4], w2[E / 4];
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
-            const float y[4] = {v[4 * q] * inv, v[4 * q + 1] * inv, v[4 * q + 2] * inv, v[4 * q + 3] * inv};
-            digits4(y, w0[q], w1[q], w2[q]);
+            const float u[4] = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            digits4_b256(u, mul, w0[q], w1[q], w2[q]);
         }
         const int P = PS ? PS : K / 4;
 #pragma unroll
@@ -895,7 +891,7 @@ struct StageIn {
                 if constexpr (E < 16) t += dpp_mov<0x4E>(t);
                 if constexpr (E < 8) t += dpp_mov<0x12C>(t);
                 static_assert(E >= 4, "at least four activations per thread");
-                if (E >= 32 || (threadIdx.x % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t;
+                if (E >= 32 || (threadIdx.x % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t * scale;
             }
         }
         __syncthreads();
@@ -1261,25 +1257,6 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
-// Base-256 digit planes of four values: Y = rint(u * mul) for |Y| < 2^22
-// (adding 1.5 * 2^23 in the fma rounds once, ties to even, and leaves Y in
-// the low mantissa bits), written as balanced base-256 digits
-// Y = 65536 d0 + 256 d1 + d2 with d1, d2 in [-128, 127]: the bytes of
-// Y + 0x808080 are d + 128, so a byte permute gathers each plane and an xor
-// with 0x80 per byte makes the digits signed. Value e in byte e of w0 (d0),
-// w1 (d1) and w2 (d2).
-__device__ __forceinline__ void digits4_b256(const float (&u)[4], float mul, uint32_t& w0, uint32_t& w1,
-                                             uint32_t& w2) {
-    uint32_t z[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) z[e] = __float_as_uint(fmaf(u[e], mul, 12582912.0f)) - 0x4ABF7F80u;  // - bits(1.5*2^23) + 0x808080
-    const uint32_t lo01 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.b0 z1.b0 z0.b1 z1.b1
-    const uint32_t lo23 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);  // z2.b0 z3.b0 z2.b1 z3.b1
-    w2 = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
-    w1 = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
-    w0 = (__builtin_amdgcn_perm(z[1], z[0], 0x0c0c0602u) | __builtin_amdgcn_perm(z[3], z[2], 0x06020c0cu)) ^ 0x80808080u;
-}
-constexpr float kB256_1 = 1.0f / 256.0f, kB256_2 = 1.0f / 65536.0f;
 
 // --------------------------------------- batched Q4_K GEMV on the matrix cores
 //
@@ -1300,10 +1277,10 @@ constexpr float kB256_1 = 1.0f / 256.0f, kB256_2 = 1.0f / 65536.0f;
 // The lane sums sc x C over the superblock's eight sub-blocks in int32 (one
 // 24-bit multiply-add a step) and the min terms m x X in f32, then takes one
 // float step per superblock: d s (A0 + A1/256 + A2/65536) - dmin sum m X
-// (q4_k_m.rs:144-214). The activations are base-256 digits of a 23-bit
-// rounding (ColStage) where the one-column kernels use base-254 digits of a
-// 24-bit one, so a batched column agrees with its one-column GEMV to within
-// both representations' bounds, not bit for bit. Waves 1.. of a team hand
+// (q4_k_m.rs:144-214). The digits are those of the one-column kernels
+// (ColStage), but the one-column kernels take a float step per 64-value unit,
+// so a batched column agrees with its one-column GEMV to float rounding, not
+// bit for bit. Waves 1.. of a team hand
 // their partial row sums to wave 0 through LDS. Digits sit in LDS (8 KB per
 // column at K = 2048: three planes and the zero plane, padded apart against
 // bank conflicts).
@@ -1439,7 +1416,7 @@ struct ColStage {
         // RMSNORM: x = u / rms (math.rs:7-22); else scale 1
         const float scale = PRO == mivi::PRO_RMSNORM ? 1.0f / sqrtf(sst / (float)K + a.eps) : 1.0f;
         const bool finite = mt > 0.f && mt <= 3.40282347e38f;
-        const float mul = finite ? 4161536.0f / mt : 0.0f;  // 127 * 2^15 / max|u|
+        const float mul = finite ? kDigMul / mt : 0.0f;
         const float sc = ((mt - mt) + mt * scale) * (2.0f / 127.0f);
 #pragma unroll
         for (int i = 0; i < NL; i++) {
@@ -1636,8 +1613,8 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
 #pragma unroll
             for (int G = 0; G < NG; G++) {
                 // q4_k_m.rs:144-214 per superblock: d * s * sum sc * (q . x~/s) - dmin * sum m * X
-                const float f = fmaf((float)(AL[G][2] + AH[G][2]), kB256_2,
-                                     fmaf((float)(AL[G][1] + AH[G][1]), kB256_1, (float)(AL[G][0] + AH[G][0])));
+                const float f = fmaf((float)(AL[G][2] + AH[G][2]), kDig2,
+                                     fmaf((float)(AL[G][1] + AH[G][1]), kDig1, (float)(AL[G][0] + AH[G][0])));
                 part[G] += (d * s[G]) * f - dmin * Mac[G];
             }
         }

@@ -290,10 +290,10 @@ def test_batched_gemv_columns_match_matvec(hip, oracle, torch_mod, t, batch, row
     # int8 matrix cores; one launch per input at other depths): every input's
     # row of outputs equals its own matvec (lib.rs:404-457) bit for bit, except
     # on the Q4_K matrix-core kernel (3+ columns at d = 2048, any batch at
-    # d = 8192), whose activation digits are base-256 planes of a 23-bit
-    # rounding (the matvecs' are base-254 planes of a 24-bit one) and which
-    # sums each superblock in int32 before its float steps: it agrees to
-    # 1e-5 ||w_row|| ||x||, a tenth of the bar; all meet the oracle bound
+    # d = 8192), which takes the matvecs' activation digits but sums each
+    # superblock in int32 before its float steps (the matvecs take a float
+    # step per 64-value unit): it agrees to 1e-5 ||w_row|| ||x||, a tenth of
+    # the bar; all meet the oracle bound
     torch = torch_mod
     w = hip.synth_random_weights(t, 70 + batch, rows, cols, 0.02)
     X = np.stack([hip.synth_normal(80 + b, cols) for b in range(batch)])
