@@ -712,9 +712,10 @@ struct StageIn {
     f32x4 cw[kConv ? E * kConvKs / 4 : 1];    // CONV: per-channel weights (mode 0)
 
     // NONE / RMSNORM / SWIGLU: chunk i of this thread is the 16 bytes at
-    // 16 (threadIdx.x + kWG i), so each wave load reads 1 KB contiguous;
-    // finish() hands the values to their owners (E consecutive per thread)
-    // through LDS. CONV: the thread's own E values directly.
+    // 16 (threadIdx.x + kWG i), so each wave load reads 1 KB contiguous, and
+    // the thread keeps them (digit dword threadIdx.x + kWG i, a 32-value
+    // sub-block over eight consecutive threads). CONV: the thread's own E
+    // consecutive values (its channels' windows are contiguous).
     __device__ __forceinline__ void load(const mivi::GemvArgs& a) {
         const int e0 = threadIdx.x * E;
         if constexpr (!kConv) {
@@ -755,22 +756,8 @@ struct StageIn {
     __device__ __forceinline__ float finish(const mivi::GemvArgs& a, uint32_t* dig, float* xsum) {
         __shared__ float red[2][kWG / 64];
         const int K = a.K, e0 = threadIdx.x * E;
-        if constexpr (!kConv) {
-            // the loaded chunks to their owners
-            constexpr bool two = PRO == mivi::PRO_RMSNORM || PRO == mivi::PRO_SWIGLU;
-            __shared__ __attribute__((aligned(16))) float tx[two ? 2 : 1][E * kWG];
-#pragma unroll
-            for (int i = 0; i < E / 4; i++) {
-                *(f32x4*)&tx[0][4 * (threadIdx.x + kWG * i)] = x[i];
-                if constexpr (two) *(f32x4*)&tx[two ? 1 : 0][4 * (threadIdx.x + kWG * i)] = y[i];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < E / 4; i++) {
-                x[i] = *(const f32x4*)&tx[0][e0 + 4 * i];
-                if constexpr (two) y[i] = *(const f32x4*)&tx[two ? 1 : 0][e0 + 4 * i];
-            }
-        }
+        // dword of values 4q .. 4q+3 of this thread
+        auto dw = [&](int q) { return kConv ? e0 / 4 + q : (int)threadIdx.x + kWG * q; };
         float v[E];
 #pragma unroll
         for (int i = 0; i < E; i++) v[i] = x[i / 4][i % 4];
@@ -874,24 +861,37 @@ struct StageIn {
         const int P = PS ? PS : K / 4;
 #pragma unroll
         for (int q = 0; q < E / 4; q++) {
-            dig[e0 / 4 + q] = w0[q];
-            dig[P + e0 / 4 + q] = w1[q];
-            dig[2 * P + e0 / 4 + q] = w2[q];
+            dig[dw(q)] = w0[q];
+            dig[P + dw(q)] = w1[q];
+            dig[2 * P + dw(q)] = w2[q];
         }
         if constexpr (SUMS) {
-            // fp32 sums of each 32-value sub-block (32 / E threads share one)
-#pragma unroll
-            for (int b = 0; b < (E >= 32 ? E / 32 : 1); b++) {
-                float t = 0.f;
-#pragma unroll
-                for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[b * 32 + i];
-                // xor 1, 2, 4 in that order (the writers, lanes with bit 2 clear,
+            static_assert(E >= 4, "at least four activations per thread");
+            if constexpr (!kConv) {
+                // fp32 sums of each 32-value sub-block: eight consecutive
+                // threads, xor 1, 2, 4 (the writers, lanes with bit 2 clear,
                 // see their exact partners; row_ror:12 reads lane (i + 4) mod 16)
-                if constexpr (E < 32) t += dpp_mov<0xB1>(t);
-                if constexpr (E < 16) t += dpp_mov<0x4E>(t);
-                if constexpr (E < 8) t += dpp_mov<0x12C>(t);
-                static_assert(E >= 4, "at least four activations per thread");
-                if (E >= 32 || (threadIdx.x % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t * scale;
+#pragma unroll
+                for (int q = 0; q < E / 4; q++) {
+                    float t = ((v[4 * q] + v[4 * q + 1]) + v[4 * q + 2]) + v[4 * q + 3];
+                    t += dpp_mov<0xB1>(t);
+                    t += dpp_mov<0x4E>(t);
+                    t += dpp_mov<0x12C>(t);
+                    if ((threadIdx.x & 7) == 0) xsum[dw(q) >> 3] = t * scale;
+                }
+            } else {
+                // fp32 sums of each 32-value sub-block (32 / E threads share one)
+#pragma unroll
+                for (int b = 0; b < (E >= 32 ? E / 32 : 1); b++) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int i = 0; i < (E >= 32 ? 32 : E); i++) t += v[b * 32 + i];
+                    // xor 1, 2, 4 in that order (as above)
+                    if constexpr (E < 32) t += dpp_mov<0xB1>(t);
+                    if constexpr (E < 16) t += dpp_mov<0x4E>(t);
+                    if constexpr (E < 8) t += dpp_mov<0x12C>(t);
+                    if (E >= 32 || (threadIdx.x % (32 / E)) == 0) xsum[(e0 + 32 * b) / 32] = t * scale;
+                }
             }
         }
         __syncthreads();
