@@ -315,6 +315,38 @@ __device__ __forceinline__ void wave_prep_head(float* dst, const float* src, con
     }
 }
 
+// wave_prep_head for heads 0 .. nh-1 (nh <= 4) of src (hd apart) into
+// dst[h]: every head's loads issued before any arithmetic, so one wave pays
+// one memory latency for all of them
+__device__ __forceinline__ void wave_prep_heads4(float (*dst)[64], const float* src, int nh, const float* nw,
+                                                 float eps, int hd, const float* cs, const float* sn) {
+    const int l = threadIdx.x & 63;
+    const bool on = 2 * l < hd;
+    float v0[4], v1[4];
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+        v0[h] = on && h < nh ? src[h * hd + 2 * l] : 0.f;
+        v1[h] = on && h < nh ? src[h * hd + 2 * l + 1] : 0.f;
+    }
+    const float w0 = nw && on ? nw[2 * l] : 1.f, w1 = nw && on ? nw[2 * l + 1] : 1.f;
+    const float c = on ? cs[l] : 0.f, s = on ? sn[l] : 0.f;
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+        if (h >= nh) break;
+        float x0 = v0[h], x1 = v1[h];
+        if (nw) {
+            const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+            const float sc = 1.0f / sqrtf(ss / (float)hd + eps);
+            x0 = x0 * sc * w0;
+            x1 = x1 * sc * w1;
+        }
+        if (on) {
+            dst[h][2 * l] = x0 * c - x1 * s;
+            dst[h][2 * l + 1] = x0 * s + x1 * c;
+        }
+    }
+}
+
 // The current token's K (per-head RMSNorm, RoPE) and V of kv head kvh into
 // the cache in its precision (cache.rs:395-461); kcur/vcur keep the values
 // as stored, which is what attention reads back (with write false only those
@@ -637,9 +669,13 @@ __global__ void __launch_bounds__(kWG) attn_tile_kernel(AttnArgs a) {
 // never used).
 constexpr int kQ8GroupTokens = 16;
 
+// CTRL a full permutation within rows (quad_perm, row mirrors): every lane
+// reads a valid source, and bound_ctrl set lets the compiler fold the move
+// into the instruction that consumes it
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    static_assert((CTRL & ~0xFF) == 0 || CTRL == 0x140 || CTRL == 0x141, "quad_perm or row mirror only");
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 // sum / max over each row of 16 lanes, result in every lane of the row
 __device__ __forceinline__ float row_sum16(float v) {
@@ -833,6 +869,224 @@ __global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
             if (base + i < g1) {  // wave-uniform
                 const i32x4 cur_s[2] = {sa[0], sa[1]};
                 scores(ring[(i + 1) % PD], sa);
+                step(ring[i], cur_s, base + i);
+            }
+            load(ring[i], base + i + PD);
+        }
+    }
+
+    // 4. sums over the token lanes; lane 16c writes head c's (m, l) and dims
+    //    16c..16c+15 of every head
+    l_run = row_sum16(l_run);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[k][i] = row_sum16(acc[k][i]);
+    if (t == 0) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            if (h >= hpk) break;
+            const size_t pi = (size_t)(kvh * hpk + h) * a.nsplit + split;
+            float* dst = a.part_acc + pi * HD + 16 * c;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *(f32x4*)(dst + i) = f32x4{acc[h][i], acc[h][i + 1], acc[h][i + 2], acc[h][i + 3]};
+        }
+        if (c < hpk) {
+            const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
+            a.part_m[pi] = m_run * 0.69314718055994531f;  // natural-log units for the combine
+            a.part_l[pi] = l_run;
+        }
+    }
+}
+
+// ------------------------------------------- fp16 attention on the matrix cores
+//
+// fp16 caches (token rows of n_kv_heads x 64 halves, the tile kernel's
+// layout) with head_dim 64 and at most 4 query heads per kv head, as the
+// Q8_0 kernel above: one wave per (kv head, split), all kv heads of a split
+// in one workgroup, each wave walking its split's 16-token groups with its
+// own online softmax and no workgroup barrier. Lane t + 16c loads dims
+// 16c..16c+15 of token t of the group (32 bytes of K, 32 of V; rows past the
+// position read the position's row, so the last group of the cache never
+// reads past it).
+//  scores  v_mfma_f32_16x16x16_f16, four per group: A row 4h + i holds the
+//          query of head h in log2 units (scale * log2 e folded in) as an
+//          fp16 hi part (i = 0) and lo part (i = 1; q = hi + lo to about
+//          2^-22), rows 4h + 2, 4h + 3 zero; B the cache's fp16 K as
+//          stored. Instruction j takes dims 16c + 4j .. +3 from k-lane
+//          group c (any order of k serves while A and B agree), so lane
+//          t + 16h receives head h's hi and lo sums for token t: products
+//          of fp16 values are exact, summed in f32;
+//  values  O[h][d] += p_h(t) v(t, d) in f32 on the VALU, as the Q8_0 kernel.
+// The owner split stores the current K/V first and uses them, as stored,
+// for its token's lanes (nothing is read back). Tokens of the last group
+// past the position get p = 0.
+struct F16Group {
+    u32x4 k0, k1;  // K dims 16c .. 16c+15 of token lane & 15 (fp16 pairs)
+    u32x4 v0, v1;  // V, the same
+};
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+inline bool attn_f16_mfma_ok(int kv_precision, int hd, int n_heads, int n_kv) {
+    return kv_precision == MIVI_KV_F16 && hd == 64 && n_kv > 0 && n_heads % n_kv == 0 && n_heads / n_kv <= 4;
+}
+
+template <int PD, int W>  // groups in flight per wave; waves (kv heads) per workgroup
+__global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
+    constexpr int HD = 64, G = kQ8GroupTokens;
+    __shared__ __attribute__((aligned(16))) float qs[W][4][HD];   // [wave][head][dim]
+    __shared__ __attribute__((aligned(16))) float cur[W][2][HD];  // owner: current K/V as stored
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    int kvg, split;
+    if (!attn_tile_of((a.n_kv_heads + W - 1) / W, a.nsplit, &kvg, &split)) return;  // workgroup-uniform
+    const int kvh = kvg * W + wave;
+    if (kvh >= a.n_kv_heads) return;  // wave-uniform (no workgroup barrier below)
+    {
+        const int b = blockIdx.y;
+        a.q += b * a.qkv_s; a.k += b * a.qkv_s; a.v += b * a.qkv_s;
+        a.kc += b * a.kv_s; a.vc += b * a.kv_s;
+        a.pos += b;
+        a.part_m += b * a.part_s; a.part_l += b * a.part_s; a.part_acc += b * a.part_s * HD;
+    }
+    const int hpk = a.n_heads / a.n_kv_heads;
+    const int pos = *a.pos;
+    const int ng = (pos + G) / G;
+    const int gps = (ng + a.nsplit - 1) / a.nsplit;
+    const int g0 = split * gps, g1 = min(ng, g0 + gps);
+    if (g0 >= g1) return;  // beyond the context
+    const float* cs = a.rope_cos + (size_t)pos * (HD / 2);
+    const float* sn = a.rope_sin + (size_t)pos * (HD / 2);
+    const int t = lane & 15, c = lane >> 4;
+
+    const bool own = g1 == ng && !a.keep_cache;  // wave-uniform: the split holding the current token
+    u32x4 ck0 = {}, ck1 = {}, cv0 = {}, cv1 = {};  // its K/V as stored (fp16 bits of dims 16c .. +15)
+
+    // 2. group loads (past the split's end the last group is re-read)
+    const size_t rb = a.row_bytes;
+    const uint8_t* kc = a.kc + (size_t)kvh * (HD * 2) + 32 * c;
+    const uint8_t* vc = a.vc + (size_t)kvh * (HD * 2) + 32 * c;
+    auto load = [&](F16Group& q, int g) {
+        g = min(g, g1 - 1);
+        const int row = g * G + t;
+        if (own && row >= pos) {
+            q.k0 = ck0; q.k1 = ck1; q.v0 = cv0; q.v1 = cv1;
+        } else {
+            const size_t o = (size_t)min(row, pos) * rb;  // streamed once per step: non-temporal
+            q.k0 = __builtin_nontemporal_load((gau32x4*)(kc + o));
+            q.k1 = __builtin_nontemporal_load((gau32x4*)(kc + o + 16));
+            q.v0 = __builtin_nontemporal_load((gau32x4*)(vc + o));
+            q.v1 = __builtin_nontemporal_load((gau32x4*)(vc + o + 16));
+        }
+    };
+    // 1. the first PD groups' loads (the current token's lanes re-read the
+    //    cache's old bytes there and are patched below), then 2. the owner
+    //    stores the current K/V and patches its lanes with them
+    F16Group ring[PD];
+#pragma unroll
+    for (int i = 0; i < PD; i++) {
+        const int g = min(g0 + i, g1 - 1);
+        const size_t o = (size_t)min(g * G + t, pos) * rb;
+        ring[i].k0 = __builtin_nontemporal_load((gau32x4*)(kc + o));
+        ring[i].k1 = __builtin_nontemporal_load((gau32x4*)(kc + o + 16));
+        ring[i].v0 = __builtin_nontemporal_load((gau32x4*)(vc + o));
+        ring[i].v1 = __builtin_nontemporal_load((gau32x4*)(vc + o + 16));
+    }
+    if (own) {
+        attn_store_current<MIVI_KV_F16>(a, kvh, pos, cs, sn, cur[wave][0], cur[wave][1], true);
+        __builtin_amdgcn_wave_barrier();
+        uint32_t kw[8], vw[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int d = 16 * c + 2 * i;
+            kw[i] = f32_to_half_bits(cur[wave][0][d]) | (f32_to_half_bits(cur[wave][0][d + 1]) << 16);
+            vw[i] = f32_to_half_bits(cur[wave][1][d]) | (f32_to_half_bits(cur[wave][1][d + 1]) << 16);
+        }
+        ck0 = u32x4{kw[0], kw[1], kw[2], kw[3]}; ck1 = u32x4{kw[4], kw[5], kw[6], kw[7]};
+        cv0 = u32x4{vw[0], vw[1], vw[2], vw[3]}; cv1 = u32x4{vw[4], vw[5], vw[6], vw[7]};
+#pragma unroll
+        for (int i = 0; i < PD; i++) {
+            if (min(g0 + i, g1 - 1) * G + t >= pos) {
+                ring[i].k0 = ck0; ring[i].k1 = ck1; ring[i].v0 = cv0; ring[i].v1 = cv1;
+            }
+        }
+    }
+
+    // 3. query heads (QK-norm, RoPE) in log2 units as fp16 hi / lo: A row
+    //    4h + i, lane = row + 16 * kg holds dims 16 kg + 4j .. +3 for instruction j
+    wave_prep_heads4(qs[wave], a.q + (size_t)(kvh * hpk) * HD, hpk, a.q_norm, a.eps, HD, cs, sn);
+    __builtin_amdgcn_wave_barrier();
+    half4_t qa[4];
+    {
+        const int qh = t >> 2, qi = t & 3;
+        const float qscale = a.scale * 1.4426950408889634f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float y = qh < hpk && qi < 2 ? qs[wave][qh][16 * c + 4 * j + e] * qscale : 0.f;
+                const _Float16 hi = (_Float16)y;
+                const _Float16 lo = (_Float16)(y - (float)hi);
+                qa[j][e] = qi == 0 ? hi : qi == 1 ? lo : (_Float16)0.0f;
+            }
+        }
+    }
+
+    float m_run = -INFINITY, l_run = 0.f;  // head c (lane t + 16c)
+    float acc[4][16];                      // head h, dim 16c + i (lane t + 16c)
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[k][i] = 0.f;
+
+    auto scores = [&](const F16Group& q) {
+        const uint32_t kw[8] = {q.k0.x, q.k0.y, q.k0.z, q.k0.w, q.k1.x, q.k1.y, q.k1.z, q.k1.w};
+        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint64_t kb = ((uint64_t)kw[2 * j + 1] << 32) | kw[2 * j];
+            s4 = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[j], __builtin_bit_cast(half4_t, kb), s4, 0, 0, 0);
+        }
+        return s4.x + s4.y;  // head c, token t: hi part + lo part
+    };
+    auto step = [&](const F16Group& q, float s, int g) {
+        const bool valid = g * G + t <= pos;
+        s = valid ? s : -INFINITY;
+        if (__builtin_amdgcn_ballot_w64(s > m_run + 8.0f)) {  // wave-uniform, rare after the first group
+            const float m_new = fmaxf(m_run, row_max16(s));
+            const float al = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
+            m_run = m_new;
+            l_run *= al;
+            float a0, a1, a2, a3;
+            rows_all(al, a0, a1, a2, a3);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                acc[0][i] *= a0; acc[1][i] *= a1; acc[2][i] *= a2; acc[3][i] *= a3;
+            }
+        }
+        const float p = __builtin_amdgcn_exp2f(s - m_run);  // v_exp_f32 (p <= 256)
+        l_run += p;
+        float p0, p1, p2, p3;  // p of token t for heads 0..3
+        rows_all(p, p0, p1, p2, p3);
+        const uint32_t vw[8] = {q.v0.x, q.v0.y, q.v0.z, q.v0.w, q.v1.x, q.v1.y, q.v1.z, q.v1.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float vf = half_bits_to_f32((i & 1) ? vw[i >> 1] >> 16 : vw[i >> 1] & 0xFFFFu);
+            acc[0][i] = fmaf(p0, vf, acc[0][i]);
+            acc[1][i] = fmaf(p1, vf, acc[1][i]);
+            acc[2][i] = fmaf(p2, vf, acc[2][i]);
+            acc[3][i] = fmaf(p3, vf, acc[3][i]);
+        }
+    };
+
+    // the score products of a group are issued one group ahead
+    float sa = scores(ring[0]);
+    for (int base = g0; base < g1; base += PD) {
+#pragma unroll
+        for (int i = 0; i < PD; i++) {
+            if (base + i < g1) {  // wave-uniform
+                const float cur_s = sa;
+                sa = scores(ring[(i + 1) % PD]);
                 step(ring[i], cur_s, base + i);
             }
             load(ring[i], base + i + PD);
@@ -1132,6 +1386,12 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
         if (w == 8) hipLaunchKernelGGL((attn_q8_mfma_kernel<3, 8>), grid, dim3(512), 0, s, a);
         else hipLaunchKernelGGL((attn_q8_mfma_kernel<3, 4>), grid, dim3(kWG), 0, s, a);
         tt = kQ8GroupTokens;
+    } else if (attn_f16_mfma_ok(c.kv_precision, (int)c.head_dim, (int)c.n_heads, (int)c.n_kv_heads)) {
+        // fp16 rows in 16-token groups on the matrix cores, one wave per
+        // workgroup (the XCD placement of attn_tile_of spreads them)
+        dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
+        hipLaunchKernelGGL((attn_f16_mfma_kernel<3, 1>), grid, dim3(64), 0, s, a);
+        tt = kQ8GroupTokens;
     } else {
         dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
 #define ATT(KVP, HDM) hipLaunchKernelGGL((attn_tile_kernel<KVP, HDM>), grid, dim3(kWG), 0, s, a)
@@ -1332,7 +1592,10 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
                 // Q8_0 group kernel: about two workgroups per CU over the
                 // batch's sequences (config 5, 8 sequences: 32 splits of
                 // 1024 tokens, 4067 against 3820 tok/s with 64)
-                a.nsplit = m->kv_packed ? attn_q8_splits(m->nsplit, (int)nb, (int)c.n_kv_heads) : m->nsplit;
+                a.nsplit = m->kv_packed || attn_f16_mfma_ok(c.kv_precision, (int)c.head_dim, (int)c.n_heads,
+                                                            (int)c.n_kv_heads)
+                               ? attn_q8_splits(m->nsplit, (int)nb, (int)c.n_kv_heads)
+                               : m->nsplit;
                 a.scale = 1.0f / sqrtf((float)c.head_dim);
                 a.part_m = s0.part_m; a.part_l = s0.part_l; a.part_acc = s0.part_acc;
                 a.qkv_s = (int64_t)z.qkv; a.kv_s = (int64_t)z.kv; a.part_s = (int64_t)z.part;
