@@ -971,23 +971,43 @@ __device__ __forceinline__ mivi::GemvArgs gemv_column(const mivi::GemvArgs& a, i
 // prologue (StageIn::finish), so out_proj's input is the same bit for bit:
 // bx = B * X, the window shifts in bx, conv = sum_k w_k * window_k from
 // zero, y = C * conv; the window goes to the column's other ping-pong buffer.
-__device__ __forceinline__ void conv_epilogue(const mivi::GemvArgs& a, int col, int c, float B, float C, float X) {
+// conv_prefetch loads what the step needs besides B, C, X (the window, the
+// weights, the buffer to write), so a kernel can issue it with its weight
+// loads; conv_epilogue = both.
+struct ConvPre {
+    float sv[kConvKs - 1];  // window values 1 .. ks-1
+    float w[kConvKs];
+    float* st_out;
+};
+__device__ __forceinline__ void conv_prefetch(const mivi::GemvArgs& a, int col, int c, ConvPre& pre) {
     const bool swap = a.phase && (a.phase[col] & 1);
     const float* st_in = (swap ? a.st_out : a.st_in) + col * a.sts + (size_t)c * kConvKs;
-    float* st_out = (swap ? (float*)a.st_in : a.st_out) + col * a.sts + (size_t)c * kConvKs;
+    pre.st_out = (swap ? (float*)a.st_in : a.st_out) + col * a.sts + (size_t)c * kConvKs;
+#pragma unroll
+    for (int k = 0; k + 1 < kConvKs; k++) pre.sv[k] = st_in[k + 1];
+#pragma unroll
+    for (int k = 0; k < kConvKs; k++)
+        pre.w[k] = a.conv_mode == 0 ? a.conv_w[(size_t)c * kConvKs + k]
+                 : a.conv_mode == 1 ? a.conv_w[k] : 1.0f / (float)kConvKs;
+}
+__device__ __forceinline__ void conv_finish(const mivi::GemvArgs& a, int col, int c, float B, float C, float X,
+                                            const ConvPre& pre) {
     const float bx = B * X;
     float conv = 0.0f;
     float sv[kConvKs];
 #pragma unroll
     for (int k = 0; k < kConvKs; k++) {
-        sv[k] = k + 1 < kConvKs ? st_in[k + 1] : bx;
-        const float w = a.conv_mode == 0 ? a.conv_w[(size_t)c * kConvKs + k]
-                      : a.conv_mode == 1 ? a.conv_w[k] : 1.0f / (float)kConvKs;
-        conv += w * sv[k];
+        sv[k] = k + 1 < kConvKs ? pre.sv[k] : bx;
+        conv += pre.w[k] * sv[k];
     }
 #pragma unroll
-    for (int k = 0; k < kConvKs; k++) st_out[k] = sv[k];
+    for (int k = 0; k < kConvKs; k++) pre.st_out[k] = sv[k];
     a.seg[0].y[col * a.ys + c] = C * conv;
+}
+__device__ __forceinline__ void conv_epilogue(const mivi::GemvArgs& a, int col, int c, float B, float C, float X) {
+    ConvPre pre;
+    conv_prefetch(a, col, c, pre);
+    conv_finish(a, col, c, B, C, X, pre);
 }
 
 // K-quant GEMV for the decode shapes (K = 2048/4096/8192). A persistent grid
@@ -2037,12 +2057,16 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_quad_kernel(const mivi::GemvArgs
         return 4 * q + g * (EPI == mivi::EPI_SWIGLU ? n0 : EPI == mivi::EPI_CONV ? D3 : 0);
     };
     Q4Item buf[PD][G][S];
+    ConvPre cpre[EPI == mivi::EPI_CONV ? PD : 1];  // lanes < 4: the step's channel's conv inputs
     auto load = [&](int p, int st) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const uint8_t* base = sg.row(quad_row(st, g));
 #pragma unroll
             for (int q = 0; q < S; q++) load_q4_item(buf[p][g][q], base + q * kQ4SubQuadBytes, lane);
+        }
+        if constexpr (EPI == mivi::EPI_CONV) {
+            if (lane < 4) conv_prefetch(a, 0, quad_row(st, 0) + jv, cpre[p]);  // channel 4q + jv
         }
     };
     // activation loads, then the first PD steps, then the activation math
@@ -2108,7 +2132,7 @@ __global__ void __launch_bounds__(kWG) gemv_q4k_quad_kernel(const mivi::GemvArgs
             if constexpr (EPI == mivi::EPI_SWIGLU) {
                 *(gfloat*)sg.out(r) = silu_f(rv[0]) * rv[1];  // math.rs:87-95
             } else if constexpr (EPI == mivi::EPI_CONV) {
-                conv_epilogue(a, 0, r, rv[0], rv[1], rv[2]);
+                conv_finish(a, 0, r, rv[0], rv[1], rv[2], cpre[p]);
             } else {
                 store_out(sg, a.accumulate, r, rv[0]);
             }
