@@ -132,6 +132,17 @@ int32_t mivi_hip_quantized_matvec_packed(float* out, size_t out_len, int32_t ggm
                                          const uint8_t* packed, size_t packed_len, const float* x,
                                          size_t x_len, size_t n, size_t d, void* stream);
 
+/* quantized_matmul_rows (lib.rs:143-251) over weights packed by
+ * mivi_hip_pack_weights (16-byte aligned): out[batch, rows] = inputs[batch,
+ * cols] * W^T, every input's row of outputs equal to its own
+ * mivi_hip_quantized_matvec_packed bit for bit (Q6_K row quads: up to eight
+ * inputs per launch, each quad read once for them); sizes and errors as
+ * mivi_hip_quantized_matmul_rows. No counterpart in the reference. */
+int32_t mivi_hip_quantized_matmul_rows_packed(float* out, size_t out_len, int32_t ggml_type,
+                                              const uint8_t* packed, size_t packed_len, const float* inputs,
+                                              size_t inputs_len, size_t batch, size_t rows, size_t cols,
+                                              void* stream);
+
 /* crates/mivi-quant/src/lib.rs:35-72 dequantize_slice: bit-exact decode of
  * out_len / block_size blocks (Q4_K, Q6_K, Q8_0) or of bytes_len / type_size
  * elements (F16, BF16, F32). */

@@ -1948,6 +1948,266 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
+// Up to eight columns (sequences) against the same row quads, so a batched
+// head reads its quads once per step. Eight waves per workgroup, wave c
+// forming column c's digits; each wave then takes its own quads as above.
+// The 3 ncol digit planes (plane 3c + p = plane p of column c) sit in LDS in
+// groups of four, laid out for the 4 x 4 x 4 instruction: entry (G, g,
+// lane 4b + v) is the 16 digits of plane 4G + v at slot g of the lane's
+// unit, so one 1 KB read gives a group's A operands for a slot, and lane
+// 4b + j receives the four planes' sums for row j. The codes enter as
+// c - 32 (signed bytes: (c + 0x60) ^ 0x80), which adds the Q6_K offset in
+// the instruction; the integer sums are the one-column kernel's. The float
+// steps run in its order, and the cross-lane sum of the eight columns is a
+// reduce-scatter over the same butterfly (lane bits 5, 4, 3, then 2), after
+// which lane l with bit 2 clear holds column (l >> 3) & 7, row l & 3: every
+// column's result equals the one-column kernel's bit for bit.
+// NGR groups (3: up to four columns, 6: up to eight); planes past 3 ncol are
+// zeros.
+constexpr int kQuad8Waves = 8, kQuad8WG = 64 * kQuad8Waves;
+
+template <int PRO, int EPI, int PD, int NGR>
+__global__ void __launch_bounds__(kQuad8WG) gemv_q6k_quad8_kernel(const mivi::GemvArgs a) {
+    constexpr int K = 2048, NL = K / 256, NCM = 4 * NGR / 3;
+    static_assert(NGR == 3 || NGR == 6, "four or eight columns");
+    __shared__ u32x4 Ab[NGR][8][64];  // [group][slot][lane]
+    __shared__ float scol[kQuad8Waves];
+    const int nquads = a.seg[0].n / 4;
+    const uint8_t* W = a.seg[0].W;
+    const int ncol = a.ncol;  // 1..NCM, workgroup-uniform
+    const int npl = 3 * ncol;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int jv = lane & 3;
+    const int nw = gridDim.x * kQuad8Waves, wid = blockIdx.x * kQuad8Waves + wave;
+    const int cnt = wid < nquads ? (nquads - wid + nw - 1) / nw : 0;  // wave-uniform
+
+    u32x4 w[PD][6];
+    u32x2 scw[PD];
+    uint32_t dw[PD];
+    auto load = [&](int p, int st) {  // as gemv_q6k_quad_kernel's
+        st = st < cnt ? st : cnt - 1;
+        int q = wid + st * nw;
+        q = q < 0 ? 0 : q < nquads ? q : nquads - 1;
+        const uint8_t* base = W + (size_t)q * kQuadBytes;
+        const uint8_t* cb = base + 64 * (q & 1);
+        const uint8_t* db = base + ((q & 1) ? 0 : 6656);
+#pragma unroll
+        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(cb + 1024 * k + 16 * lane);
+        scw[p] = *(const __attribute__((address_space(1))) u32x2*)(cb + 6144 + 8 * lane);
+        dw[p] = *(const __attribute__((address_space(1))) uint32_t*)(db + 4 * (4 * jv + (lane >> 4)));
+    };
+    // column `wave`'s activations: chunk i is values 4 (lane + 64 i) .. + 3,
+    // which thread lane + 64 (i & 3) of the one-column kernel holds
+    const bool stager = wave < ncol && wave < NCM;  // wave-uniform
+    f32x4 u[NL];
+    f32x4 nwt[PRO == mivi::PRO_RMSNORM ? NL : 1];
+    if (stager) {
+        const float* x = a.x + (size_t)wave * a.xs;
+#pragma unroll
+        for (int i = 0; i < NL; i++) u[i] = *(const gf32x4*)(x + 4 * (lane + 64 * i));
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+#pragma unroll
+            for (int i = 0; i < NL; i++) nwt[i] = *(const gf32x4*)(a.norm_w + 4 * (lane + 64 * i));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PD; p++) load(p, p);
+    __builtin_amdgcn_sched_barrier(0);
+    // planes 3 ncol .. 4 NGR - 1 read zeros
+#pragma unroll
+    for (int G = 0; G < NGR; G++)
+        if (4 * G + (int)(threadIdx.x & 3) >= npl) Ab[G][threadIdx.x >> 6][threadIdx.x & 63] = u32x4{0, 0, 0, 0};
+    if (stager) {
+        float v[NL][4];
+#pragma unroll
+        for (int i = 0; i < NL; i++) { v[i][0] = u[i].x; v[i][1] = u[i].y; v[i][2] = u[i].z; v[i][3] = u[i].w; }
+        float m = 0.f, scale = 1.0f;
+        if constexpr (PRO == mivi::PRO_RMSNORM) {
+            // the one-column kernel's order: thread lane + 64 h sums its
+            // chunks h, h + 4 in turn, each wave's sum is lane 0's butterfly
+            // sum, and the four waves add in order
+            float pw[4];
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                float t = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) t = fmaf(v[h][e], v[h][e], t);
+#pragma unroll
+                for (int e = 0; e < 4; e++) t = fmaf(v[h + 4][e], v[h + 4][e], t);
+                pw[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xsum_desc<64>(t)), 0));
+            }
+            const float ss = ((pw[0] + pw[1]) + pw[2]) + pw[3];
+            scale = 1.0f / sqrtf(ss / (float)K + a.eps);
+            // digits of u = v w (math.rs:7-22; 1 / rms goes into s)
+#pragma unroll
+            for (int i = 0; i < NL; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[i][e] = v[i][e] * nwt[i][e];
+                    m = fmaxf(m, fabsf(v[i][e]));
+                }
+        } else {
+            float nn = 0.f;  // NaN for a NaN or infinite value (fmaxf passes NaNs over)
+#pragma unroll
+            for (int i = 0; i < NL; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    m = fmaxf(m, fabsf(v[i][e]));
+                    nn = fmaf(v[i][e], 0.f, nn);
+                }
+            m += nn;
+        }
+        {
+            float lo, hi;
+            swap32(m, lo, hi);
+            m = nanmax(lo, hi);
+            swap16(m, lo, hi);
+            m = nanmax(lo, hi);
+            m = nanmax(m, dpp_mov<0x128>(m));
+            m = nanmax(m, xor4_mov(m));
+            m = nanmax(m, dpp_mov<0x4E>(m));
+            m = nanmax(m, dpp_mov<0xB1>(m));
+        }
+        const bool finite = m > 0.f && m <= 3.40282347e38f;
+        const float mul = finite ? kDigMul / m : 0.0f;
+        const float sc = ((m - m) + m * scale) * (2.0f / 127.0f);
+        // dword lane + 64 i of a plane: 16 B chunk k = lane / 4 + 16 i of
+        // unit 4 i + kb, quarter q (chunk k of a plane is unit
+        // 4 (k >> 4) + 2 ((k >> 3) & 1) + (k & 1), quarter (k >> 1) & 3),
+        // dword e of the chunk
+        uint32_t* A32 = (uint32_t*)&Ab[0][0][0];
+        const int kb = 2 * ((lane >> 5) & 1) + ((lane >> 2) & 1), q = (lane >> 3) & 3, e = lane & 3;
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            uint32_t d[3];
+            digits4_b256(v[i], mul, d[0], d[1], d[2]);
+            const int g = 4 * (i >> 2) + q, bb = 4 * (i & 3) + kb;
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                const int pl = 3 * wave + p;
+                A32[(((pl >> 2) * 8 + g) * 64 + 4 * bb + (pl & 3)) * 4 + e] = d[p];
+            }
+        }
+        if (lane == 0) scol[wave] = sc;
+    }
+    __syncthreads();
+
+    const int cl = (lane >> 3) & 7;  // this lane's column after the cross-lane sum
+    const float s_l = scol[cl < ncol ? cl : 0];
+    float best = -INFINITY;
+    int bidx = 0x7FFFFFFF;
+    auto write_part = [&]() {
+        // lanes 8c .. 8c + 3 hold column c's rows; lanes with bit 2 set carry (-inf, INT_MAX)
+        float bv = best;
+        int bi = bidx;
+#pragma unroll
+        for (int o = 1; o < 4; o <<= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((lane & 7) == 0 && cl < ncol) {
+            a.part_val[cl * a.ps + wid] = bv;
+            a.part_idx[cl * a.ps + wid] = bi;
+        }
+    };
+    if (cnt == 0) {  // wave-uniform; no barrier follows
+        if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+        return;
+    }
+
+    auto compute = [&](int p, int st) {
+        int acc[4 * NGR][2];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int D0 = 3 * g;
+            const uint32_t W0 = w[p][D0 >> 2][D0 & 3];
+            const uint32_t W1 = w[p][(D0 + 1) >> 2][(D0 + 1) & 3];
+            const uint32_t W2 = w[p][(D0 + 2) >> 2][(D0 + 2) & 3];
+            uint32_t B[4] = {W0 & 0x3F3F3F3Fu, W1 & 0x3F3F3F3Fu, W2 & 0x3F3F3F3Fu,
+                             ((W0 >> 6) & 0x03030303u) | ((W1 >> 4) & 0x0C0C0C0Cu) | ((W2 >> 2) & 0x30303030u)};
+#pragma unroll
+            for (int m = 0; m < 4; m++) B[m] = (B[m] + 0x60606060u) ^ 0x80808080u;  // c - 32 per byte
+            const int scv = __builtin_amdgcn_sbfe((int)(g < 4 ? scw[p].x : scw[p].y), 8 * (g & 3), 8);
+#pragma unroll
+            for (int G = 0; G < NGR; G++) {
+                // (volatile: read at each step, not held in registers across the loop)
+                const u32x4 A = *(volatile __attribute__((address_space(3))) u32x4*)&Ab[G][g][lane];
+                i32x4 D = {0, 0, 0, 0};
+                D = mfma4x4(A.x, B[0], D);
+                D = mfma4x4(A.y, B[1], D);
+                D = mfma4x4(A.z, B[2], D);
+                D = mfma4x4(A.w, B[3], D);
+                const int i = g >> 2;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    if ((g & 3) == 0) acc[4 * G + v][i] = mul24(D[v], scv);
+                    else acc[4 * G + v][i] += mul24(D[v], scv);
+                }
+            }
+        }
+        float vc[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            vc[c] = 0.f;
+            if (c < NCM) {  // (columns past ncol sum zeros)
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const float f = fmaf((float)acc[3 * c + 2][i], kDig2, fmaf((float)acc[3 * c + 1][i], kDig1, (float)acc[3 * c][i]));
+                    vc[c] += half_bits_to_f32(i ? dw[p] >> 16 : dw[p]) * f;
+                }
+            }
+        }
+        // reduce-scatter: lane bit 5 keeps columns 4 (bit 5) + 0..3, bit 4
+        // then halves them, bit 3 picks one; bit 2 finishes the sum
+        float r4[4], r2[2];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(vc[c]), __float_as_uint(vc[c + 4]), false, false);
+            r4[c] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(r4[c]), __float_as_uint(r4[c + 2]), false, false);
+            r2[c] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+        }
+        const bool b3 = lane & 8;
+        float y = (b3 ? r2[1] : r2[0]) + dpp_mov<0x128>(b3 ? r2[0] : r2[1]);  // row_ror:8 (lane ^ 8)
+        y += dpp_mov<0x12C>(y);                                               // row_ror:12 (lane ^ 4 where bit 2 is clear)
+        y *= s_l;
+        if (!(lane & 4) && cl < ncol) {
+            const int r = 4 * (wid + st * nw) + jv;
+            gfloat* yp = (gfloat*)(a.seg[0].y + r + cl * a.ys);
+            if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(yp, y);
+            else *yp = y;
+            // sampler.rs:305-316: strictly greater wins, so NaN never does
+            if constexpr (EPI == mivi::EPI_ARGMAX)
+                if (y > best) { best = y; bidx = r; }
+        }
+    };
+    int st = 0;
+    for (; st + 2 * PD <= cnt; st += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, st + p);
+            load(p, st + p + PD);
+        }
+    }
+    if (st + PD <= cnt) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, st + p);
+            if (st + p + PD < cnt) load(p, st + p + PD);
+        }
+        st += PD;
+    }
+#pragma unroll
+    for (int p = 0; p < PD; p++)
+        if (st + p < cnt) compute(p, st + p);
+    if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+}
+
 // ------------------------------------------ Q4_K row quads on the matrix cores
 //
 // Packed Q4_K matrices with K = 2048 S (S = 1 or 4) columns and a multiple of
@@ -2478,14 +2738,21 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
             if (t != MIVI_GGML_Q6_K || a.nseg != 1 || a.epilogue == mivi::EPI_SWIGLU)
                 return mivi::set_error(MIVI_ERR_UNSUPPORTED, "packed row quads take one Q6_K segment, store or argmax");
             if constexpr (PRO == mivi::PRO_NONE || PRO == mivi::PRO_RMSNORM) {
-                const int qgrid = mivi::quad_grid(n);
+                const int qgrid = mivi::quad_grid(n);  // even: as many waves in eight-wave workgroups
 #define LQ(EPI, NC, PD) hipLaunchKernelGGL((gemv_q6k_quad_kernel<PRO, EPI, NC, PD>), dim3(qgrid), dim3(kWG), 0, s, a)
-                if (a.epilogue == mivi::EPI_ARGMAX) {
+#define LQ8(EPI, PD, NGR) \
+    hipLaunchKernelGGL((gemv_q6k_quad8_kernel<PRO, EPI, PD, NGR>), dim3(qgrid / 2), dim3(kQuad8WG), 0, s, a)
+                if (a.ncol > 4) {
+                    if (a.epilogue == mivi::EPI_ARGMAX) LQ8(mivi::EPI_ARGMAX, 3, 6); else LQ8(mivi::EPI_STORE, 3, 6);
+                } else if (a.ncol > 2) {
+                    if (a.epilogue == mivi::EPI_ARGMAX) LQ8(mivi::EPI_ARGMAX, 3, 3); else LQ8(mivi::EPI_STORE, 3, 3);
+                } else if (a.epilogue == mivi::EPI_ARGMAX) {
                     if (a.ncol > 1) LQ(mivi::EPI_ARGMAX, 2, 2); else LQ(mivi::EPI_ARGMAX, 1, 3);
                 } else {
                     if (a.ncol > 1) LQ(mivi::EPI_STORE, 2, 2); else LQ(mivi::EPI_STORE, 1, 3);
                 }
 #undef LQ
+#undef LQ8
                 MIVI_HIP_CHECK(hipGetLastError());
                 return MIVI_OK;
             } else {
@@ -2723,8 +2990,10 @@ int stream_wg_per_cu(int n) {
 
 int quad_grid(int n) {
     // 2 workgroups per CU measured best for the 65536-row head (18.7 us vs 20.6 at 3)
+    // (even, so the eight-wave batched kernel launches as many waves)
     static const int per_cu = env_int("MIVI_GEMV_QUAD_WG_PER_CU", 2);
-    return std::max(1, std::min((n / 4 + 3) / 4, num_cus() * per_cu));
+    const int g = std::max(1, std::min((n / 4 + 3) / 4, num_cus() * per_cu));
+    return g + (g & 1);
 }
 
 int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
@@ -2737,10 +3006,11 @@ int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
 
 // Most columns one batched streaming launch takes at depth K, 1 where there
 // is no batched kernel: 8 at K = 2048 (digits in LDS: 6 KB per column), 4 at
-// K = 8192 (24 KB per column); packed rows take 2.
+// K = 8192 (24 KB per column); packed Q6_K rows take 8 (the eight-wave
+// quad kernel).
 static int gemv_max_cols(int32_t t, int K, bool packed, int pro = PRO_NONE, int epilogue = EPI_STORE) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
-    if (packed) return (t == MIVI_GGML_Q6_K && K == 2048) ? 2 : 1;
+    if (packed) return (t == MIVI_GGML_Q6_K && K == 2048) ? kMaxGemvCols : 1;
     // Q4_K at K = 8192 on the matrix cores: column groups of four run side by
     // side in one launch (one workgroup per CU each)
     if (K == 8192 && t == MIVI_GGML_Q4_K && pro == PRO_NONE && epilogue == EPI_STORE &&
@@ -3067,6 +3337,43 @@ extern "C" int32_t mivi_hip_quantized_matvec_packed(float* out, size_t out_len, 
     a.K = (int)d;
     a.x = x;
     a.packed = 1;
+    return launch_gemv_ex(t, PRO_NONE, a, (hipStream_t)stream);
+}
+
+extern "C" int32_t mivi_hip_quantized_matmul_rows_packed(float* out, size_t out_len, int32_t t,
+                                                        const uint8_t* packed, size_t packed_len, const float* in,
+                                                        size_t in_len, size_t batch, size_t rows, size_t cols,
+                                                        void* stream) {
+    // the sizes and errors of mivi_hip_quantized_matmul_rows (types.rs:188-235)
+    size_t bs, ts, row_bytes, e;
+    if (!format_sizes(t, &bs, &ts)) return err_unsupported(t);
+    if (cols % bs != 0) return err_misaligned(cols, bs);
+    if (__builtin_mul_overflow(cols / bs, ts, &row_bytes)) return err_overflow();
+    if (__builtin_mul_overflow(batch, rows, &e)) return err_overflow();
+    if (out_len < e) return err_buffer_too_small(e, out_len);
+    if (__builtin_mul_overflow(batch, cols, &e)) return err_overflow();
+    if (in_len < e) return err_buffer_too_small(e, in_len);
+    if (__builtin_mul_overflow(rows, row_bytes, &e)) return err_overflow();
+    if (packed_len < e) return err_buffer_too_small(e, packed_len);
+    if (!packable(t, cols, rows))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no packed layout for type %d with %zu rows of %zu columns", t, rows,
+                         cols);
+    if (batch == 0 || rows == 0) return clear_error();
+    if (!out || !packed || !in) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    if ((uintptr_t)packed % 16) return set_error(MIVI_ERR_INVALID_ARGUMENT, "packed rows must be 16-byte aligned");
+    if (rows > (size_t)INT32_MAX || batch > (size_t)INT32_MAX) return err_overflow();
+    clear_error();
+    // the inputs as columns of batched launches (up to eight per launch for
+    // Q6_K row quads, one per launch otherwise)
+    GemvArgs a = {};
+    a.seg[0] = {packed, out, (int)rows};
+    a.nseg = 1;
+    a.K = (int)cols;
+    a.x = in;
+    a.packed = 1;
+    a.ncol = (int)batch;
+    a.xs = (int64_t)cols;
+    a.ys = (int64_t)rows;
     return launch_gemv_ex(t, PRO_NONE, a, (hipStream_t)stream);
 }
 

@@ -126,6 +126,9 @@ pub mod ffi {
             rows: usize, cols: usize, stream: *mut c_void) -> i32;
         pub fn mivi_hip_quantized_matvec_packed(out: *mut f32, out_len: usize, ggml_type: i32, packed: *const u8,
             packed_len: usize, x: *const f32, x_len: usize, n: usize, d: usize, stream: *mut c_void) -> i32;
+        pub fn mivi_hip_quantized_matmul_rows_packed(out: *mut f32, out_len: usize, ggml_type: i32,
+            packed: *const u8, packed_len: usize, inputs: *const f32, inputs_len: usize, batch: usize, rows: usize,
+            cols: usize, stream: *mut c_void) -> i32;
         // lib.rs:35-72
         pub fn mivi_hip_dequantize_slice(ggml_type: i32, bytes: *const u8, bytes_len: usize, out: *mut f32,
             out_len: usize, stream: *mut c_void) -> i32;

@@ -116,6 +116,7 @@ _sig = {
     "mivi_hip_quantized_matmul_rows": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _S, _P], _I),
     "mivi_hip_pack_weights": ([_I, _P, _S, _P, _S, _S, _S, _P], _I),
     "mivi_hip_quantized_matvec_packed": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _P], _I),
+    "mivi_hip_quantized_matmul_rows_packed": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _S, _P], _I),
     "mivi_hip_dequantize_slice": ([_I, _P, _S, _P, _S, _P], _I),
     "mivi_hip_quantize_q8_0": ([_P, _S, _P, _S, _S, _P], _I),
     "mivi_hip_dot_q8_0_f32": ([_P, _S, _P, _S, _P, _S, _S, _P], _I),
@@ -244,6 +245,14 @@ def quantized_matvec_packed(out, ggml_type, packed, x, n: int, d: int, stream=No
     px, lx = _dev(x)
     _check(_lib.mivi_hip_quantized_matvec_packed(po, lo, int(ggml_type), C.c_void_p(packed.data_ptr()),
                                                  _nbytes(packed), px, lx, n, d, _stream(stream)))
+
+
+def quantized_matmul_rows_packed(out, ggml_type, packed, inputs, batch: int, rows: int, cols: int, stream=None):
+    """quantized_matmul_rows over rows packed by pack_weights."""
+    po, lo = _dev(out)
+    pi, li = _dev(inputs)
+    _check(_lib.mivi_hip_quantized_matmul_rows_packed(po, lo, int(ggml_type), C.c_void_p(packed.data_ptr()),
+                                                      _nbytes(packed), pi, li, batch, rows, cols, _stream(stream)))
 
 
 def quantized_matmul_rows(out, ggml_type, weights, inputs, batch: int, rows: int, cols: int, stream=None):

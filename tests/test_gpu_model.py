@@ -99,8 +99,8 @@ def test_batched_sequences_are_independent(hip, small_img):
 
 @pytest.mark.parametrize("B", [3, 8])
 def test_batched_full_width_matches_single_sequences(hip, B):
-    # dim 2048 (the decode shapes): the packed Q6_K head (two columns per
-    # launch), the multi-column Q4_K projections on the matrix cores (3 and 8
+    # dim 2048 (the decode shapes): the packed Q6_K head (3 and 8 columns in
+    # one eight-wave launch, its argmax partials per column), the multi-column Q4_K projections on the matrix cores (3 and 8
     # columns at d = 2048, 3 and 4 + 4 at d = 8192) with the RMSNorm, conv and
     # SwiGLU stages; every sequence's greedy tokens equal its own
     # single-sequence run bit for bit

@@ -456,6 +456,45 @@ def test_packed_q4k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols
         check_bound(oracle, Q4_K, w, x, a, rows, cols)
 
 
+@pytest.mark.parametrize("t,batch,rows", [(Q6_K, 2, 64), (Q6_K, 3, 1000), (Q6_K, 4, 4096), (Q6_K, 5, 260),
+                                           (Q6_K, 8, 65536), (Q6_K, 11, 4096), (Q4_K, 3, 64)])
+def test_packed_matmul_rows_bit_exact_with_packed_matvec(hip, torch_mod, t, batch, rows):
+    # the inputs as columns of batched packed launches (Q6_K row quads: up to
+    # eight per launch, 3-4 and 5-8 columns in the two eight-wave variants, 2
+    # in the two-column one): every input's outputs equal its own packed
+    # matvec bit for bit; a tiny, a huge, an all-zero and an infinite input
+    # ride along (the infinite one: NaN outputs, as the matvec's)
+    torch = torch_mod
+    cols = 2048
+    w = hip.synth_random_weights(t, 120 + batch, rows, cols, 0.02)
+    X = np.stack([hip.synth_normal(130 + b, cols) for b in range(batch)])
+    if batch > 2:
+        X[1] *= np.float32(1e-3)
+        X[2] *= np.float32(1e3)
+    if batch > 4:
+        X[3] = 0.0
+        X[4, 17] = np.inf
+    dw, dX = dev(torch, w), dev(torch, X.reshape(-1))
+    packed = torch.empty_like(dw)
+    hip.pack_weights(t, dw, packed, rows, cols)
+    out = torch.full((batch * rows + 1,), 5.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matmul_rows_packed(out[:batch * rows], t, packed, dX, batch, rows, cols)
+    ones = []
+    for b in range(batch):
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        hip.quantized_matvec_packed(y, t, packed, dX[b * cols:(b + 1) * cols], rows, cols)
+        ones.append(y)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert got[-1] == 5.0
+    for b in range(batch):
+        g, one = got[b * rows:(b + 1) * rows], ones[b].cpu().numpy()
+        if np.isinf(X[b]).any():
+            assert np.isnan(g).all() and np.isnan(one).all(), b
+        else:
+            assert np.array_equal(g.view(np.uint32), one.view(np.uint32)), b
+
+
 def test_packed_rejects_other_types_and_shapes(hip, torch_mod):
     torch = torch_mod
     w = torch.zeros(144 * 8 * 6, dtype=torch.uint8, device="cuda")
@@ -474,4 +513,7 @@ def test_packed_rejects_other_types_and_shapes(hip, torch_mod):
     x = torch.zeros(1024, dtype=torch.float32, device="cuda")
     with pytest.raises(hip.QuantError):
         hip.quantized_matvec_packed(out, Q6_K, w6, x, 4, 1024)
+    assert hip.last_error().code == 116
+    with pytest.raises(hip.QuantError):
+        hip.quantized_matmul_rows_packed(out, Q6_K, w6, x, 1, 4, 1024)
     assert hip.last_error().code == 116
