@@ -37,12 +37,45 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def graph_ms(torch, launch, n, reps=3):
+    """ms per launch of `n` dependent launches (launch(i, stream)) captured in
+    one HIP graph on a side stream, as the decode step runs its kernels:
+    WARM_S of untimed replays, then the median of `reps` replays timed with
+    HIP events on that stream. Without the graph a Python loop issues a
+    launch every 4-5 us, about a short GEMV's own duration, so the loop's
+    figure (host_loop_ms_per_call) partly times the host."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(n):
+            launch(i, s)
+    times = []
+    with torch.cuda.stream(s):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < WARM_S:
+            g.replay()
+            torch.cuda.synchronize()
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / n)
+    del g
+    return sorted(times)[len(times) // 2]
+
+
 def gemv_bench(torch, hip, t, rows, cols, steps, warmup, seed, packed=False):
     """Times `steps` launches over rotating weight copies; returns dict.
     packed: the weights are first rewritten once by mivi_hip_pack_weights
     (the same bytes rearranged; not timed) and the packed GEMV is timed.
     Then the same copies are read once each by mivi_hip_read_floor, a plain
-    coalesced read, timed the same way: the floor for these bytes."""
+    coalesced read, timed the same way: the floor for these bytes.
+    ms_per_call: the launches in one graph (graph_ms); host_loop_ms_per_call:
+    the same launches issued one by one from Python."""
     stream = torch.cuda.current_stream()
     w_host = hip.synth_random_weights(t, seed, rows, cols, 0.02)
     x_host = hip.synth_normal(seed + 1, cols)
@@ -76,20 +109,16 @@ def gemv_bench(torch, hip, t, rows, cols, steps, warmup, seed, packed=False):
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ev_ms = e0.elapsed_time(e1) / steps
+    loop_ms = e0.elapsed_time(e1) / steps
+    ev_ms = graph_ms(torch, lambda i, s: mv(y, t, ws[i % copies], x, rows, cols, stream=s), steps)
     for i in range(2 * copies):
         hip.read_floor(ws[i % copies], wbytes, stream=stream)
-    f0 = torch.cuda.Event(enable_timing=True)
-    f1 = torch.cuda.Event(enable_timing=True)
-    f0.record(stream)
-    for i in range(steps):
-        hip.read_floor(ws[i % copies], wbytes, stream=stream)
-    f1.record(stream)
     torch.cuda.synchronize()
-    floor_ms = f0.elapsed_time(f1) / steps
+    floor_ms = graph_ms(torch, lambda i, s: hip.read_floor(ws[i % copies], wbytes, stream=s), steps)
     algo = wbytes + cols * 4 + rows * 4
     return dict(rows=rows, cols=cols, weight_bytes=wbytes, algo_bytes=algo, copies=copies,
-                ms_per_call=ev_ms, wall_ms_per_call=1e3 * wall / steps, gbs=algo / (ev_ms * 1e-3) / 1e9,
+                ms_per_call=ev_ms, host_loop_ms_per_call=loop_ms, wall_ms_per_call=1e3 * wall / steps,
+                gbs=algo / (ev_ms * 1e-3) / 1e9,
                 read_floor_us=floor_ms * 1e3, frac_of_read_floor=floor_ms / ev_ms,
                 w_host=w_host, x_host=x_host)
 
@@ -523,18 +552,20 @@ def main():
     if a.only_q6k:
         return
     q4 = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200)
-    log(f"Q4_K GEMV 8192x2048 (GGUF rows): {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s; "
+    log(f"Q4_K GEMV 8192x2048 (GGUF rows): {q4['ms_per_call'] * 1e3:.2f} us/call, {q4['gbs']:.0f} GB/s "
+        f"({q4['host_loop_ms_per_call'] * 1e3:.2f} us issued from Python); "
         f"plain read of the same bytes {q4['read_floor_us']:.2f} us")
     q4p = gemv_bench(torch, hip, hip.GgmlType.Q4_K, 8192, 2048, a.steps * 4, a.warmup, 200, packed=True)
-    log(f"Q4_K GEMV 8192x2048 (packed row quads): {q4p['ms_per_call'] * 1e3:.2f} us/call, {q4p['gbs']:.0f} GB/s")
+    log(f"Q4_K GEMV 8192x2048 (packed row quads): {q4p['ms_per_call'] * 1e3:.2f} us/call, {q4p['gbs']:.0f} GB/s "
+        f"({q4p['host_loop_ms_per_call'] * 1e3:.2f} us issued from Python)")
     cpu = None
     if not a.no_cpu:
         cpu = cpu_gemv_baseline(hip.GgmlType.Q6_K, q6["w_host"], q6["x_host"], 65536, 2048, a.cpu_seconds)
         log(f"CPU oracle Q6_K GEMV: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
     extra = {
-        "q6k_gemv_config2_gguf_rows": {k: q6r[k] for k in ("ms_per_call", "gbs")},
-        "q4k_gemv_config1": {k: q4[k] for k in ("rows", "cols", "algo_bytes", "ms_per_call", "gbs", "copies",
-                                                "read_floor_us", "frac_of_read_floor")},
+        "q6k_gemv_config2_gguf_rows": {k: q6r[k] for k in ("ms_per_call", "host_loop_ms_per_call", "gbs")},
+        "q4k_gemv_config1": {k: q4[k] for k in ("rows", "cols", "algo_bytes", "ms_per_call", "host_loop_ms_per_call",
+                                                "gbs", "copies", "read_floor_us", "frac_of_read_floor")},
         "q6k_gemv_config2_read_floor": {"read_floor_us": q6["read_floor_us"],
                                         "read_floor_gbs": q6["weight_bytes"] / q6["read_floor_us"] / 1e3,
                                         "packed_frac_of_read_floor": q6["frac_of_read_floor"]},
@@ -543,7 +574,8 @@ def main():
     extra["q4k_gemv_config1"]["frac_of_peak"] = q4["gbs"] / HBM_PEAK_GBS
     # the same matrix packed once into row quads (mivi_hip_pack_weights, not
     # timed; the model's one-column decode GEMVs read this layout)
-    extra["q4k_gemv_config1_packed"] = {k: q4p[k] for k in ("ms_per_call", "gbs", "read_floor_us", "frac_of_read_floor")}
+    extra["q4k_gemv_config1_packed"] = {k: q4p[k] for k in ("ms_per_call", "host_loop_ms_per_call", "gbs",
+                                                            "read_floor_us", "frac_of_read_floor")}
     extra["q4k_gemv_config1_packed"]["frac_of_peak"] = q4p["gbs"] / HBM_PEAK_GBS
     extra["q4k_gemv_config1_packed"]["weight_layout"] = "packed row quads (matrix cores; bit-identical to GGUF rows)"
     if not a.no_cpu:
@@ -573,6 +605,7 @@ def main():
         "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": q6["ms_per_call"],
+        "host_loop_ms_per_step": q6["host_loop_ms_per_call"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
