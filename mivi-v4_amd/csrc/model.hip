@@ -1243,6 +1243,52 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
     }
 }
 
+// attn_combine_kernel for head_dim 64 and nsplit <= NS in one wave per query
+// head: lane s holds split s's (m, l), lane d sums dim d over the splits in
+// the four interleaved chains of attn_combine_kernel's thread groups g =
+// 0..3 (splits g, g + 4, ...) and adds them in the same order, with the same
+// reductions (wave_max, wave_sum), so the output is the same bit for bit;
+// without workgroup barriers or LDS the kernel waits for memory once and
+// ends.
+template <int NS>
+__global__ void __launch_bounds__(64) attn_combine64_kernel(const float* part_m, const float* part_l,
+                                                            const float* part_acc, float* out, const int* posp,
+                                                            int nsplit, int tt, int64_t part_s, int64_t out_s) {
+    constexpr int HD = 64;
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    part_m += b * part_s; part_l += b * part_s; part_acc += b * part_s * HD;
+    out += b * out_s;
+    const float* pm = part_m + (size_t)h * nsplit;
+    const float* pl = part_l + (size_t)h * nsplit;
+    const float* acc = part_acc + (size_t)h * nsplit * HD + lane;
+    const int pos = posp[b];
+    const bool own = lane < nsplit;
+    const float m0 = own ? pm[lane] : -INFINITY, l0 = own ? pl[lane] : 0.f;
+    float av[NS];
+#pragma unroll
+    for (int k = 0; k < NS; k++) av[k] = k < nsplit ? acc[(size_t)k * HD] : 0.f;
+    const int ntiles = (pos + 1 + tt - 1) / tt;
+    const int tps = (ntiles + nsplit - 1) / nsplit;
+    const int nv = (ntiles + tps - 1) / tps;  // splits that hold tiles (wave-uniform)
+    const float M = wave_max(lane < nv ? m0 : -INFINITY);
+    float ws = 0.f, L = 0.f;
+    if (lane < nv) {
+        ws = expf(m0 - M);
+        L = l0 * ws;
+    }
+    L = wave_sum(L);
+    float o = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        float og = 0.f;
+#pragma unroll
+        for (int k = g; k < NS; k += 4)
+            if (k < nv) og = fmaf(av[k], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ws), k)), og);
+        o = g == 0 ? og : o + og;
+    }
+    out[(size_t)h * HD + lane] = L > 0.f ? o * (1.0f / L) : 0.f;
+}
+
 // sampler.rs:305-316: index of the first strict maximum (NaN never wins).
 // Writes the token for the next step, records it, advances pos and the
 // ShortConv phase of the sequence.
@@ -1406,6 +1452,16 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
         }
 #undef ATT
         tt = attn_tile_tokens(c.head_dim);
+    }
+    if (c.head_dim == 64 && a.nsplit <= 64) {
+#define CMB(NS)                                                                                                    \
+    hipLaunchKernelGGL(attn_combine64_kernel<NS>, dim3((unsigned)c.n_heads, nseq), dim3(64), 0, s, a.part_m, a.part_l, \
+                       a.part_acc, out, a.pos, a.nsplit, tt, a.part_s, out_s)
+        if (a.nsplit <= 16) CMB(16);
+        else if (a.nsplit <= 32) CMB(32);
+        else CMB(64);
+#undef CMB
+        return;
     }
     hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)c.n_heads, nseq), dim3(kWG), 0, s, a.part_m, a.part_l,
                        a.part_acc, out, a.pos, a.nsplit, tt, (int)c.head_dim, a.part_s, out_s);
