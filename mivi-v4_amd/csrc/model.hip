@@ -1298,7 +1298,7 @@ __global__ void __launch_bounds__(64) attn_combine64_kernel(const float* part_m,
 // + b * vstride; tok, pos, phase + b).
 __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logits, const int* part_idx, int n,
                                                               uint32_t* tok, int* pos, int* phase, uint32_t* history,
-                                                              const int* step, int stride, int seq, int do_argmax,
+                                                              const int* pos0, int stride, int seq, int do_argmax,
                                                               int64_t vstride, EmbedNext en) {
     __shared__ float bv[16];
     __shared__ int bi[16];
@@ -1307,7 +1307,7 @@ __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logit
         const int b = blockIdx.x;
         logits += b * vstride;
         if (part_idx) part_idx += b * vstride;
-        tok += b; pos += b; phase += b;
+        tok += b; pos += b; pos0 += b; phase += b;
         seq += b;
         en.x += b * en.xs;
     }
@@ -1335,7 +1335,8 @@ __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logit
             if (id == 0x7FFFFFFF) id = 0;
             *tok = (uint32_t)id;
             chosen = (uint32_t)id;
-            if (history) history[(size_t)(*step) * stride + seq] = (uint32_t)id;
+            // step k of a generate call runs at pos0 + k (pos advances below)
+            if (history) history[(size_t)(*pos - *pos0) * stride + seq] = (uint32_t)id;
         }
         if (en.table) {
             __syncthreads();
@@ -1350,9 +1351,10 @@ __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* logit
 
 __global__ void step_counter_kernel(int* step) { *step += 1; }
 
-__global__ void set_ctrl_kernel(uint32_t* tok, int* pos, uint32_t t, int p) {
+__global__ void set_ctrl_kernel(uint32_t* tok, int* pos, int* pos0, uint32_t t, int p) {
     *tok = t;
     *pos = p;
+    *pos0 = p;
 }
 
 __global__ void set_int_kernel(int* dst, int v) { *dst = v; }
@@ -1398,8 +1400,9 @@ struct SeqStrides {
 struct Ctrl {  // device control block
     uint32_t tok[64];
     int pos[64];
+    int pos0[64];  // position at the last set_ctrl: a greedy step's index is pos - pos0
     int phase[64];
-    int step;
+    int step;      // the sampled generation's step counter
 };
 
 }  // namespace
@@ -1723,7 +1726,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
     }
     hipLaunchKernelGGL(argmax_advance_kernel, dim3((unsigned)nb), dim3(1024), 0, s, parts ? s0.part_val : s0.logits,
                        parts ? s0.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b0],
-                       &m->ctrl->pos[b0], &m->ctrl->phase[b0], argmax ? m->history : nullptr, &m->ctrl->step,
+                       &m->ctrl->pos[b0], &m->ctrl->phase[b0], argmax ? m->history : nullptr, &m->ctrl->pos0[b0],
                        (int)c.max_batch, (int)b0, (argmax && logits) ? 1 : 0,
                        (int64_t)(parts ? z.parts : z.logits), embed_next_args(m, s0.x, embed_next && argmax && logits));
     MIVI_HIP_CHECK(hipGetLastError());
@@ -2272,6 +2275,7 @@ static int32_t check_tok_pos(mivi_model* m, uint32_t token, size_t pos) {
 static int32_t set_ctrl(mivi_model* m, size_t seq, uint32_t token, size_t pos) {
     // the phase counter keeps running; only token and position are set
     hipLaunchKernelGGL(set_ctrl_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->tok[seq], &m->ctrl->pos[seq],
+                       &m->ctrl->pos0[seq],
                        token, (int)pos);
     MIVI_HIP_CHECK(hipGetLastError());
     return MIVI_OK;
@@ -2372,10 +2376,9 @@ extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, c
     }
     if (n_steps == 0) return clear_error();
     for (size_t b = 0; b < batch; b++) {
-        int32_t rc = set_ctrl(m, b, tokens[b], pos[b]);
+        int32_t rc = set_ctrl(m, b, tokens[b], pos[b]);  // (pos0: the step index is pos - pos0)
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step, 0);
     {
         // the first step's embeddings; each step embeds the next tokens itself
         const EmbedNext en = embed_next_args(m, m->seqs[0].x, true);
@@ -2391,7 +2394,6 @@ extern "C" int32_t mivi_hip_model_generate_greedy(mivi_model* m, size_t batch, c
         MIVI_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
         int32_t rc = MIVI_OK;
         rc = enqueue_batch_step(m, batch, m->stream);
-        if (!rc) hipLaunchKernelGGL(step_counter_kernel, dim3(1), dim3(1), 0, m->stream, &m->ctrl->step);
         hipError_t e = hipStreamEndCapture(m->stream, &gr);
         if (rc) return rc;
         if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
