@@ -53,6 +53,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // max|v| * 2^-e <= 1; xh/xl = fp16 hi/lo of v * 2^-e; sh/sl = fp16 hi/lo of
 // each 32-value sub-block sum of v * 2^-e (fp32). Rows >= M are zero.
 typedef _Float16 half8p __attribute__((ext_vector_type(8)));
+// R > 0: K = 2048 R, the thread's 8 R values (and norm weights or up values)
+// loaded once and held in registers through both reductions; R = 0: any K,
+// each pass re-reading them. The same operations in the same order either way.
+template <int R>
 __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ X, const float* __restrict__ X2,
                                                         const float* __restrict__ norm_w, float eps, int pro,
                                                         int64_t ldx, int M, int K, _Float16* __restrict__ xh,
@@ -75,38 +79,65 @@ __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict_
         const f32x4 a = *(const f32x4*)(p + i), b = *(const f32x4*)(p + i + 4);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     };
+    constexpr int RR = R > 0 ? R : 1;
+    float xr[RR][8], wr[RR][8];  // R > 0: x and (norm w | up) of stretch r
+    if constexpr (R > 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) { xr[r][q] = 0.f; wr[r][q] = 0.f; }
+            if (live) {
+                load8(x, 2048 * r + 8 * threadIdx.x, xr[r]);
+                if (pro == PRO_RMSNORM) load8(norm_w, 2048 * r + 8 * threadIdx.x, wr[r]);
+                else if (pro == PRO_SWIGLU) load8(x2, 2048 * r + 8 * threadIdx.x, wr[r]);
+            }
+        }
+    }
     float scale = 1.0f;
     if (pro == PRO_RMSNORM) {
         float ss = 0.f;
-        if (live)
+        if constexpr (R > 0) {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int q = 0; q < 8; q++) ss = fmaf(xr[r][q], xr[r][q], ss);
+        } else if (live) {
             for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
                 float v[8];
                 load8(x, i, v);
 #pragma unroll
                 for (int q = 0; q < 8; q++) ss = fmaf(v[q], v[q], ss);
             }
+        }
         ss = block_red(ss, false);
         scale = 1.0f / sqrtf(ss / (float)K + eps);
     }
-    auto values = [&](int i, float (&v)[8]) {  // pro(x)[i .. i + 8)
-        load8(x, i, v);
+    auto values = [&](int r, int i, float (&v)[8]) {  // pro(x)[i .. i + 8), i = 2048 r + 8 t
+        float w[8];
+        if constexpr (R > 0) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) { v[q] = xr[r][q]; w[q] = wr[r][q]; }
+        } else {
+            load8(x, i, v);
+            if (pro == PRO_RMSNORM) load8(norm_w, i, w);
+            else if (pro == PRO_SWIGLU) load8(x2, i, w);
+        }
         if (pro == PRO_RMSNORM) {
-            float w[8];
-            load8(norm_w, i, w);
 #pragma unroll
             for (int q = 0; q < 8; q++) v[q] = v[q] * scale * w[q];
         } else if (pro == PRO_SWIGLU) {
-            float u[8];
-            load8(x2, i, u);
 #pragma unroll
-            for (int q = 0; q < 8; q++) v[q] = silu_f(v[q]) * u[q];
+            for (int q = 0; q < 8; q++) v[q] = silu_f(v[q]) * w[q];
         }
     };
+    // stretch r of the thread: values [2048 r + 8 t, + 8)
+    auto more = [&](int r) { return R > 0 ? r < R : 2048 * r + 8 * (int)threadIdx.x < K; };
     float mx = 0.f;
     if (live)
-        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+        for (int r = 0; more(r); r++) {  // (R > 0: unrolled, the registers indexed statically)
+            const int i = 2048 * r + 8 * threadIdx.x;
             float v[8];
-            values(i, v);
+            values(r, i, v);
 #pragma unroll
             for (int q = 0; q < 8; q++) mx = fmaxf(mx, fabsf(v[q]));
         }
@@ -116,9 +147,10 @@ __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict_
     if (mx > 0.f && mx <= 3.40282347e38f) frexpf(mx, &e);
     const float inv = ldexpf(1.0f, -e);
     if (threadIdx.x == 0) rowscale[m] = live ? ldexpf(1.0f, e) : 0.f;
-    for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+    for (int r = 0; more(r); r++) {
+        const int i = 2048 * r + 8 * threadIdx.x;
         float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (live) values(i, v);
+        if (live) values(r, i, v);
 #pragma unroll
         for (int q = 0; q < 8; q++) v[q] *= inv;  // exact: power-of-two scaling
         half8p hv, lv;
@@ -437,7 +469,9 @@ static int32_t rows_q4k_mfma(int pro, const GemvArgs& a, hipStream_t s) {
     _Float16* sh = (_Float16*)(p + 2 * bx);
     _Float16* sl = (_Float16*)(p + 2 * bx + bs);
     float* rs = (float*)(p + 2 * bx + 2 * bs);
-    hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)mp), dim3(256), 0, s, a.x, a.x2, a.norm_w, a.eps, pro, a.xs,
+    auto prep = K == 2048 ? gemm_prep_kernel<1> : K == 4096 ? gemm_prep_kernel<2> : K == 8192 ? gemm_prep_kernel<4>
+                                                                                             : gemm_prep_kernel<0>;
+    hipLaunchKernelGGL(prep, dim3((unsigned)mp), dim3(256), 0, s, a.x, a.x2, a.norm_w, a.eps, pro, a.xs,
                        (int)batch, (int)K, xh, xl, sh, sl, rs);
     for (int i = 0; i < a.nseg; i++) {
         const int rows = a.seg[i].n;
