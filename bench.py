@@ -376,13 +376,13 @@ def config5_weight_bytes(cfg, batch):
     the d = 2048 Q4_K projections take all the batch's columns (up to 8) in one
     launch and read their weights once; the K = 8192 FFN down runs groups of
     four columns side by side, each reading the matrix; the packed Q6_K head
-    takes two columns per launch."""
+    takes up to eight columns per launch and reads each row quad once."""
     from mivi_hip.synthmodel import weight_bytes_per_token
     wb = weight_bytes_per_token(**cfg)
     down = cfg["n_layers"] * cfg["dim"] * cfg["hidden"] // 256 * 144
     head = cfg["vocab"] * cfg["dim"] // 256 * 210
     rest = wb - down - head
-    return rest * -(-batch // 8) + down * -(-batch // 4) + head * -(-batch // 2)
+    return rest * -(-batch // 8) + down * -(-batch // 4) + head * -(-batch // 8)
 
 
 def batched_decode_bench(torch, hip, batch, ctx, steps, cpu_budget_s=0.0):
@@ -428,7 +428,7 @@ def batched_decode_bench(torch, hip, batch, ctx, steps, cpu_budget_s=0.0):
                kv_gbs_over_whole_step=kv_bytes * steps / dt / 1e9, weight_bytes_per_step=wbs,
                gbs_whole_step=(kv_bytes + wbs) * steps / dt / 1e9,
                note=("weight_bytes_per_step: the d = 2048 projections read their weights once for the 8 columns, "
-                     "the K = 8192 FFN down once per group of four columns, the packed head once per two; "
+                     "the K = 8192 FFN down once per group of four columns, the packed head once per eight; "
                      "kv_gbs_over_whole_step divides the KV bytes by the whole step time, not the attention "
                      "kernels' time; caches synthetic, see docstring"),
                first_tokens=[int(v) for v in out[:4, 0]])
