@@ -1243,7 +1243,7 @@ __global__ void __launch_bounds__(kWG) attn_combine_kernel(const float* part_m, 
     }
 }
 
-// attn_combine_kernel for head_dim 64 and nsplit <= NS in one wave per query
+// attn_combine_kernel for head_dim 64 and nsplit <= NS (16 or 32) in one wave per query
 // head: lane s holds split s's (m, l), lane d sums dim d over the splits in
 // the four interleaved chains of attn_combine_kernel's thread groups g =
 // 0..3 (splits g, g + 4, ...) and adds them in the same order, with the same
@@ -1456,13 +1456,15 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
 #undef ATT
         tt = attn_tile_tokens(c.head_dim);
     }
-    if (c.head_dim == 64 && a.nsplit <= 64) {
+    // (at 33-64 splits, a wave's 64 + 3 loads exceed the 63 it may have in
+    // flight: the 256-thread merge is faster there, 2365 against 2303 tok/s
+    // on config 4 with the loads split over the wave's halves)
+    if (c.head_dim == 64 && a.nsplit <= 32) {
 #define CMB(NS)                                                                                                    \
     hipLaunchKernelGGL(attn_combine64_kernel<NS>, dim3((unsigned)c.n_heads, nseq), dim3(64), 0, s, a.part_m, a.part_l, \
                        a.part_acc, out, a.pos, a.nsplit, tt, a.part_s, out_s)
         if (a.nsplit <= 16) CMB(16);
-        else if (a.nsplit <= 32) CMB(32);
-        else CMB(64);
+        else CMB(32);
 #undef CMB
         return;
     }
