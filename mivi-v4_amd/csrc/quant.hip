@@ -2677,9 +2677,13 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                          a.st_out && (a.conv_mode == 2 || a.conv_w);
                 if (!ok) return mivi::set_error(MIVI_ERR_UNSUPPORTED, "no Q4_K row-quad GEMV for this shape");
                 const int nsteps = ep == mivi::EPI_SWIGLU ? a.seg[0].n / 4 : ep == mivi::EPI_CONV ? a.seg[0].n / 12 : n / 4;
-                // one workgroup per CU at most, each wave a whole number of steps;
-                // PD: steps in flight, no more than a wave has
-                const int qg = std::max(1, std::min((nsteps + 3) / 4, mivi::num_cus()));
+                // one workgroup per CU at most (two for gate|up), each wave a
+                // whole number of steps; PD: steps in flight, no more than a wave has
+                // (gate|up: two workgroups per CU, one step of two quads per
+                // wave: 2391 against 2365 tok/s on config 4; a store GEMV of
+                // the same step count is slower so: config 1 4.53 against 4.02 us)
+                const int qf = ep == mivi::EPI_SWIGLU ? 2 : 1;
+                const int qg = std::max(1, std::min((nsteps + 3) / 4, mivi::num_cus() * qf));
                 const int cmax = (nsteps + qg * 4 - 1) / (qg * 4);
                 const int pd = (cmax >= 4 && K == 2048) ? 4 : cmax >= 2 ? 2 : 1;  // K = 8192: 2 (registers)
 #define LQ4(EPI, S, PD) hipLaunchKernelGGL((gemv_q4k_quad_kernel<PRO, EPI, S, PD>), dim3(qg), dim3(kWG), 0, s, a)
