@@ -1520,7 +1520,16 @@ struct mivi_model {
         void* q = nullptr;
         hipError_t e = hipMalloc(&q, std::max<size_t>(1, count * sizeof(T)));
         if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "hipMalloc(%zu) failed: %s", count * sizeof(T), hipGetErrorString(e));
-        hipMemset(q, 0, std::max<size_t>(1, count * sizeof(T)));
+        // zeroed on the model's stream and waited for: the stream is
+        // non-blocking, so a null-stream memset could still be running (and
+        // overwrite data) when the stream's next copy or kernel touches the
+        // buffer, as the first prefill does right after allocating its tiles
+        e = hipMemsetAsync(q, 0, std::max<size_t>(1, count * sizeof(T)), stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) {
+            (void)hipFree(q);
+            return set_error(MIVI_ERR_HIP, "zeroing %zu bytes failed: %s", count * sizeof(T), hipGetErrorString(e));
+        }
         allocs.push_back(q);
         *p = (T*)q;
         return MIVI_OK;
