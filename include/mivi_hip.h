@@ -177,7 +177,9 @@ typedef struct mivi_model_info {
     float rope_base, rms_norm_eps;
     int32_t kv_precision, yarn;
     float yarn_scale;
-    size_t weight_bytes;   /* device bytes of the packed weights */
+    size_t weight_bytes;   /* device bytes of the weights: the GGUF tensor data plus the
+                              packed copies kept beside it (Q6_K head, Q4_K row quads);
+                              MIVI_NO_PACK=1 at create leaves the copies out */
     size_t kv_bytes;       /* device bytes of K + V for all sequences */
 } mivi_model_info;
 

@@ -2122,6 +2122,7 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         if ((rc = m->alloc(&m->head_packed, bytes))) return fail(rc);
         if ((rc = launch_pack_q6k(m->head.w, m->head_packed, c.vocab_size, c.dim, nullptr))) return fail(rc);
         if (hipDeviceSynchronize() != hipSuccess) return fail(set_error(MIVI_ERR_HIP, "packing the head failed"));
+        c.weight_bytes += bytes;
     }
     // one-column decode GEMVs stream Q4_K projections as row quads (matrix
     // cores, bit-identical to the GGUF rows): a packed copy of each, the GGUF
@@ -2146,6 +2147,7 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         }
         if (total && hipDeviceSynchronize() != hipSuccess)
             return fail(set_error(MIVI_ERR_HIP, "packing the Q4_K projections failed"));
+        c.weight_bytes += total;
     }
     {
         size_t bs, ts;
@@ -2179,8 +2181,10 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         std::vector<float> cs, sn;
         host_rope_table(cs, sn, c.head_dim, c.max_seq_len, c.rope_base, c.yarn, c.yarn_scale);
         if ((rc = m->alloc(&m->rope_cos, cs.size())) || (rc = m->alloc(&m->rope_sin, sn.size()))) return fail(rc);
-        hipMemcpy(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
-        hipMemcpy(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+        hipError_t e = hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, m->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) return fail(set_error(MIVI_ERR_HIP, "uploading the RoPE table failed: %s", hipGetErrorString(e)));
     }
 
     // run state, KV caches
@@ -2890,7 +2894,9 @@ static int32_t prefix_insert_node(mivi_prefix_cache* pc, mivi_model* m, size_t s
     nd.has_parent = has_parent;
     nd.standalone = prefix_chunk_hash(0, tokens, n_tokens);
     nd.tokens.assign(tokens, tokens + n_tokens);
-    const size_t end = m->kv_packed ? std::min<size_t>((pos + 15) / 16 * 16, m->info.max_seq_len) : pos;
+    // the group layout copies whole 16-token groups (the layer buffer holds
+    // whole groups, also past a max_seq_len that is not a multiple of 16)
+    const size_t end = m->kv_packed ? (pos + 15) / 16 * 16 : pos;
     const size_t iv = (end - kv_start) * pc->row_bytes;  // one layer's interval (rows, or whole groups)
     nd.kv_bytes = pc->n_attn * iv;
     nd.conv_bytes = pc->conv_len * 4;

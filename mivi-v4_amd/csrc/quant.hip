@@ -2816,6 +2816,8 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                 MIVI_HIP_CHECK(hipGetLastError());
                 return MIVI_OK;
             }
+            // the packed unit-plane kernel keeps two columns in registers
+            if (a.packed && a.ncol > 2) return MIVI_ERR_UNSUPPORTED;
             if (K == 2048) {
                 if (ep == mivi::EPI_STORE) {
                     if (a.packed) {
@@ -3008,13 +3010,14 @@ int gemv_argmax_parts(int32_t t, int K, int n, bool packed) {
     return 4 * std::max(1, std::min((ngroups + 3) / 4, num_cus() * per_cu));
 }
 
-// Most columns one batched streaming launch takes at depth K, 1 where there
-// is no batched kernel: 8 at K = 2048 (digits in LDS: 6 KB per column), 4 at
-// K = 8192 (24 KB per column); packed Q6_K rows take 8 (the eight-wave
-// quad kernel).
-static int gemv_max_cols(int32_t t, int K, bool packed, int pro = PRO_NONE, int epilogue = EPI_STORE) {
+// Most columns one batched streaming launch takes at depth K for n rows, 1
+// where there is no batched kernel: 8 at K = 2048 (digits in LDS: 6 KB per
+// column), 4 at K = 8192 (24 KB per column); packed Q6_K row quads take 8
+// (the eight-wave quad kernel), packed unit planes (rows not a multiple of
+// four) 2 (the streaming kernel with both columns in registers).
+static int gemv_max_cols(int32_t t, int K, int n, bool packed, int pro = PRO_NONE, int epilogue = EPI_STORE) {
     if ((t != MIVI_GGML_Q4_K && t != MIVI_GGML_Q6_K) || env_int("MIVI_GEMV_V1", 0)) return 1;
-    if (packed) return (t == MIVI_GGML_Q6_K && K == 2048) ? kMaxGemvCols : 1;
+    if (packed) return (t == MIVI_GGML_Q6_K && K == 2048) ? (quad_layout(n, K) ? kMaxGemvCols : 2) : 1;
     // Q4_K at K = 8192 on the matrix cores: column groups of four run side by
     // side in one launch (one workgroup per CU each)
     if (K == 8192 && t == MIVI_GGML_Q4_K && pro == PRO_NONE && epilogue == EPI_STORE &&
@@ -3054,7 +3057,7 @@ int32_t launch_gemv_ex(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     if (a.ncol > 1) {
         // column groups of the batched kernel; columns it cannot take run
         // one launch each
-        const int cap = gemv_max_cols(t, a.K, a.packed != 0, pro, a.epilogue);
+        const int cap = gemv_max_cols(t, a.K, n, a.packed != 0, pro, a.epilogue);
         for (int c0 = 0; c0 < a.ncol;) {
             const int nc = std::min(cap, a.ncol - c0);
             int32_t rc = nc > 1 ? launch_by_pro(t, pro, column_args(a, c0, nc), n, s) : MIVI_ERR_UNSUPPORTED;

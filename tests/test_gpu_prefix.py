@@ -260,3 +260,43 @@ def test_suffix_match(hip, img):
     assert got == (64, 128, h1)
     # suffix positions must be chunk-aligned: a 64-token suffix at absolute 70 is skipped
     assert pc.find_longest_suffix_match(6, np.concatenate([history, chunk1])) is None
+
+
+def test_q8_group_snapshots_near_unaligned_max_ctx(hip, img):
+    """A Q8_0 model whose max_ctx (1000) is not a multiple of the 16-token
+    group: a full snapshot inside the last, partial group holds whole groups
+    (every kv head's codes and scales of those tokens), and a snapshot at the
+    last chunk boundary restores and continues bit for bit."""
+    kvp = hip.KvPrecision.Q8_0
+    rng = np.random.default_rng(59)
+    prompt = rng.integers(0, SMALL["vocab"], 999).astype(np.uint32)
+
+    def mk():
+        m = hip.Model(img, max_ctx=1000, kv_precision=kvp)
+        m.set_prefill_strategy(32)
+        return m
+
+    ref = mk()
+    ref.prefill(prompt[:-1], 0)
+    want = ref.forward(int(prompt[-1]), len(prompt) - 1)
+    # snapshot bytes: 992 tokens = 62 whole groups, 996 tokens = 63
+    m = mk()
+    m.prefill(prompt[:996], 0)
+    pa, pb = hip.PrefixCache(chunk_size=496), hip.PrefixCache(chunk_size=496)
+    pa.insert_chunk(m, 0, prompt[:992], 0, 992)
+    pb.insert_chunk(m, 0, prompt[:996], 0, 996)
+    row = (SMALL["dim"] // SMALL["n_heads"] * SMALL["n_kv"]) // 32 * 34
+    n_attn = len(SMALL["attn_layers"])
+    assert pb.memory_usage_bytes() - pa.memory_usage_bytes() == 2 * n_attn * 16 * row + 4 * 4
+    # two delta chunks of 496 tokens up to 992, restored into a fresh model
+    pc = hip.PrefixCache(chunk_size=496)
+    m = mk()
+    m.prefill(prompt[:496], 0)
+    h0 = pc.insert_delta_chunk(m, 0, prompt[:496], 0, 496)
+    m.prefill(prompt[496:992], 496)
+    pc.insert_delta_chunk(m, h0, prompt[496:992], 1, 992)
+    fresh = mk()
+    matched, _ = pc.restore_longest_prefix(fresh, prompt)
+    assert matched == 992
+    fresh.prefill(prompt[992:-1], 992)
+    assert np.array_equal(fresh.forward(int(prompt[-1]), len(prompt) - 1), want)

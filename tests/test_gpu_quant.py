@@ -457,11 +457,13 @@ def test_packed_q4k_matvec_bit_exact_with_raw(hip, oracle, torch_mod, rows, cols
 
 
 @pytest.mark.parametrize("t,batch,rows", [(Q6_K, 2, 64), (Q6_K, 3, 1000), (Q6_K, 4, 4096), (Q6_K, 5, 260),
-                                           (Q6_K, 8, 65536), (Q6_K, 11, 4096), (Q4_K, 3, 64)])
+                                           (Q6_K, 8, 65536), (Q6_K, 11, 4096), (Q4_K, 3, 64),
+                                           (Q6_K, 3, 1001), (Q6_K, 6, 1002), (Q6_K, 8, 1003), (Q6_K, 5, 65535)])
 def test_packed_matmul_rows_bit_exact_with_packed_matvec(hip, torch_mod, t, batch, rows):
     # the inputs as columns of batched packed launches (Q6_K row quads: up to
     # eight per launch, 3-4 and 5-8 columns in the two eight-wave variants, 2
-    # in the two-column one): every input's outputs equal its own packed
+    # in the two-column one; unit planes, rows not a multiple of four: two
+    # columns per launch): every input's outputs equal its own packed
     # matvec bit for bit; a tiny, a huge, an all-zero and an infinite input
     # ride along (the infinite one: NaN outputs, as the matvec's)
     torch = torch_mod
