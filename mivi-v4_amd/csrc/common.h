@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/mivi_hip.h"
 
@@ -26,6 +27,12 @@ int32_t clear_error();
             return ::mivi::set_error(MIVI_ERR_HIP, "%s failed: %s", #expr,            \
                                      hipGetErrorString(e_));                          \
     } while (0)
+
+// Integer tuning knob from the environment (dflt when unset or empty).
+inline int env_knob(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
 
 inline int num_cus() {
     static int n = 0;

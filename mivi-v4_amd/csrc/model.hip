@@ -900,16 +900,55 @@ __global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
     }
 }
 
+// The query heads of one wave, loaded before anything else the wave reads
+// (lane l < 32 holds dims 2l, 2l + 1 of each head, with the per-head norm
+// weights and the RoPE row), then normalised and rotated into dst[h]
+// (transformer.rs:81-96, rope.rs:452-473), as wave_prep_heads4.
+struct QHeads {
+    float v0[4], v1[4], w0, w1, c, s;
+    __device__ __forceinline__ void load(const float* src, int nh, const float* nw, const float* cs, const float* sn) {
+        const int l = threadIdx.x & 63;
+        const bool on = l < 32;
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            v0[h] = on && h < nh ? src[h * 64 + 2 * l] : 0.f;
+            v1[h] = on && h < nh ? src[h * 64 + 2 * l + 1] : 0.f;
+        }
+        w0 = nw && on ? nw[2 * l] : 1.f;
+        w1 = nw && on ? nw[2 * l + 1] : 1.f;
+        c = on ? cs[l] : 0.f;
+        s = on ? sn[l] : 0.f;
+    }
+    __device__ __forceinline__ void finish(float (*dst)[64], int nh, bool norm, float eps) const {
+        const int l = threadIdx.x & 63;
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            if (h >= nh) break;
+            float x0 = v0[h], x1 = v1[h];
+            if (norm) {
+                const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+                const float sc = 1.0f / sqrtf(ss / 64.0f + eps);
+                x0 = x0 * sc * w0;
+                x1 = x1 * sc * w1;
+            }
+            if (l < 32) {
+                dst[h][2 * l] = x0 * c - x1 * s;
+                dst[h][2 * l + 1] = x0 * s + x1 * c;
+            }
+        }
+    }
+};
+
 // ------------------------------------------- fp16 attention on the matrix cores
 //
 // fp16 caches (token rows of n_kv_heads x 64 halves, the tile kernel's
-// layout) with head_dim 64 and at most 4 query heads per kv head, as the
-// Q8_0 kernel above: one wave per (kv head, split), all kv heads of a split
-// in one workgroup, each wave walking its split's 16-token groups with its
-// own online softmax and no workgroup barrier. Lane t + 16c loads dims
-// 16c..16c+15 of token t of the group (32 bytes of K, 32 of V; rows past the
-// position read the position's row, so the last group of the cache never
-// reads past it).
+// layout) with head_dim 64 and at most 4 query heads per kv head. One wave
+// (workgroup) per (kv head, split) of a sequence: the split holds groups
+// [split * tps, ...) of 16 tokens, tps = ceil(groups / nsplit) (the rule the
+// split merge reads back), walked with an online softmax. Lane t + 16c loads
+// dims 16c..16c+15 of token t of a group (32 bytes of K, 32 of V; rows past
+// the position read the position's row, so the last group never reads past
+// it).
 //  scores  v_mfma_f32_16x16x16_f16, four per group: A row 4h + i holds the
 //          query of head h in log2 units (scale * log2 e folded in) as an
 //          fp16 hi part (i = 0) and lo part (i = 1; q = hi + lo to about
@@ -919,9 +958,11 @@ __global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
 //          t + 16h receives head h's hi and lo sums for token t: products
 //          of fp16 values are exact, summed in f32;
 //  values  O[h][d] += p_h(t) v(t, d) in f32 on the VALU, as the Q8_0 kernel.
-// The owner split stores the current K/V first and uses them, as stored,
-// for its token's lanes (nothing is read back). Tokens of the last group
-// past the position get p = 0.
+// The wave loads its query heads (and the owner, the split holding the
+// current token, its K and V) before its cache groups, so those small loads
+// wait for no group. The owner stores the current K/V after issuing its
+// group loads and patches its token's lanes with them as stored (nothing is
+// read back). Tokens of the last group past the position get p = 0.
 struct F16Group {
     u32x4 k0, k1;  // K dims 16c .. 16c+15 of token lane & 15 (fp16 pairs)
     u32x4 v0, v1;  // V, the same
@@ -932,16 +973,14 @@ inline bool attn_f16_mfma_ok(int kv_precision, int hd, int n_heads, int n_kv) {
     return kv_precision == MIVI_KV_F16 && hd == 64 && n_kv > 0 && n_heads % n_kv == 0 && n_heads / n_kv <= 4;
 }
 
-template <int PD, int W>  // groups in flight per wave; waves (kv heads) per workgroup
-__global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
+template <int PD>  // groups in flight
+__global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
     constexpr int HD = 64, G = kQ8GroupTokens;
-    __shared__ __attribute__((aligned(16))) float qs[W][4][HD];   // [wave][head][dim]
-    __shared__ __attribute__((aligned(16))) float cur[W][2][HD];  // owner: current K/V as stored
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    int kvg, split;
-    if (!attn_tile_of((a.n_kv_heads + W - 1) / W, a.nsplit, &kvg, &split)) return;  // workgroup-uniform
-    const int kvh = kvg * W + wave;
-    if (kvh >= a.n_kv_heads) return;  // wave-uniform (no workgroup barrier below)
+    __shared__ __attribute__((aligned(16))) float qs[4][HD];       // [head][dim]
+    __shared__ __attribute__((aligned(16))) uint32_t curw[2][32];  // owner: current K/V as stored (fp16 pairs)
+    const int lane = threadIdx.x & 63;
+    int kvh, split;
+    if (!attn_tile_of(a.n_kv_heads, a.nsplit, &kvh, &split)) return;  // workgroup-uniform
     {
         const int b = blockIdx.y;
         a.q += b * a.qkv_s; a.k += b * a.qkv_s; a.v += b * a.qkv_s;
@@ -952,20 +991,32 @@ __global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
     const int hpk = a.n_heads / a.n_kv_heads;
     const int pos = *a.pos;
     const int ng = (pos + G) / G;
-    const int gps = (ng + a.nsplit - 1) / a.nsplit;
-    const int g0 = split * gps, g1 = min(ng, g0 + gps);
-    if (g0 >= g1) return;  // beyond the context
+    const int tps = (ng + a.nsplit - 1) / a.nsplit;
+    const int g0 = split * tps, g1 = min(ng, g0 + tps);
+    if (g0 >= g1) return;  // the split is beyond the context
     const float* cs = a.rope_cos + (size_t)pos * (HD / 2);
     const float* sn = a.rope_sin + (size_t)pos * (HD / 2);
     const int t = lane & 15, c = lane >> 4;
+    const bool own = g1 == ng && !a.keep_cache;  // the split holding the current token
 
-    const bool own = g1 == ng && !a.keep_cache;  // wave-uniform: the split holding the current token
-    u32x4 ck0 = {}, ck1 = {}, cv0 = {}, cv1 = {};  // its K/V as stored (fp16 bits of dims 16c .. +15)
+    // 1. the small loads: query heads (+ norm weights, RoPE row); the owner's
+    //    current K (pair 2l, 2l + 1 in lane l < 32, its norm weights) and V
+    QHeads qh;
+    qh.load(a.q + (size_t)(kvh * hpk) * HD, hpk, a.q_norm, cs, sn);
+    float k0 = 0.f, k1 = 0.f, kn0 = 1.f, kn1 = 1.f, vv0 = 0.f, vv1 = 0.f;
+    if (own && lane < 32) {
+        const float* kp = a.k + (size_t)kvh * HD + 2 * lane;
+        const float* vp = a.v + (size_t)kvh * HD + 2 * lane;
+        k0 = kp[0]; k1 = kp[1]; vv0 = vp[0]; vv1 = vp[1];
+        if (a.k_norm) { kn0 = a.k_norm[2 * lane]; kn1 = a.k_norm[2 * lane + 1]; }
+    }
 
-    // 2. group loads (past the split's end the last group is re-read)
+    // 2. the first PD groups (the current token's lanes read the cache's old
+    //    bytes there and are patched below)
     const size_t rb = a.row_bytes;
     const uint8_t* kc = a.kc + (size_t)kvh * (HD * 2) + 32 * c;
     const uint8_t* vc = a.vc + (size_t)kvh * (HD * 2) + 32 * c;
+    u32x4 ck0 = {}, ck1 = {}, cv0 = {}, cv1 = {};  // the owner's current K/V as stored (dims 16c .. +15)
     auto load = [&](F16Group& q, int g) {
         g = min(g, g1 - 1);
         const int row = g * G + t;
@@ -979,9 +1030,6 @@ __global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
             q.v1 = __builtin_nontemporal_load((gau32x4*)(vc + o + 16));
         }
     };
-    // 1. the first PD groups' loads (the current token's lanes re-read the
-    //    cache's old bytes there and are patched below), then 2. the owner
-    //    stores the current K/V and patches its lanes with them
     F16Group ring[PD];
 #pragma unroll
     for (int i = 0; i < PD; i++) {
@@ -992,18 +1040,30 @@ __global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
         ring[i].v0 = __builtin_nontemporal_load((gau32x4*)(vc + o));
         ring[i].v1 = __builtin_nontemporal_load((gau32x4*)(vc + o + 16));
     }
+
+    // 3. the owner forms its K (per-head RMSNorm, RoPE; transformer.rs:81-96,
+    //    rope.rs:452-473) and V as fp16, stores them into the cache row
+    //    (cache.rs:395-461) and patches its token's lanes
     if (own) {
-        attn_store_current<MIVI_KV_F16>(a, kvh, pos, cs, sn, cur[wave][0], cur[wave][1], true);
-        __builtin_amdgcn_wave_barrier();
-        uint32_t kw[8], vw[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int d = 16 * c + 2 * i;
-            kw[i] = f32_to_half_bits(cur[wave][0][d]) | (f32_to_half_bits(cur[wave][0][d + 1]) << 16);
-            vw[i] = f32_to_half_bits(cur[wave][1][d]) | (f32_to_half_bits(cur[wave][1][d + 1]) << 16);
+        if (a.k_norm) {
+            const float ss = wave_sum(lane < 32 ? fmaf(k0, k0, k1 * k1) : 0.f);
+            const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            k0 = k0 * sc * kn0;
+            k1 = k1 * sc * kn1;
         }
-        ck0 = u32x4{kw[0], kw[1], kw[2], kw[3]}; ck1 = u32x4{kw[4], kw[5], kw[6], kw[7]};
-        cv0 = u32x4{vw[0], vw[1], vw[2], vw[3]}; cv1 = u32x4{vw[4], vw[5], vw[6], vw[7]};
+        if (lane < 32) {
+            const float cc = cs[lane], ss = sn[lane];
+            const float r0 = k0 * cc - k1 * ss, r1 = k0 * ss + k1 * cc;
+            const uint32_t kw = f32_to_half_bits(r0) | (f32_to_half_bits(r1) << 16);
+            const uint32_t vw = f32_to_half_bits(vv0) | (f32_to_half_bits(vv1) << 16);
+            ((uint32_t*)(a.kc + (size_t)pos * rb))[kvh * (HD / 2) + lane] = kw;
+            ((uint32_t*)(a.vc + (size_t)pos * rb))[kvh * (HD / 2) + lane] = vw;
+            curw[0][lane] = kw;
+            curw[1][lane] = vw;
+        }
+        __builtin_amdgcn_wave_barrier();
+        ck0 = *(const u32x4*)&curw[0][8 * c]; ck1 = *(const u32x4*)&curw[0][8 * c + 4];
+        cv0 = *(const u32x4*)&curw[1][8 * c]; cv1 = *(const u32x4*)&curw[1][8 * c + 4];
 #pragma unroll
         for (int i = 0; i < PD; i++) {
             if (min(g0 + i, g1 - 1) * G + t >= pos) {
@@ -1012,19 +1072,19 @@ __global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
         }
     }
 
-    // 3. query heads (QK-norm, RoPE) in log2 units as fp16 hi / lo: A row
-    //    4h + i, lane = row + 16 * kg holds dims 16 kg + 4j .. +3 for instruction j
-    wave_prep_heads4(qs[wave], a.q + (size_t)(kvh * hpk) * HD, hpk, a.q_norm, a.eps, HD, cs, sn);
+    // 4. query heads in log2 units as fp16 hi / lo: A row 4h + i, lane =
+    //    row + 16 * kg holds dims 16 kg + 4j .. +3 for instruction j
+    qh.finish(qs, hpk, a.q_norm != nullptr, a.eps);
     __builtin_amdgcn_wave_barrier();
     half4_t qa[4];
     {
-        const int qh = t >> 2, qi = t & 3;
+        const int qhd = t >> 2, qi = t & 3;
         const float qscale = a.scale * 1.4426950408889634f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float y = qh < hpk && qi < 2 ? qs[wave][qh][16 * c + 4 * j + e] * qscale : 0.f;
+                const float y = qhd < hpk && qi < 2 ? qs[qhd][16 * c + 4 * j + e] * qscale : 0.f;
                 const _Float16 hi = (_Float16)y;
                 const _Float16 lo = (_Float16)(y - (float)hi);
                 qa[j][e] = qi == 0 ? hi : qi == 1 ? lo : (_Float16)0.0f;
@@ -1093,7 +1153,7 @@ __global__ void __launch_bounds__(64 * W, 2) attn_f16_mfma_kernel(AttnArgs a) {
         }
     }
 
-    // 4. sums over the token lanes; lane 16c writes head c's (m, l) and dims
+    // 5. sums over the token lanes; lane 16c writes head c's (m, l) and dims
     //    16c..16c+15 of every head
     l_run = row_sum16(l_run);
 #pragma unroll
@@ -1439,7 +1499,7 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
         // fp16 rows in 16-token groups on the matrix cores, one wave per
         // workgroup (the XCD placement of attn_tile_of spreads them)
         dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
-        hipLaunchKernelGGL((attn_f16_mfma_kernel<3, 1>), grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((attn_f16_mfma_kernel<3>), grid, dim3(64), 0, s, a);
         tt = kQ8GroupTokens;
     } else {
         dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
