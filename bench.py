@@ -317,25 +317,41 @@ def parity_record(got, want):
 
 def decode_cpu_leg(img, state, prompt, prefill, steps, ctx, gpu_toks, budget_s):
     """Config 4 on the CPU: the oracle's forward_step continuing greedily from
-    the GPU-built state (the 4096-token prefill on the CPU would take minutes),
-    timed at the process's threads and at the reference default's 2; its
-    tokens are compared with the device's (parity)."""
+    the GPU-built state (the 4096-token prefill on the CPU would take minutes).
+    Parity: all `steps` greedy tokens against the device's, with the oracle's
+    attention heads spread over its threads (the same bits as one after
+    another; not timed). Timed: the reference's own schedule, attention heads
+    one after another (transformer.rs:128) and the projections over the
+    threads, at the process's threads and at the reference default's 2, each
+    within its budget."""
     pyoracle = _oracle()
     threads, vis = cpu_threads()
     k, v, conv = state
     out = {}
-    for th, budget, n in ((threads, budget_s, steps), (REF_THREADS, budget_s / 2, steps)):
-        pyoracle.set_threads(th)
-        o = pyoracle.Model(img, max_ctx=ctx, kv_precision=pyoracle.KV_F16RT)
-        oracle_import(o, k, v, conv, prefill, 2 * 512, 6, True)
-        toks, sec = oracle_greedy(pyoracle, o, int(prompt[-1]), prefill, n, budget)
-        o.close()
-        if th == threads:
-            out.update(cpu_tok_s=1.0 / sec, cpu_threads=th, host_cpus_visible=vis,
-                       cpu_sample=f"{len(toks)} greedy steps of the oracle forward_step after importing the "
-                                  f"GPU-built state", parity=parity_record(gpu_toks, toks))
-        else:
-            out["cpu_at_reference_default_threads"] = dict(tok_s=1.0 / sec, threads=th, steps=len(toks))
+    pyoracle.set_threads(threads)
+    o = pyoracle.Model(img, max_ctx=ctx, kv_precision=pyoracle.KV_F16RT)
+    oracle_import(o, k, v, conv, prefill, 2 * 512, 6, True)
+    toks, sec_par = oracle_greedy(pyoracle, o, int(prompt[-1]), prefill, steps, 10 * budget_s)
+    o.close()
+    out["parity"] = parity_record(gpu_toks, toks)
+    pyoracle.set_serial_attention(True)
+    try:
+        for th, budget in ((threads, budget_s), (REF_THREADS, budget_s / 2)):
+            pyoracle.set_threads(th)
+            o = pyoracle.Model(img, max_ctx=ctx, kv_precision=pyoracle.KV_F16RT)
+            oracle_import(o, k, v, conv, prefill, 2 * 512, 6, True)
+            tt, sec = oracle_greedy(pyoracle, o, int(prompt[-1]), prefill, steps, budget)
+            o.close()
+            if th == threads:
+                out.update(cpu_tok_s=1.0 / sec, cpu_threads=th, host_cpus_visible=vis,
+                           cpu_sample=f"{len(tt)} greedy steps of the oracle forward_step after importing the "
+                                      f"GPU-built state; attention heads one after another as transformer.rs:128, "
+                                      f"projections over {th} threads",
+                           cpu_tok_s_heads_over_threads=1.0 / sec_par)
+            else:
+                out["cpu_at_reference_default_threads"] = dict(tok_s=1.0 / sec, threads=th, steps=len(tt))
+    finally:
+        pyoracle.set_serial_attention(False)
     return out
 
 
@@ -386,35 +402,32 @@ def config5_weight_bytes(cfg, batch):
 
 
 def batched_decode_bench(torch, hip, batch, ctx, steps, cpu_budget_s=0.0):
-    """Config 5: 8 sequences, Q8_0 KV with `ctx` cached tokens each, greedy.
-
-    The caches hold seeded synthetic Q8_0 rows (N(0, 1) values quantized with
-    this build's encoder) and the ShortConv states N(0, 0.1), imported through
-    the state-import entry point: prefilling 8 x 32768 tokens one at a time
-    would take minutes, and attention reads the same bytes whatever they hold.
-    """
+    """Config 5: 8 sequences, each a seeded uniform-random prompt of `ctx`
+    tokens prefilled in tiles of 512 rows (PrefillStrategy::Chunked) into its
+    own Q8_0 cache and ShortConv state, then `steps` greedy steps of the 8
+    together (one batched decode step per position), timed."""
+    import numpy as np
     from mivi_hip.synthmodel import LFM2_1B2, build_hybrid
     img = build_hybrid(**LFM2_1B2, ctx_len=65536, seed=2024)
     m = hip.Model(img, max_ctx=ctx + steps, kv_precision=hip.KvPrecision.Q8_0, max_batch=batch)
     info = m.info
-
-    def state(b):
-        k = hip.synth_random_weights(hip.GgmlType.Q8_0, 500 + 2 * b, info.n_attn_layers * ctx, info.kv_dim, 1.0)
-        v = hip.synth_random_weights(hip.GgmlType.Q8_0, 501 + 2 * b, info.n_attn_layers * ctx, info.kv_dim, 1.0)
-        return k, v, hip.synth_normal(600 + b, m.conv_len(), std=0.1)
-
+    m.set_prefill_strategy(512)
+    prompts = np.random.default_rng(12).integers(0, LFM2_1B2["vocab"], (batch, ctx + 1))
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for b in range(batch):
-        m.import_state(ctx, *state(b), seq=b)
-    log(f"config 5: {batch} synthetic Q8_0 caches of {ctx} tokens imported in {time.perf_counter() - t0:.1f}s")
-    rng = __import__("numpy").random.default_rng(12)
-    toks = [int(t) for t in rng.integers(0, LFM2_1B2["vocab"], batch)]
+        m.prefill(prompts[b, :-1], 0, seq=b)
+    torch.cuda.synchronize()
+    t_pf = time.perf_counter() - t0
+    log(f"config 5: {batch} prompts of {ctx} tokens prefilled in {t_pf:.1f} s (tiles of 512)")
+    states = [m.export_state(ctx, seq=b) for b in range(batch)]
+    toks = [int(prompts[b, -1]) for b in range(batch)]
     m.generate_greedy(toks, [ctx] * batch, 4)  # graph capture; rewrites positions ctx.. below
     # the warm-up advanced each sequence's ShortConv state: back to the
-    # imported one (an interval import of no rows with the state)
-    empty = __import__("numpy").empty(0, __import__("numpy").uint8)
+    # prefilled one (an interval import of no rows with the state)
+    empty = np.empty(0, np.uint8)
     for b in range(batch):
-        m.import_state_at(0, 0, empty, empty, hip.synth_normal(600 + b, m.conv_len(), std=0.1), seq=b)
+        m.import_state_at(0, 0, empty, empty, states[b][2], seq=b)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     out = m.generate_greedy(toks, [ctx] * batch, steps)
@@ -427,50 +440,63 @@ def batched_decode_bench(torch, hip, batch, ctx, steps, cpu_budget_s=0.0):
                ms_per_step=1e3 * dt / steps, kv_bytes_per_step=kv_bytes,
                kv_gbs_over_whole_step=kv_bytes * steps / dt / 1e9, weight_bytes_per_step=wbs,
                gbs_whole_step=(kv_bytes + wbs) * steps / dt / 1e9,
-               note=("weight_bytes_per_step: the d = 2048 projections read their weights once for the 8 columns, "
+               prefill_tok_s=batch * ctx / t_pf, prefill_tile=512,
+               note=("caches and ShortConv states built by the chunked prefill of seeded uniform token ids; "
+                     "weight_bytes_per_step: the d = 2048 projections read their weights once for the 8 columns, "
                      "the K = 8192 FFN down once per group of four columns, the packed head once per eight; "
                      "kv_gbs_over_whole_step divides the KV bytes by the whole step time, not the attention "
-                     "kernels' time; caches synthetic, see docstring"),
+                     "kernels' time"),
                first_tokens=[int(v) for v in out[:4, 0]])
     m.close()
     if cpu_budget_s > 0:
-        res.update(config5_cpu_leg(img, state, toks, ctx, steps, out, cpu_budget_s))
+        res.update(config5_cpu_leg(img, states, toks, ctx, steps, out, cpu_budget_s))
         res["speedup_vs_cpu"] = res["tok_s"] / res["cpu_tok_s"]
     return res
 
 
-def config5_cpu_leg(img, state, toks, ctx, steps, gpu_out, budget_s):
-    """Config 5 on the CPU: 8 sequential single-sequence decodes (the
-    reference runs one Model per sequence) from the same imported states, a
-    few greedy steps each within the budget; their tokens against the
-    device's batched ones (parity). Then sequence 0 at the reference
-    default's 2 threads."""
+def config5_cpu_leg(img, states, toks, ctx, steps, gpu_out, budget_s, parity_steps=16):
+    """Config 5 on the CPU, from each sequence's GPU-built state (the reference
+    runs one Model per sequence). Parity: `parity_steps` greedy steps of every
+    sequence against the device's batched tokens (attention heads over the
+    threads, not timed). Timed: single-sequence decodes with the reference's
+    schedule (attention heads one after another, transformer.rs:128) within
+    the budget, at the process's threads and at the reference default's 2."""
     pyoracle = _oracle()
     threads, vis = cpu_threads()
     batch = len(toks)
-    per_seq = max(1, min(steps, 3))
     pyoracle.set_threads(threads)
     o = pyoracle.Model(img, max_ctx=ctx + steps, kv_precision=pyoracle.KV_Q8_0)
     row = o.info.kv_dim // 32 * 34
-    secs, n_steps, par = 0.0, 0, []
+    par = []
     for b in range(batch):
         o.reset()
-        oracle_import(o, *state(b), ctx, row, 6, False)
-        got, sec = oracle_greedy(pyoracle, o, toks[b], ctx, per_seq, budget_s / batch)
-        secs += sec * len(got)
-        n_steps += len(got)
+        oracle_import(o, *states[b], ctx, row, 6, False)
+        got, _ = oracle_greedy(pyoracle, o, toks[b], ctx, min(steps, parity_steps), 10 * budget_s)
         par.append(parity_record(gpu_out[:, b], got))
-    res = dict(cpu_tok_s=n_steps / secs, cpu_threads=threads, host_cpus_visible=vis,
-               cpu_sample=f"{n_steps} oracle forward_step calls over the {batch} sequences "
-                          f"({per_seq} greedy steps each at {ctx}+ cached tokens), state imported, not timed",
-               parity=dict(steps_compared=sum(p["steps_compared"] for p in par),
+    res = dict(parity=dict(steps_compared=sum(p["steps_compared"] for p in par),
                            tokens_equal=all(p["tokens_equal"] for p in par),
                            per_sequence_first_divergence=[p["first_divergence"] for p in par]))
-    pyoracle.set_threads(REF_THREADS)
-    o.reset()
-    oracle_import(o, *state(0), ctx, row, 6, False)
-    got, sec = oracle_greedy(pyoracle, o, toks[0], ctx, 2, budget_s / 2)
-    res["cpu_at_reference_default_threads"] = dict(tok_s=1.0 / sec, threads=REF_THREADS, steps=len(got))
+    pyoracle.set_serial_attention(True)
+    try:
+        for th, budget in ((threads, budget_s), (REF_THREADS, budget_s / 2)):
+            pyoracle.set_threads(th)
+            secs, n_steps, b = 0.0, 0, 0
+            while secs < budget and b < batch:
+                o.reset()
+                oracle_import(o, *states[b], ctx, row, 6, False)
+                got, sec = oracle_greedy(pyoracle, o, toks[b], ctx, steps, budget - secs)
+                secs += sec * len(got)
+                n_steps += len(got)
+                b += 1
+            if th == threads:
+                res.update(cpu_tok_s=n_steps / secs, cpu_threads=th, host_cpus_visible=vis,
+                           cpu_sample=f"{n_steps} oracle forward_step calls over {b} sequence(s) at {ctx}+ cached "
+                                      f"tokens from the GPU-built states; attention heads one after another as "
+                                      f"transformer.rs:128, projections over {th} threads")
+            else:
+                res["cpu_at_reference_default_threads"] = dict(tok_s=n_steps / secs, threads=th, steps=n_steps)
+    finally:
+        pyoracle.set_serial_attention(False)
     o.close()
     return res
 

@@ -563,6 +563,9 @@ static int kv_store(or_model* m, size_t layer, size_t pos) {
     return 0;
 }
 
+static int g_serial_attention = 0;
+void or_set_serial_attention(int on) { g_serial_attention = on != 0; }
+
 /* transformer.rs:134-167 online-softmax step (shared by both precisions) */
 static inline void online_step(float score, const float* v, float* out, size_t hd, float* rmax, float* rsum) {
     if (score > -INFINITY) {
@@ -587,8 +590,10 @@ static void gqa_attention_rows(const float* q, const uint8_t* kc, const uint8_t*
     if (hpk < 1) hpk = 1;
     float scale = 1.0f / sqrtf((float)hd);
     /* query heads are independent (each keeps its own running max, sum and
-     * output, in token order), so long caches spread them over the threads */
-    int nt = seq * nh >= 65536 ? or_get_threads() : 1;
+     * output, in token order), so long caches spread them over the threads
+     * unless the reference's serial loop over heads (transformer.rs:128) is
+     * asked for (or_set_serial_attention) */
+    int nt = seq * nh >= 65536 && !g_serial_attention ? or_get_threads() : 1;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
     for (size_t h = 0; h < nh; h++) {
         float vbuf[256];

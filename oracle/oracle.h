@@ -69,6 +69,9 @@ typedef struct {
 
 /* threading: number of OpenMP threads used by row-parallel kernels */
 void or_set_threads(int n);
+/* 1: attention heads one after another, as the reference's loop
+ * (transformer.rs:128); 0 (default): heads over the threads for long caches */
+void or_set_serial_attention(int on);
 int or_get_threads(void);
 /* 1 = AVX2+FMA kernels (reference default on x86-64), 0 = scalar kernels */
 void or_set_avx2(int on);

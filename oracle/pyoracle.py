@@ -77,6 +77,7 @@ def lib():
         P = C.c_void_p
         S = C.c_size_t
         L.or_set_threads.argtypes = [C.c_int]
+        L.or_set_serial_attention.argtypes = [C.c_int]
         L.or_get_threads.restype = C.c_int
         L.or_set_avx2.argtypes = [C.c_int]
         L.or_f16_to_f32.argtypes = [C.c_uint16]
@@ -145,6 +146,13 @@ def _p(a):
 
 def set_threads(n: int):
     lib().or_set_threads(int(n))
+
+
+def set_serial_attention(on: bool):
+    """Attention heads one after another, as the reference's
+    compute_gqa_attention loops over them (transformer.rs:128); off by
+    default (long caches spread the heads over the threads)."""
+    lib().or_set_serial_attention(1 if on else 0)
 
 
 def set_avx2(on: bool):
@@ -329,7 +337,10 @@ class Model:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except TypeError:  # interpreter shutdown: the module's globals are already gone
+            pass
 
     def reset(self):
         lib().or_model_reset(self._h)

@@ -231,3 +231,24 @@ def test_q8_kv_cache_sizes(oracle):
     row_q8 = (512 // 32) * 34
     assert 2 * 6 * 65536 * row_q8 == 427_819_008
     assert 2 * 6 * 65536 * 512 * 4 == 1_610_612_736
+
+
+def test_serial_attention_is_the_parallel_result(oracle):
+    # The reference loops over the query heads one after another
+    # (transformer.rs:128); the oracle spreads long caches' heads over its
+    # threads. Each head keeps its own running state in token order, so the
+    # two schedules give the same bits (8 heads x 8200 tokens crosses the
+    # oracle's threshold for the parallel form).
+    nh, nkv, hd, seq = 8, 2, 64, 8200
+    rng = np.random.default_rng(77)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    K = rng.standard_normal((seq, nkv * hd)).astype(np.float32)
+    V = rng.standard_normal((seq, nkv * hd)).astype(np.float32)
+    oracle.set_threads(4)
+    par = oracle.attention(q, K, V, oracle.KV_F32, nh, nkv, hd, seq)
+    oracle.set_serial_attention(True)
+    try:
+        ser = oracle.attention(q, K, V, oracle.KV_F32, nh, nkv, hd, seq)
+    finally:
+        oracle.set_serial_attention(False)
+    assert np.array_equal(par.view(np.uint32), ser.view(np.uint32))
