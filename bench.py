@@ -272,10 +272,41 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
                           config="GenerationConfig::default (T 0.2, top-p 0.9, top-k 40, repetition 1.05), seed 1",
                           first_tokens=[int(v) for v in stoks[:8, 0]])
     log(f"decode: {steps / ds:.1f} tok/s with the device sampler (default GenerationConfig)")
+    m.close()
+    out["q4_k_m"] = mixed_decode_bench(torch, hip, prompt, prefill, steps, t_chunked)
     if cpu_budget_s > 0:
         out.update(decode_cpu_leg(img, state, prompt, prefill, steps, ctx, toks[:, 0], cpu_budget_s))
         out["speedup_vs_cpu"] = out["tok_s"] / out["cpu_tok_s"]
     return out
+
+
+def mixed_decode_bench(torch, hip, prompt, prefill, steps, q4k_prefill_s):
+    """The same prompt and steps on the Q4_K_M layout of the 1.2B shape
+    (8 ffn_down and 2 attn_v matrices in Q6_K, as the reference's 1.2B
+    Q4_K_M file): chunked prefill time against the all-Q4_K model's, and
+    greedy decode tok/s."""
+    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid, weight_bytes_per_token
+    img = build_hybrid(**LFM2_1B2, ctx_len=65536, seed=2024, mixed="q4_k_m")
+    m = hip.Model(img, max_ctx=prefill + steps, kv_precision=hip.KvPrecision.F16)
+    m.set_prefill_strategy(512)
+    m.prefill(prompt[:-1])
+    m.generate_greedy([int(prompt[-1])], [prefill], 8)  # warm-up + graph capture
+    m.reset_context()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    m.prefill(prompt[:-1])
+    t_chunked = time.perf_counter() - t1
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    toks = m.generate_greedy([int(prompt[-1])], [prefill], steps)
+    dt = time.perf_counter() - t2
+    m.close()
+    wb = weight_bytes_per_token(**LFM2_1B2, mixed="q4_k_m")
+    log(f"decode Q4_K_M: prefill {prefill} tokens in {t_chunked * 1e3:.0f} ms "
+        f"({t_chunked / q4k_prefill_s:.2f}x the Q4_K model), {steps / dt:.1f} tok/s")
+    return dict(layout="Q4_K_M: ffn_down of layers 0,1,4,7,10,13,14,15 and attn_v of layers 8,15 in Q6_K",
+                prefill_tok_s=prefill / t_chunked, prefill_time_vs_q4k=t_chunked / q4k_prefill_s,
+                tok_s=steps / dt, weight_bytes_per_token=wb, first_tokens=[int(v) for v in toks[:8, 0]])
 
 
 def oracle_import(o, k, v, conv, tokens, row, n_layers, f16):

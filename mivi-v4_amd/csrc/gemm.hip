@@ -1,7 +1,7 @@
 // quantized_matmul_rows (crates/mivi-quant/src/lib.rs:143-357) for gfx950.
 //
-// batch == 1 is exactly the matvec path (lib.rs:171-182). Q4_K with at least
-// kMfmaMinBatch rows runs on the matrix cores:
+// batch == 1 is exactly the matvec path (lib.rs:171-182). Q4_K and Q6_K with
+// at least kMfmaMinBatch rows run on the matrix cores:
 //
 //   gemm_prep_kernel   one workgroup per input row: scales the row by a power
 //                      of two 2^-e (so that |x| <= 1), splits it into fp16
@@ -17,9 +17,13 @@
 //                      the same MFMA shape with B = m (K = 8 sub-blocks padded
 //                      to 16) and is subtracted the same way. The row scale
 //                      2^e is applied at the store.
+//   gemm_q6k_kernel    the same tiles for Q6_K: B = q (exact in fp16), the
+//                      per-sub-block scale d * sc applied to each k-step's
+//                      chain (one 32 x 32 x 16 product per 16-value
+//                      sub-block).
 //
-// Other formats, and Q4_K with fewer rows, run the batched GEMV (the inputs
-// as its columns).
+// Other formats, and fewer rows, run the batched GEMV (the inputs as its
+// columns).
 #include <mutex>
 #include <vector>
 
@@ -403,6 +407,170 @@ __global__ void __launch_bounds__(kGT) gemm_q4k_kernel(const uint8_t* __restrict
     }
 }
 
+
+// Q6_K (q6_k.rs:8-43: y = (d * sc) * q, q = code - 32, one int8 scale per
+// 16-value sub-block) on the same tiles as gemm_q4k_kernel. The B operand
+// is q itself, exact in fp16; sc * q (up to 4096 in magnitude) is not
+// always exact in fp16, so the scale is applied per sub-block instead: a
+// 32 x 32 x 16 product is exactly one sub-block, so each k-step's chain (x
+// hi, then x lo) starts from zero and is folded into the fp32 accumulator as
+// acc += (d * sc) * C, the factor per weight row (lane) and sub-block.
+// Blocks are 210 bytes (2-byte aligned): the code bytes of a k-tile pair
+// (ql low nibbles and qh bits 0-3, then the high nibbles and bits 4-7 of the
+// same bytes) are loaded once per pair with ld16_a2.
+struct GemmStage6 {
+    u32x4 xh, xl;             // x chunk of 8 values: input row tid/8, chunk tid%8
+    u32x4 ql0, ql1, qh, scw;  // weight row bn: ql / qh bytes of the k-tile pair; the 16 scales
+    uint32_t d;               // and d (first k-tile of a super-block)
+};
+
+struct GemmBuf6 {
+    _Float16 Xh[kTm][kXs];
+    _Float16 Xl[kTm][kXs];
+    _Float16 Bq[kGN][kXs];  // q = code - 32 of the k-tile, weight-row major
+};
+
+// four 6-bit codes (nibbles of ql at bit 4p, two qh bits at 4p + 2j) as
+// fp16 q = code - 32: 1024 + code has the bits 0x6400 | code
+__device__ __forceinline__ void q6_codes8(uint32_t l0, uint32_t l1, uint32_t h0, uint32_t h1, int p, int j,
+                                          _Float16* dst) {
+    const uint32_t sn = 4u * (uint32_t)p, sh = 4u * (uint32_t)p + 2u * (uint32_t)j;
+    const uint32_t c0 = ((l0 >> sn) & 0x0F0F0F0Fu) | (((h0 >> sh) & 0x03030303u) << 4);
+    const uint32_t c1 = ((l1 >> sn) & 0x0F0F0F0Fu) | (((h1 >> sh) & 0x03030303u) << 4);
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, c0, 0x07010700u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, c0, 0x07030702u);
+    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, c1, 0x07010700u);
+    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, c1, 0x07030702u);
+    const half2v off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const half2v h0v = __builtin_bit_cast(half2v, p0) + off, h1v = __builtin_bit_cast(half2v, p1) + off;
+    const half2v h2v = __builtin_bit_cast(half2v, p2) + off, h3v = __builtin_bit_cast(half2v, p3) + off;
+    *(half8*)dst = half8{h0v.x, h0v.y, h1v.x, h1v.y, h2v.x, h2v.y, h3v.x, h3v.y};
+}
+
+__global__ void __launch_bounds__(kGT) gemm_q6k_kernel(const uint8_t* __restrict__ W, int N, int K,
+                                                       const _Float16* __restrict__ xh,
+                                                       const _Float16* __restrict__ xl,
+                                                       const float* __restrict__ rowscale, float* __restrict__ Y,
+                                                       int M, int64_t ldy, int accumulate) {
+    __shared__ __attribute__((aligned(16))) GemmBuf6 buf[2];
+    // per super-block (by its parity): the 16 int8 scales and d of each
+    // weight row (rows 20 B apart, so the 32 rows a wave reads fall in
+    // distinct banks)
+    __shared__ __attribute__((aligned(16))) uint8_t Wh[2][kGN][20];
+    const int n0 = blockIdx.x * kGN, m0 = blockIdx.y * kTm;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const size_t rb = (size_t)(K / 256) * 210;
+    const int li = lane & 31, lh = lane >> 5;
+    const int bn = 8 * (tid >> 4) + (tid & 7), bc = (tid >> 3) & 1;
+    const uint8_t* brow = W + (size_t)(n0 + bn < N ? n0 + bn : N - 1) * rb;
+    const int xr = tid >> 3, xc = tid & 7;
+
+    f32x16 acc[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) acc[nt] = f32x16{};
+
+    const int ntiles = K / kTk;
+    auto load_tile = [&](GemmStage6& S, int t) {
+        const int k0 = t * kTk;
+        const size_t o = (size_t)(m0 + xr) * K + k0 + 8 * xc;
+        S.xh = *(const u32x4*)(xh + o);
+        S.xl = *(const u32x4*)(xl + o);
+        const int b = k0 / 256, g = (k0 % 256) / 64, h = g >> 1;
+        const uint8_t* blk = brow + (size_t)b * 210;
+        // branch-free: both k-tiles of a pair load the pair's bytes, every
+        // k-tile the block's scales and d (used at its first k-tile)
+        S.ql0 = ld16_a2(blk + 64 * h + 16 * bc);
+        S.ql1 = ld16_a2(blk + 64 * h + 32 + 16 * bc);
+        S.qh = ld16_a2(blk + 128 + 32 * h + 16 * bc);
+        S.scw = ld16_a2(blk + 192);
+        S.d = ld_u16(blk + 208);
+    };
+    auto store_tile = [&](const GemmStage6& S, int t) {
+        GemmBuf6& B = buf[t & 1];
+        *(u32x4*)&B.Xh[xr][8 * xc] = S.xh;
+        *(u32x4*)&B.Xl[xr][8 * xc] = S.xl;
+        const int g = t & 3, p = g & 1, sp = (t >> 2) & 1;
+        const u32x4 ql0 = S.ql0, ql1 = S.ql1, qh = S.qh;
+        if (g == 0 && bc == 0) {
+            uint32_t* w = (uint32_t*)&Wh[sp][bn][0];
+            w[0] = S.scw.x; w[1] = S.scw.y; w[2] = S.scw.z; w[3] = S.scw.w; w[4] = S.d;
+        }
+        // values 16 bc .. +15 of the tile's two 32-value quarters (codes of
+        // ql0 / ql1 with the qh bit pairs 2p, 2p + 1)
+        q6_codes8(ql0.x, ql0.y, qh.x, qh.y, p, 0, &B.Bq[bn][16 * bc]);
+        q6_codes8(ql0.z, ql0.w, qh.z, qh.w, p, 0, &B.Bq[bn][16 * bc + 8]);
+        q6_codes8(ql1.x, ql1.y, qh.x, qh.y, p, 1, &B.Bq[bn][32 + 16 * bc]);
+        q6_codes8(ql1.z, ql1.w, qh.z, qh.w, p, 1, &B.Bq[bn][32 + 16 * bc + 8]);
+    };
+
+    const int ar = 32 * wm + li;
+    auto compute = [&](int t) {
+        const GemmBuf6& B = buf[t & 1];
+        const int g = t & 3, sp = (t >> 2) & 1;
+        // d * sc of this lane's two weight rows for the tile's four sub-blocks
+        float ds[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int r = 64 * wn + 32 * nt + li;
+            const uint32_t scs = *(const uint32_t*)&Wh[sp][r][4 * g];
+            const float d = half_bits_to_f32(*(const uint32_t*)&Wh[sp][r][16]);
+#pragma unroll
+            for (int s = 0; s < 4; s++) ds[nt][s] = d * (float)(int)(int8_t)(scs >> (8 * s));
+        }
+        // k-step s: sub-block 4g + s, its chain (x hi, then x lo) scaled into acc
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const half8 a_h = *(const half8*)&B.Xh[ar][16 * s + 8 * lh];
+            const half8 a_l = *(const half8*)&B.Xl[ar][16 * s + 8 * lh];
+            half8 bq[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) bq[nt] = *(const half8*)&B.Bq[64 * wn + 32 * nt + li][16 * s + 8 * lh];
+            f32x16 c[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) c[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, bq[nt], f32x16{}, 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) c[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, bq[nt], c[nt], 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[nt][r] = fmaf(ds[nt][s], c[nt][r], acc[nt][r]);
+        }
+    };
+    // two register stages (gemm_q4k_kernel's three would not fit the
+    // registers), each loaded two k-tiles ahead: at step t the stage holding
+    // tile t + 1 is built into LDS and then reloaded with tile t + 3
+    GemmStage6 S0, S1;
+    load_tile(S0, 0);
+    if (1 < ntiles) load_tile(S1, 1);
+    store_tile(S0, 0);
+    if (2 < ntiles) load_tile(S0, 2);
+    __syncthreads();
+    auto step = [&](GemmStage6& Snext, int t) {  // Snext holds tile t + 1
+        compute(t);
+        if (t + 1 < ntiles) store_tile(Snext, t + 1);  // the other buffer: every wave is past tile t - 1
+        if (t + 3 < ntiles) load_tile(Snext, t + 3);
+        __syncthreads();
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+        step(S1, t);
+        if (t + 1 < ntiles) step(S0, t + 1);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const int n = n0 + 64 * wn + 32 * nt + li;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4);
+            if (m < M && n < N) {
+                float* y = Y + m * ldy + n;
+                const float v = acc[nt][r] * rowscale[m];
+                *y = accumulate ? *y + v : v;  // one writer per output
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // types.rs:188-235 validate_matmul_args after lib.rs:152-166
@@ -441,8 +609,9 @@ static GemmWorkspace& gemm_workspace(int dev) {
 }
 
 // Y_s[m * ys + n] (=|+=) sum_k W_s[n, k] * pro(X)[m, k] for the segments s
-// of a (Q4_K, K % 2048 == 0): one activation split, one GEMM per segment.
-static int32_t rows_q4k_mfma(int pro, const GemvArgs& a, hipStream_t s) {
+// of a (Q4_K or Q6_K, K % 2048 == 0): one activation split, one GEMM per
+// segment.
+static int32_t rows_mfma(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     const size_t batch = (size_t)a.ncol;
     if (batch > (size_t)INT32_MAX - kTm) return err_overflow();
     const size_t mp = (batch + kTm - 1) / kTm * kTm, K = (size_t)a.K;
@@ -477,8 +646,12 @@ static int32_t rows_q4k_mfma(int pro, const GemvArgs& a, hipStream_t s) {
         const int rows = a.seg[i].n;
         if (rows == 0) continue;
         dim3 grid((unsigned)((rows + kGN - 1) / kGN), (unsigned)(mp / kTm));
-        hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(kGT), 0, s, a.seg[i].W, rows, (int)K, xh, xl, sh, sl, rs,
-                           a.seg[i].y, (int)batch, a.ys, a.accumulate);
+        if (t == MIVI_GGML_Q6_K)
+            hipLaunchKernelGGL(gemm_q6k_kernel, grid, dim3(kGT), 0, s, a.seg[i].W, rows, (int)K, xh, xl, rs,
+                               a.seg[i].y, (int)batch, a.ys, a.accumulate);
+        else
+            hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(kGT), 0, s, a.seg[i].W, rows, (int)K, xh, xl, sh, sl, rs,
+                               a.seg[i].y, (int)batch, a.ys, a.accumulate);
     }
     MIVI_HIP_CHECK(hipGetLastError());
     MIVI_HIP_CHECK(hipEventRecord(ws.done, s));
@@ -492,7 +665,8 @@ int32_t launch_rows(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     // the activation split reads 16-byte vectors of every row
     auto a16 = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
     const bool aligned = a16(a.x) && a16(a.x2) && a16(a.norm_w) && a.xs % 4 == 0;
-    if (t == MIVI_GGML_Q4_K && a.ncol >= kMfmaMinBatch && a.K % 2048 == 0 && aligned) return rows_q4k_mfma(pro, a, s);
+    if ((t == MIVI_GGML_Q4_K || t == MIVI_GGML_Q6_K) && a.ncol >= kMfmaMinBatch && a.K % 2048 == 0 && aligned)
+        return rows_mfma(t, pro, a, s);
     return launch_gemv_ex(t, pro, a, s);
 }
 }  // namespace mivi
@@ -511,7 +685,7 @@ extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, in
     clear_error();
     hipStream_t s = (hipStream_t)stream;
     if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || batch > (size_t)INT32_MAX - kTm) return err_overflow();
-    // Q4_K with batch >= kMfmaMinBatch and cols % 2048 == 0: the matrix cores;
+    // Q4_K / Q6_K with batch >= kMfmaMinBatch and cols % 2048 == 0: the matrix cores;
     // otherwise one GEMV over the batch's input rows as columns: the streaming
     // kernel reads each weight row once per two inputs, with every input's
     // result bit-identical to its own matvec (lib.rs:404-457); other shapes

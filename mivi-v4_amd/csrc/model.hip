@@ -1425,7 +1425,9 @@ struct Mat {
     int32_t type = 0;
     const uint8_t* w = nullptr;  // device
     size_t rows = 0, cols = 0;
-    const uint8_t* quad = nullptr;  // Q4_K: the same rows packed as row quads (one-column GEMVs), else null
+    // the same rows packed for one-column GEMVs (Q4_K row quads; Q6_K row
+    // quads at 2048 columns, unit planes at 4096 or 8192), else null
+    const uint8_t* quad = nullptr;
 };
 
 struct Layer {
@@ -1619,9 +1621,27 @@ EmbedNext embed_next_args(mivi_model* m, float* x, bool on) {
     return en;
 }
 
+// The segments of g (matrices ms, in order) in runs of equal weight type:
+// launch(type, the run's arguments, its matrices, their count) per run.
+template <class F>
+int32_t by_type_runs(const GemvArgs& g, std::initializer_list<const Mat*> ms, F&& launch) {
+    const Mat* const* v = ms.begin();
+    for (int i = 0; i < g.nseg;) {
+        int j = i + 1;
+        while (j < g.nseg && v[j]->type == v[i]->type) j++;
+        GemvArgs r = g;
+        r.nseg = j - i;
+        for (int k = i; k < j; k++) r.seg[k - i] = g.seg[k];
+        const int32_t rc = launch(v[i]->type, r, v + i, j - i);
+        if (rc) return rc;
+        i = j;
+    }
+    return MIVI_OK;
+}
+
 // A decode projection over the matrices ms[0 .. g.nseg): with one column and
-// every matrix held as Q4_K row quads, the matrix-core GEMV on the quads
-// (the same results bit for bit); otherwise the GGUF rows.
+// every matrix held packed, the GEMV on the packed rows (the same results
+// bit for bit); otherwise the GGUF rows.
 int32_t launch_proj(int32_t t, int pro, const GemvArgs& g, std::initializer_list<const Mat*> ms, hipStream_t s) {
     bool quads = g.ncol <= 1 && (int)ms.size() == g.nseg;
     for (const Mat* x : ms) quads = quads && x->quad;
@@ -1696,17 +1716,14 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.seg[2] = {L.wv.w, s0.v, KV};
             g.nseg = 3; g.K = D; g.x = s0.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = ncol; g.xs = z.x; g.ys = z.qkv;
-            if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
-                if ((rc = launch_proj(L.wq.type, PRO_RMSNORM, g, {&L.wq, &L.wk, &L.wv}, s))) return rc;
-            } else {
-                const Mat* ms[3] = {&L.wq, &L.wk, &L.wv};
-                for (int i = 0; i < 3; i++) {
-                    GemvArgs g1 = g;
-                    g1.seg[0] = g.seg[i];
-                    g1.nseg = 1;
-                    if ((rc = launch_proj(ms[i]->type, PRO_RMSNORM, g1, {ms[i]}, s))) return rc;
-                }
-            }
+            // one launch per run of equal weight types (a Q4_K_M file's
+            // Q6_K attn_v runs apart from q|k)
+            rc = by_type_runs(g, {&L.wq, &L.wk, &L.wv}, [&](int32_t t, const GemvArgs& gr, const Mat* const* mr, int n) {
+                if (n == 3) return launch_proj(t, PRO_RMSNORM, gr, {mr[0], mr[1], mr[2]}, s);
+                if (n == 2) return launch_proj(t, PRO_RMSNORM, gr, {mr[0], mr[1]}, s);
+                return launch_proj(t, PRO_RMSNORM, gr, {mr[0]}, s);
+            });
+            if (rc) return rc;
             {
                 // one launch for the nb sequences (blockIdx.y = sequence)
                 AttnArgs a = {};
@@ -1880,17 +1897,10 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
             g.seg[2] = {L.wv.w, m->pf_p1 + D + KV, KV};
             g.nseg = 3; g.K = D; g.x = m->pf_x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = R; g.xs = D; g.ys = (int64_t)ldq;
-            if (L.wq.type == L.wk.type && L.wk.type == L.wv.type) {
-                if ((rc = launch_rows(L.wq.type, PRO_RMSNORM, g, s))) return rc;
-            } else {
-                const Mat* ms[3] = {&L.wq, &L.wk, &L.wv};
-                for (int i = 0; i < 3; i++) {
-                    GemvArgs g1 = g;
-                    g1.seg[0] = g.seg[i];
-                    g1.nseg = 1;
-                    if ((rc = launch_rows(ms[i]->type, PRO_RMSNORM, g1, s))) return rc;
-                }
-            }
+            rc = by_type_runs(g, {&L.wq, &L.wk, &L.wv}, [&](int32_t t, const GemvArgs& gr, const Mat* const*, int) {
+                return launch_rows(t, PRO_RMSNORM, gr, s);
+            });
+            if (rc) return rc;
             AttnArgs a = {};
             a.q = m->pf_p1; a.k = m->pf_p1 + D; a.v = m->pf_p1 + D + KV;
             a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.eps = c.rms_norm_eps;
@@ -2184,29 +2194,36 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         if (hipDeviceSynchronize() != hipSuccess) return fail(set_error(MIVI_ERR_HIP, "packing the head failed"));
         c.weight_bytes += bytes;
     }
-    // one-column decode GEMVs stream Q4_K projections as row quads (matrix
-    // cores, bit-identical to the GGUF rows): a packed copy of each, the GGUF
-    // rows staying for the batched and prefill products
+    // one-column decode GEMVs stream the projections packed (bit-identical
+    // to the GGUF rows): Q4_K as row quads (matrix cores), Q6_K (the
+    // attn_v / ffn_down of a Q4_K_M file) as row quads at 2048 columns and
+    // unit planes at 4096 or 8192; a packed copy of each, the GGUF rows
+    // staying for the batched and prefill products
     if (!getenv("MIVI_NO_PACK")) {
         std::vector<Mat*> qm;
         for (size_t i = 0; i < c.n_layers; i++) {
             Layer& L = m->layers[i];
             Mat* all[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.in_proj, &L.out_proj, &L.gate, &L.up, &L.down};
             for (Mat* x : all)
-                if (x->w && x->type == MIVI_GGML_Q4_K && q4k_quad_layout(x->rows, x->cols) && (uintptr_t)x->w % 16 == 0)
+                if (x->w && (uintptr_t)x->w % 16 == 0 &&
+                    ((x->type == MIVI_GGML_Q4_K && q4k_quad_layout(x->rows, x->cols)) ||
+                     (x->type == MIVI_GGML_Q6_K && (x->cols == 2048 || x->cols == 4096 || x->cols == 8192))))
                     qm.push_back(x);
         }
+        auto bytes = [](const Mat* x) { return x->rows * (x->cols / 256) * (x->type == MIVI_GGML_Q6_K ? 210 : 144); };
         size_t total = 0;
-        for (Mat* x : qm) total += x->rows * (x->cols / 256) * 144;
+        for (Mat* x : qm) total += bytes(x);  // each a multiple of 16 bytes
         uint8_t* q = nullptr;
         if (total && (rc = m->alloc(&q, total))) return fail(rc);
         for (Mat* x : qm) {
-            if ((rc = launch_pack_q4k(x->w, q, x->rows, x->cols, nullptr))) return fail(rc);
+            rc = x->type == MIVI_GGML_Q6_K ? launch_pack_q6k(x->w, q, x->rows, x->cols, nullptr)
+                                           : launch_pack_q4k(x->w, q, x->rows, x->cols, nullptr);
+            if (rc) return fail(rc);
             x->quad = q;
-            q += x->rows * (x->cols / 256) * 144;
+            q += bytes(x);
         }
         if (total && hipDeviceSynchronize() != hipSuccess)
-            return fail(set_error(MIVI_ERR_HIP, "packing the Q4_K projections failed"));
+            return fail(set_error(MIVI_ERR_HIP, "packing the projections failed"));
         c.weight_bytes += total;
     }
     {

@@ -11,6 +11,13 @@ random-init model, these are the values this build uses.
 
 Tensor names and metadata keys are the ones the reference loader resolves
 (loader.rs:33-177, 253-415).
+
+mixed="q4_k_m" gives the mixed-format layout of a Q4_K_M file: ffn_down of
+the first and last eighth of the layers and of every third layer in
+between, and attn_v of the same selection over the attention layers, in
+Q6_K, everything else `weight_type`. For the 1.2B shape that is 8 ffn_down
+and 2 attn_v matrices, 11 Q6_K matrices with the embedding: the count the
+reference reports for its 1.2B Q4_K_M file (CHANGELOG.md:584-586).
 """
 from __future__ import annotations
 
@@ -23,10 +30,28 @@ LFM2_1B2 = dict(dim=2048, hidden=8192, n_layers=16, attn_layers=(2, 5, 8, 11, 13
                 vocab=65536)
 
 
+def more_bits(i: int, n: int) -> bool:
+    """Whether the i-th of n like matrices of a Q4_K_M file is Q6_K: the
+    first and last eighth, and every third one in between."""
+    return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+
+def q6k_matrices(n_layers: int, attn_layers, mixed) -> set:
+    """Names of the projections a `mixed` layout stores as Q6_K."""
+    if mixed is None:
+        return set()
+    if mixed != "q4_k_m":
+        raise ValueError(f"unknown mixed layout {mixed!r}")
+    attn = sorted(attn_layers)
+    out = {f"blk.{i}.ffn_down.weight" for i in range(n_layers) if more_bits(i, n_layers)}
+    out |= {f"blk.{l}.attn_v.weight" for j, l in enumerate(attn) if more_bits(j, len(attn))}
+    return out
+
+
 def build_hybrid(dim: int, hidden: int, n_layers: int, attn_layers, n_heads: int, n_kv: int, vocab: int,
                  ctx_len: int = 65536, weight_type=GgmlType.Q4_K, embd_type=GgmlType.Q6_K, seed: int = 1234,
                  std: float = 0.02, conv_std: float = 0.02, tied: bool = True, qk_norm: bool = False,
-                 rope_base: float = 1_000_000.0) -> np.ndarray:
+                 rope_base: float = 1_000_000.0, mixed=None) -> np.ndarray:
     head_dim = dim // n_heads
     kv_dim = n_kv * head_dim
     g = GgufWriter()
@@ -49,7 +74,10 @@ def build_hybrid(dim: int, hidden: int, n_layers: int, attn_layers, n_heads: int
         s[0] += 1
         return s[0]
 
-    def mat(name, rows, cols, t=weight_type):
+    q6 = q6k_matrices(n_layers, attn_layers, mixed)
+
+    def mat(name, rows, cols, t=None):
+        t = t if t is not None else GgmlType.Q6_K if name in q6 else weight_type
         g.add_matrix(name, rows, cols, int(t), synth_random_weights(t, nxt(), rows, cols, std))
 
     ones = np.ones(dim, np.float32)
@@ -84,19 +112,23 @@ def build_hybrid(dim: int, hidden: int, n_layers: int, attn_layers, n_heads: int
 
 
 def weight_bytes_per_token(dim, hidden, n_layers, attn_layers, n_heads, n_kv, vocab, weight_type=GgmlType.Q4_K,
-                           embd_type=GgmlType.Q6_K, **_) -> int:
+                           embd_type=GgmlType.Q6_K, mixed=None, **_) -> int:
     """Packed weight bytes a decode step streams (every projection + head)."""
     wt, et = GgmlType(weight_type), GgmlType(embd_type)
+    q6 = q6k_matrices(n_layers, attn_layers, mixed)
 
-    def rb(t, cols):
+    def rb(name, cols):
+        t = GgmlType.Q6_K if name in q6 else wt
         return cols // t.block_size() * t.type_size()
 
     kv_dim = n_kv * (dim // n_heads)
-    total = vocab * rb(et, dim)
+    total = vocab * (dim // et.block_size() * et.type_size())
     for i in range(n_layers):
+        p = f"blk.{i}."
         if i in attn_layers:
-            total += (2 * dim + 2 * kv_dim) * rb(wt, dim)
+            total += 2 * dim * rb(p + "attn_q.weight", dim) + kv_dim * rb(p + "attn_k.weight", dim)
+            total += kv_dim * rb(p + "attn_v.weight", dim)
         else:
-            total += 4 * dim * rb(wt, dim)
-        total += 2 * hidden * rb(wt, dim) + dim * rb(wt, hidden)
+            total += 4 * dim * rb(p + "shortconv.in_proj.weight", dim)
+        total += 2 * hidden * rb(p + "ffn_gate.weight", dim) + dim * rb(p + "ffn_down.weight", hidden)
     return total

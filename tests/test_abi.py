@@ -94,3 +94,24 @@ def test_synthetic_model_loads_in_the_oracle(oracle):
     # the config-4 shape streams 692,846,592 weight bytes per token
     from mivi_hip.synthmodel import LFM2_1B2
     assert weight_bytes_per_token(**LFM2_1B2) == 692_846_592
+
+
+def test_q4_k_m_layout_counts():
+    # a Q4_K_M file of the 1.2B shape keeps 11 matrices in Q6_K, the
+    # embedding among them (CHANGELOG.md:584-586); the mixed layout of the
+    # synthetic builder gives the same count (8 ffn_down, 2 attn_v), checked
+    # on the GGUF it writes for a smaller model of the same layer pattern
+    from mivi_hip.gguf import read_tensor_index
+    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid, q6k_matrices, weight_bytes_per_token
+    q6 = q6k_matrices(LFM2_1B2["n_layers"], LFM2_1B2["attn_layers"], "q4_k_m")
+    assert len(q6) + 1 == 11
+    assert sum(n.endswith("ffn_down.weight") for n in q6) == 8 and sum(n.endswith("attn_v.weight") for n in q6) == 2
+    small = dict(LFM2_1B2, dim=256, hidden=512, n_heads=4, n_kv=2, vocab=256)
+    idx = read_tensor_index(build_hybrid(**small, ctx_len=256, mixed="q4_k_m"))
+    got = {n for n, (t, dims, off, ln) in idx.items() if t == 14 and len(dims) == 2}
+    assert got == q6 | {"token_embd.weight"}
+    # every other matrix is Q4_K (the F32 ShortConv weights aside)
+    assert all(t == 12 for n, (t, dims, off, ln) in idx.items() if len(dims) == 2 and n not in got and t != 0)
+    # 10 matrices of 1.46x the Q4_K bytes: 35.1 MB more per token
+    assert weight_bytes_per_token(**LFM2_1B2, mixed="q4_k_m") - weight_bytes_per_token(**LFM2_1B2) == (
+        8 * 2048 * 32 + 2 * 512 * 8) * (210 - 144)

@@ -264,19 +264,31 @@ def test_matmul_rows_config3_shape(hip, oracle, torch_mod):
     _matmul_check(hip, oracle, torch, Q4_K, w, X, rows, cols)
 
 
-@pytest.mark.parametrize("batch,rows", [(16, 128), (127, 200), (129, 384)])
-def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, batch, rows):
-    # row magnitudes from 0 to 1e3 (the per-row power-of-two scaling), ragged M and N
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("batch,rows,cols", [(16, 128, 2048), (127, 200, 2048), (129, 384, 4096), (70, 300, 8192)])
+def test_matmul_rows_mfma_ragged_and_scaled_rows(hip, oracle, torch_mod, t, batch, rows, cols):
+    # the matrix-core GEMM (at least 16 rows, cols % 2048 == 0): row
+    # magnitudes from 0 to 1e3 (the per-row power-of-two scaling), ragged M
+    # and N, Q4_K and Q6_K
     torch = torch_mod
-    cols = 1024
-    w = hip.synth_random_weights(Q4_K, 80 + batch, rows, cols, 0.02)
+    w = hip.synth_random_weights(t, 80 + batch, rows, cols, 0.02)
     X = hip.synth_normal(81 + batch, batch * cols).reshape(batch, cols).astype(np.float32)
     X[0] = 0.0
     X[1] *= np.float32(1e-3)
     X[2] *= np.float32(1e3)
     X[3] = 0.0
     X[3, 5] = np.float32(7.5e3)      # one dominant value
-    _matmul_check(hip, oracle, torch, Q4_K, w, X, rows, cols)
+    _matmul_check(hip, oracle, torch, t, w, X, rows, cols)
+
+
+def test_matmul_rows_q6k_ffn_down_prefill_shape(hip, oracle, torch_mod):
+    # a Q4_K_M file's Q6_K ffn_down [2048 x 8192] on a prefill tile of 512
+    # rows (the matrix-core GEMM with the per-sub-block scale)
+    torch = torch_mod
+    rows, cols, batch = 2048, 8192, 512
+    w = hip.synth_random_weights(Q6_K, 83, rows, cols, 0.02)
+    X = hip.synth_normal(84, batch * cols).reshape(batch, cols)
+    _matmul_check(hip, oracle, torch, Q6_K, w, X, rows, cols)
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
