@@ -1149,32 +1149,42 @@ __global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
                 sa = scores(ring[(i + 1) % PD]);
                 step(ring[i], cur_s, base + i);
             }
-            load(ring[i], base + i + PD);
+            // only groups of the split (no re-reads past its end: the wave
+            // would wait for them before it ends)
+            if (base + i + PD < g1) load(ring[i], base + i + PD);
         }
     }
 
-    // 5. sums over the token lanes; lane 16c writes head c's (m, l) and dims
-    //    16c..16c+15 of every head
+    // 5. sums over the 16 token lanes of a row: l by a butterfly; the 64
+    //    (head, dim) values by a reduce-scatter, each level halving a lane's
+    //    values while the partner (across bit b of t) adds the other half
+    //    (row mirror, half-row mirror, then xor 2 and xor 1 within quads), so
+    //    lane t ends with values 4t .. 4t + 3: head t / 4, dims 16c + 4 (t % 4) .. + 3
     l_run = row_sum16(l_run);
+    float v[64];
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[k][i] = row_sum16(acc[k][i]);
-    if (t == 0) {
+        for (int i = 0; i < 16; i++) v[16 * k + i] = acc[k][i];
+    auto level = [&](auto mov, int n, bool keep_lo) {
 #pragma unroll
-        for (int h = 0; h < 4; h++) {
-            if (h >= hpk) break;
-            const size_t pi = (size_t)(kvh * hpk + h) * a.nsplit + split;
-            float* dst = a.part_acc + pi * HD + 16 * c;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4)
-                *(f32x4*)(dst + i) = f32x4{acc[h][i], acc[h][i + 1], acc[h][i + 2], acc[h][i + 3]};
+        for (int k = 0; k < n; k++) {
+            const float lo = v[k], hi = v[k + n];
+            v[k] = (keep_lo ? lo : hi) + mov(keep_lo ? hi : lo);
         }
-        if (c < hpk) {
-            const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
-            a.part_m[pi] = m_run * 0.69314718055994531f;  // natural-log units for the combine
-            a.part_l[pi] = l_run;
-        }
+    };
+    level([](float x) { return dpp_f<0x140>(x); }, 32, (t & 8) == 0);  // row_mirror: t <-> 15 - t
+    level([](float x) { return dpp_f<0x141>(x); }, 16, (t & 4) == 0);  // row_half_mirror: t <-> 7 - t (mod 8)
+    level([](float x) { return dpp_f<0x4E>(x); }, 8, (t & 2) == 0);    // quad_perm [2,3,0,1]
+    level([](float x) { return dpp_f<0xB1>(x); }, 4, (t & 1) == 0);    // quad_perm [1,0,3,2]
+    if ((t >> 2) < hpk) {
+        const size_t pi = (size_t)(kvh * hpk + (t >> 2)) * a.nsplit + split;
+        *(f32x4*)(a.part_acc + pi * HD + 16 * c + 4 * (t & 3)) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+    if (t == 0 && c < hpk) {
+        const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
+        a.part_m[pi] = m_run * 0.69314718055994531f;  // natural-log units for the combine
+        a.part_l[pi] = l_run;
     }
 }
 
@@ -1501,7 +1511,7 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
         // fp16 rows in 16-token groups on the matrix cores, one wave per
         // workgroup (the XCD placement of attn_tile_of spreads them)
         dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
-        hipLaunchKernelGGL((attn_f16_mfma_kernel<3>), grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((attn_f16_mfma_kernel<4>), grid, dim3(64), 0, s, a);
         tt = kQ8GroupTokens;
     } else {
         dim3 grid(attn_tile_grid((int)c.n_kv_heads, a.nsplit), nseq);
