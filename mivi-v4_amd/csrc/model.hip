@@ -723,6 +723,45 @@ __device__ __forceinline__ void rows_all(float x, float& r0, float& r1, float& r
     r1 = __uint_as_float(o[0]); r3 = __uint_as_float(o[1]);
 }
 
+// The end of a matrix-core attention wave: lane t + 16c holds head c's
+// running (m, l) and acc[h][i] = dims 16c + i of head h for token lanes t.
+// Sums over the 16 token lanes of each row: l by a butterfly; the 64 (head,
+// dim) values by a reduce-scatter, each level halving a lane's values while
+// the partner (across bit b of t) adds the other half (row mirror, half-row
+// mirror, then xor 2 and xor 1 within quads), so lane t ends with values
+// 4t .. 4t + 3: head t / 4, dims 16c + 4 (t % 4) .. + 3. Writes the split's
+// partials (m in natural-log units for the combine).
+__device__ __forceinline__ void attn_write_partials(const AttnArgs& a, float (&acc)[4][16], float m_run,
+                                                    float l_run, int kvh, int hpk, int split, int t, int c) {
+    constexpr int HD = 64;
+    l_run = row_sum16(l_run);
+    float v[64];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[16 * k + i] = acc[k][i];
+    auto level = [&](auto mov, int n, bool keep_lo) {
+#pragma unroll
+        for (int k = 0; k < n; k++) {
+            const float lo = v[k], hi = v[k + n];
+            v[k] = (keep_lo ? lo : hi) + mov(keep_lo ? hi : lo);
+        }
+    };
+    level([](float x) { return dpp_f<0x140>(x); }, 32, (t & 8) == 0);  // row_mirror: t <-> 15 - t
+    level([](float x) { return dpp_f<0x141>(x); }, 16, (t & 4) == 0);  // row_half_mirror: t <-> 7 - t (mod 8)
+    level([](float x) { return dpp_f<0x4E>(x); }, 8, (t & 2) == 0);    // quad_perm [2,3,0,1]
+    level([](float x) { return dpp_f<0xB1>(x); }, 4, (t & 1) == 0);    // quad_perm [1,0,3,2]
+    if ((t >> 2) < hpk) {
+        const size_t pi = (size_t)(kvh * hpk + (t >> 2)) * a.nsplit + split;
+        *(f32x4*)(a.part_acc + pi * HD + 16 * c + 4 * (t & 3)) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+    if (t == 0 && c < hpk) {
+        const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
+        a.part_m[pi] = m_run * 0.69314718055994531f;
+        a.part_l[pi] = l_run;
+    }
+}
+
 template <int PD, int W>  // groups in flight per wave; waves (kv heads) per workgroup
 __global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
     constexpr int HD = 64, G = kQ8GroupTokens;
@@ -871,33 +910,14 @@ __global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
                 scores(ring[(i + 1) % PD], sa);
                 step(ring[i], cur_s, base + i);
             }
+            // (unconditional, past the split's end a re-read of its last
+            // group: a branch here makes the compiler wait for every load)
             load(ring[i], base + i + PD);
         }
     }
 
-    // 4. sums over the token lanes; lane 16c writes head c's (m, l) and dims
-    //    16c..16c+15 of every head
-    l_run = row_sum16(l_run);
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc[k][i] = row_sum16(acc[k][i]);
-    if (t == 0) {
-#pragma unroll
-        for (int h = 0; h < 4; h++) {
-            if (h >= hpk) break;
-            const size_t pi = (size_t)(kvh * hpk + h) * a.nsplit + split;
-            float* dst = a.part_acc + pi * HD + 16 * c;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4)
-                *(f32x4*)(dst + i) = f32x4{acc[h][i], acc[h][i + 1], acc[h][i + 2], acc[h][i + 3]};
-        }
-        if (c < hpk) {
-            const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
-            a.part_m[pi] = m_run * 0.69314718055994531f;  // natural-log units for the combine
-            a.part_l[pi] = l_run;
-        }
-    }
+    // 4. the split's partials
+    attn_write_partials(a, acc, m_run, l_run, kvh, hpk, split, t, c);
 }
 
 // The query heads of one wave, loaded before anything else the wave reads
@@ -1155,37 +1175,8 @@ __global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
         }
     }
 
-    // 5. sums over the 16 token lanes of a row: l by a butterfly; the 64
-    //    (head, dim) values by a reduce-scatter, each level halving a lane's
-    //    values while the partner (across bit b of t) adds the other half
-    //    (row mirror, half-row mirror, then xor 2 and xor 1 within quads), so
-    //    lane t ends with values 4t .. 4t + 3: head t / 4, dims 16c + 4 (t % 4) .. + 3
-    l_run = row_sum16(l_run);
-    float v[64];
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) v[16 * k + i] = acc[k][i];
-    auto level = [&](auto mov, int n, bool keep_lo) {
-#pragma unroll
-        for (int k = 0; k < n; k++) {
-            const float lo = v[k], hi = v[k + n];
-            v[k] = (keep_lo ? lo : hi) + mov(keep_lo ? hi : lo);
-        }
-    };
-    level([](float x) { return dpp_f<0x140>(x); }, 32, (t & 8) == 0);  // row_mirror: t <-> 15 - t
-    level([](float x) { return dpp_f<0x141>(x); }, 16, (t & 4) == 0);  // row_half_mirror: t <-> 7 - t (mod 8)
-    level([](float x) { return dpp_f<0x4E>(x); }, 8, (t & 2) == 0);    // quad_perm [2,3,0,1]
-    level([](float x) { return dpp_f<0xB1>(x); }, 4, (t & 1) == 0);    // quad_perm [1,0,3,2]
-    if ((t >> 2) < hpk) {
-        const size_t pi = (size_t)(kvh * hpk + (t >> 2)) * a.nsplit + split;
-        *(f32x4*)(a.part_acc + pi * HD + 16 * c + 4 * (t & 3)) = f32x4{v[0], v[1], v[2], v[3]};
-    }
-    if (t == 0 && c < hpk) {
-        const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
-        a.part_m[pi] = m_run * 0.69314718055994531f;  // natural-log units for the combine
-        a.part_l[pi] = l_run;
-    }
+    // 5. the split's partials
+    attn_write_partials(a, acc, m_run, l_run, kvh, hpk, split, t, c);
 }
 
 // Prefill tile: K/V of tile row blockIdx.x (position pos0 + row, k/v at
