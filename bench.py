@@ -280,6 +280,24 @@ def decode_bench(torch, hip, prefill, steps, cpu_budget_s):
     return out
 
 
+def config4_decode_only(torch, hip, prefill, steps):
+    """Config 4's chunked prefill and greedy steps and nothing else, for
+    counter and trace runs: every batch-1 attention launch of the run is then
+    a decode step's (the token-path prefill launches the same grid)."""
+    from mivi_hip.synthmodel import LFM2_1B2, build_hybrid
+    img = build_hybrid(**LFM2_1B2, ctx_len=65536, seed=2024)
+    m = hip.Model(img, max_ctx=prefill + steps, kv_precision=hip.KvPrecision.F16)
+    prompt = __import__("numpy").random.default_rng(11).integers(0, LFM2_1B2["vocab"], prefill + 1)
+    m.set_prefill_strategy(512)
+    m.prefill(prompt[:-1])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.generate_greedy([int(prompt[-1])], [prefill], steps)
+    dt = time.perf_counter() - t0
+    m.close()
+    return dict(tok_s=steps / dt, steps=steps, prefill=prefill)
+
+
 def mixed_decode_bench(torch, hip, prompt, prefill, steps, q4k_prefill_s):
     """The same prompt and steps on the Q4_K_M layout of the 1.2B shape
     (8 ffn_down and 2 attn_v matrices in Q6_K, as the reference's 1.2B
@@ -576,6 +594,8 @@ def main():
     ap.add_argument("--only-q6k", action="store_true", help="config 2 only (counter runs)")
     ap.add_argument("--only-gemm", action="store_true", help="config 3 only (counter runs)")
     ap.add_argument("--only-config5", action="store_true", help="config 5 only (counter runs)")
+    ap.add_argument("--only-config4", action="store_true",
+                    help="config 4 chunked prefill + greedy decode only (counter runs)")
     ap.add_argument("--no-config5", action="store_true")
     ap.add_argument("--config5-ctx", type=int, default=32768)
     ap.add_argument("--config5-steps", type=int, default=128)
@@ -594,6 +614,10 @@ def main():
     if a.only_gemm:
         g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3)
         log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s")
+        return
+    if a.only_config4:
+        c4 = config4_decode_only(torch, hip, a.decode_prefill, a.decode_steps)
+        log(f"config 4: {c4['tok_s']:.1f} tok/s over {c4['steps']} greedy steps (graph capture included)")
         return
     if a.only_config5:
         c5 = batched_decode_bench(torch, hip, 8, a.config5_ctx, a.config5_steps)

@@ -1,10 +1,12 @@
 """Text summaries of rocprofv3 result databases (rocpd SQLite).
 
-    python -m mivi_hip.rocpd_summary DB [--filter SUBSTR] [--pmc]
+    python -m mivi_hip.rocpd_summary DB [--filter SUBSTR] [--pmc [--by-grid]]
 
 Kernel mode prints dispatch count and duration statistics per kernel name.
 With --pmc it prints, per kernel name, the mean per-dispatch value of every
-collected counter (FETCH_SIZE / WRITE_SIZE are reported by rocprofv3 in KiB).
+collected counter (FETCH_SIZE / WRITE_SIZE are reported by rocprofv3 in KiB);
+--by-grid splits each kernel's dispatches by grid size (e.g. the decode
+launches of a kernel from its prefill launches).
 """
 from __future__ import annotations
 
@@ -29,17 +31,19 @@ def kernel_stats(db: str, filt: str = ""):
     return out
 
 
-def pmc_stats(db: str, filt: str = ""):
+def pmc_stats(db: str, filt: str = "", by_grid: bool = False):
     cur = sqlite3.connect(db).cursor()
-    rows = cur.execute("select kernel_name, counter_name, value, dispatch_id from counters_collection").fetchall()
+    rows = cur.execute("select kernel_name, counter_name, value, dispatch_id, grid_size_x, grid_size_y "
+                       "from counters_collection").fetchall()
     per = collections.defaultdict(lambda: collections.defaultdict(float))
-    for name, counter, value, disp in rows:
+    for name, counter, value, disp, gx, gy in rows:
         if filt in name:
-            per[(name, counter)][disp] += value  # summed over the counter's instances
+            grid = (gx, gy) if by_grid else None
+            per[(name, grid, counter)][disp] += value  # summed over the counter's instances
     out = []
-    for (name, counter), d in sorted(per.items()):
+    for (name, grid, counter), d in sorted(per.items(), key=lambda kv: (kv[0][0], kv[0][1] or (0, 0), kv[0][2])):
         vals = list(d.values())
-        out.append(dict(name=name, counter=counter, dispatches=len(vals), mean=statistics.mean(vals),
+        out.append(dict(name=name, grid=grid, counter=counter, dispatches=len(vals), mean=statistics.mean(vals),
                         median=statistics.median(vals)))
     return out
 
@@ -72,15 +76,17 @@ def main():
     ap.add_argument("db")
     ap.add_argument("--filter", default="")
     ap.add_argument("--pmc", action="store_true")
+    ap.add_argument("--by-grid", action="store_true", help="with --pmc: one line per (kernel, grid size)")
     ap.add_argument("--period-marker", default="", help="per-repetition breakdown ending at this kernel")
     ap.add_argument("--periods", type=int, default=32)
     a = ap.parse_args()
     if a.period_marker:
         per_period(a.db, a.period_marker, a.periods)
     elif a.pmc:
-        for r in pmc_stats(a.db, a.filter):
+        for r in pmc_stats(a.db, a.filter, a.by_grid):
+            grid = f"grid {r['grid'][0]}x{r['grid'][1]}  " if r["grid"] else ""
             print(f"{r['counter']:16s} dispatches {r['dispatches']:6d}  mean {r['mean']:14.2f}  "
-                  f"median {r['median']:14.2f}  {r['name'][:110]}")
+                  f"median {r['median']:14.2f}  {grid}{r['name'][:110]}")
     else:
         print(f"{'count':>6s} {'mean_us':>10s} {'median_us':>10s} {'min_us':>9s} {'total_ms':>9s}  kernel")
         for r in kernel_stats(a.db, a.filter):
