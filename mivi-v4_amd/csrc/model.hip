@@ -1492,7 +1492,10 @@ void enqueue_attention(const mivi_model_info& c, const AttnArgs& a, unsigned nse
     int tt;
     if (a.packed) {  // Q8_0 group layout (attn_q8_mfma_ok shapes)
         // three groups in flight per wave: other depths measured slower
-        // (config 5: 6583 tok/s at 2, 7095 at 3, 6645 at 4, 6356 at 6)
+        // (config 5: 6583 tok/s at 2, 7095 at 3, 6645 at 4, 6356 at 6; at
+        // one workgroup per CU and up to 256 registers 8090 at 3 and 4, 7450
+        // at 6, against 8400 here). The kernel waits on memory: its score and
+        // value arithmetic taken out, a launch is under 2 us shorter.
         const int w = attn_q8_waves((int)c.n_kv_heads);
         dim3 grid(attn_tile_grid(((int)c.n_kv_heads + w - 1) / w, a.nsplit), nseq);
         if (w == 8) hipLaunchKernelGGL((attn_q8_mfma_kernel<3, 8>), grid, dim3(512), 0, s, a);

@@ -18,6 +18,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "gemv.h"
@@ -1330,7 +1331,6 @@ struct ColStage {
     static_assert(PRO != mivi::PRO_SWIGLU, "no SwiGLU prologue here");
     static constexpr int V = K / P, NL = V / 256;
     f32x4 u[NL];
-    f32x4 aux[PRO == mivi::PRO_RMSNORM ? NL : 1];
     float t4[NL];  // sums of the lane's four values
     float m = 0.f, ss = 0.f;
 
@@ -1343,12 +1343,9 @@ struct ColStage {
         const int l = threadIdx.x & 63, o = h * V;
 #pragma unroll
         for (int i = 0; i < NL; i++) u[i] = *(const gf32x4*)(a.x + o + 4 * (l + 64 * ch(i)));
-        if constexpr (PRO == mivi::PRO_RMSNORM) {
-#pragma unroll
-            for (int i = 0; i < NL; i++) aux[i] = *(const gf32x4*)(a.norm_w + o + 4 * (l + 64 * ch(i)));
-        }
     }
-    __device__ __forceinline__ void part(const mivi::GemvArgs& a, int h) {
+    // nwl: RMSNORM's weight vector in LDS (loaded once by the workgroup)
+    __device__ __forceinline__ void part(const mivi::GemvArgs& a, int h, const float* nwl = nullptr) {
         const int l = threadIdx.x & 63, o = h * V;
         float nn = 0.f;  // NaN for a NaN value (fmaxf passes it over)
         if constexpr (PRO == mivi::PRO_CONV) {
@@ -1403,7 +1400,8 @@ struct ColStage {
         for (int i = 0; i < NL; i++) {
             float x[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
             if constexpr (PRO == mivi::PRO_RMSNORM) {
-                const float nw[4] = {aux[i].x, aux[i].y, aux[i].z, aux[i].w};
+                const f32x4 w4 = *(const f32x4*)&nwl[o + 4 * (l + 64 * ch(i))];
+                const float nw[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     ss = fmaf(x[e], x[e], ss);  // (non-finite x: ss, so s, NaN)
@@ -1470,17 +1468,26 @@ __device__ __forceinline__ mivi::GemvArgs gemv_col_group(const mivi::GemvArgs& a
     return v;
 }
 
-template <int PRO, int EPI, int KT, int NG, int DQ>
+template <int PRO, int EPI, int KT, int NG, int DQ, int KS = 1>
 __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
-    static_assert(KT == 2048 || KT == 8192, "decode depths");
+    static_assert(KT == 1024 || KT == 2048 || KT == 8192, "decode depths (per K split)");
     static_assert(DQ == 4 || DQ == 8, "depth slices per team");
-    // NG = 1 launched with several column groups: column group blockIdx.y,
-    // at most four columns
-    const mivi::GemvArgs a = (NG == 1 && gridDim.y > 1) ? gemv_col_group(a0, 4 * (int)blockIdx.y) : a0;
+    // KS > 1: the depth a0.K = KS * KT in KS slices, slice blockIdx.y; the
+    // workgroup stages and reads only its slice and adds its partial sums
+    // into y (the residual add: other slices add theirs)
+    static_assert(KS == 1 || (PRO == mivi::PRO_NONE && EPI == mivi::EPI_STORE), "K splits: products added into y");
+    // NG = 1 launched with several column groups (KS = 1): column group
+    // blockIdx.y, at most four columns
+    const mivi::GemvArgs a = (KS == 1 && NG == 1 && gridDim.y > 1) ? gemv_col_group(a0, 4 * (int)blockIdx.y) : a0;
+    const int ks = KS > 1 ? (int)blockIdx.y : 0;
     constexpr int K = KT, nb = K / 256;
     constexpr int R = kColWaves / DQ;       // teams
-    constexpr int SQ = nb / DQ;             // superblocks per wave and group: 1, 2, 4 or 8
-    constexpr int PD = SQ < 4 ? SQ : 4;     // superblock chunks in flight per wave
+    constexpr int SQ = nb / DQ;             // superblocks per wave and group: 1, 2 or 4
+    // U group steps' chunks in flight per wave, all of a step's SQ (more, the
+    // weights then loaded whole at the start, delays the activations)
+    constexpr int U = 1;
+    constexpr int PD = SQ * U;
+    static_assert(PD <= 4, "ring of at most four superblock chunks");
     constexpr int NCM = 4 * NG;
     constexpr int P = kColWaves / NCM;      // staging parts per column (one per wave)
     constexpr int PS = K / 4 + 4;           // digit plane stride (dwords)
@@ -1489,7 +1496,9 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     __shared__ float scol[NCM];
     __shared__ float red[2][NCM][P];        // parts' max |u| and sum x^2
     __shared__ float xq[R][2][DQ - 1][NG][64];  // waves 1.. -> wave 0 of a team, by group-step parity
-    const Segs sg(a, nb * 144);
+    // RMSNORM: the weight vector, loaded once for the workgroup's columns
+    __shared__ __attribute__((aligned(16))) float nwl[PRO == mivi::PRO_RMSNORM ? K : 4];
+    const Segs sg(a, (size_t)nb * KS * 144);
     const int n = sg.n, n0 = a.seg[0].n;
     const int ncol = a.ncol;  // 1..NCM, workgroup-uniform
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1524,25 +1533,37 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     const int task_c = wave / P, task_h = wave % P;  // this wave's column and part
     const bool stager = task_c < ncol;               // wave-uniform
     ColStage<PRO, K, P> stg;
-    if (stager) stg.issue(gemv_column(a, task_c), task_h);
-    // ring of superblock chunks: this wave's superblock bb of step st in slot bb % PD
+    mivi::GemvArgs ax = a;  // the staged slice
+    if constexpr (KS > 1) ax.x = a.x + ks * KT;
+    static_assert(PRO != mivi::PRO_RMSNORM || K == 4 * kColWG, "one norm weight quad per thread");
+    f32x4 nw4;
+    if constexpr (PRO == mivi::PRO_RMSNORM) nw4 = *(const gf32x4*)(a.norm_w + 4 * threadIdx.x);
+    if (stager) stg.issue(gemv_column(ax, task_c), task_h);
+    // ring of superblock chunks: this wave's superblock bb of step st in slot
+    // (st mod U) SQ + bb. Every load is unconditional (a step past the last
+    // one re-reads the last): a branch around a load makes the compiler wait
+    // for it before the next chunk's use, a memory latency per superblock.
     u32x4 hdr[PD];
     u32x2 cq[PD][4];
     auto load = [&](int slot, int st, int bb) {
         st = st < cnt ? st : cnt - 1;
         const int r = row_of(st < 0 ? 0 : st);
-        const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (wq * SQ + bb);
+        const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (ks * nb + wq * SQ + bb);
         hdr[slot] = ldg16(p);
 #pragma unroll
         for (int g = 0; g < 4; g++) cq[slot][g] = *(const __attribute__((address_space(1))) u32x2*)(p + 16 + 32 * g + 8 * kg);
     };
 #pragma unroll
-    for (int q = 0; q < PD; q++) load(q, 0, q);
+    for (int q = 0; q < PD; q++) load(q, q / SQ, q % SQ);
     // the zero plane of every column
 #pragma unroll
     for (int c = 0; c < NCM; c++)
         for (int i = threadIdx.x; i < PS / 4; i += kColWG) *(u32x4*)&dig[c][3 * PS + 4 * i] = u32x4{0u, 0u, 0u, 0u};
-    if (stager) stg.part(gemv_column(a, task_c), task_h);
+    if constexpr (PRO == mivi::PRO_RMSNORM) {
+        *(f32x4*)&nwl[4 * threadIdx.x] = nw4;
+        __syncthreads();
+    }
+    if (stager) stg.part(gemv_column(ax, task_c), task_h, nwl);
     if constexpr (P > 1) {
         if (stager && lane == 0) {
             red[0][task_c][task_h] = stg.m;
@@ -1561,7 +1582,7 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
                 sst += red[1][task_c][h];
             }
         }
-        const float sc = stg.template finish<PS>(gemv_column(a, task_c), task_h, mt, sst, dig[task_c], xsum[task_c]);
+        const float sc = stg.template finish<PS>(gemv_column(ax, task_c), task_h, mt, sst, dig[task_c], xsum[task_c]);
         if (lane == 0 && task_h == 0) scol[task_c] = sc;
     }
     __syncthreads();
@@ -1574,7 +1595,9 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
 #pragma unroll
     for (int G = 0; G < NG; G++) dA[G] = dig[min(4 * G + ci, ncol - 1)] + pi * PS + 2 * kg;
 
-    for (int st = 0; st < cnt; st++) {
+    // group step st from slots s0 .. s0 + SQ - 1; REFILL: reload them with
+    // step st + U's chunks
+    auto step = [&](const int st, const int s0, auto refill) {
         // this wave's superblocks of the group, each summed in int32 over its
         // four units before the float steps
         float part[NG];
@@ -1582,14 +1605,12 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
         for (int G = 0; G < NG; G++) part[G] = 0.f;
 #pragma unroll
         for (int bb = 0; bb < SQ; bb++) {
-            const int slot = bb % PD, b = wq * SQ + bb;
+            const int slot = s0 + bb, b = wq * SQ + bb;
             const u32x4 h = hdr[slot];
             u32x2 q[4];
 #pragma unroll
             for (int g = 0; g < 4; g++) q[g] = cq[slot][g];
-            // refill with the chunk PD ahead (of the next group, if any)
-            if (bb + PD < SQ) load(slot, st, bb + PD);
-            else if (st + 1 < cnt) load(slot, st + 1, bb + PD - SQ);
+            if constexpr (decltype(refill)::value) load(slot, st + U, bb);
             const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
             int AL[NG][3], AH[NG][3];  // low- and high-nibble sub-blocks, one product per step
             float Mac[NG];
@@ -1664,12 +1685,24 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
                 } else {
                     if (r >= 0 && cc < ncol) {
                         gfloat* y = (gfloat*)(sg.out(r) + cc * a.ys);
-                        if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(y, v);
+                        if (KS > 1 || a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(y, v);
                         else *y = v;
                     }
                 }
             }
         }
+    };
+    // blocks of U steps: every block but the last refills the ring with the
+    // next block's chunks; the last one (its steps up to cnt) loads nothing
+    const int nblk = (cnt + U - 1) / U;
+    for (int blk = 0; blk + 1 < nblk; blk++) {
+#pragma unroll
+        for (int u = 0; u < U; u++) step(blk * U + u, u * SQ, std::true_type{});
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int st = (nblk - 1) * U + u;
+        if (st < cnt) step(st, u * SQ, std::false_type{});  // workgroup-uniform
     }
 }
 
@@ -1689,6 +1722,23 @@ void launch_cols(const mivi::GemvArgs& a, int ngr, int gy, hipStream_t s) {
     }
     const int gc = std::max(1, std::min(ngr, cus));
     hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+}
+
+// Products added into y (the residual adds: the FFN down projection at K =
+// 8192, the attention and ShortConv output projections at K = 2048) in KS
+// slices of the depth KFULL: KS workgroups per row group, each staging only
+// its slice of the columns (at KS = 8 one eighth of the activation bytes,
+// which bound the unsplit launch) and adding its partial sums into y. Two
+// teams of four waves a workgroup; gc row-group workgroups per slice, a
+// multiple of 8, so that a row group's slices share an XCD.
+template <int KFULL, int KS, int NG>
+void launch_cols_ksplit(const mivi::GemvArgs& a, int ngr, hipStream_t s) {
+    constexpr int KT = KFULL / KS;
+    const int cus = mivi::num_cus();
+    int gc = std::min((ngr + 1) / 2, std::max(8, cus / KS));
+    gc = std::max(8, gc / 8 * 8);
+    hipLaunchKernelGGL((gemv_q4k_cols_kernel<mivi::PRO_NONE, mivi::EPI_STORE, KT, NG, 4, KS>), dim3(gc, KS),
+                       dim3(kColWG), 0, s, a);
 }
 
 // ------------------------------------------ Q6_K row quads on the matrix cores
@@ -2796,13 +2846,27 @@ int32_t launch_pro(int32_t t, const mivi::GemvArgs& a, int n, hipStream_t s) {
                 const int gy = (a.ncol + 3) / 4;
                 if constexpr (PRO == mivi::PRO_SWIGLU) {
                 } else if (K == 8192) {
-                    if constexpr (PRO == mivi::PRO_NONE) launch_cols<PRO, mivi::EPI_STORE, 8192, 1>(a, ngr, gy, s);
+                    // added into y: eight slices of the depth (config 5: 8320
+                    // tok/s, 8300 at four slices, 7735 unsplit)
+                    if constexpr (PRO == mivi::PRO_NONE) {
+                        if (a.accumulate) {
+                            if (a.ncol > 4) launch_cols_ksplit<8192, 8, 2>(a, ngr, s);
+                            else launch_cols_ksplit<8192, 8, 1>(a, ngr, s);
+                        } else {
+                            launch_cols<PRO, mivi::EPI_STORE, 8192, 1>(a, ngr, gy, s);
+                        }
+                    }
                 } else if (ep == mivi::EPI_SWIGLU) {
                     if (a.ncol > 4 && PRO != mivi::PRO_CONV) {
                         if constexpr (PRO != mivi::PRO_CONV) launch_cols<PRO, mivi::EPI_SWIGLU, 2048, 2>(a, ngr, 1, s);
                     } else {
                         launch_cols<PRO, mivi::EPI_SWIGLU, 2048, 1>(a, ngr, gy, s);
                     }
+                } else if (PRO == mivi::PRO_NONE && a.accumulate && a.ncol > 4) {
+                    // added into y, five or more columns: all of them in one
+                    // workgroup over half the depth (8430 tok/s, 8390 as two
+                    // groups of four columns over the whole depth)
+                    if constexpr (PRO == mivi::PRO_NONE) launch_cols_ksplit<2048, 2, 2>(a, ngr, s);
                 } else if (a.ncol > 4 && (ngr < mivi::num_cus() || PRO == mivi::PRO_CONV)) {
                     // fewer row groups than CUs (the 2048-row projections), or
                     // the conv prologue (whose eight columns at once would not
