@@ -178,8 +178,10 @@ typedef struct mivi_model_info {
     int32_t kv_precision, yarn;
     float yarn_scale;
     size_t weight_bytes;   /* device bytes of the weights: the GGUF tensor data plus the
-                              packed copies kept beside it (Q6_K head, Q4_K row quads);
-                              MIVI_NO_PACK=1 at create leaves the copies out */
+                              packed copies kept beside it (Q6_K head, Q4_K and Q6_K row
+                              quads; with max_batch > 1 the Q4_K projections in the batched
+                              column kernels' group order); MIVI_NO_PACK=1 at create leaves
+                              the copies out, MIVI_NO_COLS_PACK=1 the batched ones */
     size_t kv_bytes;       /* device bytes of K + V for all sequences */
 } mivi_model_info;
 

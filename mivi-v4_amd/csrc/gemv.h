@@ -52,6 +52,9 @@ struct GemvArgs {
     // argmax partials at + c*ps). ncol 0 or 1: one column.
     int ncol;
     int64_t xs, sts, ys, ps;
+    // Batched Q4_K columns (the column kernels): the launch's rows packed by
+    // launch_pack_q4k_cols in the kernel's group order, else null (GGUF rows)
+    const uint8_t* cw;
 };
 
 // Most columns one batched streaming launch takes (more are split into
@@ -102,6 +105,43 @@ int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t co
 // results to the streaming kernel on the GGUF rows
 inline bool q4k_quad_layout(size_t rows, size_t cols) { return (cols == 2048 || cols == 8192) && rows % 4 == 0; }
 int32_t launch_pack_q4k(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
+
+// The batched Q4_K column kernel takes 16-row groups: lane row j of group grp
+// is row cols_group_row(...) of the launch's concatenated segments (n rows,
+// n0 in the first), or -1 (none; its lanes then read row 0 and store
+// nothing). EPI_SWIGLU groups: gate rows 8 grp .. 8 grp + 7, then the same up
+// rows; EPI_CONV groups: channels 5 grp .. 5 grp + 4 of the D = n0 / 3, each
+// as its B, C, X rows (j = 3i + k; row 15 repeats row 14); other epilogues:
+// rows 16 grp .. 16 grp + 15.
+__host__ __device__ inline int cols_group_row(int epi, int grp, int j, int n0, int n) {
+    if (epi == EPI_SWIGLU) {
+        const int c = 8 * grp + (j & 7);
+        return c < n0 ? c + (j >> 3) * n0 : -1;
+    }
+    if (epi == EPI_CONV) {
+        const int D3 = n0 / 3, jj = j < 15 ? j : 14, c = 5 * grp + jj / 3;
+        return c < D3 ? c + (jj % 3) * D3 : -1;
+    }
+    const int r = 16 * grp + j;
+    return r < n ? r : -1;
+}
+__host__ __device__ inline int cols_groups(int epi, int n0, int n) {
+    return epi == EPI_SWIGLU ? (n0 + 7) / 8 : epi == EPI_CONV ? (n0 / 3 + 4) / 5 : (n + 15) / 16;
+}
+
+// Q4_K rows in the column kernel's order (launch_pack_q4k_cols): per group,
+// per superblock s of the row (cols / 256 of them), kColsChunkBytes: the 16
+// rows' 16-byte headers (d, dmin, scales), then the code bytes as two 1 KB
+// halves, lane l = j + 16 kg holding in each 16 bytes of row j: codes
+// [32 g + 8 kg, + 8) for g = 0, 1 (first half) and g = 2, 3 (second), the
+// bytes of its two B operands per 64-value unit. Every load of the kernel
+// is then one contiguous 256 B or 1 KB (the GGUF rows give it 16 rows x 32
+// bytes per load instruction, bound by the L1's cache-line rate).
+// rows_host[16 grp + j]: the device address of group grp's row j (any valid
+// row where the group has none there).
+constexpr int kColsChunkBytes = 16 * 144;
+int32_t launch_pack_q4k_cols(const uint8_t* const* rows_host, int ngroups, size_t cols, uint8_t* dst,
+                             hipStream_t s);
 
 // Row `id` of an embedding table (model.rs:358-375, the token's row
 // dequantized: Q6_K, Q4_K, Q8_0, F16, BF16 or F32) into x, by threads

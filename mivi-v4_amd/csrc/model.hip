@@ -1441,6 +1441,10 @@ struct Layer {
     size_t conv_len = 0;
     const float* ffn_norm = nullptr;
     int cache_idx = -1;
+    // batched Q4_K launches' rows in the column kernel's group order
+    // (launch_pack_q4k_cols; models with max_batch > 1), else null: q|k|v,
+    // wo or out_proj, in_proj (conv groups), gate|up (SwiGLU groups), down
+    const uint8_t *cw_qkv = nullptr, *cw_o = nullptr, *cw_in = nullptr, *cw_gu = nullptr, *cw_down = nullptr;
 };
 
 struct SeqState {
@@ -1696,11 +1700,13 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.phase = &m->ctrl->phase[b0];
             g.sts = z.conv;
             g.epilogue = EPI_CONV;
+            g.cw = ncol > 1 ? L.cw_in : nullptr;
             rc = launch_proj(L.in_proj.type, PRO_RMSNORM, g, {&L.in_proj}, s);
             const bool conv_fused = rc == MIVI_OK;
             if (rc && rc != MIVI_ERR_UNSUPPORTED) return rc;
             if (!conv_fused) {
                 g.epilogue = EPI_STORE;
+                g.cw = nullptr;  // packed in the conv groups' order
                 if ((rc = launch_gemv_ex(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
             }
             // out_proj on the gated conv, residual add into x
@@ -1709,6 +1715,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             go.nseg = 1; go.K = D; go.x = s0.sc_in;
             go.accumulate = 1;
             go.ncol = ncol; go.xs = z.sc_in; go.ys = z.x;
+            go.cw = ncol > 1 ? L.cw_o : nullptr;
             if (!conv_fused) {
                 go.conv_w = g.conv_w; go.conv_mode = g.conv_mode; go.ksize = g.ksize;
                 go.st_in = g.st_in; go.st_out = g.st_out; go.phase = g.phase; go.sts = g.sts;
@@ -1720,6 +1727,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.seg[2] = {L.wv.w, s0.v, KV};
             g.nseg = 3; g.K = D; g.x = s0.x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = ncol; g.xs = z.x; g.ys = z.qkv;
+            g.cw = ncol > 1 ? L.cw_qkv : nullptr;  // (all three Q4_K: one run)
             // one launch per run of equal weight types (a Q4_K_M file's
             // Q6_K attn_v runs apart from q|k)
             rc = by_type_runs(g, {&L.wq, &L.wk, &L.wv}, [&](int32_t t, const GemvArgs& gr, const Mat* const* mr, int n) {
@@ -1756,6 +1764,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             g.seg[0] = {L.wo.w, s0.x, D};
             g.nseg = 1; g.K = D; g.x = s0.attn_out; g.accumulate = 1;
             g.ncol = ncol; g.xs = z.x; g.ys = z.x;
+            g.cw = ncol > 1 ? L.cw_o : nullptr;
             if ((rc = launch_proj(L.wo.type, PRO_NONE, g, {&L.wo}, s))) return rc;
         }
         // ffn.rs:56-108
@@ -1769,10 +1778,12 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
             // gate|up with the SwiGLU epilogue writes silu(gate) * up into hb
             // directly where the streaming kernel takes the shape
             g.epilogue = EPI_SWIGLU;
+            g.cw = ncol > 1 ? L.cw_gu : nullptr;
             rc = launch_proj(L.gate.type, PRO_RMSNORM, g, {&L.gate, &L.up}, s);
             fused = rc == MIVI_OK;
             if (rc && rc != MIVI_ERR_UNSUPPORTED) return rc;
             g.epilogue = EPI_STORE;
+            g.cw = nullptr;  // packed in the SwiGLU groups' order
         }
         if (fused) {
         } else if (L.gate.type == L.up.type) {
@@ -1788,6 +1799,7 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
         g.seg[0] = {L.down.w, s0.x, D};
         g.nseg = 1; g.K = H; g.x = s0.hb; g.x2 = s0.hb2; g.accumulate = 1;
         g.ncol = ncol; g.xs = z.hb; g.ys = z.x;
+        g.cw = ncol > 1 && fused ? L.cw_down : nullptr;
         if ((rc = launch_proj(L.down.type, fused ? PRO_NONE : PRO_SWIGLU, g, {&L.down}, s))) return rc;
     }
     if (!do_head) {
@@ -2228,6 +2240,59 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         }
         if (total && hipDeviceSynchronize() != hipSuccess)
             return fail(set_error(MIVI_ERR_HIP, "packing the projections failed"));
+        c.weight_bytes += total;
+    }
+    // batched decode GEMVs (max_batch > 1) stream each all-Q4_K projection
+    // launch packed in the column kernel's group order: one more copy of
+    // those rows (not with MIVI_NO_PACK or MIVI_NO_COLS_PACK)
+    if (!getenv("MIVI_NO_PACK") && !getenv("MIVI_NO_COLS_PACK") && max_batch > 1) {
+        struct Job {
+            const uint8_t** dst;
+            std::vector<const Mat*> ms;
+            int epi;
+        };
+        std::vector<Job> jobs;
+        auto q4 = [](const Mat& x) { return x.w && x.type == MIVI_GGML_Q4_K && x.cols % 256 == 0; };
+        for (size_t i = 0; i < c.n_layers; i++) {
+            Layer& L = m->layers[i];
+            if (L.attn) {
+                if (q4(L.wq) && q4(L.wk) && q4(L.wv)) jobs.push_back({&L.cw_qkv, {&L.wq, &L.wk, &L.wv}, EPI_STORE});
+                if (q4(L.wo)) jobs.push_back({&L.cw_o, {&L.wo}, EPI_STORE});
+            } else {
+                if (q4(L.in_proj)) jobs.push_back({&L.cw_in, {&L.in_proj}, EPI_CONV});
+                if (q4(L.out_proj)) jobs.push_back({&L.cw_o, {&L.out_proj}, EPI_STORE});
+            }
+            if (q4(L.gate) && q4(L.up) && L.gate.rows == L.up.rows) jobs.push_back({&L.cw_gu, {&L.gate, &L.up}, EPI_SWIGLU});
+            if (q4(L.down)) jobs.push_back({&L.cw_down, {&L.down}, EPI_STORE});
+        }
+        auto groups = [](const Job& j) {
+            size_t n = 0;
+            for (const Mat* x : j.ms) n += x->rows;
+            return cols_groups(j.epi, (int)j.ms[0]->rows, (int)n);
+        };
+        size_t total = 0;
+        for (const Job& j : jobs) total += (size_t)groups(j) * (j.ms[0]->cols / 256) * kColsChunkBytes;
+        uint8_t* q = nullptr;
+        if (total && (rc = m->alloc(&q, total))) return fail(rc);
+        std::vector<const uint8_t*> rows;
+        for (const Job& j : jobs) {
+            const int ng = groups(j), n0 = (int)j.ms[0]->rows;
+            int n = 0;
+            for (const Mat* x : j.ms) n += (int)x->rows;
+            const size_t rb = j.ms[0]->cols / 256 * 144;
+            rows.assign((size_t)ng * 16, nullptr);
+            for (int grp = 0; grp < ng; grp++)
+                for (int jj = 0; jj < 16; jj++) {
+                    int r = cols_group_row(j.epi, grp, jj, n0, n);
+                    r = r < 0 ? 0 : r;  // (its lanes store nothing)
+                    size_t k = 0;
+                    while (r >= (int)j.ms[k]->rows) r -= (int)j.ms[k++]->rows;
+                    rows[(size_t)grp * 16 + jj] = j.ms[k]->w + (size_t)r * rb;
+                }
+            if ((rc = launch_pack_q4k_cols(rows.data(), ng, j.ms[0]->cols, q, nullptr))) return fail(rc);
+            *j.dst = q;
+            q += (size_t)ng * (j.ms[0]->cols / 256) * kColsChunkBytes;
+        }
         c.weight_bytes += total;
     }
     {

@@ -1468,7 +1468,7 @@ __device__ __forceinline__ mivi::GemvArgs gemv_col_group(const mivi::GemvArgs& a
     return v;
 }
 
-template <int PRO, int EPI, int KT, int NG, int DQ, int KS = 1>
+template <int PRO, int EPI, int KT, int NG, int DQ, int KS = 1, bool CW = false>
 __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
     static_assert(KT == 1024 || KT == 2048 || KT == 8192, "decode depths (per K split)");
     static_assert(DQ == 4 || DQ == 8, "depth slices per team");
@@ -1507,8 +1507,7 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     // EPI_CONV: a group holds channels 5g .. 5g+4, lane row j = 3i + k their
     // B, C, X rows (k = 0, 1, 2); lane row 15 repeats row 14 and is not stored
     static_assert(EPI != mivi::EPI_CONV || KT == 2048, "the conv epilogue is the K = 2048 in_proj");
-    const int D3 = n0 / 3;
-    const int ngroups = EPI == mivi::EPI_SWIGLU ? (n0 + 7) / 8 : EPI == mivi::EPI_CONV ? (D3 + 4) / 5 : (n + 15) / 16;
+    const int ngroups = mivi::cols_groups(EPI, n0, n);
     // group steps (workgroup-uniform): team t takes group
     // blockIdx.x + (st R + t) gridDim.x in step st
     const int stride = R * (int)gridDim.x;
@@ -1517,17 +1516,7 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     // row of lane row j in group step st (-1: none; loads then use row 0)
     auto row_of = [&](int st) {
         const int grp = (int)blockIdx.x + (st * R + team) * (int)gridDim.x;
-        if constexpr (EPI == mivi::EPI_SWIGLU) {
-            const int c = 8 * grp + (j & 7);
-            return c < n0 ? c + (j >> 3) * n0 : -1;
-        } else if constexpr (EPI == mivi::EPI_CONV) {
-            const int jj = j < 15 ? j : 14;
-            const int c = 5 * grp + jj / 3;
-            return c < D3 ? c + (jj % 3) * D3 : -1;
-        } else {
-            const int r = 16 * grp + j;
-            return r < n ? r : -1;
-        }
+        return mivi::cols_group_row(EPI, grp, j, n0, n);
     };
     // the activations first (see ColStage), then the weight ring
     const int task_c = wave / P, task_h = wave % P;  // this wave's column and part
@@ -1547,11 +1536,25 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     u32x2 cq[PD][4];
     auto load = [&](int slot, int st, int bb) {
         st = st < cnt ? st : cnt - 1;
-        const int r = row_of(st < 0 ? 0 : st);
-        const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (ks * nb + wq * SQ + bb);
-        hdr[slot] = ldg16(p);
+        if constexpr (CW) {
+            // launch_pack_q4k_cols layout: group grp's chunk of this superblock
+            int grp = (int)blockIdx.x + ((st < 0 ? 0 : st) * R + team) * (int)gridDim.x;
+            grp = grp < ngroups ? grp : ngroups - 1;
+            const uint8_t* p = a.cw + ((size_t)grp * (nb * KS) + ks * nb + wq * SQ + bb) * mivi::kColsChunkBytes;
+            hdr[slot] = ldg16(p + 16 * j);
+            const u32x4 c0 = ldg16(p + 256 + 16 * lane), c1 = ldg16(p + 256 + 1024 + 16 * lane);
+            cq[slot][0] = u32x2{c0.x, c0.y};
+            cq[slot][1] = u32x2{c0.z, c0.w};
+            cq[slot][2] = u32x2{c1.x, c1.y};
+            cq[slot][3] = u32x2{c1.z, c1.w};
+        } else {
+            const int r = row_of(st < 0 ? 0 : st);
+            const uint8_t* p = sg.row(r < 0 ? 0 : r) + 144 * (ks * nb + wq * SQ + bb);
+            hdr[slot] = ldg16(p);
 #pragma unroll
-        for (int g = 0; g < 4; g++) cq[slot][g] = *(const __attribute__((address_space(1))) u32x2*)(p + 16 + 32 * g + 8 * kg);
+            for (int g = 0; g < 4; g++)
+                cq[slot][g] = *(const __attribute__((address_space(1))) u32x2*)(p + 16 + 32 * g + 8 * kg);
+        }
     };
 #pragma unroll
     for (int q = 0; q < PD; q++) load(q, q / SQ, q % SQ);
@@ -1716,12 +1719,19 @@ void launch_cols(const mivi::GemvArgs& a, int ngr, int gy, hipStream_t s) {
     if constexpr (KT == 2048) {
         if (2 * ngr >= 3 * cus) {
             const int gc = std::max(1, std::min((ngr + 1) / 2, cus));
-            hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 4>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+            if (a.cw)
+                hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 4, 1, true>), dim3(gc, gy), dim3(kColWG), 0,
+                                   s, a);
+            else
+                hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 4>), dim3(gc, gy), dim3(kColWG), 0, s, a);
             return;
         }
     }
     const int gc = std::max(1, std::min(ngr, cus));
-    hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+    if (a.cw)
+        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8, 1, true>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8>), dim3(gc, gy), dim3(kColWG), 0, s, a);
 }
 
 // Products added into y (the residual adds: the FFN down projection at K =
@@ -1737,8 +1747,12 @@ void launch_cols_ksplit(const mivi::GemvArgs& a, int ngr, hipStream_t s) {
     const int cus = mivi::num_cus();
     int gc = std::min((ngr + 1) / 2, std::max(8, cus / KS));
     gc = std::max(8, gc / 8 * 8);
-    hipLaunchKernelGGL((gemv_q4k_cols_kernel<mivi::PRO_NONE, mivi::EPI_STORE, KT, NG, 4, KS>), dim3(gc, KS),
-                       dim3(kColWG), 0, s, a);
+    if (a.cw)
+        hipLaunchKernelGGL((gemv_q4k_cols_kernel<mivi::PRO_NONE, mivi::EPI_STORE, KT, NG, 4, KS, true>), dim3(gc, KS),
+                           dim3(kColWG), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemv_q4k_cols_kernel<mivi::PRO_NONE, mivi::EPI_STORE, KT, NG, 4, KS>), dim3(gc, KS),
+                           dim3(kColWG), 0, s, a);
 }
 
 // ------------------------------------------ Q6_K row quads on the matrix cores
@@ -3299,6 +3313,50 @@ int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t co
     hipLaunchKernelGGL(pack_q6k_kernel, dim3((unsigned)((threads + kWG - 1) / kWG)), dim3(kWG), 0, s, src, dst, rows,
                        nu, (cols / 256) * 210);
     MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+// One thread per (group, superblock, lane slot l = j + 16 kg): its 32 code
+// bytes, and (kg = 0) row j's header.
+__global__ void __launch_bounds__(kWG) pack_q4k_cols_kernel(const uint64_t* __restrict__ rows, int ngroups, int nbt,
+                                                            uint8_t* __restrict__ dst) {
+    const size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= (size_t)ngroups * nbt * 64) return;
+    const int l = (int)(i & 63), j = l & 15, kg = l >> 4;
+    const size_t gsb = i >> 6;  // group * nbt + superblock
+    const int sb = (int)(gsb % nbt);
+    const uint8_t* src = (const uint8_t*)rows[(gsb / nbt) * 16 + j] + 144 * sb;
+    uint8_t* d = dst + gsb * kColsChunkBytes;
+    u32x2 c[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) c[g] = *(const u32x2*)(src + 16 + 32 * g + 8 * kg);
+    *(u32x4*)(d + 256 + 16 * l) = u32x4{c[0].x, c[0].y, c[1].x, c[1].y};
+    *(u32x4*)(d + 256 + 1024 + 16 * l) = u32x4{c[2].x, c[2].y, c[3].x, c[3].y};
+    if (kg == 0) *(u32x4*)(d + 16 * j) = *(const u32x4*)src;
+}
+
+int32_t launch_pack_q4k_cols(const uint8_t* const* rows_host, int ngroups, size_t cols, uint8_t* dst,
+                             hipStream_t s) {
+    if (ngroups <= 0) return MIVI_OK;
+    if (cols % 256) return set_error(MIVI_ERR_INVALID_ARGUMENT, "Q4_K rows of %zu columns", cols);
+    for (size_t i = 0; i < (size_t)ngroups * 16; i++)
+        if ((uintptr_t)rows_host[i] % 16)
+            return set_error(MIVI_ERR_INVALID_ARGUMENT, "Q4_K rows must be 16-byte aligned to pack");
+    uint64_t* d = nullptr;
+    const size_t tb = (size_t)ngroups * 16 * sizeof(uint64_t);
+    MIVI_HIP_CHECK(hipMalloc(&d, tb));
+    hipError_t e = hipMemcpy(d, rows_host, tb, hipMemcpyHostToDevice);
+    const int nbt = (int)(cols / 256);
+    const size_t threads = (size_t)ngroups * nbt * 64;
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(pack_q4k_cols_kernel, dim3((unsigned)((threads + kWG - 1) / kWG)), dim3(kWG), 0, s, d,
+                           ngroups, nbt, dst);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    const hipError_t f = hipFree(d);
+    if (e != hipSuccess) return set_error(MIVI_ERR_HIP, "packing Q4_K rows for the column kernel: %s", hipGetErrorString(e));
+    if (f != hipSuccess) return set_error(MIVI_ERR_HIP, "hipFree: %s", hipGetErrorString(f));
     return MIVI_OK;
 }
 

@@ -120,6 +120,41 @@ def test_batched_full_width_matches_single_sequences(hip, B):
         assert np.array_equal(out[:, b], one), (b, out[:, b], one)
 
 
+@pytest.mark.parametrize("B", [3, 8])
+def test_batched_column_layout_matches_gguf_rows(hip, monkeypatch, B):
+    # a model with max_batch > 1 keeps its all-Q4_K projections packed in the
+    # batched column kernels' group order (q|k|v, out_proj / wo, in_proj in
+    # conv-channel groups, gate|up in SwiGLU groups, down); against the same
+    # model on its GGUF rows (MIVI_NO_COLS_PACK) the products are the same up
+    # to the order in which the residual adds' depth slices land (atomic
+    # adds): logits within 1e-5 of their largest value, same greedy tokens
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
+                       ctx_len=1024, seed=11)
+    rng = np.random.default_rng(13)
+    prompts = [rng.integers(0, 4096, 5 + 2 * b) for b in range(B)]
+
+    def run(packed):
+        if packed:
+            monkeypatch.delenv("MIVI_NO_COLS_PACK", raising=False)
+        else:
+            monkeypatch.setenv("MIVI_NO_COLS_PACK", "1")
+        m = hip.Model(img, max_ctx=256, max_batch=B)
+        for b, pr in enumerate(prompts):
+            m.prefill(pr[:-1], seq=b)
+        lg = m.forward_batch([int(p[-1]) for p in prompts], [len(p) - 1 for p in prompts])
+        toks = m.generate_greedy([int(np.argmax(lg[b])) for b in range(B)], [len(p) for p in prompts], 6)
+        wb = m.info.weight_bytes
+        m.close()
+        return lg, toks, wb
+
+    lp, tp, wp = run(True)
+    lr, tr, wr = run(False)
+    assert wp > wr  # the packed copy is counted
+    assert np.max(np.abs(lp - lr)) <= 1e-5 * np.max(np.abs(lr)), np.max(np.abs(lp - lr))
+    assert np.array_equal(tp, tr)
+
+
 @pytest.mark.parametrize("prec,oprec", [(0, 0), (2, 100), (1, 1)])
 def test_chunked_prefill_matches_token_prefill_and_oracle(hip, oracle, small_img, prec, oprec):
     # PrefillStrategy::Chunked vs ::Token (model.rs:2110 tile == token): 149
