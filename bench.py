@@ -190,28 +190,43 @@ def cpu_gemm_baseline(w, x, batch, rows, cols, budget_s):
 
 
 def gemm_bench(torch, hip, steps, warmup, cpu_budget_s=0.0):
-    """Config 3: X [512 x 2048] ~ N(0,1) times W [8192 x 2048]^T Q4_K on MFMA."""
+    """Config 3: X [512 x 2048] ~ N(0,1) times W [8192 x 2048]^T Q4_K on MFMA: the row products on the
+    weights' operand-layout copy (sc * q converted once, as the model keeps it; packing not timed), and
+    the same products staging B from the GGUF rows per call (bit-identical results)."""
     rows, cols, batch = 8192, 2048, 512
-    w_host = hip.synth_random_weights(hip.GgmlType.Q4_K, 300, rows, cols, 0.02)
+    t = hip.GgmlType.Q4_K
+    w_host = hip.synth_random_weights(t, 300, rows, cols, 0.02)
     x_host = hip.synth_normal(301, batch * cols)
     w = torch.from_numpy(w_host).cuda()
     x = torch.from_numpy(x_host).cuda()
+    wg = torch.empty(hip.gemm_packed_size(t, rows, cols), dtype=torch.uint8, device="cuda")
+    hip.pack_weights_gemm(t, w, wg, rows, cols)
     y = torch.empty(batch * rows, dtype=torch.float32, device="cuda")
+    y2 = torch.empty(batch * rows, dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        hip.quantized_matmul_rows(y, hip.GgmlType.Q4_K, w, x, batch, rows, cols, stream=stream)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(lambda: hip.quantized_matmul_rows_gemm_packed(y, t, w, wg, x, batch, rows, cols, stream=stream))
+    ms_gguf = timed(lambda: hip.quantized_matmul_rows(y2, t, w, x, batch, rows, cols, stream=stream))
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        hip.quantized_matmul_rows(y, hip.GgmlType.Q4_K, w, x, batch, rows, cols, stream=stream)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
     flop = 2.0 * batch * rows * cols
     res = dict(batch=batch, rows=rows, cols=cols, algo_flop=flop, ms_per_call=ms,
                tflops=flop / (ms * 1e-3) / 1e12, frac_of_fp16_mfma_peak=flop / (ms * 1e-3) / 2.5e15,
+               weight_layout="B operand converted once (mivi_hip_pack_weights_gemm, not timed)",
+               bit_identical_to_gguf_rows=bool(torch.equal(y, y2)),
+               gguf_rows=dict(ms_per_call=ms_gguf, tflops=flop / (ms_gguf * 1e-3) / 1e12),
                note="includes the activation split kernel (fp16 hi/lo + sub-block sums) run per call")
     if cpu_budget_s > 0:
         res["cpu_baseline"] = cpu_gemm_baseline(w_host, x_host, batch, rows, cols, cpu_budget_s)
@@ -613,7 +628,8 @@ def main():
 
     if a.only_gemm:
         g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3)
-        log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s")
+        log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s "
+            f"(GGUF rows staged per call {g3['gguf_rows']['ms_per_call'] * 1e3:.1f} us)")
         return
     if a.only_config4:
         c4 = config4_decode_only(torch, hip, a.decode_prefill, a.decode_steps)
@@ -663,7 +679,8 @@ def main():
         extra["q4k_gemv_config1"]["cpu_baseline"] = cpu_gemv_baseline(hip.GgmlType.Q4_K, q4["w_host"], q4["x_host"],
                                                                        8192, 2048, a.cpu_seconds / 2)
     g3 = gemm_bench(torch, hip, max(5, a.steps // 10), 3, 0 if a.no_cpu else a.cpu_seconds / 2)
-    log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s")
+    log(f"Q4_K GEMM 512x8192x2048: {g3['ms_per_call'] * 1e3:.1f} us/call, {g3['tflops']:.0f} TFLOP/s "
+        f"(GGUF rows staged per call {g3['gguf_rows']['ms_per_call'] * 1e3:.1f} us)")
     extra["q4k_gemm_config3"] = g3
     if not a.no_decode:
         dec = decode_bench(torch, hip, a.decode_prefill, a.decode_steps, 0 if a.no_cpu else a.cpu_seconds)

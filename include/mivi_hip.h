@@ -143,6 +143,34 @@ int32_t mivi_hip_quantized_matmul_rows_packed(float* out, size_t out_len, int32_
                                               size_t inputs_len, size_t batch, size_t rows, size_t cols,
                                               void* stream);
 
+/* No counterpart in the reference (its Rust kernels read the GGUF layout):
+ * the size in bytes of mivi_hip_pack_weights_gemm's copy of rows x cols
+ * weights, 0 when it has none (Q4_K only, rows a multiple of 32, cols of
+ * 2048): rows * cols * 2 + (rows / 32) * (cols / 256) * 640. */
+size_t mivi_hip_gemm_packed_size(int32_t ggml_type, size_t rows, size_t cols);
+
+/* No counterpart in the reference: rewrites rows x cols Q4_K weights into the
+ * operand layout of the matrix-core row products (the fp16 values sc * q of
+ * every weight in MFMA B-operand order, then d, dmin and the sub-block mins
+ * per row and super-block), mivi_hip_gemm_packed_size bytes; src and dst
+ * 16-byte aligned and distinct. For callers that run row products on
+ * resident weights (the model loader packs every Q4_K projection once for
+ * the chunked prefill). Other types/shapes return MIVI_ERR_UNSUPPORTED. */
+int32_t mivi_hip_pack_weights_gemm(int32_t ggml_type, const uint8_t* src, size_t src_len, uint8_t* dst,
+                                   size_t dst_len, size_t rows, size_t cols, void* stream);
+
+/* quantized_matmul_rows (lib.rs:143-251) over weights with their
+ * mivi_hip_pack_weights_gemm copy (wg): batch >= 16 runs the matrix cores on
+ * wg, fewer inputs the GEMVs on the GGUF rows w; the results equal
+ * mivi_hip_quantized_matmul_rows' bit for bit; sizes and errors as there
+ * (wg_len below mivi_hip_gemm_packed_size: buffer too small). No counterpart
+ * in the reference. */
+int32_t mivi_hip_quantized_matmul_rows_gemm_packed(float* out, size_t out_len, int32_t ggml_type,
+                                                   const uint8_t* weights, size_t weights_len,
+                                                   const uint8_t* wg, size_t wg_len, const float* inputs,
+                                                   size_t inputs_len, size_t batch, size_t rows, size_t cols,
+                                                   void* stream);
+
 /* crates/mivi-quant/src/lib.rs:35-72 dequantize_slice: bit-exact decode of
  * out_len / block_size blocks (Q4_K, Q6_K, Q8_0) or of bytes_len / type_size
  * elements (F16, BF16, F32). */
@@ -180,8 +208,10 @@ typedef struct mivi_model_info {
     size_t weight_bytes;   /* device bytes of the weights: the GGUF tensor data plus the
                               packed copies kept beside it (Q6_K head, Q4_K and Q6_K row
                               quads; with max_batch > 1 the Q4_K projections in the batched
-                              column kernels' group order); MIVI_NO_PACK=1 at create leaves
-                              the copies out, MIVI_NO_COLS_PACK=1 the batched ones */
+                              column kernels' group order; the Q4_K projections' fp16 sc * q
+                              for the prefill's row products); MIVI_NO_PACK=1 at create leaves
+                              the copies out, MIVI_NO_COLS_PACK=1 the batched ones,
+                              MIVI_NO_GEMM_PACK=1 the row products' */
     size_t kv_bytes;       /* device bytes of K + V for all sequences */
 } mivi_model_info;
 

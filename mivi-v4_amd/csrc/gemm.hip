@@ -25,6 +25,7 @@
 // Other formats, and fewer rows, run the batched GEMV (the inputs as its
 // columns).
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -218,6 +219,41 @@ __device__ __forceinline__ half8 nib8_times(uint32_t w0, uint32_t w1, bool high,
     return half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
 }
 
+// The outputs of one lane, 2 x 16 registers: acc[i][r] is row row(i, r),
+// column col(i); y (=|+=) acc * rowscale[row]. Every row scale and (with
+// accumulate) every old value is loaded before the first store: the stores
+// could alias later loads as far as the compiler knows, and each load would
+// otherwise wait for the store before it and then for its own memory trip.
+template <class RowF, class ColF>
+__device__ __forceinline__ void gemm_store(float* __restrict__ Y, int64_t ldy, int M, int N,
+                                           const float* __restrict__ rowscale, const f32x16 (&acc)[2], RowF row,
+                                           ColF col, int accumulate) {
+    float rs[2][16], old[2][16];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int n = col(i);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = row(i, r);
+            const bool in = m < M && n < N;
+            rs[i][r] = in ? rowscale[m] : 0.f;
+            old[i][r] = in && accumulate ? Y[m * ldy + n] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int n = col(i);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = row(i, r);
+            if (m < M && n < N) {
+                const float v = acc[i][r] * rs[i][r];
+                Y[m * ldy + n] = accumulate ? old[i][r] + v : v;  // one writer per output
+            }
+        }
+    }
+}
+
 // grid = (ceil(N / 256), Mp / 64), 512 threads = 8 waves: wave w computes
 // input rows 32 (w & 1) .. +32 of the tile against weight rows 64 (w >> 1)
 // .. +64 (two 32 x 32 MFMA tiles). Per 64-value k-tile the workgroup stages x
@@ -392,19 +428,217 @@ __global__ void __launch_bounds__(kGT) gemm_q4k_kernel(const uint8_t* __restrict
         if (t + 2 < ntiles) step(S0, S1, t + 2);
     }
     // store: D[i][j] in lane j + 32*((i/4)%2), register 4*(i/8) + i%4
+    gemm_store(
+        Y, ldy, M, N, rowscale, acc, [&](int, int r) { return m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4); },
+        [&](int nt) { return n0 + 64 * wn + 32 * nt + li; }, accumulate);
+}
+
+
+// ------------------------------------------------ Q4_K B operand converted once
+//
+// launch_pack_q4k_gemm layout of a rows x cols Q4_K matrix (rows % 32 == 0,
+// cols % 256 == 0), read by gemm_q4k_b16_kernel:
+//   B section: per 32-row tile nt and 64-value k-tile kt (Q4_K group g = kt %
+//   4 of super-block kt / 4: sub-block 2g from the low nibbles of its 32 code
+//   bytes, 2g + 1 from the high ones), per k-step s (values 16s .. 16s + 15
+//   of the k-tile), the v_mfma_f32_32x32x16_f16 B operand: lane l (row 32 nt +
+//   l % 32, values 16 s + 8 (l / 32) .. + 7) holds the 8 fp16 sc * q, exact
+//   (<= 945), at byte ((nt * KT + kt) * 4 + s) * 1024 + 16 l (KT = cols / 64);
+//   H section (after the rows * cols * 2 bytes of B): per (nt, super-block
+//   sb), 640 bytes: the 32 rows' d | dmin << 16 (their header's first dword),
+//   then their 8 sub-block mins as fp16 (16 bytes a row).
+// The values are those gemm_q4k_kernel builds in LDS for every tile of
+// input rows; here they are built once and every k-step's B is one
+// contiguous 1 KB load.
+constexpr int kGemmHBytes = 640;
+
+__global__ void __launch_bounds__(256) pack_q4k_gemm_kernel(const uint8_t* __restrict__ src,
+                                                            uint8_t* __restrict__ dst, int rows, int cols) {
+    const int KT = cols / kTk, NB = cols / 256;
+    const size_t rb = (size_t)NB * 144;
+    const size_t nb16 = (size_t)rows / 32 * KT * 4 * 64;  // 16-byte B entries
+    const size_t nh = (size_t)rows / 32 * NB * 32;        // (row, super-block) header entries
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < nb16) {
+        const int l = (int)(i & 63);
+        size_t q = i >> 6;
+        const int s = (int)(q & 3);
+        q >>= 2;
+        const int kt = (int)(q % KT);
+        const size_t nt = q / KT;
+        const int kk0 = 16 * s + 8 * (l >> 5), g = kt % 4;  // values kk0 .. kk0 + 7 of the group
+        const uint8_t* blk = src + (32 * nt + (l & 31)) * rb + (size_t)(kt / 4) * 144;
+        uint32_t sc, mn;
+        scale_min_k4(blk + 4, 2 * g + (kk0 >= 32), sc, mn);
+        half8 v;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int n = n0 + 64 * wn + 32 * nt + li;
+        for (int e = 0; e < 8; e++) {
+            const uint32_t byte = blk[16 + 32 * g + ((kk0 + e) & 31)];
+            v[e] = (_Float16)(float)((kk0 >= 32 ? byte >> 4 : byte & 15u) * sc);
+        }
+        *(half8*)(dst + i * 16) = v;
+    } else if (i < nb16 + nh) {
+        const size_t h = i - nb16, q = h >> 5;  // q = nt * NB + sb
+        const int r = (int)(h & 31), sb = (int)(q % NB);
+        const size_t nt = q / NB;
+        const uint8_t* blk = src + (32 * nt + r) * rb + (size_t)sb * 144;
+        uint8_t* H = dst + (size_t)rows * cols * 2 + q * kGemmHBytes;
+        *(uint32_t*)(H + 4 * r) = *(const uint32_t*)blk;
+        half8 mv;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4);
-            if (m < M && n < N) {
-                float* y = Y + m * ldy + n;
-                const float v = acc[nt][r] * rowscale[m];
-                *y = accumulate ? *y + v : v;  // one writer per output
+        for (int j = 0; j < 8; j++) {
+            uint32_t sc, mn;
+            scale_min_k4(blk + 4, j, sc, mn);
+            mv[j] = (_Float16)(float)mn;
+        }
+        *(half8*)(H + 128 + 16 * r) = mv;
+    }
+}
+
+// gemm_q4k_kernel's tiles (64 input rows x 256 weight rows, 512 threads) on
+// the converted B: wave w takes weight rows 32 w .. 32 w + 31 of the tile for
+// all 64 input rows (two 32 x 32 MFMA tiles), its B operands loaded straight
+// into registers (one 1 KB load per k-step), only x (fp16 hi and lo) staged
+// in LDS. Four register stages in a ring, k-tile t + 3 loading while t
+// computes, unrolled by four so that the tiles that start a super-block
+// (and bring its header and sub-block sums) are known at compile time:
+// every load is unconditional (the last tiles re-read tile KT - 1), so the
+// compiler counts them exactly and waits only for the tile in hand. The
+// same MFMA chains in the same order as gemm_q4k_kernel: the same results,
+// bit for bit.
+struct GemmStageB {
+    u32x4 xh, xl, ps;  // x chunk of 8 values (input row tid/8, chunk tid%8); sub-block sums (super-block start)
+    u32x4 b[4];        // the wave's B operand of each k-step
+};
+
+__global__ void __launch_bounds__(kGT) gemm_q4k_b16_kernel(const uint8_t* __restrict__ Wg, int N, int K,
+                                                           const _Float16* __restrict__ xh,
+                                                           const _Float16* __restrict__ xl,
+                                                           const _Float16* __restrict__ sh,
+                                                           const _Float16* __restrict__ sl,
+                                                           const float* __restrict__ rowscale,
+                                                           float* __restrict__ Y, int M, int64_t ldy, int accumulate) {
+    __shared__ __attribute__((aligned(16))) _Float16 Xh[2][kTm][kXs];
+    __shared__ __attribute__((aligned(16))) _Float16 Xl[2][kTm][kXs];
+    __shared__ __attribute__((aligned(16))) _Float16 Sh[2][kTm][8];
+    __shared__ __attribute__((aligned(16))) _Float16 Sl[2][kTm][8];
+    const int n0 = blockIdx.x * kGN, m0 = blockIdx.y * kTm;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int KT = K / kTk, NB = K / 256;  // KT: a multiple of 32 (K % 2048 == 0)
+    // this wave's 32-row tile (past N: the last one, loaded and not stored)
+    const bool live = n0 + 32 * wave < N;
+    const int nt = live ? (n0 >> 5) + wave : N / 32 - 1;
+    const uint8_t* Bw = Wg + (size_t)nt * KT * 4096 + 16 * lane;
+    const uint8_t* Hw = Wg + (size_t)N * K * 2 + (size_t)nt * NB * kGemmHBytes;
+    const int xr = tid >> 3, xc = tid & 7;
+    const int pr = (tid >> 1) & (kTm - 1);  // sub-block sums: row pr, hi (even) or lo (odd)
+    const _Float16* ps_src = ((tid & 1) ? sl : sh) + (size_t)(m0 + pr) * (K / 32);
+
+    f32x16 acc[2], c1[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        acc[mt] = f32x16{};
+        c1[mt] = f32x16{};
+    }
+    uint32_t hd = 0, hd_n = 0;  // the lane's row: d | dmin << 16 of the super-block computing, of the next
+    u32x4 hm = {}, hm_n = {};   // their 8 mins (fp16)
+    // SB: t starts a super-block (t % 4 == 0): its sub-block sums into the
+    // stage, its header into hd_n / hm_n
+    auto load = [&](GemmStageB& S, int t, auto SB) {
+        t = t < KT ? t : KT - 4 + (t & 3);  // (KT % 4 == 0: keeps t % 4)
+        const size_t o = (size_t)(m0 + xr) * K + t * kTk + 8 * xc;
+        S.xh = *(const u32x4*)(xh + o);
+        S.xl = *(const u32x4*)(xl + o);
+#pragma unroll
+        for (int s = 0; s < 4; s++) S.b[s] = *(const u32x4*)(Bw + ((size_t)t * 4 + s) * 1024);
+        if constexpr (decltype(SB)::value) {
+            S.ps = *(const u32x4*)(ps_src + 8 * (t >> 2));
+            const uint8_t* h = Hw + (size_t)(t >> 2) * kGemmHBytes;
+            hd_n = *(const uint32_t*)(h + 4 * li);
+            hm_n = *(const u32x4*)(h + 128 + 16 * li);
+        }
+    };
+    auto store_x = [&](const GemmStageB& S, int t) {
+        const int bf = t & 1;
+        *(u32x4*)&Xh[bf][xr][8 * xc] = S.xh;
+        *(u32x4*)&Xl[bf][xr][8 * xc] = S.xl;
+        if ((t & 3) == 0 && tid < 2 * kTm) {
+            const int p = (t >> 2) & 1;
+            if (tid & 1) *(u32x4*)&Sl[p][pr][0] = S.ps;
+            else *(u32x4*)&Sh[p][pr][0] = S.ps;
+        }
+    };
+    auto compute = [&](const GemmStageB& S, int t) {
+        const int bf = t & 1;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const half8 bq = __builtin_bit_cast(half8, S.b[s]);
+            half8 a_h[2], a_l[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                a_h[mt] = *(const half8*)&Xh[bf][32 * mt + li][16 * s + 8 * lh];
+                a_l[mt] = *(const half8*)&Xl[bf][32 * mt + li][16 * s + 8 * lh];
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) c1[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h[mt], bq, c1[mt], 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) c1[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l[mt], bq, c1[mt], 0, 0, 0);
+        }
+        if ((t & 3) == 3) {
+            // end of super-block: acc += d * C, then the min term on the same MFMA shape
+            const int p = (t >> 2) & 1;
+            const float d = half_bits_to_f32(hd), dm = half_bits_to_f32(hd >> 16);
+            const half8 bm = lh == 0 ? __builtin_bit_cast(half8, hm) : half8{};
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                acc[mt] += d * c1[mt];
+                c1[mt] = f32x16{};
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                const half8 s_h = lh == 0 ? *(const half8*)&Sh[p][32 * mt + li][0] : half8{};
+                const half8 s_l = lh == 0 ? *(const half8*)&Sl[p][32 * mt + li][0] : half8{};
+                f32x16 c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_h, bm, f32x16{}, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(s_l, bm, c2, 0, 0, 0);
+                acc[mt] -= dm * c2;
             }
         }
+    };
+    GemmStageB S0, S1, S2, S3;
+    load(S0, 0, std::true_type{});
+    hd = hd_n;
+    hm = hm_n;
+    load(S1, 1, std::false_type{});
+    load(S2, 2, std::false_type{});
+    store_x(S0, 0);
+    __syncthreads();
+    // step t: tile t computes from Sc (its x already in LDS), tile t + 1's x
+    // goes into the other LDS buffer from Sn, tile t + 3 loads into Sf (the
+    // stage tile t - 1 used); the step that loads a super-block's first tile
+    // (t % 4 == 1) brings its header, taken over after the last k-tile of
+    // the super-block before it
+    auto step = [&](const GemmStageB& Sc, const GemmStageB& Sn, GemmStageB& Sf, int t, auto SB) {
+        load(Sf, t + 3, SB);
+        compute(Sc, t);
+        if ((t & 3) == 3) {
+            hd = hd_n;
+            hm = hm_n;
+        }
+        if (t + 1 < KT) store_x(Sn, t + 1);
+        __syncthreads();
+    };
+    for (int t = 0; t < KT; t += 4) {
+        step(S0, S1, S3, t, std::false_type{});
+        step(S1, S2, S0, t + 1, std::true_type{});
+        step(S2, S3, S1, t + 2, std::false_type{});
+        step(S3, S0, S2, t + 3, std::false_type{});
     }
+    if (!live) return;
+    // store: D[i][j] in lane j + 32*((i/4)%2), register 4*(i/8) + i%4
+    gemm_store(
+        Y, ldy, M, N, rowscale, acc, [&](int mt, int r) { return m0 + 32 * mt + 8 * (r / 4) + 4 * lh + (r % 4); },
+        [&](int) { return n0 + 32 * wave + li; }, accumulate);
 }
 
 
@@ -556,19 +790,9 @@ __global__ void __launch_bounds__(kGT) gemm_q6k_kernel(const uint8_t* __restrict
         step(S1, t);
         if (t + 1 < ntiles) step(S0, t + 1);
     }
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int n = n0 + 64 * wn + 32 * nt + li;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int m = m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4);
-            if (m < M && n < N) {
-                float* y = Y + m * ldy + n;
-                const float v = acc[nt][r] * rowscale[m];
-                *y = accumulate ? *y + v : v;  // one writer per output
-            }
-        }
-    }
+    gemm_store(
+        Y, ldy, M, N, rowscale, acc, [&](int, int r) { return m0 + 32 * wm + 8 * (r / 4) + 4 * lh + (r % 4); },
+        [&](int nt) { return n0 + 64 * wn + 32 * nt + li; }, accumulate);
 }
 
 }  // namespace
@@ -649,6 +873,9 @@ static int32_t rows_mfma(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
         if (t == MIVI_GGML_Q6_K)
             hipLaunchKernelGGL(gemm_q6k_kernel, grid, dim3(kGT), 0, s, a.seg[i].W, rows, (int)K, xh, xl, rs,
                                a.seg[i].y, (int)batch, a.ys, a.accumulate);
+        else if (a.seg[i].wg && rows % 32 == 0)
+            hipLaunchKernelGGL(gemm_q4k_b16_kernel, grid, dim3(kGT), 0, s, a.seg[i].wg, rows, (int)K, xh, xl, sh, sl,
+                               rs, a.seg[i].y, (int)batch, a.ys, a.accumulate);
         else
             hipLaunchKernelGGL(gemm_q4k_kernel, grid, dim3(kGT), 0, s, a.seg[i].W, rows, (int)K, xh, xl, sh, sl, rs,
                                a.seg[i].y, (int)batch, a.ys, a.accumulate);
@@ -659,6 +886,17 @@ static int32_t rows_mfma(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
 }
 
 namespace mivi {
+int32_t launch_pack_q4k_gemm(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s) {
+    if (rows % 32 || cols % 256 || rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX)
+        return set_error(MIVI_ERR_UNSUPPORTED, "no row-product layout for %zu rows of %zu columns", rows, cols);
+    const size_t n = rows / 32 * (cols / kTk) * 4 * 64 + rows / 32 * (cols / 256) * 32;
+    if (n == 0) return MIVI_OK;
+    hipLaunchKernelGGL(pack_q4k_gemm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, (int)rows,
+                       (int)cols);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
 int32_t launch_rows(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     if (pro == PRO_CONV || a.epilogue != EPI_STORE)
         return set_error(MIVI_ERR_UNSUPPORTED, "row products take no conv prologue or fused epilogue");
@@ -670,6 +908,64 @@ int32_t launch_rows(int32_t t, int pro, const GemvArgs& a, hipStream_t s) {
     return launch_gemv_ex(t, pro, a, s);
 }
 }  // namespace mivi
+
+static bool gemm_packable(int32_t t, size_t rows, size_t cols) {
+    return t == MIVI_GGML_Q4_K && rows % 32 == 0 && cols % 2048 == 0;
+}
+
+extern "C" size_t mivi_hip_gemm_packed_size(int32_t t, size_t rows, size_t cols) {
+    return gemm_packable(t, rows, cols) ? mivi::q4k_gemm_packed_bytes(rows, cols) : 0;
+}
+
+extern "C" int32_t mivi_hip_pack_weights_gemm(int32_t t, const uint8_t* src, size_t src_len, uint8_t* dst,
+                                              size_t dst_len, size_t rows, size_t cols, void* stream) {
+    size_t bs, ts, need;
+    if (!format_sizes(t, &bs, &ts)) return err_unsupported(t);
+    if (cols % bs != 0) return err_misaligned(cols, bs);
+    if (!gemm_packable(t, rows, cols))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no row-product layout for type %d with %zu rows of %zu columns", t,
+                         rows, cols);
+    if (__builtin_mul_overflow(rows, (cols / bs) * ts, &need)) return err_overflow();
+    if (src_len < need) return err_buffer_too_small(need, src_len);
+    const size_t out = mivi::q4k_gemm_packed_bytes(rows, cols);
+    if (dst_len < out) return err_buffer_too_small(out, dst_len);
+    if (rows && (!src || !dst)) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    if ((uintptr_t)src % 16 || (uintptr_t)dst % 16)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "weights and packed copy must be 16-byte aligned");
+    if (rows && src < dst + out && dst < src + need)
+        return set_error(MIVI_ERR_INVALID_ARGUMENT, "packing needs distinct buffers");
+    clear_error();
+    return mivi::launch_pack_q4k_gemm(src, dst, rows, cols, (hipStream_t)stream);
+}
+
+extern "C" int32_t mivi_hip_quantized_matmul_rows_gemm_packed(float* out, size_t out_len, int32_t t,
+                                                              const uint8_t* w, size_t w_len, const uint8_t* wg,
+                                                              size_t wg_len, const float* in, size_t in_len,
+                                                              size_t batch, size_t rows, size_t cols, void* stream) {
+    int32_t rc = validate_matmul(t, out_len, w_len, in_len, batch, rows, cols);
+    if (rc) return rc;
+    if (!gemm_packable(t, rows, cols))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no row-product layout for type %d with %zu rows of %zu columns", t,
+                         rows, cols);
+    const size_t need = mivi::q4k_gemm_packed_bytes(rows, cols);
+    if (wg_len < need) return err_buffer_too_small(need, wg_len);
+    if (batch == 0 || rows == 0) return clear_error();
+    if (!out || !w || !wg || !in) return set_error(MIVI_ERR_INVALID_ARGUMENT, "null buffer");
+    if ((uintptr_t)wg % 16) return set_error(MIVI_ERR_INVALID_ARGUMENT, "packed copy must be 16-byte aligned");
+    if (rows > (size_t)INT32_MAX || cols > (size_t)INT32_MAX || batch > (size_t)INT32_MAX - kTm) return err_overflow();
+    clear_error();
+    // batch >= kMfmaMinBatch: the matrix cores on the packed copy; fewer
+    // rows: the GEMVs on the GGUF rows
+    mivi::GemvArgs a = {};
+    a.seg[0] = {w, out, (int)rows, wg};
+    a.nseg = 1;
+    a.K = (int)cols;
+    a.x = in;
+    a.ncol = (int)batch;
+    a.xs = (int64_t)cols;
+    a.ys = (int64_t)rows;
+    return mivi::launch_rows(t, mivi::PRO_NONE, a, (hipStream_t)stream);
+}
 
 extern "C" int32_t mivi_hip_quantized_matmul_rows(float* out, size_t out_len, int32_t t, const uint8_t* w,
                                                   size_t w_len, const float* in, size_t in_len, size_t batch,

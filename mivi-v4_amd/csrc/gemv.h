@@ -23,6 +23,9 @@ struct GemvSeg {
     const uint8_t* W;  // rows of this segment
     float* y;          // outputs of this segment
     int n;             // rows
+    // Q4_K: the same rows in the row products' operand layout
+    // (launch_pack_q4k_gemm), read by the matrix-core row products, else null
+    const uint8_t* wg;
 };
 
 // y_s[r] (=|+=) W_s[r, :] . prologue(x) for up to three weight matrices that
@@ -140,6 +143,15 @@ __host__ __device__ inline int cols_groups(int epi, int n0, int n) {
 // rows_host[16 grp + j]: the device address of group grp's row j (any valid
 // row where the group has none there).
 constexpr int kColsChunkBytes = 16 * 144;
+
+// rows x cols Q4_K (rows % 32 == 0, cols % 256 == 0) into the operand layout
+// of the matrix-core row products (launch_rows with GemvSeg::wg): the fp16
+// values sc * q in MFMA B-operand order, then d, dmin and the sub-block mins
+// per row and super-block; q4k_gemm_packed_bytes(rows, cols) bytes
+inline size_t q4k_gemm_packed_bytes(size_t rows, size_t cols) {
+    return rows * cols * 2 + rows / 32 * (cols / 256) * 640;
+}
+int32_t launch_pack_q4k_gemm(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
 int32_t launch_pack_q4k_cols(const uint8_t* const* rows_host, int ngroups, size_t cols, uint8_t* dst,
                              hipStream_t s);
 

@@ -1429,6 +1429,9 @@ struct Mat {
     // the same rows packed for one-column GEMVs (Q4_K row quads; Q6_K row
     // quads at 2048 columns, unit planes at 4096 or 8192), else null
     const uint8_t* quad = nullptr;
+    // Q4_K: the rows in the row products' operand layout (prefill tiles of
+    // 16+ rows on the matrix cores; launch_pack_q4k_gemm), else null
+    const uint8_t* gemm = nullptr;
 };
 
 struct Layer {
@@ -1893,7 +1896,7 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
         GemvArgs g = {};
         if (!L.attn) {
             if (c.ssm_conv_kernel == 0) continue;  // ssm.rs:60-62
-            g.seg[0] = {L.in_proj.w, m->pf_p1, 3 * D};
+            g.seg[0] = {L.in_proj.w, m->pf_p1, 3 * D, L.in_proj.gemm};
             g.nseg = 1; g.K = D; g.x = m->pf_x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = R; g.xs = D; g.ys = 3 * D;
             if ((rc = launch_rows(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
@@ -1903,14 +1906,14 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
                                m->pf_ao, R, D, (int)ks, L.conv, mode, st.conv_a + l * (size_t)D * ks,
                                st.conv_b + l * (size_t)D * ks, &m->ctrl->phase[b]);
             g = {};
-            g.seg[0] = {L.out_proj.w, m->pf_x, D};
+            g.seg[0] = {L.out_proj.w, m->pf_x, D, L.out_proj.gemm};
             g.nseg = 1; g.K = D; g.x = m->pf_ao; g.accumulate = 1;
             g.ncol = R; g.xs = D; g.ys = D;
             if ((rc = launch_rows(L.out_proj.type, PRO_NONE, g, s))) return rc;
         } else {
-            g.seg[0] = {L.wq.w, m->pf_p1, D};
-            g.seg[1] = {L.wk.w, m->pf_p1 + D, KV};
-            g.seg[2] = {L.wv.w, m->pf_p1 + D + KV, KV};
+            g.seg[0] = {L.wq.w, m->pf_p1, D, L.wq.gemm};
+            g.seg[1] = {L.wk.w, m->pf_p1 + D, KV, L.wk.gemm};
+            g.seg[2] = {L.wv.w, m->pf_p1 + D + KV, KV, L.wv.gemm};
             g.nseg = 3; g.K = D; g.x = m->pf_x; g.norm_w = L.norm; g.eps = c.rms_norm_eps;
             g.ncol = R; g.xs = D; g.ys = (int64_t)ldq;
             rc = by_type_runs(g, {&L.wq, &L.wk, &L.wv}, [&](int32_t t, const GemvArgs& gr, const Mat* const*, int) {
@@ -1945,15 +1948,15 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
             a.keep_cache = 1;
             enqueue_attention(c, a, (unsigned)R, m->pf_ao, (int64_t)D, s);
             g = {};
-            g.seg[0] = {L.wo.w, m->pf_x, D};
+            g.seg[0] = {L.wo.w, m->pf_x, D, L.wo.gemm};
             g.nseg = 1; g.K = D; g.x = m->pf_ao; g.accumulate = 1;
             g.ncol = R; g.xs = D; g.ys = D;
             if ((rc = launch_rows(L.wo.type, PRO_NONE, g, s))) return rc;
         }
         // ffn.rs:56-108 on the rows
         g = {};
-        g.seg[0] = {L.gate.w, m->pf_p1, H};
-        g.seg[1] = {L.up.w, m->pf_p2, H};
+        g.seg[0] = {L.gate.w, m->pf_p1, H, L.gate.gemm};
+        g.seg[1] = {L.up.w, m->pf_p2, H, L.up.gemm};
         g.nseg = 2; g.K = D; g.x = m->pf_x; g.norm_w = L.ffn_norm; g.eps = c.rms_norm_eps;
         g.ncol = R; g.xs = D; g.ys = H;
         if (L.gate.type == L.up.type) {
@@ -1966,7 +1969,7 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
             if ((rc = launch_rows(L.up.type, PRO_RMSNORM, g1, s))) return rc;
         }
         g = {};
-        g.seg[0] = {L.down.w, m->pf_x, D};
+        g.seg[0] = {L.down.w, m->pf_x, D, L.down.gemm};
         g.nseg = 1; g.K = H; g.x = m->pf_p1; g.x2 = m->pf_p2; g.accumulate = 1;
         g.ncol = R; g.xs = H; g.ys = D;
         if ((rc = launch_rows(L.down.type, PRO_SWIGLU, g, s))) return rc;
@@ -2293,6 +2296,32 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
             *j.dst = q;
             q += (size_t)ng * (j.ms[0]->cols / 256) * kColsChunkBytes;
         }
+        c.weight_bytes += total;
+    }
+    // the chunked prefill's row products (tiles of 16+ rows) read each Q4_K
+    // projection's B operand converted once, sc * q in fp16 in MFMA operand
+    // order (3.6x the Q4_K bytes; not with MIVI_NO_PACK or MIVI_NO_GEMM_PACK)
+    if (!getenv("MIVI_NO_PACK") && !getenv("MIVI_NO_GEMM_PACK")) {
+        std::vector<Mat*> gm;
+        for (size_t i = 0; i < c.n_layers; i++) {
+            Layer& L = m->layers[i];
+            Mat* all[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.in_proj, &L.out_proj, &L.gate, &L.up, &L.down};
+            for (Mat* x : all)
+                if (x->w && x->type == MIVI_GGML_Q4_K && x->rows % 32 == 0 && x->cols % 2048 == 0 &&
+                    (uintptr_t)x->w % 16 == 0)
+                    gm.push_back(x);
+        }
+        size_t total = 0;
+        for (Mat* x : gm) total += q4k_gemm_packed_bytes(x->rows, x->cols);  // multiples of 128 bytes
+        uint8_t* q = nullptr;
+        if (total && (rc = m->alloc(&q, total))) return fail(rc);
+        for (Mat* x : gm) {
+            if ((rc = launch_pack_q4k_gemm(x->w, q, x->rows, x->cols, nullptr))) return fail(rc);
+            x->gemm = q;
+            q += q4k_gemm_packed_bytes(x->rows, x->cols);
+        }
+        if (total && hipDeviceSynchronize() != hipSuccess)
+            return fail(set_error(MIVI_ERR_HIP, "packing the projections for the row products failed"));
         c.weight_bytes += total;
     }
     {

@@ -117,6 +117,9 @@ _sig = {
     "mivi_hip_pack_weights": ([_I, _P, _S, _P, _S, _S, _S, _P], _I),
     "mivi_hip_quantized_matvec_packed": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _P], _I),
     "mivi_hip_quantized_matmul_rows_packed": ([_P, _S, _I, _P, _S, _P, _S, _S, _S, _S, _P], _I),
+    "mivi_hip_gemm_packed_size": ([_I, _S, _S], _S),
+    "mivi_hip_pack_weights_gemm": ([_I, _P, _S, _P, _S, _S, _S, _P], _I),
+    "mivi_hip_quantized_matmul_rows_gemm_packed": ([_P, _S, _I, _P, _S, _P, _S, _P, _S, _S, _S, _S, _P], _I),
     "mivi_hip_dequantize_slice": ([_I, _P, _S, _P, _S, _P], _I),
     "mivi_hip_quantize_q8_0": ([_P, _S, _P, _S, _S, _P], _I),
     "mivi_hip_dot_q8_0_f32": ([_P, _S, _P, _S, _P, _S, _S, _P], _I),
@@ -253,6 +256,27 @@ def quantized_matmul_rows_packed(out, ggml_type, packed, inputs, batch: int, row
     pi, li = _dev(inputs)
     _check(_lib.mivi_hip_quantized_matmul_rows_packed(po, lo, int(ggml_type), C.c_void_p(packed.data_ptr()),
                                                       _nbytes(packed), pi, li, batch, rows, cols, _stream(stream)))
+
+
+def gemm_packed_size(ggml_type, rows: int, cols: int) -> int:
+    """Bytes of pack_weights_gemm's copy (0: the shape has none)."""
+    return int(_lib.mivi_hip_gemm_packed_size(int(ggml_type), rows, cols))
+
+
+def pack_weights_gemm(ggml_type, src, dst, rows: int, cols: int, stream=None):
+    """Q4_K rows into the row products' operand layout (u8 GPU tensors; dst of gemm_packed_size bytes)."""
+    _check(_lib.mivi_hip_pack_weights_gemm(int(ggml_type), C.c_void_p(src.data_ptr()), _nbytes(src),
+                                           C.c_void_p(dst.data_ptr()), _nbytes(dst), rows, cols, _stream(stream)))
+
+
+def quantized_matmul_rows_gemm_packed(out, ggml_type, weights, wg, inputs, batch: int, rows: int, cols: int,
+                                      stream=None):
+    """quantized_matmul_rows with the weights' pack_weights_gemm copy wg (the matrix-core path reads it)."""
+    po, lo = _dev(out)
+    pi, li = _dev(inputs)
+    _check(_lib.mivi_hip_quantized_matmul_rows_gemm_packed(po, lo, int(ggml_type), C.c_void_p(weights.data_ptr()),
+                                                           _nbytes(weights), C.c_void_p(wg.data_ptr()), _nbytes(wg),
+                                                           pi, li, batch, rows, cols, _stream(stream)))
 
 
 def quantized_matmul_rows(out, ggml_type, weights, inputs, batch: int, rows: int, cols: int, stream=None):

@@ -36,6 +36,23 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_gemm_packed_size_and_validation_need_no_gpu():
+    # the row products' operand layout: Q4_K, rows % 32 == 0, cols % 2048 == 0
+    import mivi_hip
+    lib = mivi_hip.lib()
+    assert mivi_hip.gemm_packed_size(12, 8192, 2048) == 8192 * 2048 * 2 + 256 * 8 * 640
+    assert mivi_hip.gemm_packed_size(12, 2048, 8192) == 2048 * 8192 * 2 + 64 * 32 * 640
+    assert mivi_hip.gemm_packed_size(12, 8200, 2048) == 0   # rows % 32
+    assert mivi_hip.gemm_packed_size(12, 8192, 1024) == 0   # cols % 2048
+    assert mivi_hip.gemm_packed_size(14, 8192, 2048) == 0   # Q6_K
+    # validated on the host before anything is launched
+    rc = lib.mivi_hip_pack_weights_gemm(12, None, 32 * 8 * 144, None, 16, 32, 2048, None)
+    assert rc == 2 and mivi_hip.last_error().expected == mivi_hip.gemm_packed_size(12, 32, 2048)
+    rc = lib.mivi_hip_quantized_matmul_rows_gemm_packed(None, 16 * 32, 12, None, 32 * 8 * 144, None, 0, None,
+                                                        16 * 2048, 16, 32, 2048, None)
+    assert rc == 2
+
+
 def test_python_binding_imports():
     import mivi_hip
     assert "gfx950" in mivi_hip.version()

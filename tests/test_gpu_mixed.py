@@ -59,8 +59,17 @@ def test_mixed_model_types_and_weight_bytes(hip, mixed_img):
     assert q6 == ["blk.2.ffn_down.weight", "blk.3.attn_v.weight", "blk.3.ffn_down.weight", "token_embd.weight"]
     data = len(mixed_img) - min(off for (t, dims, off, ln) in idx.values())
     packed = sum(ln for (t, dims, off, ln) in idx.values() if t in (12, 14) and len(dims) == 2)
+    # the Q4_K projections' B operand for the prefill's row products: fp16
+    # sc * q plus 640 bytes per 32 rows and super-block (dims: cols, rows)
+    gemm = sum(d[1] * d[0] * 2 + d[1] // 32 * (d[0] // 256) * 640 for (t, d, off, ln) in idx.values()
+               if t == 12 and len(d) == 2 and d[1] % 32 == 0 and d[0] % 2048 == 0)
     # every projection packed beside its GGUF rows, the (tied) head too
-    assert hip.Model(mixed_img, max_ctx=256).info.weight_bytes == data + packed
+    assert hip.Model(mixed_img, max_ctx=256).info.weight_bytes == data + packed + gemm
+    os.environ["MIVI_NO_GEMM_PACK"] = "1"
+    try:
+        assert hip.Model(mixed_img, max_ctx=256).info.weight_bytes == data + packed
+    finally:
+        del os.environ["MIVI_NO_GEMM_PACK"]
     os.environ["MIVI_NO_PACK"] = "1"
     try:
         assert hip.Model(mixed_img, max_ctx=256).info.weight_bytes == data

@@ -291,6 +291,39 @@ def test_matmul_rows_q6k_ffn_down_prefill_shape(hip, oracle, torch_mod):
     _matmul_check(hip, oracle, torch, Q6_K, w, X, rows, cols)
 
 
+@pytest.mark.parametrize("batch,rows,cols", [(16, 256, 2048), (512, 8192, 2048), (70, 2080, 2048), (33, 512, 8192),
+                                             (129, 6144, 2048), (8, 64, 2048)])
+def test_matmul_rows_gemm_packed_bit_exact(hip, torch_mod, batch, rows, cols):
+    # the row products on the weights' operand-layout copy (sc * q converted
+    # once, B loaded straight into the MFMA registers) against the same
+    # products on the GGUF rows: the same MFMA chains in the same order, so
+    # equal bit for bit (below 16 inputs both run the GEMVs on the GGUF rows)
+    torch = torch_mod
+    w = hip.synth_random_weights(Q4_K, 90 + batch, rows, cols, 0.02)
+    X = hip.synth_normal(91 + batch, batch * cols)
+    dw, dX = dev(torch, w), dev(torch, X)
+    wg = torch.full((hip.gemm_packed_size(Q4_K, rows, cols),), 0xAB, dtype=torch.uint8, device="cuda")
+    hip.pack_weights_gemm(Q4_K, dw, wg, rows, cols)
+    a = torch.full((batch * rows + 1,), 7.0, dtype=torch.float32, device="cuda")
+    b = torch.full((batch * rows + 1,), 7.0, dtype=torch.float32, device="cuda")
+    hip.quantized_matmul_rows(a[:-1], Q4_K, dw, dX, batch, rows, cols)
+    hip.quantized_matmul_rows_gemm_packed(b[:-1], Q4_K, dw, wg, dX, batch, rows, cols)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert b[-1].item() == 7.0
+
+
+def test_gemm_pack_rejects_unsupported_shapes(hip, torch_mod):
+    torch = torch_mod
+    w = dev(torch, hip.synth_random_weights(Q4_K, 5, 40, 2048, 0.02))
+    wg = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    with pytest.raises(hip.QuantError):
+        hip.pack_weights_gemm(Q4_K, w, wg, 40, 2048)   # rows % 32
+    w6 = dev(torch, hip.synth_random_weights(Q6_K, 5, 32, 2048, 0.02))
+    with pytest.raises(hip.QuantError):
+        hip.pack_weights_gemm(Q6_K, w6, wg, 32, 2048)  # Q4_K only
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
 @pytest.mark.parametrize("batch,rows,cols", [(2, 64, 2048), (3, 1001, 2048), (5, 6144, 2048), (4, 65536, 2048),
                                              (7, 1001, 2048), (8, 8192, 2048), (15, 260, 2048),
