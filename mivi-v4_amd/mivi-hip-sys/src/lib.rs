@@ -129,6 +129,13 @@ pub mod ffi {
         pub fn mivi_hip_quantized_matmul_rows_packed(out: *mut f32, out_len: usize, ggml_type: i32,
             packed: *const u8, packed_len: usize, inputs: *const f32, inputs_len: usize, batch: usize, rows: usize,
             cols: usize, stream: *mut c_void) -> i32;
+        // the row products' operand layout (no counterpart in the reference)
+        pub fn mivi_hip_gemm_packed_size(ggml_type: i32, rows: usize, cols: usize) -> usize;
+        pub fn mivi_hip_pack_weights_gemm(ggml_type: i32, src: *const u8, src_len: usize, dst: *mut u8,
+            dst_len: usize, rows: usize, cols: usize, stream: *mut c_void) -> i32;
+        pub fn mivi_hip_quantized_matmul_rows_gemm_packed(out: *mut f32, out_len: usize, ggml_type: i32,
+            weights: *const u8, weights_len: usize, wg: *const u8, wg_len: usize, inputs: *const f32,
+            inputs_len: usize, batch: usize, rows: usize, cols: usize, stream: *mut c_void) -> i32;
         // lib.rs:35-72
         pub fn mivi_hip_dequantize_slice(ggml_type: i32, bytes: *const u8, bytes_len: usize, out: *mut f32,
             out_len: usize, stream: *mut c_void) -> i32;
