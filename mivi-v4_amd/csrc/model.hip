@@ -1193,36 +1193,59 @@ __global__ void __launch_bounds__(64) kv_store_rows_kernel(AttnArgs a, int pos0)
     attn_store_current<KVP>(a, kvh, pos, cs, sn, kcur, vcur, true);
 }
 
-// Prefill tile ShortConv (ssm.rs:174-300, kernel size ks <= 8): channel d
-// walks the tile's rows in order, r = 0..rows-1, with the window of the
-// sequence's current state (the phase's buffer, updated in place): bx =
-// B*X, window shift, conv = sum_k w_k s_k, out = C * conv. proj rows are
-// [B | C | X] (3 * dim), out rows dim.
+// Prefill tile ShortConv (ssm.rs:174-300, kernel size ks <= 8): out row r =
+// C_r * conv_r, conv_r = sum_k w_k s_k over the window s_k = BX(r - ks + 1 +
+// k), BX(j) = B_j * X_j for the tile's rows j >= 0 and the sequence's state
+// (the phase's buffer) before them, st[ks + j] for j < 0; the state becomes
+// BX(rows - ks + k), updated in place. proj rows are [B | C | X] (3 * dim),
+// out rows dim. Thread (channel d, chunk c) computes rows 8c .. 8c + 7 with
+// every load issued up front (the window of each row depends only on its
+// inputs, not on the rows before); chunk 0's thread of a channel is the
+// only one that reads the state (rows below ks - 1), so it writes the new
+// one after. The same products and sums, in the same order, as the
+// sequential window: bx = B * X, conv = w_0 s_0 + w_1 s_1 + ...
+constexpr int kConvRowsChunk = 8;
 __global__ void __launch_bounds__(256) conv_rows_kernel(const float* proj, float* out, int rows, int dim, int ks,
                                                         const float* conv_w, int conv_mode, float* st_a, float* st_b,
                                                         const int* phase) {
+    constexpr int R = kConvRowsChunk;
     const int d = blockIdx.x * 256 + threadIdx.x;
     if (d >= dim) return;
+    const int r0 = blockIdx.y * R;
     float* st = ((*phase) & 1 ? st_b : st_a) + (size_t)d * ks;
-    float s[8], w[8];
-    for (int k = 0; k < ks; k++) {
-        s[k] = st[k];
+    float w[8];
+    for (int k = 0; k < ks; k++)
         w[k] = conv_mode == 0 ? conv_w[(size_t)d * ks + k] : conv_mode == 1 ? conv_w[k] : 1.0f / (float)ks;
+    // BX(j) for j = r0 - (ks - 1) .. r0 + R - 1: bx[j - r0 + ks - 1]
+    float bx[R + 7], cv[R];
+    auto BX = [&](int j) {
+        if (j < 0) return st[ks + j];
+        const float* p = proj + (size_t)j * 3 * dim;
+        return p[d] * p[2 * dim + d];
+    };
+#pragma unroll
+    for (int i = 0; i < R + 7; i++) {
+        const int j = r0 - (ks - 1) + i;
+        bx[i] = i < R + ks - 1 && j < rows ? BX(j) : 0.f;
     }
-    for (int r = 0; r < rows; r++) {
-        const float* p = proj + (size_t)r * 3 * dim;
-        const float bx = p[d] * p[2 * dim + d];
-        for (int k = 0; k + 1 < ks; k++) s[k] = s[k + 1];
-        s[ks - 1] = bx;
+#pragma unroll
+    for (int i = 0; i < R; i++) cv[i] = r0 + i < rows ? proj[(size_t)(r0 + i) * 3 * dim + dim + d] : 0.f;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        if (r0 + i >= rows) break;
         float conv = 0.f;
         if (ks == 3) {
-            conv = w[0] * s[0] + w[1] * s[1] + w[2] * s[2];  // ssm.rs:250-252
+            conv = w[0] * bx[i] + w[1] * bx[i + 1] + w[2] * bx[i + 2];  // ssm.rs:250-252
         } else {
-            for (int k = 0; k < ks; k++) conv += w[k] * s[k];
+            for (int k = 0; k < ks; k++) conv += w[k] * bx[i + k];
         }
-        out[(size_t)r * dim + d] = p[dim + d] * conv;
+        out[(size_t)(r0 + i) * dim + d] = cv[i] * conv;
     }
-    for (int k = 0; k < ks; k++) st[k] = s[k];
+    if (blockIdx.y == 0) {
+        float ns[8];
+        for (int k = 0; k < ks; k++) ns[k] = BX(rows - ks + k);  // (reads the old state before the writes)
+        for (int k = 0; k < ks; k++) st[k] = ns[k];
+    }
 }
 
 __global__ void iota_kernel(int* dst, int base, int n) {
@@ -1902,7 +1925,9 @@ int32_t enqueue_prefill_tile(mivi_model* m, size_t b, size_t p0, size_t rows, hi
             if ((rc = launch_rows(L.in_proj.type, PRO_RMSNORM, g, s))) return rc;
             const size_t ks = c.ssm_conv_kernel;
             const int mode = (L.conv && L.conv_len >= (size_t)D * ks) ? 0 : (L.conv && L.conv_len >= ks) ? 1 : 2;
-            hipLaunchKernelGGL(conv_rows_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, m->pf_p1,
+            hipLaunchKernelGGL(conv_rows_kernel,
+                               dim3((unsigned)((D + 255) / 256), (unsigned)((R + kConvRowsChunk - 1) / kConvRowsChunk)),
+                               dim3(256), 0, s, m->pf_p1,
                                m->pf_ao, R, D, (int)ks, L.conv, mode, st.conv_a + l * (size_t)D * ks,
                                st.conv_b + l * (size_t)D * ks, &m->ctrl->phase[b]);
             g = {};
