@@ -133,16 +133,23 @@ __host__ __device__ inline int cols_groups(int epi, int n0, int n) {
 }
 
 // Q4_K rows in the column kernel's order (launch_pack_q4k_cols): per group,
-// per superblock s of the row (cols / 256 of them), kColsChunkBytes: the 16
-// rows' 16-byte headers (d, dmin, scales), then the code bytes as two 1 KB
-// halves, lane l = j + 16 kg holding in each 16 bytes of row j: codes
-// [32 g + 8 kg, + 8) for g = 0, 1 (first half) and g = 2, 3 (second), the
-// bytes of its two B operands per 64-value unit. Every load of the kernel
-// is then one contiguous 256 B or 1 KB (the GGUF rows give it 16 rows x 32
-// bytes per load instruction, bound by the L1's cache-line rate).
+// per superblock s of the row (cols / 256 of them), kColsChunkBytes:
+//   [0, 256)      the 16 rows' headers, 16 bytes at 16 j: d | dmin << 16
+//                 (fp16), the sub-block scales sc0..sc7 and the mins
+//                 m0..m3 as bytes (get_scale_min_k4 decoded, q4_k_m.rs:11-58)
+//   [256, 320)    the mins m4..m7 of row j, 4 bytes at 256 + 4 j
+//   [320, 2368)   the code bytes as two 1 KB halves, lane l = j + 16 kg
+//                 holding in each 16 bytes of row j: codes [32 g + 8 kg, + 8)
+//                 for g = 0, 1 (first half) and g = 2, 3 (second), the bytes
+//                 of its two B operands per 64-value unit.
+// Every load of the kernel is then one contiguous 256 B, 64 B or 1 KB (the
+// GGUF rows give it 16 rows x 32 bytes per load instruction, bound by the
+// L1's cache-line rate), and no scale needs unpacking beyond a byte select.
 // rows_host[16 grp + j]: the device address of group grp's row j (any valid
 // row where the group has none there).
-constexpr int kColsChunkBytes = 16 * 144;
+constexpr int kColsMinsOff = 256;
+constexpr int kColsCodesOff = 320;
+constexpr int kColsChunkBytes = kColsCodesOff + 2048;
 
 // rows x cols Q4_K (rows % 32 == 0, cols % 256 == 0) into the operand layout
 // of the matrix-core row products (launch_rows with GemvSeg::wg): the fp16

@@ -1426,16 +1426,34 @@ struct ColStage {
         m = nanmax(m, dpp_mov<0x4E>(m));
         m = nanmax(m, dpp_mov<0xB1>(m));
     }
-    // mt, sst: the column's max |u| and sum x^2 over its P parts
-    template <int PS>
+    // mt, sst: the column's max |u| and sum x^2 over its P parts. HL: the
+    // sub-block sums go out as fp16 hi / lo pairs of X / sx (the min-term
+    // operands of the packed-row kernel, see gemv_q4k_cols_kernel), sx = the
+    // power of two returned in *sxo with |X| / sx < 2^15
+    template <int PS, bool HL = false>
     __device__ __forceinline__ float finish(const mivi::GemvArgs& a, int h, float mt, float sst, uint32_t* dig,
-                                            float* xsum) {
+                                            float* xsum, float* sxo = nullptr) {
         const int l = threadIdx.x & 63, o = h * V;
         // RMSNORM: x = u / rms (math.rs:7-22); else scale 1
         const float scale = PRO == mivi::PRO_RMSNORM ? 1.0f / sqrtf(sst / (float)K + a.eps) : 1.0f;
         const bool finite = mt > 0.f && mt <= 3.40282347e38f;
         const float mul = finite ? kDigMul / mt : 0.0f;
         const float sc = ((mt - mt) + mt * scale) * (2.0f / 127.0f);
+        // |X| <= 32 max|u| scale < 2^e (non-finite or zero: 1; the product
+        // is then NaN through sc or zero anyway)
+        float inv_sx = 1.0f;
+        if constexpr (HL) {
+            const float bound = 32.0f * mt * scale;
+            int e = 0;
+            if (bound > 0.f && bound <= 3.40282347e38f) {
+                frexpf(bound, &e);
+                e = e < -100 ? -100 : e;
+            } else {
+                e = 15;
+            }
+            inv_sx = ldexpf(1.0f, 15 - e);
+            if (sxo) *sxo = ldexpf(1.0f, e - 15);
+        }
 #pragma unroll
         for (int i = 0; i < NL; i++) {
             const int w = (o >> 2) + l + 64 * ch(i);  // the dword of values 4w .. 4w + 3
@@ -1452,7 +1470,22 @@ struct ColStage {
             t += dpp_mov<0xB1>(t);
             t += dpp_mov<0x4E>(t);
             t += dpp_mov<0x12C>(t);
-            if ((l & 7) == 0) xsum[w >> 3] = t * scale;
+            if ((l & 7) == 0) {
+                if constexpr (HL) {
+                    // sub-block q = w >> 3: halves 4 (q >> 1) + (q & 1) (hi)
+                    // and + 2 (lo), i.e. per superblock b and lane group kg
+                    // of the products: Xhi[2kg], Xhi[2kg+1], Xlo[2kg], Xlo[2kg+1]
+                    const float xs = (t * scale) * inv_sx;
+                    const _Float16 hi = (_Float16)xs;
+                    const _Float16 lo = (_Float16)(xs - (float)hi);
+                    _Float16* xh = (_Float16*)xsum;
+                    const int q = w >> 3;
+                    xh[4 * (q >> 1) + (q & 1)] = hi;
+                    xh[4 * (q >> 1) + 2 + (q & 1)] = lo;
+                } else {
+                    xsum[w >> 3] = t * scale;
+                }
+            }
         }
         return sc;
     }
@@ -1468,8 +1501,12 @@ __device__ __forceinline__ mivi::GemvArgs gemv_col_group(const mivi::GemvArgs& a
     return v;
 }
 
-template <int PRO, int EPI, int KT, int NG, int DQ, int KS = 1, bool CW = false>
-__global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// WPE: waves per SIMD the launch places (2: one workgroup per CU, whose
+// waves may then take up to 256 registers; 4: two workgroups per CU)
+template <int PRO, int EPI, int KT, int NG, int DQ, int KS = 1, bool CW = false, int WPE = 2>
+__global__ void __launch_bounds__(kColWG) __attribute__((amdgpu_waves_per_eu(2, WPE))) gemv_q4k_cols_kernel(const mivi::GemvArgs a0) {
     static_assert(KT == 1024 || KT == 2048 || KT == 8192, "decode depths (per K split)");
     static_assert(DQ == 4 || DQ == 8, "depth slices per team");
     // KS > 1: the depth a0.K = KS * KT in KS slices, slice blockIdx.y; the
@@ -1494,6 +1531,7 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     __shared__ __attribute__((aligned(16))) uint32_t dig[NCM][4 * PS];
     __shared__ __attribute__((aligned(16))) float xsum[NCM][K / 32];
     __shared__ float scol[NCM];
+    __shared__ float sxc[CW ? NCM : 1];     // CW: the columns' min-term scales sx
     __shared__ float red[2][NCM][P];        // parts' max |u| and sum x^2
     __shared__ float xq[R][2][DQ - 1][NG][64];  // waves 1.. -> wave 0 of a team, by group-step parity
     // RMSNORM: the weight vector, loaded once for the workgroup's columns
@@ -1533,6 +1571,7 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     // one re-reads the last): a branch around a load makes the compiler wait
     // for it before the next chunk's use, a memory latency per superblock.
     u32x4 hdr[PD];
+    uint32_t mxr[CW ? PD : 1];  // CW: mins m4..m7 of row j
     u32x2 cq[PD][4];
     auto load = [&](int slot, int st, int bb) {
         st = st < cnt ? st : cnt - 1;
@@ -1542,7 +1581,9 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
             grp = grp < ngroups ? grp : ngroups - 1;
             const uint8_t* p = a.cw + ((size_t)grp * (nb * KS) + ks * nb + wq * SQ + bb) * mivi::kColsChunkBytes;
             hdr[slot] = ldg16(p + 16 * j);
-            const u32x4 c0 = ldg16(p + 256 + 16 * lane), c1 = ldg16(p + 256 + 1024 + 16 * lane);
+            mxr[slot] = *(const __attribute__((address_space(1))) uint32_t*)(p + mivi::kColsMinsOff + 4 * j);
+            const u32x4 c0 = ldg16(p + mivi::kColsCodesOff + 16 * lane);
+            const u32x4 c1 = ldg16(p + mivi::kColsCodesOff + 1024 + 16 * lane);
             cq[slot][0] = u32x2{c0.x, c0.y};
             cq[slot][1] = u32x2{c0.z, c0.w};
             cq[slot][2] = u32x2{c1.x, c1.y};
@@ -1585,14 +1626,27 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
                 sst += red[1][task_c][h];
             }
         }
-        const float sc = stg.template finish<PS>(gemv_column(ax, task_c), task_h, mt, sst, dig[task_c], xsum[task_c]);
+        const float sc = stg.template finish<PS, CW>(gemv_column(ax, task_c), task_h, mt, sst, dig[task_c],
+                                                      xsum[task_c], (lane == 0 && task_h == 0) ? &sxc[task_c] : nullptr);
         if (lane == 0 && task_h == 0) scol[task_c] = sc;
     }
     __syncthreads();
     if (cnt == 0) return;  // workgroup-uniform
-    float s[NG];
+    float s[NG], sx[NG];
 #pragma unroll
-    for (int G = 0; G < NG; G++) s[G] = scol[min(4 * G + kg, ncol - 1)];
+    for (int G = 0; G < NG; G++) {
+        s[G] = scol[min(4 * G + kg, ncol - 1)];
+        sx[G] = CW ? sxc[min(4 * G + kg, ncol - 1)] : 0.f;
+    }
+    // CW min-term product (v_mfma_f32_16x16x16_f16): A row i = j = 4q + t is
+    // column 4t + q (rows of t >= NG or past ncol repeat a column; their
+    // outputs are not used), its k-group kg the fp16 pairs
+    // Xhi[2kg], Xhi[2kg+1], Xlo[2kg], Xlo[2kg+1] of a superblock; B column j
+    // the mins m[2kg], m[2kg+1], m[2kg], m[2kg+1] of row j. Lane (j, kg)
+    // receives D[4kg + G][j] = sum over the superblock of m X / sx for row j
+    // and column 4G + kg. msel picks bytes 2kg, 2kg+1 of {mins m4..m7 : m0..m3}.
+    const _Float16* xhA = (const _Float16*)xsum[min(4 * (j & 3) + (j >> 2), ncol - 1)] + 4 * kg;
+    const uint32_t msel = (uint32_t)(2 * kg) | (uint32_t)(2 * kg + 1) << 8 | 0x0C0C0000u;
     const int ci = j >> 2, pi = j & 3;  // A operand of this lane: column 4G + ci, plane pi
     const uint32_t* dA[NG];
 #pragma unroll
@@ -1603,9 +1657,9 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
     auto step = [&](const int st, const int s0, auto refill) {
         // this wave's superblocks of the group, each summed in int32 over its
         // four units before the float steps
-        float part[NG];
+        float part[NG], pm[NG];
 #pragma unroll
-        for (int G = 0; G < NG; G++) part[G] = 0.f;
+        for (int G = 0; G < NG; G++) part[G] = pm[G] = 0.f;
 #pragma unroll
         for (int bb = 0; bb < SQ; bb++) {
             const int slot = s0 + bb, b = wq * SQ + bb;
@@ -1613,6 +1667,73 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
             u32x2 q[4];
 #pragma unroll
             for (int g = 0; g < 4; g++) q[g] = cq[slot][g];
+            if constexpr (CW) {
+                // packed header: h.x = d | dmin << 16, h.y, h.z the scales
+                // sc0..sc7 as bytes, h.w and mxr the mins m0..m7 as bytes
+                const uint32_t mx = mxr[slot];
+                if constexpr (decltype(refill)::value) load(slot, st + U, bb);
+                const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
+                const uint32_t mp = __builtin_amdgcn_perm(mx, h.w, msel);
+                const float ma = (float)(mp & 0xFFu), mb = (float)((mp >> 8) & 0xFFu);
+                const f16x4 Bm = {(_Float16)ma, (_Float16)mb, (_Float16)ma, (_Float16)mb};
+                const f16x4 Ax = *(const f16x4*)(xhA + 16 * b);
+                const f32x4 Dm = __builtin_amdgcn_mfma_f32_16x16x16f16(Ax, Bm, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                // the eight 6-bit scales, each extracted once (a byte select
+                // folded into every multiply costs a multiply and an add per
+                // product instead of one v_mad_i32_i24)
+                int scs[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) scs[k] = (int)(((k < 4 ? h.y : h.z) >> (8 * (k & 3))) & 63u);
+                // every digit operand of the superblock from LDS, then every
+                // product, then the scale chains: the LDS and matrix-core
+                // latencies overlap instead of adding up per sub-block pair
+                long Al[4][NG], Ah[4][NG];
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+#pragma unroll
+                    for (int G = 0; G < NG; G++) {
+                        const int w0 = (256 * b + 64 * g) / 4;
+                        const u32x2 alo = *(const u32x2*)(dA[G] + w0);
+                        const u32x2 ahi = *(const u32x2*)(dA[G] + w0 + 8);
+                        Al[g][G] = (long)(((uint64_t)alo.y << 32) | alo.x);
+                        Ah[g][G] = (long)(((uint64_t)ahi.y << 32) | ahi.x);
+                    }
+                i32x4 Dl[4][NG], Dh[4][NG];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const long blo = (long)(((uint64_t)(q[g].y & 0x0F0F0F0Fu) << 32) | (q[g].x & 0x0F0F0F0Fu));
+                    const long bhi = (long)(((uint64_t)((q[g].y >> 4) & 0x0F0F0F0Fu) << 32) | ((q[g].x >> 4) & 0x0F0F0F0Fu));
+                    const i32x4 z = {0, 0, 0, 0};
+#pragma unroll
+                    for (int G = 0; G < NG; G++) {
+                        Dl[g][G] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Al[g][G], blo, z, 0, 0, 0);
+                        Dh[g][G] = __builtin_amdgcn_mfma_i32_16x16x32_i8(Ah[g][G], bhi, z, 0, 0, 0);
+                    }
+                }
+                // one chain per plane over the superblock's eight sub-blocks:
+                // |D| < 2^16, sc < 64, below 2^31 (exact)
+                int Ac[NG][3];
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+#pragma unroll
+                    for (int G = 0; G < NG; G++)
+#pragma unroll
+                        for (int e = 0; e < 3; e++) {
+                            Ac[G][e] = g == 0 ? mul24(Dl[g][G][e], scs[2 * g]) : mad24(Dl[g][G][e], scs[2 * g], Ac[G][e]);
+                            asm("" : "+v"(Ac[G][e]));
+                            Ac[G][e] = mad24(Dh[g][G][e], scs[2 * g + 1], Ac[G][e]);
+                            asm("" : "+v"(Ac[G][e]));
+                        }
+#pragma unroll
+                for (int G = 0; G < NG; G++) {
+                    // q4_k_m.rs:144-214 per superblock: d s sum sc (q . x~/s),
+                    // and the min term dmin sum m X / sx, taken off at the end
+                    const float f = fmaf((float)Ac[G][2], kDig2, fmaf((float)Ac[G][1], kDig1, (float)Ac[G][0]));
+                    part[G] = fmaf(d * s[G], f, part[G]);
+                    pm[G] = fmaf(dmin, Dm[G], pm[G]);
+                }
+                continue;
+            }
             if constexpr (decltype(refill)::value) load(slot, st + U, bb);
             const float d = half_bits_to_f32(h.x), dmin = half_bits_to_f32(h.x >> 16);
             int AL[NG][3], AH[NG][3];  // low- and high-nibble sub-blocks, one product per step
@@ -1661,6 +1782,10 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
                                      fmaf((float)(AL[G][1] + AH[G][1]), kDig1, (float)(AL[G][0] + AH[G][0])));
                 part[G] += (d * s[G]) * f - dmin * Mac[G];
             }
+        }
+        if constexpr (CW) {
+#pragma unroll
+            for (int G = 0; G < NG; G++) part[G] = fmaf(-sx[G], pm[G], part[G]);
         }
         // the team's DQ slices of the depth, summed by its wave 0 in slice
         // order (one LDS exchange; the buffer alternates with the step's parity)
@@ -1712,26 +1837,34 @@ __global__ void __launch_bounds__(kColWG) gemv_q4k_cols_kernel(const mivi::GemvA
 // Launch of the batched kernel over ngr row groups and gy column groups:
 // two teams of four waves a workgroup (DQ = 4) where the groups fill 1.5
 // workgroups per CU at K = 2048, else one team of eight (DQ = 8); at most one
-// workgroup per CU, whose staging its waves then share.
+// workgroup per CU and column group, whose staging its waves then share
+// (two column groups may then place two workgroups on a CU).
 template <int PRO, int EPI, int KT, int NG>
 void launch_cols(const mivi::GemvArgs& a, int ngr, int gy, hipStream_t s) {
     const int cus = mivi::num_cus();
+    auto go = [&](auto dq, int gc) {
+        constexpr int DQ = decltype(dq)::value;
+        const dim3 grid(gc, gy);
+        if (NG == 1 && (size_t)gc * gy > (size_t)cus) {
+            if constexpr (NG == 1) {
+                if (a.cw)
+                    hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, DQ, 1, true, 4>), grid, dim3(kColWG), 0, s, a);
+                else
+                    hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, DQ, 1, false, 4>), grid, dim3(kColWG), 0, s, a);
+            }
+        } else if (a.cw) {
+            hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, DQ, 1, true>), grid, dim3(kColWG), 0, s, a);
+        } else {
+            hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, DQ>), grid, dim3(kColWG), 0, s, a);
+        }
+    };
     if constexpr (KT == 2048) {
         if (2 * ngr >= 3 * cus) {
-            const int gc = std::max(1, std::min((ngr + 1) / 2, cus));
-            if (a.cw)
-                hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 4, 1, true>), dim3(gc, gy), dim3(kColWG), 0,
-                                   s, a);
-            else
-                hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 4>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+            go(std::integral_constant<int, 4>{}, std::max(1, std::min((ngr + 1) / 2, cus)));
             return;
         }
     }
-    const int gc = std::max(1, std::min(ngr, cus));
-    if (a.cw)
-        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8, 1, true>), dim3(gc, gy), dim3(kColWG), 0, s, a);
-    else
-        hipLaunchKernelGGL((gemv_q4k_cols_kernel<PRO, EPI, KT, NG, 8>), dim3(gc, gy), dim3(kColWG), 0, s, a);
+    go(std::integral_constant<int, 8>{}, std::max(1, std::min(ngr, cus)));
 }
 
 // Products added into y (the residual adds: the FFN down projection at K =
@@ -3317,7 +3450,7 @@ int32_t launch_pack_q6k(const uint8_t* src, uint8_t* dst, size_t rows, size_t co
 }
 
 // One thread per (group, superblock, lane slot l = j + 16 kg): its 32 code
-// bytes, and (kg = 0) row j's header.
+// bytes, and (kg = 0) row j's header with the scales and mins decoded.
 __global__ void __launch_bounds__(kWG) pack_q4k_cols_kernel(const uint64_t* __restrict__ rows, int ngroups, int nbt,
                                                             uint8_t* __restrict__ dst) {
     const size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
@@ -3330,9 +3463,17 @@ __global__ void __launch_bounds__(kWG) pack_q4k_cols_kernel(const uint64_t* __re
     u32x2 c[4];
 #pragma unroll
     for (int g = 0; g < 4; g++) c[g] = *(const u32x2*)(src + 16 + 32 * g + 8 * kg);
-    *(u32x4*)(d + 256 + 16 * l) = u32x4{c[0].x, c[0].y, c[1].x, c[1].y};
-    *(u32x4*)(d + 256 + 1024 + 16 * l) = u32x4{c[2].x, c[2].y, c[3].x, c[3].y};
-    if (kg == 0) *(u32x4*)(d + 16 * j) = *(const u32x4*)src;
+    *(u32x4*)(d + kColsCodesOff + 16 * l) = u32x4{c[0].x, c[0].y, c[1].x, c[1].y};
+    *(u32x4*)(d + kColsCodesOff + 1024 + 16 * l) = u32x4{c[2].x, c[2].y, c[3].x, c[3].y};
+    if (kg == 0) {
+        const u32x4 h = *(const u32x4*)src;
+        uint32_t sc[8], mn[8];
+#pragma unroll
+        for (int g = 0; g < 4; g++) q4k_scales(h.y, h.z, h.w, g, sc[2 * g], mn[2 * g], sc[2 * g + 1], mn[2 * g + 1]);
+        auto bytes4 = [](const uint32_t* v) { return v[0] | v[1] << 8 | v[2] << 16 | v[3] << 24; };
+        *(u32x4*)(d + 16 * j) = u32x4{h.x, bytes4(sc), bytes4(sc + 4), bytes4(mn)};
+        *(uint32_t*)(d + kColsMinsOff + 4 * j) = bytes4(mn + 4);
+    }
 }
 
 int32_t launch_pack_q4k_cols(const uint8_t* const* rows_host, int ngroups, size_t cols, uint8_t* dst,

@@ -125,9 +125,10 @@ def test_batched_column_layout_matches_gguf_rows(hip, monkeypatch, B):
     # a model with max_batch > 1 keeps its all-Q4_K projections packed in the
     # batched column kernels' group order (q|k|v, out_proj / wo, in_proj in
     # conv-channel groups, gate|up in SwiGLU groups, down); against the same
-    # model on its GGUF rows (MIVI_NO_COLS_PACK) the products are the same up
-    # to the order in which the residual adds' depth slices land (atomic
-    # adds): logits within 1e-5 of their largest value, same greedy tokens
+    # model on its GGUF rows (MIVI_NO_COLS_PACK) the products agree to float
+    # rounding (the packed rows' min terms run on the fp16 matrix cores, and
+    # the residual adds' depth slices land in any order): logits within 1e-5
+    # of their largest value, same greedy tokens
     from mivi_hip.synthmodel import build_hybrid
     img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
                        ctx_len=1024, seed=11)
