@@ -789,11 +789,15 @@ __global__ void __launch_bounds__(64 * W, 2) attn_q8_mfma_kernel(AttnArgs a) {
     const float* sn = a.rope_sin + (size_t)pos * (HD / 2);
 
     // 1. the split holding the current token stores its K/V first (then reads
-    //    it back like any cached token)
+    //    it back like any cached token). Only this wave reads that row in this
+    //    launch (the token's group lies in no other split, and later launches
+    //    see it across the kernel boundary), so the store needs workgroup
+    //    scope: an agent-scope fence would write back and invalidate the
+    //    XCD's whole L2 under every other workgroup there (4 us a launch)
     if (g1 == ng && !a.keep_cache) {
         attn_store_current<MIVI_KV_Q8_0>(a, kvh, pos, cs, sn, cur[wave][0], cur[wave][1], true);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
 
     // 2. group loads, q8g_* layout: a wave-uniform group address plus fixed
