@@ -1301,7 +1301,10 @@ __global__ void __launch_bounds__(kWG) gemv_kq_stream_kernel(const mivi::GemvArg
 // (q4_k_m.rs:144-214). The digits are those of the one-column kernels
 // (ColStage), but the one-column kernels take a float step per 64-value unit,
 // so a batched column agrees with its one-column GEMV to float rounding, not
-// bit for bit. Waves 1.. of a team hand
+// bit for bit. On rows packed by launch_pack_q4k_cols (CW) the scales and
+// mins arrive decoded, the eight scales feed a single chain per plane, and
+// the min terms run on v_mfma_f32_16x16x16_f16 (the columns' sub-block sums
+// as fp16 hi / lo pairs against the rows' mins; see the kernel). Waves 1.. of a team hand
 // their partial row sums to wave 0 through LDS. Digits sit in LDS (8 KB per
 // column at K = 2048: three planes and the zero plane, padded apart against
 // bank conflicts).
