@@ -1602,6 +1602,17 @@ __global__ void __launch_bounds__(kColWG) __attribute__((amdgpu_waves_per_eu(2, 
     };
 #pragma unroll
     for (int q = 0; q < PD; q++) load(q, q / SQ, q % SQ);
+    // EPI_CONV: the first group step's conv windows and weights (wave 0 of a
+    // team, lanes j = 3i < 15 of each column), loaded with the weights so the
+    // epilogue waits for no memory
+    ConvPre cpre0[EPI == mivi::EPI_CONV ? NG : 1];
+    if constexpr (EPI == mivi::EPI_CONV) {
+        const int r0 = row_of(0);
+#pragma unroll
+        for (int G = 0; G < NG; G++)
+            if (wq == 0 && cnt > 0 && j < 15 && j % 3 == 0 && r0 >= 0 && 4 * G + kg < ncol)
+                conv_prefetch(a, 4 * G + kg, r0, cpre0[G]);
+    }
     // the zero plane of every column
 #pragma unroll
     for (int c = 0; c < NCM; c++)
@@ -1812,7 +1823,10 @@ __global__ void __launch_bounds__(kColWG) __attribute__((amdgpu_waves_per_eu(2, 
                 } else if constexpr (EPI == mivi::EPI_CONV) {
                     // lanes j = 3i hold B of channel 5g + i, j + 1 its C, j + 2 its X
                     const float cv = __shfl(v, lane + 1, 64), xv = __shfl(v, lane + 2, 64);
-                    if (j < 15 && j % 3 == 0 && r >= 0 && cc < ncol) conv_epilogue(a, cc, r, v, cv, xv);
+                    if (j < 15 && j % 3 == 0 && r >= 0 && cc < ncol) {
+                        if (st == 0) conv_finish(a, cc, r, v, cv, xv, cpre0[G]);
+                        else conv_epilogue(a, cc, r, v, cv, xv);
+                    }
                 } else {
                     if (r >= 0 && cc < ncol) {
                         gfloat* y = (gfloat*)(sg.out(r) + cc * a.ys);
