@@ -208,10 +208,12 @@ typedef struct mivi_model_info {
     size_t weight_bytes;   /* device bytes of the weights: the GGUF tensor data plus the
                               packed copies kept beside it (Q6_K head, Q4_K and Q6_K row
                               quads; with max_batch > 1 the Q4_K projections in the batched
-                              column kernels' group order; the Q4_K projections' fp16 sc * q
-                              for the prefill's row products); MIVI_NO_PACK=1 at create leaves
-                              the copies out, MIVI_NO_COLS_PACK=1 the batched ones,
-                              MIVI_NO_GEMM_PACK=1 the row products' */
+                              column kernels' group order and the Q6_K head in 32-row tiles;
+                              the Q4_K projections' fp16 sc * q for the prefill's row
+                              products); MIVI_NO_PACK=1 at create leaves the copies out,
+                              MIVI_NO_COLS_PACK=1 the batched projections',
+                              MIVI_NO_HEAD_T32=1 the batched head's, MIVI_NO_GEMM_PACK=1 the
+                              row products' */
     size_t kv_bytes;       /* device bytes of K + V for all sequences */
 } mivi_model_info;
 

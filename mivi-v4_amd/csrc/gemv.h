@@ -159,6 +159,17 @@ inline size_t q4k_gemm_packed_bytes(size_t rows, size_t cols) {
     return rows * cols * 2 + rows / 32 * (cols / 256) * 640;
 }
 int32_t launch_pack_q4k_gemm(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
+// Q6_K in 32-row tiles (K = 2048, rows % 32 == 0), the batched head's copy:
+// each superblock of 32 rows laid out as the B operand of the 32 x 32 x 16
+// int8 matrix instruction, the size of the GGUF rows (launch_pack_q6k_t32).
+// launch_gemv_t32 runs ncol columns over it, eight per launch (one segment,
+// no or RMSNorm prologue, store or argmax epilogue; x 16-byte aligned, xs %
+// 4 == 0), every column's result equal to the one-column packed kernel's bit
+// for bit; an argmax launch writes t32_argmax_parts(n) partials per column.
+inline bool t32_layout(size_t rows, size_t cols) { return cols == 2048 && rows > 0 && rows % 32 == 0; }
+int32_t launch_pack_q6k_t32(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s);
+int32_t launch_gemv_t32(int pro, const GemvArgs& a, hipStream_t s);
+int t32_argmax_parts(int n);
 int32_t launch_pack_q4k_cols(const uint8_t* const* rows_host, int ngroups, size_t cols, uint8_t* dst,
                              hipStream_t s);
 

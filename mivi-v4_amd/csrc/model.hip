@@ -1579,6 +1579,7 @@ struct mivi_model {
     float* d_aux = nullptr;  // decoded f32 vectors
     Mat embd, head;
     uint8_t* head_packed = nullptr;  // Q6_K head in the packed unit-plane layout (else null)
+    uint8_t* head_t32 = nullptr;     // max_batch > 1: the Q6_K head in 32-row tiles for batched steps (else null)
     const float* out_norm = nullptr;
     std::vector<Layer> layers;
     float *rope_cos = nullptr, *rope_sin = nullptr;
@@ -1845,18 +1846,24 @@ int32_t enqueue_step(mivi_model* m, size_t b0, size_t nb, bool logits, bool argm
         g.packed = m->head_packed ? 1 : 0;
         g.ncol = ncol; g.xs = z.x; g.ys = z.logits;
         const int pro = m->out_norm ? PRO_RMSNORM : PRO_NONE;
-        const int np = argmax ? gemv_argmax_parts(m->head.type, D, (int)c.vocab_size, m->head_packed != nullptr) : 0;
+        // batched: the 32-row tile copy when there is one
+        const bool t32 = ncol > 1 && m->head_t32;
+        if (t32) { g.seg[0].W = m->head_t32; g.packed = 0; }
+        auto launch = [&]() { return t32 ? launch_gemv_t32(pro, g, s) : launch_gemv_ex(m->head.type, pro, g, s); };
+        const int np = !argmax ? 0
+                       : t32   ? t32_argmax_parts((int)c.vocab_size)
+                               : gemv_argmax_parts(m->head.type, D, (int)c.vocab_size, m->head_packed != nullptr);
         if (np > 0 && np <= kMaxArgmaxParts) {
             g.epilogue = EPI_ARGMAX;
             g.part_val = s0.part_val;
             g.part_idx = s0.part_idx;
             g.ps = z.parts;
-            rc = launch_gemv_ex(m->head.type, pro, g, s);
+            rc = launch();
             if (rc == MIVI_OK) parts = np;
             else if (rc != MIVI_ERR_UNSUPPORTED) return rc;
             g.epilogue = EPI_STORE;
         }
-        if (!parts && (rc = launch_gemv_ex(m->head.type, pro, g, s))) return rc;
+        if (!parts && (rc = launch())) return rc;
     }
     hipLaunchKernelGGL(argmax_advance_kernel, dim3((unsigned)nb), dim3(1024), 0, s, parts ? s0.part_val : s0.logits,
                        parts ? s0.part_idx : nullptr, parts ? parts : (int)c.vocab_size, &m->ctrl->tok[b0],
@@ -2241,6 +2248,15 @@ extern "C" int32_t mivi_hip_model_create(const uint8_t* img, size_t len, size_t 
         if ((rc = launch_pack_q6k(m->head.w, m->head_packed, c.vocab_size, c.dim, nullptr))) return fail(rc);
         if (hipDeviceSynchronize() != hipSuccess) return fail(set_error(MIVI_ERR_HIP, "packing the head failed"));
         c.weight_bytes += bytes;
+        // batched steps read the head once for up to eight sequences on the
+        // 32 x 32 x 16 int8 matrix instruction (same results bit for bit)
+        if (max_batch > 1 && t32_layout(c.vocab_size, c.dim) && !getenv("MIVI_NO_HEAD_T32")) {
+            if ((rc = m->alloc(&m->head_t32, bytes))) return fail(rc);
+            if ((rc = launch_pack_q6k_t32(m->head.w, m->head_t32, c.vocab_size, c.dim, nullptr))) return fail(rc);
+            if (hipDeviceSynchronize() != hipSuccess)
+                return fail(set_error(MIVI_ERR_HIP, "packing the batched head failed"));
+            c.weight_bytes += bytes;
+        }
     }
     // one-column decode GEMVs stream the projections packed (bit-identical
     // to the GGUF rows): Q4_K as row quads (matrix cores), Q6_K (the

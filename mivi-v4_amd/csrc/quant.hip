@@ -563,6 +563,7 @@ constexpr float kDig1 = 1.0f / 256.0f, kDig2 = 1.0f / 65536.0f;
 constexpr float kDigMul = 4161536.0f;  // 127 * 2^15: Y = rint(x * kDigMul / max|x|)
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float nanmax(float a, float b) { return (b > a || b != b) ? b : a; }
 
@@ -2162,61 +2163,19 @@ __global__ void __launch_bounds__(kWG) gemv_q6k_quad_kernel(const mivi::GemvArgs
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
-// Up to eight columns (sequences) against the same row quads, so a batched
-// head reads its quads once per step. Eight waves per workgroup, wave c
-// forming column c's digits; each wave then takes its own quads as above.
-// The 3 ncol digit planes (plane 3c + p = plane p of column c) sit in LDS in
-// groups of four, laid out for the 4 x 4 x 4 instruction: entry (G, g,
-// lane 4b + v) is the 16 digits of plane 4G + v at slot g of the lane's
-// unit, so one 1 KB read gives a group's A operands for a slot, and lane
-// 4b + j receives the four planes' sums for row j. The codes enter as
-// c - 32 (signed bytes: (c + 0x60) ^ 0x80), which adds the Q6_K offset in
-// the instruction; the integer sums are the one-column kernel's. The float
-// steps run in its order, and the cross-lane sum of the eight columns is a
-// reduce-scatter over the same butterfly (lane bits 5, 4, 3, then 2), after
-// which lane l with bit 2 clear holds column (l >> 3) & 7, row l & 3: every
-// column's result equals the one-column kernel's bit for bit.
-// NGR groups (3: up to four columns, 6: up to eight); planes past 3 ncol are
-// zeros.
-constexpr int kQuad8Waves = 8, kQuad8WG = 64 * kQuad8Waves;
-
-template <int PRO, int EPI, int PD, int NGR>
-__global__ void __launch_bounds__(kQuad8WG) gemv_q6k_quad8_kernel(const mivi::GemvArgs a) {
-    constexpr int K = 2048, NL = K / 256, NCM = 4 * NGR / 3;
-    static_assert(NGR == 3 || NGR == 6, "four or eight columns");
-    __shared__ u32x4 Ab[NGR][8][64];  // [group][slot][lane]
-    __shared__ float scol[kQuad8Waves];
-    const int nquads = a.seg[0].n / 4;
-    const uint8_t* W = a.seg[0].W;
-    const int ncol = a.ncol;  // 1..NCM, workgroup-uniform
-    const int npl = 3 * ncol;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int jv = lane & 3;
-    const int nw = gridDim.x * kQuad8Waves, wid = blockIdx.x * kQuad8Waves + wave;
-    const int cnt = wid < nquads ? (nquads - wid + nw - 1) / nw : 0;  // wave-uniform
-
-    u32x4 w[PD][6];
-    u32x2 scw[PD];
-    uint32_t dw[PD];
-    auto load = [&](int p, int st) {  // as gemv_q6k_quad_kernel's
-        st = st < cnt ? st : cnt - 1;
-        int q = wid + st * nw;
-        q = q < 0 ? 0 : q < nquads ? q : nquads - 1;
-        const uint8_t* base = W + (size_t)q * kQuadBytes;
-        const uint8_t* cb = base + 64 * (q & 1);
-        const uint8_t* db = base + ((q & 1) ? 0 : 6656);
-#pragma unroll
-        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(cb + 1024 * k + 16 * lane);
-        scw[p] = *(const __attribute__((address_space(1))) u32x2*)(cb + 6144 + 8 * lane);
-        dw[p] = *(const __attribute__((address_space(1))) uint32_t*)(db + 4 * (4 * jv + (lane >> 4)));
-    };
-    // column `wave`'s activations: chunk i is values 4 (lane + 64 i) .. + 3,
-    // which thread lane + 64 (i & 3) of the one-column kernel holds
-    const bool stager = wave < ncol && wave < NCM;  // wave-uniform
+// One column of the eight-column kernels' activations (K = 2048) as
+// base-256 digit planes, formed in the one-column kernel's order so that
+// every column's sums are that kernel's: load() issues the column's loads
+// (chunk i is values 4 (lane + 64 i) .. + 3, which thread lane + 64 (i & 3)
+// of the one-column kernel holds), finish() forms each chunk's three plane
+// dwords, hands them to put(i, d) and returns the column's scale s.
+template <int PRO>
+struct ColB256 {
+    static constexpr int K = 2048, NL = K / 256;
     f32x4 u[NL];
     f32x4 nwt[PRO == mivi::PRO_RMSNORM ? NL : 1];
-    if (stager) {
-        const float* x = a.x + (size_t)wave * a.xs;
+    __device__ __forceinline__ void load(const mivi::GemvArgs& a, int col, int lane) {
+        const float* x = a.x + (size_t)col * a.xs;
 #pragma unroll
         for (int i = 0; i < NL; i++) u[i] = *(const gf32x4*)(x + 4 * (lane + 64 * i));
         if constexpr (PRO == mivi::PRO_RMSNORM) {
@@ -2224,15 +2183,8 @@ __global__ void __launch_bounds__(kQuad8WG) gemv_q6k_quad8_kernel(const mivi::Ge
             for (int i = 0; i < NL; i++) nwt[i] = *(const gf32x4*)(a.norm_w + 4 * (lane + 64 * i));
         }
     }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int p = 0; p < PD; p++) load(p, p);
-    __builtin_amdgcn_sched_barrier(0);
-    // planes 3 ncol .. 4 NGR - 1 read zeros
-#pragma unroll
-    for (int G = 0; G < NGR; G++)
-        if (4 * G + (int)(threadIdx.x & 3) >= npl) Ab[G][threadIdx.x >> 6][threadIdx.x & 63] = u32x4{0, 0, 0, 0};
-    if (stager) {
+    template <class Put>
+    __device__ __forceinline__ float finish(const mivi::GemvArgs& a, Put put) {
         float v[NL][4];
 #pragma unroll
         for (int i = 0; i < NL; i++) { v[i][0] = u[i].x; v[i][1] = u[i].y; v[i][2] = u[i].z; v[i][3] = u[i].w; }
@@ -2285,24 +2237,90 @@ __global__ void __launch_bounds__(kQuad8WG) gemv_q6k_quad8_kernel(const mivi::Ge
         }
         const bool finite = m > 0.f && m <= 3.40282347e38f;
         const float mul = finite ? kDigMul / m : 0.0f;
-        const float sc = ((m - m) + m * scale) * (2.0f / 127.0f);
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            uint32_t d[3];
+            digits4_b256(v[i], mul, d[0], d[1], d[2]);
+            put(i, d);
+        }
+        return ((m - m) + m * scale) * (2.0f / 127.0f);
+    }
+};
+
+// Up to eight columns (sequences) against the same row quads, so a batched
+// head reads its quads once per step. Eight waves per workgroup, wave c
+// forming column c's digits; each wave then takes its own quads as above.
+// The 3 ncol digit planes (plane 3c + p = plane p of column c) sit in LDS in
+// groups of four, laid out for the 4 x 4 x 4 instruction: entry (G, g,
+// lane 4b + v) is the 16 digits of plane 4G + v at slot g of the lane's
+// unit, so one 1 KB read gives a group's A operands for a slot, and lane
+// 4b + j receives the four planes' sums for row j. The codes enter as
+// c - 32 (signed bytes: (c + 0x60) ^ 0x80), which adds the Q6_K offset in
+// the instruction; the integer sums are the one-column kernel's. The float
+// steps run in its order, and the cross-lane sum of the eight columns is a
+// reduce-scatter over the same butterfly (lane bits 5, 4, 3, then 2), after
+// which lane l with bit 2 clear holds column (l >> 3) & 7, row l & 3: every
+// column's result equals the one-column kernel's bit for bit.
+// NGR groups (3: up to four columns, 6: up to eight); planes past 3 ncol are
+// zeros.
+constexpr int kQuad8Waves = 8, kQuad8WG = 64 * kQuad8Waves;
+
+template <int PRO, int EPI, int PD, int NGR>
+__global__ void __launch_bounds__(kQuad8WG) gemv_q6k_quad8_kernel(const mivi::GemvArgs a) {
+    constexpr int NCM = 4 * NGR / 3;
+    static_assert(NGR == 3 || NGR == 6, "four or eight columns");
+    __shared__ u32x4 Ab[NGR][8][64];  // [group][slot][lane]
+    __shared__ float scol[kQuad8Waves];
+    const int nquads = a.seg[0].n / 4;
+    const uint8_t* W = a.seg[0].W;
+    const int ncol = a.ncol;  // 1..NCM, workgroup-uniform
+    const int npl = 3 * ncol;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int jv = lane & 3;
+    const int nw = gridDim.x * kQuad8Waves, wid = blockIdx.x * kQuad8Waves + wave;
+    const int cnt = wid < nquads ? (nquads - wid + nw - 1) / nw : 0;  // wave-uniform
+
+    u32x4 w[PD][6];
+    u32x2 scw[PD];
+    uint32_t dw[PD];
+    auto load = [&](int p, int st) {  // as gemv_q6k_quad_kernel's
+        st = st < cnt ? st : cnt - 1;
+        int q = wid + st * nw;
+        q = q < 0 ? 0 : q < nquads ? q : nquads - 1;
+        const uint8_t* base = W + (size_t)q * kQuadBytes;
+        const uint8_t* cb = base + 64 * (q & 1);
+        const uint8_t* db = base + ((q & 1) ? 0 : 6656);
+#pragma unroll
+        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(cb + 1024 * k + 16 * lane);
+        scw[p] = *(const __attribute__((address_space(1))) u32x2*)(cb + 6144 + 8 * lane);
+        dw[p] = *(const __attribute__((address_space(1))) uint32_t*)(db + 4 * (4 * jv + (lane >> 4)));
+    };
+    const bool stager = wave < ncol && wave < NCM;  // wave-uniform
+    ColB256<PRO> col;
+    if (stager) col.load(a, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PD; p++) load(p, p);
+    __builtin_amdgcn_sched_barrier(0);
+    // planes 3 ncol .. 4 NGR - 1 read zeros
+#pragma unroll
+    for (int G = 0; G < NGR; G++)
+        if (4 * G + (int)(threadIdx.x & 3) >= npl) Ab[G][threadIdx.x >> 6][threadIdx.x & 63] = u32x4{0, 0, 0, 0};
+    if (stager) {
         // dword lane + 64 i of a plane: 16 B chunk k = lane / 4 + 16 i of
         // unit 4 i + kb, quarter q (chunk k of a plane is unit
         // 4 (k >> 4) + 2 ((k >> 3) & 1) + (k & 1), quarter (k >> 1) & 3),
         // dword e of the chunk
         uint32_t* A32 = (uint32_t*)&Ab[0][0][0];
         const int kb = 2 * ((lane >> 5) & 1) + ((lane >> 2) & 1), q = (lane >> 3) & 3, e = lane & 3;
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            uint32_t d[3];
-            digits4_b256(v[i], mul, d[0], d[1], d[2]);
+        const float sc = col.finish(a, [&](int i, const uint32_t (&d)[3]) {
             const int g = 4 * (i >> 2) + q, bb = 4 * (i & 3) + kb;
 #pragma unroll
             for (int p = 0; p < 3; p++) {
                 const int pl = 3 * wave + p;
                 A32[(((pl >> 2) * 8 + g) * 64 + 4 * bb + (pl & 3)) * 4 + e] = d[p];
             }
-        }
+        });
         if (lane == 0) scol[wave] = sc;
     }
     __syncthreads();
@@ -2419,6 +2437,268 @@ __global__ void __launch_bounds__(kQuad8WG) gemv_q6k_quad8_kernel(const mivi::Ge
 #pragma unroll
     for (int p = 0; p < PD; p++)
         if (st + p < cnt) compute(p, st + p);
+    if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+}
+
+// ------------------------------------ Q6_K 32-row tiles for batched columns
+//
+// The batched head's copy of a Q6_K matrix with K = 2048 and a multiple of 32
+// rows (launch_pack_q6k_t32, the model loader for max_batch > 1): chunk
+// c = 8 T + s holds superblock s of rows 32 T .. 32 T + 31 in 6720 bytes at
+// 6720 c, laid out as the B operand of v_mfma_i32_32x32x16_i8: lane
+// l = n + 32 hh supplies row 32 T + n at values 8 hh .. 8 hh + 7 of every
+// 16-value sub-block. Offsets from o = 64 for odd c (0 for even c):
+//   [0, 6144)     codes, 16 B per lane at 1024 k + 16 l (k = 0..5). Sub-blocks
+//                 2P and 2P + 1 are dwords 3P .. 3P + 2 of the lane's 24:
+//                 sixteen 6-bit codes, c_0..c_7 of sub-block 2P and
+//                 c_8..c_15 of 2P + 1, packed as the row quads pack a slot
+//                 (byte e of dword 3P + m: c_{4m+e} in bits 0-5, bits 2m,
+//                 2m + 1 of c_{12+e} in bits 6-7)
+//   [6144, 6656)  row n's sixteen sub-block scales at 6144 + 16 n
+// and the 64 bytes of d (row n's fp16 at 2 n) follow at 6656 for even c and
+// lead at 0 for odd c, so every 1 KB wave load of codes is line-aligned (as
+// in the row quads). The copy has the GGUF matrix's size.
+constexpr int kT32Bytes = 6720;
+
+// f(std::integral_constant<int, I>) for I = I0 .. N - 1, unrolled at compile
+// time (register arrays indexed by I stay in registers)
+template <int I0, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I0 < N) {
+        f(std::integral_constant<int, I0>{});
+        static_for<I0 + 1, N>(f);
+    }
+}
+
+// Superblock of step j of a tile: 0, 4, 2, 6, 1, 5, 3, 7 (j's bits reversed),
+// the order in which the row's unit values fold into the one-column
+// kernel's cross-lane sum.
+__host__ __device__ constexpr int t32_superblock(int j) { return ((j & 1) << 2) | (j & 2) | (j >> 2); }
+
+// Up to eight columns against 32-row tiles on v_mfma_i32_32x32x16_i8, one
+// 16-value sub-block per instruction. A row m = 8 p + c is digit plane p of
+// column c (staged into LDS as the eight-column quad kernel stages them; rows
+// 24-31 and columns past ncol are zeros), B the tile's codes as c - 32 (signed
+// bytes (c + 0x60) ^ 0x80), so lane l = n + 32 hh receives, for row n of the
+// tile, the plane sums of columns 4 hh .. 4 hh + 3 (register 4 p + j: plane
+// p, column 4 hh + j). Each sum is scaled by its sub-block's scale with exact
+// 24-bit multiplies and summed over the four sub-blocks of a unit of the
+// one-column kernel (half h, sub-blocks 8 h + jj + 2 q of one superblock), so
+// the unit sums are that kernel's integers; each unit's float step, and the
+// sum of the row's 32 unit values in the order of that kernel's butterfly
+// over its 16 lanes (units b and b + 16 in lane b; b xor 8, 4, 2, 1), run
+// in registers as superblocks arrive in t32_superblock order. Every column's
+// result therefore equals the one-column kernel's bit for bit. PD
+// superblocks in flight per wave; the waves take tiles wid, wid + nw, ...
+template <int PRO, int EPI, int PD>
+__global__ void __launch_bounds__(kQuad8WG) gemv_q6k_t32_kernel(const mivi::GemvArgs a) {
+    constexpr int K = 2048, NS = K / 256, NSB = K / 16;
+    constexpr int AROW = 65;  // u32x2 per sub-block row of A in LDS (64 lanes and one of padding)
+    static_assert(NS % PD == 0, "ring slots at fixed superblock steps");
+    __shared__ u32x2 Ab[NSB * AROW];  // A operands: [sub-block][lane], eight digits each
+    __shared__ float scol[kQuad8Waves];
+    const int ntiles = a.seg[0].n / 32;
+    const uint8_t* W = a.seg[0].W;
+    const int ncol = a.ncol;  // 1..8, workgroup-uniform
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 31, hh = lane >> 5;
+    const int nw = gridDim.x * kQuad8Waves, wid = blockIdx.x * kQuad8Waves + wave;
+    const int cnt = wid < ntiles ? (ntiles - wid + nw - 1) / nw : 0;  // tiles, wave-uniform
+
+    u32x4 w[PD][6];
+    u32x4 scw[PD];
+    uint32_t dbits[PD];
+    // step t = 8 i + j: tile wid + i nw, superblock t32_superblock(j)
+    auto load = [&](int p, int i, int j) __attribute__((always_inline)) {
+        const size_t c = (size_t)(wid + i * nw) * NS + t32_superblock(j);
+        const uint8_t* base = W + c * kT32Bytes;
+        const uint8_t* cb = base + 64 * (c & 1);
+        const uint8_t* db = base + ((c & 1) ? 0 : 6656);
+#pragma unroll
+        for (int k = 0; k < 6; k++) w[p][k] = ldg16_nt(cb + 1024 * k + 16 * lane);
+        scw[p] = *(const __attribute__((address_space(1))) u32x4*)(cb + 6144 + 16 * n);
+        dbits[p] = *(const __attribute__((address_space(1))) uint16_t*)(db + 2 * n);
+    };
+    const bool stager = wave < ncol;  // wave-uniform
+    ColB256<PRO> col;
+    if (stager) col.load(a, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    if (cnt > 0) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) load(p, 0, p);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // rows without a column (m >= 24, or column m % 8 >= ncol) read zeros
+    for (int idx = threadIdx.x; idx < NSB * 64; idx += kQuad8WG) {
+        const int m = idx & 31;
+        if (m >= 24 || (m & 7) >= ncol) Ab[(idx >> 6) * AROW + (idx & 63)] = u32x2{0, 0};
+    }
+    if (stager) {
+        // chunk i, dword j4 = lane + 64 i of the column: values 4 j4 .. + 3,
+        // sub-block j4 / 4, lane half (j4 >> 1) & 1, dword j4 & 1 of the 8 B
+        uint32_t* A32 = (uint32_t*)Ab;
+        const float sc = col.finish(a, [&](int i, const uint32_t (&d)[3]) {
+            const int j4 = lane + 64 * i;
+            const int base = ((j4 >> 2) * AROW + wave + 32 * ((j4 >> 1) & 1)) * 2 + (j4 & 1);
+#pragma unroll
+            for (int p = 0; p < 3; p++) A32[base + 16 * p] = d[p];  // row 8 p + wave
+        });
+        if (lane == 0) scol[wave] = sc;
+    }
+    __syncthreads();
+
+    float s_c[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) s_c[cc] = scol[4 * hh + cc < ncol ? 4 * hh + cc : 0];
+    float best[4];
+    int bidx[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) { best[cc] = -INFINITY; bidx[cc] = 0x7FFFFFFF; }
+    auto write_part = [&]() {
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            float bv = best[cc];
+            int bi = bidx[cc];
+#pragma unroll
+            for (int o = 1; o < 32; o <<= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+            const int cl = 4 * hh + cc;
+            if (n == 0 && cl < ncol) {
+                a.part_val[cl * a.ps + wid] = bv;
+                a.part_idx[cl * a.ps + wid] = bi;
+            }
+        }
+    };
+    if (cnt == 0) {  // wave-uniform; no barrier follows
+        if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
+        return;
+    }
+
+    // unit values of the row (per column cc): W the first superblock's term,
+    // V a unit's value v_b (b < 8), A4 the first level of the sum
+    float Wu[4][4], Vu[4][4], A4[4][4];
+    auto compute = [&](auto J, int tile) __attribute__((always_inline)) {
+        constexpr int j = decltype(J)::value, p = j % PD, sb = t32_superblock(j);
+        const float d = half_bits_to_f32(dbits[p]);
+        const i32x16 zero = {};
+#pragma unroll
+        for (int uu = 0; uu < 4; uu++) {
+            const int h = uu >> 1, jj = uu & 1;
+            // (opaque from here: this unit's code and scale decode is not
+            // hoisted above it, which would hold every unit's decoded
+            // codes and scales at once)
+#pragma unroll
+            for (int k = 0; k < 6; k++) asm volatile("" : "+v"(w[p][k]));
+            asm volatile("" : "+v"(scw[p]));
+            i32x16 D[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                // sub-block isl = 8 h + 2 q + jj: pair P = 4 h + q, codes c_0..c_7
+                // (jj = 0) or c_8..c_15 (jj = 1) of its three dwords, as c - 32
+                const int isl = 8 * h + 2 * q + jj, D0 = 3 * (isl >> 1);
+                const uint32_t W0 = w[p][D0 >> 2][D0 & 3];
+                const uint32_t W1 = w[p][(D0 + 1) >> 2][(D0 + 1) & 3];
+                const uint32_t W2 = w[p][(D0 + 2) >> 2][(D0 + 2) & 3];
+                uint32_t b0, b1;
+                if (jj == 0) {
+                    b0 = W0 & 0x3F3F3F3Fu;
+                    b1 = W1 & 0x3F3F3F3Fu;
+                } else {
+                    b0 = W2 & 0x3F3F3F3Fu;
+                    b1 = ((W0 >> 6) & 0x03030303u) | ((W1 >> 4) & 0x0C0C0C0Cu) | ((W2 >> 2) & 0x30303030u);
+                }
+                b0 = (b0 + 0x60606060u) ^ 0x80808080u;
+                b1 = (b1 + 0x60606060u) ^ 0x80808080u;
+                // (volatile: read at each step, not hoisted out of the tile loop)
+                const u32x2 A = *(volatile __attribute__((address_space(3))) u32x2*)&Ab[(16 * sb + isl) * AROW + lane];
+                D[q] = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)(((uint64_t)A.y << 32) | A.x),
+                                                             (long)(((uint64_t)b1 << 32) | b0), zero, 0, 0, 0);
+            }
+            int acc[3][4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int isl = 8 * h + 2 * q + jj;
+                const int scv = __builtin_amdgcn_sbfe((int)scw[p][isl >> 2], 8 * (isl & 3), 8);
+                // |D| < 2^17, |sc| <= 128: exact 24-bit multiplies (as the quad
+                // kernels); each sum passes an empty asm so the four steps stay
+                // a chain of multiply-adds (v_mad_i32_i24) instead of separate
+                // multiplies and three-way adds
+#pragma unroll
+                for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+                    for (int cc = 0; cc < 4; cc++) {
+                        if (q == 0) acc[pl][cc] = mul24(D[q][4 * pl + cc], scv);
+                        else acc[pl][cc] += mul24(D[q][4 * pl + cc], scv);
+                        asm volatile("" : "+v"(acc[pl][cc]));
+                    }
+            }
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const float f = fmaf((float)acc[2][cc], kDig2, fmaf((float)acc[1][cc], kDig1, (float)acc[0][cc]));
+                // unit b = 4 (sb & 3) + uu of the one-column kernel, term i = sb >> 2
+                // (each result passes an empty volatile asm, which keeps this
+                // unit's arithmetic ahead of the next unit's loads and products:
+                // the products would otherwise all be issued first and spilled)
+                if ((j & 1) == 0) {  // superblock sb < 4: the first term of v_b
+                    float v = 0.f;
+                    v += d * f;
+                    asm volatile("" : "+v"(v));
+                    Wu[uu][cc] = v;
+                } else {  // sb + 4: v_b complete
+                    float v = Wu[uu][cc];
+                    v += d * f;
+                    if (j == 1 || j == 5) v = v;                        // v_b, b = uu or 4 + uu
+                    else if (j == 3) v = Vu[uu][cc] + v;                // a_b = v_b + v_(b+8), b = uu
+                    else v = A4[uu][cc] + (Vu[uu][cc] + v);             // j = 7: a_(4+uu), then + a_uu
+                    asm volatile("" : "+v"(v));
+                    if (j == 3) A4[uu][cc] = v;
+                    else Vu[uu][cc] = v;
+                }
+            }
+            // one unit's four results live at a time (hoisting the next
+            // unit's products spills)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (j == NS - 1) {
+            // Vu[b][cc] = a_b + a_(b+4) (b < 4); then b xor 2, b xor 1
+            const int r = 32 * tile + n;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                float y = (Vu[0][cc] + Vu[2][cc]) + (Vu[1][cc] + Vu[3][cc]);
+                y *= s_c[cc];
+                const int cl = 4 * hh + cc;
+                if (cl < ncol) {
+                    gfloat* yp = (gfloat*)(a.seg[0].y + r + cl * a.ys);
+                    if (a.accumulate) __builtin_amdgcn_global_atomic_fadd_f32(yp, y);
+                    else *yp = y;
+                    // sampler.rs:305-316: strictly greater wins, so NaN never does
+                    if constexpr (EPI == mivi::EPI_ARGMAX)
+                        if (y > best[cc]) { best[cc] = y; bidx[cc] = r; }
+                }
+            }
+        }
+    };
+    // Tiles with a successor refill every slot branch-free; the last tile
+    // refills only the steps that exist.
+    for (int i = 0; i < cnt; i++) {
+        const int tile = wid + i * nw;
+        if (i + 1 < cnt) {  // wave-uniform
+            static_for<0, NS>([&](auto J) __attribute__((always_inline)) {
+                constexpr int j = decltype(J)::value;
+                compute(J, tile);
+                load(j % PD, i + (j + PD) / NS, (j + PD) % NS);
+            });
+        } else {
+            static_for<0, NS>([&](auto J) __attribute__((always_inline)) {
+                constexpr int j = decltype(J)::value;
+                compute(J, tile);
+                if constexpr (j + PD < NS) load(j % PD, i, j + PD);
+            });
+        }
+    }
     if constexpr (EPI == mivi::EPI_ARGMAX) write_part();
 }
 
@@ -3269,6 +3549,34 @@ static GemvArgs column_args(const GemvArgs& a, int c0, int nc) {
     return v;
 }
 
+// one eight-wave workgroup per CU at most (64 KB of LDS each)
+int t32_grid(int n) { return std::max(1, std::min((n / 32 + kQuad8Waves - 1) / kQuad8Waves, num_cus())); }
+int t32_argmax_parts(int n) { return kQuad8Waves * t32_grid(n); }
+
+int32_t launch_gemv_t32(int pro, const GemvArgs& a, hipStream_t s) {
+    const int ncol = std::max(1, a.ncol);
+    if (a.nseg != 1 || !t32_layout((size_t)a.seg[0].n, (size_t)a.K) || (a.epilogue != EPI_STORE && a.epilogue != EPI_ARGMAX) ||
+        (pro != PRO_NONE && pro != PRO_RMSNORM) || (pro == PRO_RMSNORM && !a.norm_w) || ((uintptr_t)a.seg[0].W % 16) ||
+        ((uintptr_t)a.x % 16) || (ncol > 1 && a.xs % 4) ||
+        (a.epilogue == EPI_ARGMAX && (!a.part_val || !a.part_idx || (ncol > 1 && a.ps < t32_argmax_parts(a.seg[0].n)))))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no 32-row tile GEMV for this shape");
+    const dim3 grid((unsigned)t32_grid(a.seg[0].n));
+    // groups of at most eight columns
+    for (int c0 = 0; c0 < ncol; c0 += kMaxGemvCols) {
+        const GemvArgs v = column_args(a, c0, std::min(kMaxGemvCols, ncol - c0));
+#define LT(P, E) hipLaunchKernelGGL((gemv_q6k_t32_kernel<P, E, 2>), grid, dim3(kQuad8WG), 0, s, v)
+        if (pro == PRO_RMSNORM) {
+            if (a.epilogue == EPI_ARGMAX) LT(PRO_RMSNORM, EPI_ARGMAX); else LT(PRO_RMSNORM, EPI_STORE);
+        } else {
+            if (a.epilogue == EPI_ARGMAX) LT(PRO_NONE, EPI_ARGMAX); else LT(PRO_NONE, EPI_STORE);
+        }
+#undef LT
+    }
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
+}
+
+
 static int32_t launch_by_pro(int32_t t, int pro, const GemvArgs& a, int n, hipStream_t s) {
     switch (pro) {
     case PRO_NONE: return launch_pro<PRO_NONE>(t, a, n, s);
@@ -3445,6 +3753,39 @@ __global__ void __launch_bounds__(kWG) pack_q6k_kernel(const uint8_t* __restrict
         q[52 * nu + 2 * b + 1] = p[209];
     }
 }
+
+// One thread per (chunk, lane) of the 32-row tile layout (gemv_q6k_t32_kernel):
+// the lane's 96 code bytes and, for lanes l < 32, its row's scales and d.
+__global__ void __launch_bounds__(kWG) pack_q6k_t32_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                           size_t nchunks) {
+    const size_t i = (size_t)blockIdx.x * kWG + threadIdx.x;
+    if (i >= nchunks * 64) return;
+    const size_t c = i >> 6;
+    const int l = (int)(i & 63), n = l & 31, hh = l >> 5;
+    const size_t T = c / 8;
+    const int sb = (int)(c % 8);
+    const uint8_t* blk = src + (32 * T + n) * 1680 + (size_t)sb * 210;
+    uint8_t* o = dst + c * kT32Bytes + 64 * (c & 1);  // codes and scales
+    uint8_t* od = dst + c * kT32Bytes + ((c & 1) ? 0 : 6656);
+    for (int P = 0; P < 8; P++) {
+        uint32_t cd[16];
+        for (int e = 0; e < 16; e++) {
+            const int v = 16 * (2 * P + (e >> 3)) + 8 * hh + (e & 7);  // value of the superblock
+            cd[e] = q6_code(blk, v >> 7, (v >> 5) & 3, v & 31);
+        }
+        for (int m = 0; m < 3; m++) {
+            uint32_t word = 0;
+            for (int e = 0; e < 4; e++) word |= (cd[4 * m + e] | (((cd[12 + e] >> (2 * m)) & 3u) << 6)) << (8 * e);
+            const int D = 3 * P + m;
+            *(uint32_t*)(o + 1024 * (D >> 2) + 16 * l + 4 * (D & 3)) = word;
+        }
+    }
+    if (hh == 0) {
+        for (int k = 0; k < 16; k++) o[6144 + 16 * n + k] = blk[192 + k];
+        od[2 * n] = blk[208];
+        od[2 * n + 1] = blk[209];
+    }
+}
 }  // namespace
 
 namespace mivi {
@@ -3491,6 +3832,16 @@ __global__ void __launch_bounds__(kWG) pack_q4k_cols_kernel(const uint64_t* __re
         *(u32x4*)(d + 16 * j) = u32x4{h.x, bytes4(sc), bytes4(sc + 4), bytes4(mn)};
         *(uint32_t*)(d + kColsMinsOff + 4 * j) = bytes4(mn + 4);
     }
+}
+
+int32_t launch_pack_q6k_t32(const uint8_t* src, uint8_t* dst, size_t rows, size_t cols, hipStream_t s) {
+    if (!t32_layout(rows, cols) || ((uintptr_t)dst % 16))
+        return set_error(MIVI_ERR_UNSUPPORTED, "no 32-row tile layout for %zu x %zu Q6_K", rows, cols);
+    const size_t nchunks = rows / 32 * (cols / 256);
+    hipLaunchKernelGGL(pack_q6k_t32_kernel, dim3((unsigned)((nchunks * 64 + kWG - 1) / kWG)), dim3(kWG), 0, s, src,
+                       dst, nchunks);
+    MIVI_HIP_CHECK(hipGetLastError());
+    return MIVI_OK;
 }
 
 int32_t launch_pack_q4k_cols(const uint8_t* const* rows_host, int ngroups, size_t cols, uint8_t* dst,

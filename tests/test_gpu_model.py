@@ -156,6 +156,44 @@ def test_batched_column_layout_matches_gguf_rows(hip, monkeypatch, B):
     assert np.array_equal(tp, tr)
 
 
+@pytest.mark.parametrize("B", [3, 8, 11])
+def test_batched_head_tiles_match_row_quads(hip, monkeypatch, B):
+    # a model with max_batch > 1 keeps its Q6_K head also in 32-row tiles for
+    # the batched steps (gemv_q6k_t32_kernel, v_mfma_i32_32x32x16_i8, eight
+    # sequences per launch); its logits equal the row-quad heads' (which equal
+    # the one-column head's) bit for bit. Q8_0 projections, whose batched
+    # products are the one-column ones, keep the rest of the step
+    # deterministic; 2085 tiles give some waves two tiles; 11 sequences take
+    # two launches
+    from mivi_hip import GgmlType
+    from mivi_hip.synthmodel import build_hybrid
+    vocab = 32 * 2085
+    img = build_hybrid(dim=2048, hidden=2048, n_layers=2, attn_layers=(1,), n_heads=32, n_kv=8, vocab=vocab,
+                       ctx_len=1024, weight_type=GgmlType.Q8_0, seed=17)
+    rng = np.random.default_rng(19)
+    prompts = [rng.integers(0, vocab, 4 + b) for b in range(B)]
+
+    def run(tiles):
+        if tiles:
+            monkeypatch.delenv("MIVI_NO_HEAD_T32", raising=False)
+        else:
+            monkeypatch.setenv("MIVI_NO_HEAD_T32", "1")
+        m = hip.Model(img, max_ctx=128, max_batch=B, kv_precision=2)
+        for b, pr in enumerate(prompts):
+            m.prefill(pr[:-1], seq=b)
+        lg = m.forward_batch([int(p[-1]) for p in prompts], [len(p) - 1 for p in prompts])
+        toks = m.generate_greedy([int(np.argmax(lg[b])) for b in range(B)], [len(p) for p in prompts], 4)
+        wb = m.info.weight_bytes
+        m.close()
+        return lg, toks, wb
+
+    lt, tt, wt = run(True)
+    lq, tq, wq = run(False)
+    assert wt - wq == vocab * 8 * 210  # the tile copy is counted
+    assert np.array_equal(lt, lq), np.max(np.abs(lt - lq))
+    assert np.array_equal(tt, tq)
+
+
 @pytest.mark.parametrize("prec,oprec", [(0, 0), (2, 100), (1, 1)])
 def test_chunked_prefill_matches_token_prefill_and_oracle(hip, oracle, small_img, prec, oprec):
     # PrefillStrategy::Chunked vs ::Token (model.rs:2110 tile == token): 149
