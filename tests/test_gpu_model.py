@@ -156,7 +156,7 @@ def test_batched_column_layout_matches_gguf_rows(hip, monkeypatch, B):
     assert np.array_equal(tp, tr)
 
 
-@pytest.mark.parametrize("B", [3, 8, 11])
+@pytest.mark.parametrize("B", [2, 3, 5, 8, 11])
 def test_batched_head_tiles_match_row_quads(hip, monkeypatch, B):
     # a model with max_batch > 1 keeps its Q6_K head also in 32-row tiles for
     # the batched steps (gemv_q6k_t32_kernel, v_mfma_i32_32x32x16_i8, eight
