@@ -1002,6 +1002,11 @@ __global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
     constexpr int HD = 64, G = kQ8GroupTokens;
     __shared__ __attribute__((aligned(16))) float qs[4][HD];       // [head][dim]
     __shared__ __attribute__((aligned(16))) uint32_t curw[2][32];  // owner: current K/V as stored (fp16 pairs)
+    // a group's p [head][token] and V [token][dim] (rows of 68 halves: the
+    // operand reads of four rows 4 apart fall in four bank ranges)
+    constexpr int VROW = 68;
+    __shared__ __attribute__((aligned(16))) float pt[4][G];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[G][VROW];
     const int lane = threadIdx.x & 63;
     int kvh, split;
     if (!attn_tile_of(a.n_kv_heads, a.nsplit, &kvh, &split)) return;  // workgroup-uniform
@@ -1117,11 +1122,15 @@ __global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
     }
 
     float m_run = -INFINITY, l_run = 0.f;  // head c (lane t + 16c)
-    float acc[4][16];                      // head h, dim 16c + i (lane t + 16c)
+    // P.V on v_mfma_f32_16x16x16_f16, K = the group's 16 tokens: A row 4h + i
+    // is head h's p as fp16 hi (i = 0) and lo (i = 1) parts (rows 4h + 2,
+    // 4h + 3 zero), B the V values as stored (dims 16j .. 16j + 15 for
+    // instruction j), so lane n + 16h accumulates head h's hi and lo sums
+    // for dim 16j + n in pv[j][0], pv[j][1], over every group of the split
+    f32x4 pv[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc[k][i] = 0.f;
+    for (int j = 0; j < 4; j++) pv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int am = lane & 15, akg = lane >> 4;  // operand lane: row / column, k group
 
     auto scores = [&](const F16Group& q) {
         const uint32_t kw[8] = {q.k0.x, q.k0.y, q.k0.z, q.k0.w, q.k1.x, q.k1.y, q.k1.z, q.k1.w};
@@ -1141,26 +1150,40 @@ __global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
             const float al = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
             m_run = m_new;
             l_run *= al;
-            float a0, a1, a2, a3;
-            rows_all(al, a0, a1, a2, a3);
+            // (the accumulator lanes n + 16c hold head c: the lane's own al)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                acc[0][i] *= a0; acc[1][i] *= a1; acc[2][i] *= a2; acc[3][i] *= a3;
-            }
+            for (int j = 0; j < 4; j++) pv[j] *= al;
         }
         const float p = __builtin_amdgcn_exp2f(s - m_run);  // v_exp_f32 (p <= 256)
         l_run += p;
-        float p0, p1, p2, p3;  // p of token t for heads 0..3
-        rows_all(p, p0, p1, p2, p3);
-        const uint32_t vw[8] = {q.v0.x, q.v0.y, q.v0.z, q.v0.w, q.v1.x, q.v1.y, q.v1.z, q.v1.w};
+        // p and V to LDS, read back in operand order
+        pt[c][t] = p;
+        uint2* vrow = (uint2*)&vt[t][16 * c];
+        vrow[0] = uint2{q.v0.x, q.v0.y}; vrow[1] = uint2{q.v0.z, q.v0.w};
+        vrow[2] = uint2{q.v1.x, q.v1.y}; vrow[3] = uint2{q.v1.z, q.v1.w};
+        __builtin_amdgcn_wave_barrier();
+        const f32x4 p4 = *(const f32x4*)&pt[am >> 2][4 * akg];
+        const int ai = am & 3;
+        half4_t A;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float vf = half_bits_to_f32((i & 1) ? vw[i >> 1] >> 16 : vw[i >> 1] & 0xFFFFu);
-            acc[0][i] = fmaf(p0, vf, acc[0][i]);
-            acc[1][i] = fmaf(p1, vf, acc[1][i]);
-            acc[2][i] = fmaf(p2, vf, acc[2][i]);
-            acc[3][i] = fmaf(p3, vf, acc[3][i]);
+        for (int r = 0; r < 4; r++) {
+            const _Float16 hi = (_Float16)p4[r];
+            const _Float16 lo = (_Float16)(p4[r] - (float)hi);  // exact: p = hi + lo to about 2^-22
+            A[r] = ai == 0 ? hi : ai == 1 ? lo : (_Float16)0.0f;
         }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // ds_read_b64_tr_b16: in each 16-lane group, lane 4r + q gives the
+            // address of 4 halves and lane i receives half i % 4 of the
+            // segments of lanes 4r + i / 4, r = 0..3 (checked on the GPU). Lane
+            // 16 kg + 4r + q addresses token 4 kg + r, dims 16j + 4q .. + 3, so
+            // lane n + 16 kg receives dim 16j + n of tokens 4 kg .. 4 kg + 3
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const s16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)&vt[4 * akg + (am >> 2)][16 * j + 4 * (am & 3)]);
+            pv[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(A, __builtin_bit_cast(half4_t, raw), pv[j], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();  // (the next group's writes after these reads)
     };
 
     // the score products of a group are issued one group ahead
@@ -1179,8 +1202,18 @@ __global__ void __launch_bounds__(64, 2) attn_f16_mfma_kernel(AttnArgs a) {
         }
     }
 
-    // 5. the split's partials
-    attn_write_partials(a, acc, m_run, l_run, kvh, hpk, split, t, c);
+    // 5. the split's partials: lane n + 16h holds head h's dims 16j + n
+    //    (hi + lo rows); l summed over the token lanes
+    l_run = row_sum16(l_run);
+    if (c < hpk) {
+        const size_t pi = (size_t)(kvh * hpk + c) * a.nsplit + split;
+#pragma unroll
+        for (int j = 0; j < 4; j++) a.part_acc[pi * HD + 16 * j + t] = pv[j][0] + pv[j][1];
+        if (t == 0) {
+            a.part_m[pi] = m_run * 0.69314718055994531f;
+            a.part_l[pi] = l_run;
+        }
+    }
 }
 
 // Prefill tile: K/V of tile row blockIdx.x (position pos0 + row, k/v at
