@@ -981,7 +981,11 @@ struct QHeads {
 //          group c (any order of k serves while A and B agree), so lane
 //          t + 16h receives head h's hi and lo sums for token t: products
 //          of fp16 values are exact, summed in f32;
-//  values  O[h][d] += p_h(t) v(t, d) in f32 on the VALU, as the Q8_0 kernel.
+//  values  v_mfma_f32_16x16x16_f16, four per group (dims 16j .. 16j + 15):
+//          A row 4h + i is head h's p at the group's tokens as fp16 hi
+//          (i = 0) and lo (i = 1) parts, B the V values as stored, both
+//          passed through a per-wave LDS tile; the accumulators hold the
+//          token sums across the split (lane n + 16h: dim 16j + n of head h).
 // The wave loads its query heads (and the owner, the split holding the
 // current token, its K and V) before its cache groups, so those small loads
 // wait for no group. The owner stores the current K/V after issuing its
