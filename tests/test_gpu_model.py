@@ -57,6 +57,24 @@ def test_small_model_steps_match_oracle(hip, oracle, small_img, prec, oprec):
     assert worst <= 1e-3, worst
 
 
+@pytest.mark.parametrize("n_heads,n_kv", [(4, 4), (12, 4)])
+def test_fp16_attention_heads_per_kv_match_oracle(hip, oracle, n_heads, n_kv):
+    # the fp16 matrix-core attention (P.V on v_mfma_f32_16x16x16_f16) with
+    # one and three query heads per kv head (the other shapes run in the
+    # tests above and the workloads: two and four), head_dim 64, 80 steps
+    # over a context that crosses several 16-token groups and splits
+    from mivi_hip.synthmodel import build_hybrid
+    img = build_hybrid(dim=64 * n_heads, hidden=512, n_layers=3, attn_layers=(0, 2), n_heads=n_heads, n_kv=n_kv,
+                       vocab=1024, ctx_len=4096, seed=31 + n_heads)
+    m = hip.Model(img, max_ctx=4096, kv_precision=2)
+    o = oracle.Model(img, max_ctx=4096, kv_precision=100)
+    toks = np.random.default_rng(37).integers(0, 1024, 80)
+    worst = 0.0
+    for p, t in enumerate(toks):
+        worst = max(worst, rel_err(m.forward(int(t), p), o.forward(int(t), p)))
+    assert worst <= 1e-3, worst
+
+
 def test_small_model_greedy_matches_oracle(hip, oracle, small_img):
     m = hip.Model(small_img, max_ctx=4096)
     o = oracle.Model(small_img, max_ctx=4096)
@@ -97,19 +115,20 @@ def test_batched_sequences_are_independent(hip, small_img):
         assert np.array_equal(out[:, b], one)
 
 
-@pytest.mark.parametrize("B", [3, 8])
-def test_batched_full_width_matches_single_sequences(hip, B):
+@pytest.mark.parametrize("B,vocab", [(3, 4096), (8, 4096), (5, 4100)])
+def test_batched_full_width_matches_single_sequences(hip, B, vocab):
     # dim 2048 (the decode shapes): the packed Q6_K head (3 and 8 columns in
     # one eight-wave launch, its argmax partials per column), the multi-column Q4_K projections on the matrix cores (3 and 8
     # columns at d = 2048, 3 and 4 + 4 at d = 8192) with the RMSNorm, conv and
     # SwiGLU stages; every sequence's greedy tokens equal its own
-    # single-sequence run bit for bit
+    # single-sequence run bit for bit (a vocabulary of 4100 rows, not a
+    # multiple of 32, keeps the batched head on the eight-column row quads)
     from mivi_hip.synthmodel import build_hybrid
-    img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=4096,
+    img = build_hybrid(dim=2048, hidden=8192, n_layers=3, attn_layers=(1,), n_heads=32, n_kv=8, vocab=vocab,
                        ctx_len=1024, seed=11)
     mb = hip.Model(img, max_ctx=256, max_batch=B)
     rng = np.random.default_rng(12)
-    prompts = [rng.integers(0, 4096, 6 + 3 * b) for b in range(B)]
+    prompts = [rng.integers(0, vocab, 6 + 3 * b) for b in range(B)]
     for b, pr in enumerate(prompts):
         mb.prefill(pr[:-1], seq=b)
     out = mb.generate_greedy([int(p[-1]) for p in prompts], [len(p) - 1 for p in prompts], 12)
